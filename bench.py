@@ -1,0 +1,166 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 token sampler on the headline configuration:
+B=64 rows x V=262144 fp32 logits, T 0.8, top-k 64, top-p 0.95, repetition penalty 1.05 over 512-token histories.
+
+A step is one fs_sample_batch call over the whole batch (penalty -> top-k -> softmax/top-p -> draw, one fused
+kernel) with inputs already resident in HBM. The logits rotate over enough copies (> 256 MB MALL) that every step
+streams its rows from HBM. Prints ONE JSON line with rows/s, the kernel's HBM roofline fraction (HIP events on
+the launch stream) and the CPU baseline (ferro's own sampler.cpp compiled by oracle/Makefile when present, else
+the oracle restatement) timed on this host's cores on a bounded sample of the same rows.
+"""
+import argparse
+import ctypes
+import json
+import os
+import re
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "sampled rows/s + logits HBM GB/s (% of peak), top-k/top-p, B=64, V=262144"
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "sample_kernel_cfg3_traffic.md")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def read_traffic():
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, calibrated)."""
+    try:
+        txt = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", txt)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(w, gpu_tok, budget_s):
+    """Rows of the same workload through ferro's CPU sampler on 1 core, repeated up to ~budget_s seconds."""
+    from oracle import oracle as O
+    kind = "reference" if O.ref_available() else "port"
+    rows_done, t_used, mism = 0, 0.0, 0
+    B = w.B
+    chunk = 8
+    b = 0
+    while t_used < budget_s:
+        sl = slice(b, b + chunk)
+        x = np.ascontiguousarray(w.logits[sl]).copy()
+        off = w.hist_off[b:b + chunk + 1] - w.hist_off[b]
+        h = w.hist[w.hist_off[b]:w.hist_off[b + chunk]]
+        t0 = time.perf_counter()
+        if kind == "reference":
+            tok = O.ref_sample_batch(x, h, off, w.params[sl], w.seeds[sl], nthreads=1, inplace=True)
+        else:
+            tok = O.sample_batch(x, h, off, w.params[sl], w.u[sl], nthreads=1)["tok"]
+        t_used += time.perf_counter() - t0
+        mism += int((tok != gpu_tok[sl]).sum())
+        rows_done += x.shape[0]
+        b = (b + chunk) % B
+    return dict(value=rows_done / t_used, unit="rows/s", cores=1, kind=kind,
+                sample=f"{rows_done} rows of the same B=64 x V=262144 workload (rows cycled), serial on 1 core "
+                       f"as ferro's server samples them ({t_used:.1f} s)",
+                token_mismatches_vs_gpu=mism)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the sampler path is built and measured on a single MI355X "
+              f"(--gpus {args.gpus} is not supported in this build)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from ferro_amd import workloads as W
+    from ferro_amd import _lib
+    from ferro_amd.sampler import Context
+
+    t0 = time.time()
+    w = W.config3()
+    log(f"workload {w.name}: B={w.B} V={w.V} generated in {time.time() - t0:.1f}s")
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    nrot = max(2, -(-2 * MALL_BYTES // w.logits.nbytes))
+    base = torch.from_numpy(w.logits).to(dev)
+    bufs = [base] + [base.clone() for _ in range(nrot - 1)]
+    params = torch.from_numpy(w.params.view(np.uint8).copy()).to(dev)
+    hist = torch.from_numpy(w.hist).to(dev)
+    hoff = torch.from_numpy(w.hist_off).to(dev)
+    u = torch.from_numpy(w.u).to(dev)
+    tok = torch.empty(w.B, dtype=torch.int32, device=dev)
+    keep = torch.empty(w.B, dtype=torch.int32, device=dev)
+    ctx = Context.default(dev)
+    L = _lib.lib()
+    stream = torch.cuda.current_stream()
+    sh = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    fixed = (w.B, w.V, P(hist), P(hoff), P(params), P(u), P(tok), 0, None, None, P(keep), sh)
+
+    def step(i):
+        x = bufs[i % nrot]
+        rc = L.fs_sample_batch(ctx.h, P(x), w.V, *fixed)
+        if rc != 0:
+            raise RuntimeError(f"fs_sample_batch returned {rc}")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    gpu_tok = tok.cpu().numpy().copy()
+
+    K = args.steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for i in range(K):
+        ev[i][0].record(stream)
+        step(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    t_end = time.perf_counter()
+    wall = t_end - t_start
+    kern_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    if not np.array_equal(tok.cpu().numpy(), gpu_tok):
+        raise RuntimeError("tokens changed between steps on identical inputs")
+
+    alg_bytes = w.algorithmic_bytes()
+    achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
+    traffic = read_traffic()
+    out = {
+        "metric": METRIC,
+        "value": w.B * K / wall,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": wall / K * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded: 90% N(0,1.5) + 10% 4*Student-t(3) logits, Zipf(1.1) histories)",
+        "config": {"workload": "cfg3_gemma_serving: B=64 x V=262144 fp32, T 0.8, top-k 64, top-p 0.95, "
+                               "repetition 1.05 over 512-token histories", "B": w.B, "V": w.V,
+                   "logit_copies_rotated": nrot},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "kernel": "fs::sample_kernel<32>", "kernel_ms": kern_ms, "algorithmic_bytes": alg_bytes},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(w, gpu_tok, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

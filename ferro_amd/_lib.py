@@ -1,0 +1,77 @@
+"""ctypes binding of the gfx950 sampler library (libferro_sampler.so, C ABI of include/ferro_sampler.h).
+
+There is no CPU fallback: if the library is missing or fails to load, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libferro_sampler.so")
+
+FS_OK = 0
+FS_E_INVALID = -1
+FS_E_HIP = -2
+FS_E_NOMEM = -3
+FS_E_DEVICE = -4
+FS_DEVERR_COUNT_OVERFLOW = 1
+FS_DEVERR_LARGE_K = 4
+
+# fs_row_params (include/ferro_sampler.h); field order follows ferro's SamplerParams (src/sampler.h:12-21).
+PARAMS_DTYPE = np.dtype([
+    ("temperature", np.float32), ("top_k", np.int32), ("top_p", np.float32), ("min_p", np.float32),
+    ("repetition_penalty", np.float32), ("frequency_penalty", np.float32), ("presence_penalty", np.float32),
+    ("repeat_last_n", np.int32), ("penalty_from", np.int32), ("reserved", np.int32),
+])
+assert PARAMS_DTYPE.itemsize == 40
+
+# Every symbol include/ferro_sampler.h declares, with its ctypes signature.
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+SIGNATURES = {
+    "fs_create": (ctypes.c_int, [_P]),
+    "fs_destroy": (ctypes.c_int, [_P]),
+    "fs_sample_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P]),
+    "fs_argmax_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P]),
+    "fs_verify": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P]),
+    "fs_device_error": (ctypes.c_int, [_P, _P, _P]),
+    "fs_rng_create": (ctypes.c_int, [ctypes.c_uint64, _P]),
+    "fs_rng_destroy": (ctypes.c_int, [_P]),
+    "fs_rng_next_u": (ctypes.c_int, [_P, _P, _I32]),
+    "fs_rng_copy": (ctypes.c_int, [_P, _P]),
+    "fs_strerror": (ctypes.c_char_p, [ctypes.c_int]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class SamplerError(RuntimeError):
+    pass
+
+
+def lib():
+    """Load the library (raises if it has not been built: run ferro_amd/build.py or __graft_entry__.build())."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise SamplerError(f"{LIB_PATH} is missing: build it with `python ferro_amd/build.py`")
+            L = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                f = getattr(L, name)
+                f.restype = res
+                f.argtypes = args
+            _lib = L
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != FS_OK:
+        msg = lib().fs_strerror(rc).decode()
+        raise SamplerError(f"{what} failed: {msg} ({rc})")

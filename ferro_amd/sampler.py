@@ -1,0 +1,261 @@
+"""Host-side mirror of ferro's sampler interface over the gfx950 kernels.
+
+- `SamplerParams` / `Sampler` mirror ferro::SamplerParams / ferro::Sampler (reference src/sampler.h:12-34): same
+  field names, defaults and meaning; `Sampler.sample(logits, n_vocab, history)` returns the token id exactly as
+  `int Sampler::sample(float*, int, const std::vector<int>&)` does, drawing from the same libstdc++ mt19937_64
+  stream (one draw per non-greedy call, none for greedy: sampler.cpp:19-23, 45-46).
+- `sample_batch`, `argmax_batch`, `verify` are the batched device entry points (fs_sample_batch, fs_argmax_batch,
+  fs_verify) on torch CUDA tensors, launched on torch's current stream.
+
+PyTorch only supplies device memory and streams; all sampling arithmetic runs in libferro_sampler.so.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from ._lib import PARAMS_DTYPE, FS_OK, SamplerError, check, lib
+
+__all__ = ["SamplerParams", "Sampler", "Context", "Rng", "params_array", "sample_batch", "argmax_batch", "verify",
+           "device_error", "PARAMS_DTYPE", "SamplerError"]
+
+
+@dataclass
+class SamplerParams:
+    """ferro::SamplerParams (src/sampler.h:12-21) plus the frequency/presence extension (0 = off)."""
+    temperature: float = 0.05
+    top_k: int = 50
+    top_p: float = 1.0
+    min_p: float = 0.0
+    repetition_penalty: float = 1.05
+    repeat_last_n: int = -1
+    penalty_from: int = 0
+    seed: int = 0
+    frequency_penalty: float = 0.0
+    presence_penalty: float = 0.0
+
+    def validate(self) -> None:
+        """The server's range check (src/server.cpp:1071)."""
+        if (self.temperature < 0 or self.top_p <= 0 or self.top_p > 1 or self.top_k < 0
+                or self.repetition_penalty <= 0 or self.repeat_last_n < -1):
+            raise ValueError("sampling parameter out of range")
+
+    def is_greedy(self) -> bool:
+        return np.float32(self.temperature) <= 0 or self.top_k == 1
+
+
+def params_array(params) -> np.ndarray:
+    """fs_row_params records from SamplerParams objects (or pass a PARAMS_DTYPE array through)."""
+    if isinstance(params, np.ndarray) and params.dtype == PARAMS_DTYPE:
+        return np.ascontiguousarray(params)
+    if isinstance(params, SamplerParams):
+        params = [params]
+    out = np.zeros(len(params), PARAMS_DTYPE)
+    for i, p in enumerate(params):
+        out[i] = (p.temperature, p.top_k, p.top_p, p.min_p, p.repetition_penalty, p.frequency_penalty,
+                  p.presence_penalty, p.repeat_last_n, p.penalty_from, 0)
+    return out
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _dev_params(params, device) -> torch.Tensor:
+    if isinstance(params, torch.Tensor):
+        if params.dtype != torch.uint8 or params.numel() % PARAMS_DTYPE.itemsize:
+            raise SamplerError("params tensor must be uint8 bytes of fs_row_params records")
+        return params.to(device)
+    a = params_array(params)
+    return torch.from_numpy(a.view(np.uint8).copy()).to(device)
+
+
+class Context:
+    """An fs_context (device workspace); calls on one context are serialised by a lock."""
+
+    _default = {}
+    _dlock = threading.Lock()
+
+    def __init__(self):
+        h = ctypes.c_void_p()
+        check(lib().fs_create(ctypes.byref(h)), "fs_create")
+        self.h = h
+        self.lock = threading.Lock()
+
+    def __del__(self):
+        h = getattr(self, "h", None)
+        if h is not None and h.value:
+            try:
+                lib().fs_destroy(h)
+            except Exception:
+                pass
+
+    @classmethod
+    def default(cls, device=None) -> "Context":
+        dev = torch.device("cuda", torch.cuda.current_device() if device is None else torch.device(device).index or 0)
+        with cls._dlock:
+            if dev not in cls._default:
+                cls._default[dev] = Context()
+            return cls._default[dev]
+
+
+class Rng:
+    """fs_rng: libstdc++ std::mt19937_64 + generate_canonical, ferro::Sampler's draw stream (sampler.h:25,32)."""
+
+    def __init__(self, seed: int = 0):
+        h = ctypes.c_void_p()
+        check(lib().fs_rng_create(ctypes.c_uint64(seed), ctypes.byref(h)), "fs_rng_create")
+        self.h = h
+
+    def __del__(self):
+        h = getattr(self, "h", None)
+        if h is not None and h.value:
+            try:
+                lib().fs_rng_destroy(h)
+            except Exception:
+                pass
+
+    def next_u(self, n: int = 1) -> np.ndarray:
+        out = np.zeros(n, np.float64)
+        check(lib().fs_rng_next_u(self.h, out.ctypes.data_as(ctypes.c_void_p), n), "fs_rng_next_u")
+        return out
+
+    def copy(self) -> "Rng":
+        r = Rng(1)
+        check(lib().fs_rng_copy(self.h, r.h), "fs_rng_copy")
+        return r
+
+
+def _check_logits(logits: torch.Tensor, V: int | None):
+    if not (isinstance(logits, torch.Tensor) and logits.is_cuda and logits.dtype == torch.float32):
+        raise SamplerError("logits must be a float32 CUDA tensor")
+    if logits.dim() == 1:
+        logits = logits.unsqueeze(0)
+    if logits.dim() != 2:
+        raise SamplerError("logits must be [B, V]")
+    n = logits.shape[1] if V is None else V
+    if n > logits.shape[1]:
+        raise SamplerError("V exceeds the row length")
+    ld = logits.stride(0) if logits.shape[0] > 1 else n + (-n) % 4
+    if logits.stride(1) != 1 or ld % 4 or ld < n or logits.data_ptr() % 16:
+        # the kernels take 16-byte aligned rows: repack into a padded copy
+        padded = torch.zeros((logits.shape[0], n + (-n) % 4), dtype=torch.float32, device=logits.device)
+        padded[:, :n] = logits[:, :n]
+        logits, ld = padded, padded.stride(0)
+    return logits, ld, n
+
+
+def _hist_tensors(hist, hist_off, B, device):
+    if hist is None:
+        return None, None
+    hist = torch.as_tensor(hist, dtype=torch.int32, device=device)
+    hist_off = torch.as_tensor(hist_off, dtype=torch.int64, device=device)
+    if hist_off.numel() != B + 1:
+        raise SamplerError("hist_off must have B+1 entries")
+    return hist, hist_off
+
+
+def sample_batch(logits, params, u, hist=None, hist_off=None, V=None, kcap=0, ctx=None, stream=None):
+    """fs_sample_batch on device tensors: logits [B, ld] fp32 (rows 16-byte aligned), params (B records),
+    u [B] float64 draws, hist/hist_off CSR histories. Returns dict(tok, keep, cand_ids, cand_probs) (device)."""
+    logits, ld, n = _check_logits(logits, V)
+    B = logits.shape[0]
+    dev = logits.device
+    p = _dev_params(params, dev)
+    if p.numel() != B * PARAMS_DTYPE.itemsize:
+        raise SamplerError("one params record per row")
+    u = torch.as_tensor(u, dtype=torch.float64, device=dev)
+    hist, hist_off = _hist_tensors(hist, hist_off, B, dev)
+    tok = torch.empty(B, dtype=torch.int32, device=dev)
+    keep = torch.empty(B, dtype=torch.int32, device=dev)
+    ids = torch.empty((B, kcap), dtype=torch.int32, device=dev) if kcap else None
+    probs = torch.empty((B, kcap), dtype=torch.float64, device=dev) if kcap else None
+    ctx = ctx or Context.default(dev)
+    with ctx.lock:
+        check(lib().fs_sample_batch(ctx.h, _ptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p), _ptr(u),
+                                    _ptr(tok), kcap, _ptr(ids), _ptr(probs), _ptr(keep), _stream(stream)),
+              "fs_sample_batch")
+    return dict(tok=tok, keep=keep, cand_ids=ids, cand_probs=probs, _keepalive=(p, u, hist, hist_off))
+
+
+def argmax_batch(logits, hist=None, hist_off=None, params=None, V=None, ctx=None, stream=None):
+    """fs_argmax_batch: greedy token per row after the penalties of `params` (None = no penalty)."""
+    logits, ld, n = _check_logits(logits, V)
+    B = logits.shape[0]
+    dev = logits.device
+    p = _dev_params(params, dev) if params is not None else None
+    hist, hist_off = _hist_tensors(hist, hist_off, B, dev)
+    tok = torch.empty(B, dtype=torch.int32, device=dev)
+    ctx = ctx or Context.default(dev)
+    with ctx.lock:
+        check(lib().fs_argmax_batch(ctx.h, _ptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p), _ptr(tok),
+                                    _stream(stream)), "fs_argmax_batch")
+    return tok
+
+
+def verify(logits, rows, row_off, params, u=None, hist=None, hist_off=None, eos_id=-1, V=None, ctx=None,
+           stream=None):
+    """fs_verify: per-row tokens and per-stream accepted prefix lengths of a speculative window."""
+    logits, ld, n = _check_logits(logits, V)
+    R = logits.shape[0]
+    dev = logits.device
+    rows = torch.as_tensor(rows, dtype=torch.int32, device=dev)
+    row_off = torch.as_tensor(row_off, dtype=torch.int64, device=dev)
+    S = row_off.numel() - 1
+    p = _dev_params(params, dev)
+    if p.numel() != S * PARAMS_DTYPE.itemsize:
+        raise SamplerError("one params record per stream")
+    u = torch.as_tensor(np.zeros(R) if u is None else u, dtype=torch.float64, device=dev)
+    hist, hist_off = _hist_tensors(hist, hist_off, S, dev)
+    tok = torch.empty(R, dtype=torch.int32, device=dev)
+    acc = torch.empty(S, dtype=torch.int32, device=dev)
+    ctx = ctx or Context.default(dev)
+    with ctx.lock:
+        check(lib().fs_verify(ctx.h, _ptr(logits), ld, S, R, n, _ptr(rows), _ptr(row_off), _ptr(hist),
+                              _ptr(hist_off), _ptr(p), _ptr(u), int(eos_id), _ptr(tok), _ptr(acc), _stream(stream)),
+              "fs_verify")
+    return tok, acc
+
+
+def device_error(ctx=None, stream=None) -> int:
+    ctx = ctx or Context.default()
+    bits = ctypes.c_int32(0)
+    check(lib().fs_device_error(ctx.h, _stream(stream), ctypes.byref(bits)), "fs_device_error")
+    return bits.value
+
+
+class Sampler:
+    """Mirror of ferro::Sampler (src/sampler.h:23-34) running on the GPU.
+
+    sample(logits, n_vocab, history) -> int, with logits a CUDA float32 tensor (device-resident, the intended
+    use) or a host array/tensor (copied to the device). Unlike ferro, the logits are not modified in place: the
+    penalty is applied on the fly inside the kernel."""
+
+    def __init__(self, p: SamplerParams, device=None):
+        self._p = p
+        self._rng = Rng(int(p.seed))
+        self._dev = torch.device("cuda" if device is None else device)
+        self._rec = torch.from_numpy(params_array(p).view(np.uint8).copy()).to(self._dev)
+        self._ctx = Context.default(self._dev)
+
+    def params(self) -> SamplerParams:
+        return self._p
+
+    def sample(self, logits, n_vocab: int, history) -> int:
+        if not (isinstance(logits, torch.Tensor) and logits.is_cuda):
+            logits = torch.as_tensor(np.asarray(logits, np.float32)).to(self._dev)
+        row = logits.reshape(-1)[:n_vocab]
+        h = np.asarray(history, np.int32).reshape(-1)
+        u = np.zeros(1) if self._p.is_greedy() else self._rng.next_u(1)
+        out = sample_batch(row.reshape(1, -1), self._rec, u, hist=h, hist_off=[0, h.size], V=n_vocab,
+                           ctx=self._ctx)
+        return int(out["tok"].item())

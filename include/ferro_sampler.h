@@ -1,0 +1,116 @@
+/* ferro_sampler.h - C ABI of the MI355X (gfx950) token sampler.
+ *
+ * Drop-in device replacement for ferro's host sampler, ferro::Sampler (reference src/sampler.h:23-34,
+ * src/sampler.cpp:10-50): repetition penalty -> greedy | top-k -> softmax at temperature -> min-p -> top-p ->
+ * multinomial draw, plus the speculative-draft verification rule of the server (src/server.cpp:627-637).
+ *
+ * Conventions (all entry points):
+ *   - every pointer named d_* is device memory owned by the caller; nothing is retained after the call returns;
+ *   - work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the default stream);
+ *   - the return value is FS_OK or a negative FS_E_* code; nothing throws across the ABI;
+ *   - a context may be used from any thread, but calls on one context must not overlap in time (they share its
+ *     device workspace): serialise them on one stream, or use one context per stream;
+ *   - logits rows are fp32, row b starts at d_logits + b*ld, ld >= V, ld % 4 == 0, d_logits 16-byte aligned;
+ *     only elements [0, V) of each row are read. Logits are read only: the penalty is applied on the fly and
+ *     never written back (ferro's sample() penalises its host row in place).
+ *   - per-row draws d_u are doubles in [0,1): r = u * tot replaces ferro's uniform_real_distribution(0, tot)
+ *     draw from its mt19937_64 (libstdc++ computes exactly generate_canonical * tot). Greedy rows ignore u.
+ */
+#ifndef FERRO_SAMPLER_H
+#define FERRO_SAMPLER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FS_OK 0
+#define FS_E_INVALID (-1)   /* bad argument: null pointer, size out of range, misalignment */
+#define FS_E_HIP (-2)       /* a HIP runtime call failed */
+#define FS_E_NOMEM (-3)     /* workspace allocation failed */
+#define FS_E_DEVICE (-4)    /* a kernel reported a row it could not process (see fs_device_error) */
+
+/* Device-side error bits (fs_device_error). */
+#define FS_DEVERR_COUNT_OVERFLOW 1   /* one token occurs > 65535 times in a penalty window */
+#define FS_DEVERR_INTERNAL 2         /* an internal invariant failed (a bug: please report) */
+#define FS_DEVERR_LARGE_K 4          /* a sampled row needs k > 2048 candidates (not yet on the device path): token -1 */
+
+/* Limits. */
+#define FS_MAX_VOCAB (1 << 30)
+
+/* Per-row sampling parameters. Fields 1-5 and 8-9 are ferro's SamplerParams (src/sampler.h:12-21) with the
+ * same meaning and defaults; the seed is replaced by the per-row draw u. frequency_penalty / presence_penalty
+ * extend ferro (llama.cpp convention: l -= cnt*freq + (cnt>0)*pres over the penalty window, after the
+ * repetition step); 0 leaves a row bit-identical to ferro. */
+typedef struct fs_row_params {
+    float temperature;        /* <= 0: greedy (argmax after penalties)        sampler.h:13 */
+    int32_t top_k;            /* 0 = all tokens; 1 = greedy                   sampler.h:14 */
+    float top_p;              /* 1 = off                                      sampler.h:15 */
+    float min_p;              /* 0 = off                                      sampler.h:16 */
+    float repetition_penalty; /* 1 = off                                      sampler.h:17 */
+    float frequency_penalty;  /* 0 = off (extension) */
+    float presence_penalty;   /* 0 = off (extension) */
+    int32_t repeat_last_n;    /* -1 whole history, 0 off, N last tokens       sampler.h:18 */
+    int32_t penalty_from;     /* history positions before this never count    sampler.h:19 */
+    int32_t reserved;         /* must be 0 */
+} fs_row_params;
+
+typedef struct fs_context fs_context;
+
+/* Create / destroy a context (owns a device workspace that grows on demand). Replaces constructing one
+ * ferro::Sampler per stream (src/sampler.h:25); the per-stream RNG lives with the caller (u). */
+int fs_create(fs_context** out);
+int fs_destroy(fs_context* ctx);
+
+/* Batched sample(): one token per row. Replaces the per-row loop
+ *   for i: tok = sampler->sample(S.lg.data() + i*V, V, hist)          (src/server.cpp:603-606, sampler.cpp:10)
+ * Row b's history is d_hist[d_hist_off[b] .. d_hist_off[b+1]) (d_hist_off has B+1 entries; d_hist may be NULL
+ * when every row's history is empty). Outputs: d_tok[B]. Optional (NULL to skip): d_cand_ids / d_cand_probs
+ * [B][kcap] receive the first min(k, kcap) candidates in ferro's candidate order (logit desc, id asc) and their
+ * normalised probabilities pr[i] (sampler.cpp:37-41); d_keep[B] the kept prefix length after min-p / top-p.
+ * Greedy rows report k = keep = 1 with probability 1. */
+int fs_sample_batch(fs_context* ctx, const float* d_logits, int64_t ld, int32_t B, int32_t V,
+                    const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params,
+                    const double* d_u, int32_t* d_tok, int32_t kcap, int32_t* d_cand_ids, double* d_cand_probs,
+                    int32_t* d_keep, void* stream);
+
+/* Greedy batch: argmax after penalties, lowest index on ties (sampler.cpp:19-23). d_params may be NULL (no
+ * penalties); otherwise only the penalty fields are read and every row is treated as greedy. */
+int fs_argmax_batch(fs_context* ctx, const float* d_logits, int64_t ld, int32_t B, int32_t V,
+                    const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params,
+                    int32_t* d_tok, void* stream);
+
+/* Speculative verification window (src/server.cpp:613-651). Stream s owns logits rows
+ * d_row_off[s] .. d_row_off[s+1]-1 (d_row_off has n_streams+1 entries, total rows = d_row_off[n_streams]);
+ * d_rows[r] is the token fed at row r: d_rows[d_row_off[s]] is the stream's last sampled token, the rest are its
+ * drafts. Row r of stream s is sampled with history = d_hist[d_hist_off[s] .. d_hist_off[s+1]) followed by the
+ * drafts fed before it (d_rows[d_row_off[s]+1 .. d_row_off[s]+r]), with params d_params[s] and draw d_u[row].
+ * Outputs: d_tok[row] for every row, and d_accepted[s] = 1 + the number of leading rows r < m-1 whose token
+ * equals the next draft; a row whose token is eos_id (>= 0; -1 = none) ends the window at that row. */
+int fs_verify(fs_context* ctx, const float* d_logits, int64_t ld, int32_t n_streams, int32_t total_rows,
+              int32_t V, const int32_t* d_rows, const int64_t* d_row_off, const int32_t* d_hist,
+              const int64_t* d_hist_off, const fs_row_params* d_params, const double* d_u, int32_t eos_id,
+              int32_t* d_tok, int32_t* d_accepted, void* stream);
+
+/* Host draw source matching ferro::Sampler's std::mt19937_64 stream (src/sampler.h:25,32; sampler.cpp:45-46):
+ * fs_rng_next_u returns generate_canonical<double,53> values, so u * tot is ferro's draw r. seed 0 = random.
+ * A sampled (non-greedy) row consumes one u; greedy rows consume none (sampler.cpp:19-23). fs_rng_copy lets a
+ * verifier draw a window's u ahead and commit only the accepted count (fs_rng_next_u on the original). */
+typedef struct fs_rng fs_rng;
+int fs_rng_create(uint64_t seed, fs_rng** out);
+int fs_rng_destroy(fs_rng* r);
+int fs_rng_next_u(fs_rng* r, double* u, int32_t n);
+int fs_rng_copy(const fs_rng* src, fs_rng* dst);
+
+/* Waits for `stream`, then returns and clears the device error bits (FS_DEVERR_*) kernels of this context set. */
+int fs_device_error(fs_context* ctx, void* stream, int32_t* bits);
+
+/* Static description of the error code. */
+const char* fs_strerror(int code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FERRO_SAMPLER_H */

@@ -1,0 +1,202 @@
+"""Pins the CPU oracle (oracle/sampler_oracle.c) before it is trusted as the GPU checker.
+
+- reference known-answer test: tests/test_kernels.cpp:348-358 (penalty window / scope, five cases);
+- golden vectors written by the compiled reference sampler (tests/golden/sampler_golden.npz): 160 single calls,
+  two 40-call streams (draw-stream consumption), the full config-1 row under 32 seeds;
+- brute force: a full numpy lexsort gives the candidate order for tiny rows (membership, order, ties, +-0);
+- closed forms: top-p keeps the crossing element, min-p, greedy, u at the CDF edges, the extension's arithmetic;
+- the verification rule (server.cpp:627-637) on hand-built windows;
+- the live reference (if oracle/_ref is built) on fresh random rows.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from ferro_amd import workloads as W
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "sampler_golden.npz")
+
+
+def test_known_answer_penalty_window_scope():
+    # tests/test_kernels.cpp:348-358: logits {0,9,10,9.5,6,0}, history {1,2,3}, penalty 2, greedy
+    row = np.array([0, 9, 10, 9.5, 6, 0], np.float32)
+    want = {(-1, 0): 4, (-1, 2): 2, (2, 0): 1, (0, 0): 2, (2, 2): 2}
+    for (last_n, frm), tok in want.items():
+        p = O.make_params(temperature=0.0, repetition_penalty=2.0, repeat_last_n=last_n, penalty_from=frm)
+        assert O.sample(row, [1, 2, 3], p)[0] == tok, (last_n, frm)
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+def test_golden_rows(golden):
+    g = golden
+    params = g["rows_params"].view(O.PARAMS_DTYPE)
+    n = len(g["rows_tok"])
+    assert n == 160
+    bad = []
+    for i in range(n):
+        x = g["rows_x"][g["rows_x_off"][i]:g["rows_x_off"][i + 1]]
+        h = g["rows_h"][g["rows_h_off"][i]:g["rows_h_off"][i + 1]]
+        u = W.first_u(int(g["rows_seed"][i]))
+        tok = O.sample(x, h, params[i], u)[0]
+        if tok != g["rows_tok"][i]:
+            bad.append(i)
+    assert not bad
+
+
+def test_golden_streams(golden):
+    g = golden
+    params = g["stream_params"].view(O.PARAMS_DTYPE)
+    for s in range(len(params)):
+        p = params[s]
+        mt = W.MT19937_64(int(g["stream_seed"][s]))
+        greedy = p["temperature"] <= 0 or p["top_k"] == 1
+        hist = list(g["stream_h0"][s])
+        for i, row in enumerate(g["stream_x"][s]):
+            u = 0.0 if greedy else W.canonical(mt.next())     # one draw per non-greedy call, none for greedy
+            tok = O.sample(row, np.array(hist, np.int32), p, u)[0]
+            assert tok == g["stream_tok"][s][i], (s, i)
+            hist.append(tok)
+
+
+def test_golden_cfg1(golden):
+    w = W.config1()
+    for s, t in zip(golden["cfg1_seed"], golden["cfg1_tok"]):
+        assert O.sample(w.logits[0], w.hist, w.params[0], W.first_u(int(s)))[0] == t
+
+
+def test_mt64_and_canonical():
+    # std::mt19937_64 with the default seed 5489: the standard fixes the 10000th output (C++11 [rand.predef])
+    mt = W.MT19937_64(5489)
+    for _ in range(9999):
+        mt.next()
+    assert mt.next() == 9981545732273789042
+    # the C restatement agrees with the Python one
+    a, b = O.MT64(12345), W.MT19937_64(12345)
+    for _ in range(700):
+        assert a.next() == b.next()
+    assert W.canonical(0) == 0.0
+    assert W.canonical(2**64 - 1) == float(np.nextafter(1.0, 0.0))
+    assert O.canonical(2**64 - 1) == W.canonical(2**64 - 1)
+    assert O.canonical(2**63) == 0.5
+
+
+def brute_order(x):
+    """Candidate order by brute force: value desc, id asc; -0 == +0 (add 0.0 folds -0 onto +0)."""
+    v = x.astype(np.float64) + 0.0
+    return np.lexsort((np.arange(len(x)), -v))
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_topk_membership_and_order_brute_force(seed):
+    rng = np.random.default_rng(seed)
+    V = int(rng.integers(1, 200))
+    x = (np.round(rng.standard_normal(V) * 3) / 2).astype(np.float32)     # ties
+    x[rng.random(V) < 0.2] = -0.0
+    k = int(rng.integers(1, V + 3))
+    p = O.make_params(temperature=1.0, top_k=k if k != 1 else 2, repetition_penalty=1.0)
+    tok, ids, probs, keep, ncand = O.sample(x, [], p, 0.5, kcap=V)
+    kk = p["top_k"][0] if 0 < p["top_k"][0] < V else V
+    assert ncand == kk
+    np.testing.assert_array_equal(ids, brute_order(x)[:kk])
+
+
+def test_softmax_topp_minp_closed_form():
+    # 4 candidates with logits log(4), log(3), log(2), log(1) at T=1 -> p = .4 .3 .2 .1
+    x = np.log(np.array([1, 4, 2, 3], np.float64)).astype(np.float32)
+    p = O.make_params(temperature=1.0, top_k=0, repetition_penalty=1.0)
+    tok, ids, probs, keep, ncand = O.sample(x, [], p, 0.0, kcap=4)
+    np.testing.assert_array_equal(ids, [1, 3, 2, 0])
+    np.testing.assert_allclose(probs, [0.4, 0.3, 0.2, 0.1], rtol=1e-6)
+    assert keep == 4 and tok == 1
+    # top-p keeps the element whose cumulative sum crosses: .4 < .5 <= .7 -> keep 2
+    p["top_p"] = 0.5
+    assert O.sample(x, [], p, 0.0, kcap=4)[3] == 2
+    p["top_p"] = 0.4                  # .4 >= .4 (within float rounding of the stored top_p) -> keep 1 or 2
+    assert O.sample(x, [], p, 0.0, kcap=4)[3] in (1, 2)
+    p["top_p"] = 1.0
+    p["min_p"] = 0.6                  # thr = .24: keeps .4 .3
+    assert O.sample(x, [], p, 0.0, kcap=4)[3] == 2
+    p["min_p"] = 2.0                  # thr above pr[0]: keep shrinks to 1
+    assert O.sample(x, [], p, 0.999, kcap=4)[3] == 1
+    # draw: u*tot against the cumulative sums .4 .7 .9 1.0
+    p["min_p"] = 0.0
+    for u, want in [(0.0, 1), (0.39, 1), (0.41, 3), (0.69, 3), (0.71, 2), (0.89, 2), (0.91, 0), (0.999999, 0)]:
+        assert O.sample(x, [], p, u)[0] == want, u
+
+
+def test_greedy_ties_nan_and_topk1():
+    p = O.make_params(temperature=0.0, repetition_penalty=1.0)
+    assert O.sample(np.array([1, 3, 3, 2], np.float32), [], p)[0] == 1
+    assert O.sample(np.array([-0.0, 0.0], np.float32), [], p)[0] == 0
+    assert O.sample(np.array([np.nan, 5, 6], np.float32), [], p)[0] == 0      # nothing compares > NaN at 0
+    assert O.sample(np.array([1, np.nan, 6], np.float32), [], p)[0] == 2
+    p = O.make_params(temperature=1.0, top_k=1, repetition_penalty=1.0)        # top_k 1 is greedy
+    assert O.sample(np.array([1, 3, 3, 2], np.float32), [], p, 0.99)[0] == 1
+
+
+def test_frequency_presence_extension():
+    row = np.array([2.0, -1.0, 0.5, 3.0], np.float32)
+    h = [0, 0, 0, 1, 3, 3]
+    # freq = pres = 0 must leave ferro's repetition step alone, bit for bit
+    p = O.make_params(repetition_penalty=1.3)
+    base = O.penalize(row, h, p)
+    p2 = O.make_params(repetition_penalty=1.3, frequency_penalty=0.0, presence_penalty=0.0)
+    np.testing.assert_array_equal(O.penalize(row, h, p2).view(np.uint32), base.view(np.uint32))
+    # llama.cpp convention after the repetition step: l -= cnt*freq + pres (float32 ops)
+    p3 = O.make_params(repetition_penalty=1.0, frequency_penalty=0.5, presence_penalty=0.25)
+    out = O.penalize(row, h, p3)
+    f32 = np.float32
+    np.testing.assert_array_equal(out, np.array([f32(2.0) - (f32(3) * f32(0.5) + f32(0.25)),
+                                                 f32(-1.0) - (f32(1) * f32(0.5) + f32(0.25)),
+                                                 f32(0.5),
+                                                 f32(3.0) - (f32(2) * f32(0.5) + f32(0.25))], np.float32))
+
+
+def test_verify_rule_hand_built():
+    V = 8
+    # stream 0: rows predict 5, 6, 7; drafts fed are [x, 5, 6] -> both drafts accepted -> acc 3
+    # stream 1: rows predict 1, 2; drafts fed [x, 3] -> first draft rejected -> acc 1
+    # stream 2: rows predict 4 (= eos), 0; drafts fed [x, 4] -> eos ends the window at row 0 -> acc 1
+    preds = [5, 6, 7, 1, 2, 4, 0]
+    logits = np.zeros((7, V), np.float32)
+    logits[np.arange(7), preds] = 10.0
+    rows = np.array([0, 5, 6, 0, 3, 0, 4], np.int32)
+    row_off = np.array([0, 3, 5, 7], np.int64)
+    p = O.make_params(3, temperature=0.0, repetition_penalty=1.0)
+    tok, acc = O.verify(logits, rows, row_off, np.zeros(0, np.int32), np.zeros(4, np.int64), p, np.zeros(7),
+                        eos_id=4)
+    assert list(tok) == preds
+    assert list(acc) == [3, 1, 1]
+
+
+def test_verify_row_history_includes_drafts():
+    # repetition penalty on the drafts: row 1 sees history [base..., draft1]; its argmax moves off draft1
+    V = 4
+    logits = np.array([[0, 0, 5, 0], [0, 0, 5, 4.9]], np.float32)
+    rows = np.array([1, 2], np.int32)
+    p = O.make_params(1, temperature=0.0, repetition_penalty=2.0)
+    tok, acc = O.verify(logits, rows, np.array([0, 2]), np.array([1], np.int32), np.array([0, 1]), p, np.zeros(2))
+    assert list(tok) == [2, 3] and list(acc) == [2]
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (needs /root/reference)")
+def test_live_reference_random():
+    rng = np.random.default_rng(99)
+    for s in range(1, 200):
+        V = int(rng.integers(1, 5000))
+        x = (rng.standard_normal(V) * rng.uniform(0.5, 5)).astype(np.float32)
+        if s % 3 == 0:
+            x = (np.round(x) / 2).astype(np.float32)
+        h = rng.integers(0, V, int(rng.integers(0, 300))).astype(np.int32)
+        p = O.make_params(temperature=float(rng.choice([0, 0.2, 0.8, 1.5])), top_k=int(rng.integers(0, 300)),
+                          top_p=float(rng.uniform(0.3, 1.0)), min_p=float(rng.choice([0, 0.1])),
+                          repetition_penalty=float(rng.uniform(0.8, 1.6)),
+                          repeat_last_n=int(rng.choice([-1, 0, 5, 64])), penalty_from=int(rng.choice([0, 3])))
+        assert O.sample(x, h, p, W.first_u(s))[0] == O.ref_sample_stream(p, s, [x], [h])[0], s
