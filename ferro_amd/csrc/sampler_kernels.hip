@@ -1,20 +1,25 @@
 // sampler_kernels.hip - gfx950 (CDNA4) kernels of the token sampler and the C ABI of include/ferro_sampler.h.
 //
-// One fused kernel per call. A row of V fp32 logits is split into chunks of BLOCK*EPT elements, one workgroup per
-// chunk (grid = B * nchunks, XCD-aware block order). Each chunk workgroup:
-//   1. streams its chunk into registers with 16-byte loads (the only pass over the logits in HBM);
-//   2. applies the penalty pass on the fly: the row's history window is scattered into an LDS count table of the
-//      chunk's ids, and each thread patches the few penalised elements it holds (reference src/sampler.cpp:11-18);
-//   3. maps each logit to an order-preserving 32-bit key (-0 folded onto +0) and, for a top-k row, finds a
-//      threshold T0 that at least k of the chunk's elements reach: the chunk's group maxima are histogrammed on
-//      the key's top 11 bits and T0 is the floor of the bin where the count from the top reaches k;
-//   4. compacts the elements with key >= T0 (about k of them) into LDS with wave ballots and writes them as
-//      64-bit composites (key << 32 | ~id: larger = earlier in ferro's candidate order, sampler.cpp:30) to the
-//      workspace; a chunk with too many ties falls back to an exact radix select over its registers.
-// The last workgroup of a row to finish (an agent-scope counter) merges: L = max of the chunks' T0 is a lower
-// bound of the row's k-th key, the candidates >= L are sorted in LDS, and the first k feed the double-precision
-// softmax / min-p / top-p / draw (sampler.cpp:37-49), with block scans in place of the sequential sums.
-// Greedy rows (temperature <= 0 or top_k == 1, sampler.cpp:19) reduce to one (key, lowest id) maximum per chunk.
+// One fused kernel per call. A row of V fp32 logits is split into chunks of BLOCK*EPT elements, one 512-thread
+// workgroup per chunk (grid = B * nchunks, rows in order so early rows merge while later rows stream).
+// Each chunk workgroup:
+//   1. issues all of its 16-byte loads first (EPT/4 per thread, the chunk's only pass over HBM);
+//   2. applies the penalty pass on the fly: the row's history window is scattered into an LDS table of 16-bit
+//      counts over the chunk's ids and each thread patches the few penalised elements it holds
+//      (reference src/sampler.cpp:11-18, plus the frequency/presence extension);
+//   3. maps each logit to an order-preserving 32-bit key (-0 folded onto +0); for a top-k row it histograms the
+//      maxima of >= 2k disjoint groups of its elements over their [min, max] key range and takes the floor T0 of
+//      the bin where the count from the top reaches k - at least k of the chunk's elements reach T0;
+//   4. compacts the elements with key >= T0 (a little over k) into LDS with wave ballots and publishes them as
+//      64-bit composites (key << 32 | ~id: larger = earlier in ferro's candidate order, sampler.cpp:30); a chunk
+//      with too many ties at T0 falls back to an exact radix select over its registers.
+// Hand-off without an L2 write-back: the lists are written with agent-scope (sc1, write-through) stores, each wave
+// drains its stores (s_waitcnt vmcnt(0)), then one agent-scope counter add per workgroup; the last workgroup of a
+// row reads the lists with agent-scope loads and merges: L = max T0 bounds the row's k-th key from below, a
+// histogram of the candidates >= L over [L, max] gives a tight T1, the ~k candidates >= T1 are rank-sorted in LDS,
+// and the first k feed the double-precision softmax / min-p / top-p / draw (sampler.cpp:37-49), with block scans
+// in place of the sequential sums. Greedy rows (temperature <= 0 or top_k == 1, sampler.cpp:19) publish one
+// (key, lowest id) maximum per chunk.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -30,15 +35,17 @@
 
 namespace fs {
 
-constexpr int BLOCK = 256;                // threads per workgroup: 4 wave64s
+constexpr int BLOCK = 512;                // threads per workgroup: 8 wave64s, two workgroups per CU
 constexpr int WAVE = 64;
 constexpr int NWAVES = BLOCK / WAVE;
-constexpr int KMAX = 2048;                // largest k on the fused select path (ferro's server caps nothing)
-constexpr int CAP = 4096;                 // candidate capacity: per chunk in the workspace, and in the merge
-constexpr int HBITS = 11;                 // threshold histogram: top 11 key bits
-constexpr int NBINS = 1 << HBITS;
-constexpr int MAX_CHUNKS = 1024;          // chunks per row (V <= 4M at 4096-element chunks)
-constexpr int SPEC = 8;                   // candidates per thread fetched in the merge's first round
+constexpr int KMAX = 2048;                // largest k on the fused select path
+constexpr int KPT = KMAX / BLOCK;         // candidates per thread in the softmax / draw phase
+constexpr int CAP = 8192;                 // candidates per chunk in the workspace; merge gather capacity in LDS
+constexpr int HBITS = 11;
+constexpr int NBINS = 1 << HBITS;         // threshold histograms
+constexpr int SMALL = 512;                // rank-sort capacity of the merge
+constexpr int MAX_CHUNKS = 1024;
+constexpr int SPEC = 4;                   // merge gather: loads in flight per thread per round
 
 enum Mode : int { MODE_SAMPLE = 0, MODE_ARGMAX = 1, MODE_VERIFY = 2 };
 
@@ -63,7 +70,6 @@ struct Args {
     int32_t* accepted;
     int mode;
     int nchunks;
-    int xcd_remap;
     uint64_t* cand;                // [B*nchunks][CAP]
     uint32_t* meta;                // [B*nchunks][2]: T0, count
     uint32_t* row_cnt;             // [B] chunk completion counters, left at 0
@@ -89,6 +95,30 @@ __device__ __forceinline__ uint64_t comp_of(uint32_t key, uint32_t id) {
     return ((uint64_t)key << 32) | (uint64_t)(0xFFFFFFFFu - id);
 }
 __device__ __forceinline__ uint32_t comp_id(uint64_t c) { return 0xFFFFFFFFu - (uint32_t)c; }
+__device__ __forceinline__ uint32_t comp_key(uint64_t c) { return (uint32_t)(c >> 32); }
+
+// ------------------------------------------------------------------------------------------------ hand-off I/O
+// Agent-scope relaxed accesses compile to sc1 loads/stores: coherent across the XCDs' L2s without a write-back.
+__device__ __forceinline__ void st_agent(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(int32_t* p, int32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_agent(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t ld_agent(const int32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until this wave's vector memory operations (the sc1 stores above) have completed.
+__device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ------------------------------------------------------------------------------------------------ wave/block
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
@@ -96,27 +126,16 @@ __device__ __forceinline__ uint32_t mbcnt(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+template <class T>
+__device__ __forceinline__ T wave_max(T v) {
 #pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) {
-        const uint64_t w = __shfl_xor(v, o);
-        v = w > v ? w : v;
-    }
+    for (int o = WAVE / 2; o > 0; o >>= 1) { const T w = __shfl_xor(v, o); v = w > v ? w : v; }
     return v;
 }
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+template <class T>
+__device__ __forceinline__ T wave_min(T v) {
 #pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) { const uint32_t w = __shfl_xor(v, o); v = w > v ? w : v; }
-    return v;
-}
-__device__ __forceinline__ int wave_min_i32(int v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) { const int w = __shfl_xor(v, o); v = w < v ? w : v; }
-    return v;
-}
-__device__ __forceinline__ int wave_max_i32(int v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) { const int w = __shfl_xor(v, o); v = w > v ? w : v; }
+    for (int o = WAVE / 2; o > 0; o >>= 1) { const T w = __shfl_xor(v, o); v = w < v ? w : v; }
     return v;
 }
 __device__ __forceinline__ double wave_sum_f64(double v) {
@@ -128,14 +147,16 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 // Small shared scratch for block-wide reductions and broadcasts.
 struct Red {
     uint64_t u64[NWAVES];
+    uint64_t u64b[NWAVES];
     double f64[NWAVES];
     int i32[NWAVES];
+    uint32_t u32[NWAVES];
     uint32_t misc[8];
     double dmisc[4];
 };
 
 __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, Red& r) {
-    v = wave_max_u64(v);
+    v = wave_max(v);
     if (lane_id() == 0) r.u64[threadIdx.x / WAVE] = v;
     __syncthreads();
     uint64_t m = r.u64[0];
@@ -144,8 +165,24 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, Red& r) {
     __syncthreads();
     return m;
 }
+// max and min in one round
+__device__ __forceinline__ void block_minmax_u32(uint32_t& mn, uint32_t& mx, Red& r) {
+    uint32_t a = wave_max(mx), b = wave_min(mn);
+    if (lane_id() == 0) { r.u32[threadIdx.x / WAVE] = a; r.i32[threadIdx.x / WAVE] = (int)b; }
+    __syncthreads();
+    a = r.u32[0];
+    b = (uint32_t)r.i32[0];
+#pragma unroll
+    for (int w = 1; w < NWAVES; ++w) {
+        a = r.u32[w] > a ? r.u32[w] : a;
+        b = (uint32_t)r.i32[w] < b ? (uint32_t)r.i32[w] : b;
+    }
+    __syncthreads();
+    mx = a;
+    mn = b;
+}
 __device__ __forceinline__ int block_min_i32(int v, Red& r) {
-    v = wave_min_i32(v);
+    v = wave_min(v);
     if (lane_id() == 0) r.i32[threadIdx.x / WAVE] = v;
     __syncthreads();
     int m = r.i32[0];
@@ -155,7 +192,7 @@ __device__ __forceinline__ int block_min_i32(int v, Red& r) {
     return m;
 }
 __device__ __forceinline__ int block_max_i32(int v, Red& r) {
-    v = wave_max_i32(v);
+    v = wave_max(v);
     if (lane_id() == 0) r.i32[threadIdx.x / WAVE] = v;
     __syncthreads();
     int m = r.i32[0];
@@ -214,6 +251,84 @@ __device__ __forceinline__ void wave_append(bool pred, uint64_t v, uint64_t* lis
     }
 }
 
+// wave_append for a register element: the 64-bit composite is formed only when some lane of the wave appends.
+__device__ __forceinline__ void wave_append_kv(bool pred, uint32_t key, uint32_t id, uint64_t* list, uint32_t* count,
+                                               uint32_t cap) {
+    const uint64_t m = __ballot(pred);
+    if (m == 0) return;
+    uint32_t base = 0;
+    const int leader = __ffsll((unsigned long long)m) - 1;
+    if (lane_id() == leader) base = atomicAdd(count, (uint32_t)__popcll(m));
+    base = __shfl(base, leader);
+    if (pred) {
+        const uint32_t pos = base + mbcnt(m);
+        if (pos < cap) list[pos] = comp_of(key, id);
+    }
+}
+
+// Histogram helpers over keys in [base, base + (NBINS << shift)): bin = (key - base) >> shift.
+__device__ __forceinline__ int range_shift(uint32_t lo, uint32_t hi) {
+    const uint32_t span = hi - lo;                       // keys lo..hi map to bins 0..span>>shift < NBINS
+    int s = 0;
+    while ((span >> s) >= (uint32_t)NBINS) ++s;
+    return s;
+}
+// From a filled histogram, the bin b holding the kk-th largest entry: count(bins > b) < kk <= count(bins >= b).
+// *above = count(bins > b), *atb = count(bins >= b). Requires 1 <= kk <= total.
+__device__ int hist_locate(const uint32_t* bins, int kk, uint32_t* above_out, uint32_t* atb_out, uint32_t* wsum,
+                           Red& r) {
+    constexpr int BPT = NBINS / BLOCK;
+    const int tid = threadIdx.x;
+    uint32_t mine = 0;
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) mine += bins[NBINS - 1 - (tid * BPT + i)];
+    uint32_t tot;
+    const uint32_t above = block_excl_scan<uint32_t>(mine, wsum, &tot);
+    if (above < (uint32_t)kk && above + mine >= (uint32_t)kk) {
+        uint32_t c = above;
+        for (int i = 0; i < BPT; ++i) {
+            const int bin = NBINS - 1 - (tid * BPT + i);
+            const uint32_t nb = bins[bin];
+            if (c + nb >= (uint32_t)kk) { r.misc[4] = (uint32_t)bin; r.misc[5] = c; r.misc[6] = c + nb; break; }
+            c += nb;
+        }
+    }
+    __syncthreads();
+    const int b = (int)r.misc[4];
+    *above_out = r.misc[5];
+    *atb_out = r.misc[6];
+    __syncthreads();
+    return b;
+}
+
+// From a filled histogram: the largest bin b such that count(bins >= b) >= k. Returns T = base + (b << shift) and
+// *cnt = count(bins >= b); T = 0 and *cnt = total when the histogram holds fewer than k entries.
+__device__ uint32_t hist_threshold(const uint32_t* bins, uint32_t base, int shift, int k, uint32_t* cnt,
+                                   uint32_t* wsum, Red& r) {
+    constexpr int BPT = NBINS / BLOCK;
+    const int tid = threadIdx.x;
+    uint32_t mine = 0;
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) mine += bins[NBINS - 1 - (tid * BPT + i)];
+    uint32_t tot;
+    const uint32_t above = block_excl_scan<uint32_t>(mine, wsum, &tot);
+    if (tid == 0) { r.misc[4] = 0u; r.misc[5] = tot; }
+    __syncthreads();
+    if (tot >= (uint32_t)k && above < (uint32_t)k && above + mine >= (uint32_t)k) {
+        uint32_t c = above;
+        for (int i = 0; i < BPT; ++i) {
+            const int bin = NBINS - 1 - (tid * BPT + i);
+            c += bins[bin];
+            if (c >= (uint32_t)k) { r.misc[4] = base + ((uint32_t)bin << shift); r.misc[5] = c; break; }
+        }
+    }
+    __syncthreads();
+    *cnt = r.misc[5];
+    const uint32_t T = r.misc[4];
+    __syncthreads();
+    return T;
+}
+
 // Exact k-th largest composite among the candidates a visitor yields (all distinct, 0 = absent; 1 <= k <= count).
 // Radix select from the top byte: 8 passes of a 256-bin LDS histogram. each(f) calls f(c) for every candidate the
 // calling thread holds.
@@ -221,18 +336,19 @@ template <class Each>
 __device__ uint64_t radix_kth(Each each, int k, uint32_t* hist256, uint32_t* wsum, Red& r) {
     uint64_t prefix = 0, mask = 0;
     int kk = k;
+    const int tid = threadIdx.x;
     for (int shift = 56; shift >= 0; shift -= 8) {
-        hist256[threadIdx.x] = 0;
+        if (tid < 256) hist256[tid] = 0;
         __syncthreads();
         each([&](uint64_t c) {
             if (c != 0 && (c & mask) == prefix) atomicAdd(&hist256[(c >> shift) & 255], 1u);
         });
         __syncthreads();
-        const uint32_t cnt = hist256[255 - threadIdx.x];          // thread t owns bin 255 - t: scan from the top
+        const uint32_t cnt = tid < 256 ? hist256[255 - tid] : 0u;   // thread t owns bin 255 - t: scan from the top
         uint32_t tot;
         const uint32_t above = block_excl_scan<uint32_t>(cnt, wsum, &tot);
-        if (above < (uint32_t)kk && above + cnt >= (uint32_t)kk) {
-            r.misc[0] = 255 - threadIdx.x;
+        if (tid < 256 && above < (uint32_t)kk && above + cnt >= (uint32_t)kk) {
+            r.misc[0] = 255 - tid;
             r.misc[1] = above;
         }
         __syncthreads();
@@ -261,6 +377,17 @@ __device__ void bitonic_desc(uint64_t* a, int n) {
     }
 }
 
+// Rank sort of n <= SMALL distinct composites: out[rank] = in[i] for ranks < k.
+__device__ void rank_sort(const uint64_t* in, int n, uint64_t* out, int k) {
+    for (int i = threadIdx.x; i < n; i += BLOCK) {
+        const uint64_t c = in[i];
+        int rank = 0;
+        for (int m = 0; m < n; ++m) rank += in[m] > c ? 1 : 0;
+        if (rank < k) out[rank] = c;
+    }
+    __syncthreads();
+}
+
 __device__ __forceinline__ int64_t window_begin(int64_t len, const fs_row_params& p) {
     int64_t b = (p.repeat_last_n > 0 && (int64_t)p.repeat_last_n < len) ? len - (int64_t)p.repeat_last_n : 0;
     if (p.penalty_from > 0 && (int64_t)p.penalty_from > b) b = p.penalty_from;
@@ -269,27 +396,42 @@ __device__ __forceinline__ int64_t window_begin(int64_t len, const fs_row_params
 
 // ------------------------------------------------------------------------------------------------ kernel
 template <int EPT>
-__global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
+__global__ __launch_bounds__(BLOCK, 4) void sample_kernel(Args a) {
     constexpr int NV = EPT / 4;                 // float4 loads per thread
     constexpr int CHUNK = BLOCK * EPT;
-    static_assert(CHUNK / 2 <= CAP * 2, "count table must fit the candidate list storage");
+    static_assert(CHUNK * 2 <= CAP * 8, "the 16-bit count table must fit the candidate storage");
+    static_assert(2 * SMALL * 8 <= NBINS * 4, "rank-sort buffers alias the histogram");
 
-    __shared__ __align__(16) uint64_t s_list[CAP];   // counts (chunk phase) / candidate list / merge list
-    __shared__ __align__(16) uint32_t s_bins[NBINS]; // threshold histogram / chunk counts / rank-sort output
+    __shared__ __align__(16) uint64_t s_big[CAP];    // counts (chunk phase) / chunk candidates / merge gather
+    __shared__ __align__(16) uint32_t s_bins[NBINS]; // histograms; merge: rank-sort input and output
     __shared__ uint32_t s_off[MAX_CHUNKS + 1];       // merge: flat offsets of the chunk lists
     __shared__ uint32_t s_wsum[NWAVES];
     __shared__ uint32_t s_count;
     __shared__ Red red;
 
     const int tid = threadIdx.x;
-    int bid = blockIdx.x;
-    if (a.xcd_remap) bid = (bid & 7) * ((int)gridDim.x >> 3) + (bid >> 3);   // consecutive rows share an XCD's L2
-    const int row = bid / a.nchunks;
-    const int chunk = bid - row * a.nchunks;
+    const int row = blockIdx.x / a.nchunks;
+    const int chunk = blockIdx.x - row * a.nchunks;
     const int V = a.V;
     const int lo = chunk * CHUNK;
+    const float* rowp = a.logits + (int64_t)row * a.ld;
 
-    // ---- row descriptor: params, history segments (verify rows see base history + earlier drafts)
+    // ---- 1. stream the chunk: every load is issued before anything waits
+    float x[NV][4];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int e = lo + (j * BLOCK + tid) * 4;
+        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (e + 4 <= V) t = *reinterpret_cast<const float4*>(rowp + e);
+        else if (e < V) {                            // row tail: never read past element V-1
+            t.x = rowp[e];
+            if (e + 1 < V) t.y = rowp[e + 1];
+            if (e + 2 < V) t.z = rowp[e + 2];
+        }
+        x[j][0] = t.x; x[j][1] = t.y; x[j][2] = t.z; x[j][3] = t.w;
+    }
+
+    // ---- 2. row descriptor: params, history segments (verify rows see base history + earlier drafts)
     int pidx = row;
     int64_t hA0 = 0, lenA = 0, lenB = 0;
     const int32_t* segB = nullptr;
@@ -319,29 +461,13 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
     int k = greedy ? 1 : ((p.top_k > 0 && p.top_k < V) ? p.top_k : V);
     const bool large = k > KMAX;                 // not on the fused select path: reported, token -1
 
-    // ---- 1. stream the chunk (issued before anything waits)
-    const float* rowp = a.logits + (int64_t)row * a.ld;
-    float x[NV][4];
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const int e = lo + (j * BLOCK + tid) * 4;
-        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (e + 4 <= V && !large) t = *reinterpret_cast<const float4*>(rowp + e);
-        else if (e < V && !large) {                  // row tail: never read past element V-1
-            t.x = rowp[e];
-            if (e + 1 < V) t.y = rowp[e + 1];
-            if (e + 2 < V) t.z = rowp[e + 2];
-        }
-        x[j][0] = t.x; x[j][1] = t.y; x[j][2] = t.z; x[j][3] = t.w;
-    }
-
-    // ---- 2. penalties (sampler.cpp:11-18; frequency/presence extension)
+    // ---- 3. penalties (sampler.cpp:11-18; frequency/presence extension)
     const bool rep_on = p.repetition_penalty != 1.0f;
     const bool fp_on = p.frequency_penalty != 0.0f || p.presence_penalty != 0.0f;
     const int64_t len = lenA + lenB;
-    const bool pen = !large && (rep_on || fp_on) && p.repeat_last_n != 0 && len > 0 && (lenB > 0 || a.hist != nullptr);
+    const bool pen = !large && (rep_on || fp_on) && p.repeat_last_n != 0 && len > 0;
     if (pen) {
-        uint32_t* cnt = reinterpret_cast<uint32_t*>(s_list);   // CHUNK 16-bit counters, two per word
+        uint32_t* cnt = reinterpret_cast<uint32_t*>(s_big);   // CHUNK 16-bit counters, two per word
         for (int i = tid; i < CHUNK / 8; i += BLOCK) reinterpret_cast<uint4*>(cnt)[i] = make_uint4(0u, 0u, 0u, 0u);
         __syncthreads();
         const int64_t b = window_begin(len, p);
@@ -378,7 +504,7 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
         __syncthreads();                                     // the count table's storage is reused below
     }
 
-    // ---- 3. keys (0 marks an element past V)
+    // ---- 4. keys (0 marks an element past V)
     uint32_t key[NV][4];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
@@ -391,10 +517,11 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
         return e < V ? comp_of(key[j][q], (uint32_t)e) : 0ull;
     };
 
+    // ---- 5. chunk selection, published with agent-scope stores
     const int slot = row * a.nchunks + chunk;
     uint64_t* gout = a.cand + (int64_t)slot * CAP;
     if (large) {
-        if (tid == 0) { a.meta[2 * slot] = 0u; a.meta[2 * slot + 1] = 0u; }
+        if (tid == 0) { st_agent(&a.meta[2 * slot], 0u); st_agent(&a.meta[2 * slot + 1], 0u); }
     } else if (greedy) {
         uint64_t best = 0;
 #pragma unroll
@@ -403,54 +530,55 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
             for (int q = 0; q < 4; ++q) { const uint64_t c = comp_at(j, q); best = c > best ? c : best; }
         best = block_max_u64(best, red);
         if (tid == 0) {
-            gout[0] = best;
-            a.meta[2 * slot] = (uint32_t)(best >> 32);
-            a.meta[2 * slot + 1] = 1u;
+            st_agent(gout, best);
+            st_agent(&a.meta[2 * slot], comp_key(best));
+            st_agent(&a.meta[2 * slot + 1], 1u);
         }
     } else {
         const int nvalid = min(CHUNK, V - lo);
         uint32_t T0 = 0;
         if (k < nvalid) {
-            // group maxima: G groups per thread, 256*G >= k
+            // maxima of G groups per thread, BLOCK*G >= 2k groups in all (G <= EPT)
             int G = 1;
-            while (G * BLOCK < k && G < EPT) G <<= 1;
+            while (G * BLOCK < 2 * k && G < EPT) G <<= 1;
             const int per = EPT / G;                 // elements per group, in thread-local order j*4+q
-            for (int i = tid; i < NBINS; i += BLOCK) s_bins[i] = 0u;
-            __syncthreads();
-            uint32_t gm = 0;
-            bool any = false;
+            uint32_t gmin = 0xFFFFFFFFu, gmax = 0u;
+            {
+                uint32_t gm = 0;
+                bool any = false;
 #pragma unroll
-            for (int j = 0; j < NV; ++j)
+                for (int j = 0; j < NV; ++j)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int e = lo + (j * BLOCK + tid) * 4 + q;
-                    if (e < V) { gm = key[j][q] > gm ? key[j][q] : gm; any = true; }
-                    if ((j * 4 + q + 1) % per == 0) {
-                        if (any) atomicAdd(&s_bins[gm >> (32 - HBITS)], 1u);
-                        gm = 0;
-                        any = false;
+                    for (int q = 0; q < 4; ++q) {
+                        if (lo + (j * BLOCK + tid) * 4 + q < V) { gm = key[j][q] > gm ? key[j][q] : gm; any = true; }
+                        if ((j * 4 + q + 1) % per == 0) {
+                            if (any) { gmin = gm < gmin ? gm : gmin; gmax = gm > gmax ? gm : gmax; }
+                            gm = 0;
+                            any = false;
+                        }
                     }
-                }
-            __syncthreads();
-            // scan bins from the top: thread t owns bins [NBINS-1-8t-7, NBINS-1-8t]
-            constexpr int BPT = NBINS / BLOCK;
-            uint32_t mine = 0;
+            }
+            for (int i = tid; i < NBINS; i += BLOCK) s_bins[i] = 0u;
+            block_minmax_u32(gmin, gmax, red);
+            const int sh = range_shift(gmin, gmax);
+            {
+                uint32_t gm = 0;
+                bool any = false;
 #pragma unroll
-            for (int i = 0; i < BPT; ++i) mine += s_bins[NBINS - 1 - (tid * BPT + i)];
-            uint32_t tot;
-            const uint32_t above = block_excl_scan<uint32_t>(mine, s_wsum, &tot);
-            if (tid == 0) red.misc[2] = 0u;
-            __syncthreads();
-            if (tot >= (uint32_t)k && above < (uint32_t)k && above + mine >= (uint32_t)k) {
-                uint32_t c = above;
-                for (int i = 0; i < BPT; ++i) {
-                    const int bin = NBINS - 1 - (tid * BPT + i);
-                    c += s_bins[bin];
-                    if (c >= (uint32_t)k) { red.misc[2] = (uint32_t)bin << (32 - HBITS); break; }
-                }
+                for (int j = 0; j < NV; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        if (lo + (j * BLOCK + tid) * 4 + q < V) { gm = key[j][q] > gm ? key[j][q] : gm; any = true; }
+                        if ((j * 4 + q + 1) % per == 0) {
+                            if (any) atomicAdd(&s_bins[(gm - gmin) >> sh], 1u);
+                            gm = 0;
+                            any = false;
+                        }
+                    }
             }
             __syncthreads();
-            T0 = red.misc[2];                        // 0 when the groups could not certify k (take all)
+            uint32_t c0;
+            T0 = hist_threshold(s_bins, gmin, sh, k, &c0, s_wsum, red);   // 0: groups could not certify k
         }
         // compaction of keys >= T0
         if (tid == 0) s_count = 0u;
@@ -459,54 +587,105 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
         for (int j = 0; j < NV; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const uint64_t c = comp_at(j, q);
-                wave_append(c != 0 && key[j][q] >= T0, c, s_list, &s_count, CAP);
+                const int e = lo + (j * BLOCK + tid) * 4 + q;
+                wave_append_kv(e < V && key[j][q] >= T0, key[j][q], (uint32_t)e, s_big, &s_count, CAP);
             }
         __syncthreads();
         uint32_t n = s_count;
         if (n > (uint32_t)CAP) {
-            // too many ties near the threshold: exact k-th composite over the registers
-            __syncthreads();
-            const uint64_t X = radix_kth(
-                [&](auto&& f) {
-#pragma unroll
-                    for (int j = 0; j < NV; ++j)
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) f(comp_at(j, q));
-                },
-                k, s_bins, s_wsum, red);
-            if (tid == 0) s_count = 0u;
-            __syncthreads();
+            // Too many keys >= T0 (a flat distribution or ties): narrow [rlo, rhi] onto the exact k-th key with
+            // histogram levels over the registers (2048x per level, 4 levels reach a single key value).
+            // Invariant: count(key > rhi) == above < k <= count(key >= rlo).
+            uint32_t rlo = T0, rhi = 0u, above = 0u, cnt_ge = n;
 #pragma unroll
             for (int j = 0; j < NV; ++j)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint64_t c = comp_at(j, q);
-                    wave_append(c != 0 && c >= X, c, s_list, &s_count, CAP);
-                }
+                for (int q = 0; q < 4; ++q) rhi = key[j][q] > rhi ? key[j][q] : rhi;   // invalid keys are 0
+            {
+                uint32_t dummy = 0u;
+                block_minmax_u32(dummy, rhi, red);
+            }
+            for (int level = 0; level < 4 && cnt_ge > (uint32_t)CAP && rlo != rhi; ++level) {
+                const int sh = range_shift(rlo, rhi);
+                for (int i = tid; i < NBINS; i += BLOCK) s_bins[i] = 0u;
+                __syncthreads();
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t kq = key[j][q];
+                        if (lo + (j * BLOCK + tid) * 4 + q < V && kq >= rlo && kq <= rhi)
+                            atomicAdd(&s_bins[(kq - rlo) >> sh], 1u);
+                    }
+                __syncthreads();
+                uint32_t ab, atb;
+                const int bsel = hist_locate(s_bins, k - (int)above, &ab, &atb, s_wsum, red);
+                const uint64_t nlo = (uint64_t)rlo + ((uint64_t)bsel << sh);
+                const uint64_t nhi = (uint64_t)rlo + (((uint64_t)bsel + 1) << sh) - 1;
+                rlo = (uint32_t)nlo;
+                rhi = nhi < rhi ? (uint32_t)nhi : rhi;
+                above += ab;
+                cnt_ge = above + atb;
+            }
+            if (tid == 0) s_count = 0u;
             __syncthreads();
-            n = s_count;                              // == k
-            T0 = (uint32_t)(X >> 32);
+            if (cnt_ge <= (uint32_t)CAP) {
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int e = lo + (j * BLOCK + tid) * 4 + q;
+                        wave_append_kv(e < V && key[j][q] >= rlo, key[j][q], (uint32_t)e, s_big, &s_count, CAP);
+                    }
+            } else {
+                // rlo == rhi is the k-th key t and it is tied: keep every key > t and the (k - above) lowest ids
+                // with key == t; ids run in (j, thread, q) order, so one block scan per j ranks the ties
+                const uint32_t t = rlo;
+                const uint32_t need = (uint32_t)k - above;
+                uint32_t run = 0u;
+#pragma unroll
+                for (int j = 0; j < NV; ++j) {
+                    uint32_t mine = 0u;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        mine += (lo + (j * BLOCK + tid) * 4 + q < V && key[j][q] == t) ? 1u : 0u;
+                    uint32_t tot;
+                    uint32_t pos = run + block_excl_scan<uint32_t>(mine, s_wsum, &tot);
+                    run += tot;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int e = lo + (j * BLOCK + tid) * 4 + q;
+                        const bool valid = e < V;
+                        const bool tie = valid && key[j][q] == t;
+                        const bool take = (valid && key[j][q] > t) || (tie && pos < need);
+                        pos += tie ? 1u : 0u;
+                        wave_append_kv(take, key[j][q], (uint32_t)e, s_big, &s_count, CAP);
+                    }
+                }
+            }
+            __syncthreads();
+            n = s_count;
+            T0 = rlo;
         }
-        for (uint32_t i = tid; i < n; i += BLOCK) gout[i] = s_list[i];
+        for (uint32_t i = tid; i < n; i += BLOCK) st_agent(gout + i, s_big[i]);
         if (tid == 0) {
-            a.meta[2 * slot] = T0;
-            a.meta[2 * slot + 1] = n;
+            st_agent(&a.meta[2 * slot], T0);
+            st_agent(&a.meta[2 * slot + 1], n);
         }
     }
 
-    // ---- completion: the last chunk of the row merges
-    __threadfence();
+    // ---- 6. hand-off: drain this wave's stores, then one agent-scope count per chunk; the last one merges
+    vm_drain();
     __syncthreads();
     if (tid == 0) {
-        const uint32_t old = atomicAdd(&a.row_cnt[row], 1u);
+        const uint32_t old = __hip_atomic_fetch_add(&a.row_cnt[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         red.misc[3] = (old == (uint32_t)a.nchunks - 1u) ? 1u : 0u;
     }
     __syncthreads();
     if (red.misc[3] == 0u) return;
-    __threadfence();
-    if (tid == 0) a.row_cnt[row] = 0u;
+    if (tid == 0) st_agent(&a.row_cnt[row], 0u);
 
+    // ---- 7. merge
     const int nch = a.nchunks;
     const int slot0 = row * nch;
     int tok = 0, keep = 1;
@@ -517,7 +696,7 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
     } else if (greedy) {
         uint64_t best = 0;
         for (int c = tid; c < nch; c += BLOCK) {
-            const uint64_t v = a.cand[(int64_t)(slot0 + c) * CAP];
+            const uint64_t v = ld_agent(a.cand + (int64_t)(slot0 + c) * CAP);
             best = v > best ? v : best;
         }
         best = block_max_u64(best, red);
@@ -529,24 +708,21 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
             if (a.cand_probs && a.kcap > 0) a.cand_probs[(int64_t)row * a.kcap] = 1.0;
         }
     } else {
-        // ---- merge round 1: metas and the first SPEC entries of every chunk in one round trip
-        // thread t serves chunk (t % nch) for nch <= BLOCK; larger nch loop (rare: V > 4M at EPT 16)
-        uint32_t Lloc = 0;
-        for (int c = tid; c < nch; c += BLOCK) {
-            const uint32_t t0 = a.meta[2 * (slot0 + c)];
+        // metas: L = max T0 (a lower bound of the row's k-th key), flat offsets of the chunk lists
+        uint32_t Lloc = 0, nmine = 0;
+        for (int c = 2 * tid; c < 2 * tid + 2 && c < nch; ++c) {
+            const uint32_t t0 = ld_agent(&a.meta[2 * (slot0 + c)]);
+            const uint32_t cn = ld_agent(&a.meta[2 * (slot0 + c) + 1]);
             Lloc = t0 > Lloc ? t0 : Lloc;
-            s_bins[c] = a.meta[2 * (slot0 + c) + 1];
+            s_off[c] = cn;
+            nmine += cn;
         }
-        const uint32_t L = (uint32_t)(block_max_u64(Lloc, red));
-        // flat offsets of the chunk lists: s_off[c] exclusive offset, s_off[nch] = total
-        if (tid == 0) {
-            uint32_t o = 0;
-            for (int c = 0; c < nch; ++c) { const uint32_t n = s_bins[c]; s_off[c] = o; o += n; }
-            s_off[nch] = o;
-            s_count = 0u;
-        }
+        const uint32_t L = (uint32_t)block_max_u64(Lloc, red);
+        uint32_t total;
+        uint32_t o = block_excl_scan<uint32_t>(nmine, s_wsum, &total);
+        for (int c = 2 * tid; c < 2 * tid + 2 && c < nch; ++c) { const uint32_t cn = s_off[c]; s_off[c] = o; o += cn; }
+        if (tid == 0) { s_off[nch] = total; s_count = 0u; }
         __syncthreads();
-        const uint32_t total = s_off[nch];
         auto fetch = [&](uint32_t f) -> uint64_t {          // flat index -> candidate (0 past the end)
             if (f >= total) return 0ull;
             int c0 = 0, c1 = nch;                            // largest c with s_off[c] <= f
@@ -554,62 +730,103 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
                 const int m = (c0 + c1) >> 1;
                 if (s_off[m] <= f) c0 = m; else c1 = m;
             }
-            return a.cand[(int64_t)(slot0 + c0) * CAP + (f - s_off[c0])];
+            return ld_agent(a.cand + (int64_t)(slot0 + c0) * CAP + (f - s_off[c0]));
         };
+        // gather the candidates >= L into LDS (counted past CAP), tracking their max key
+        uint32_t kmax = L;
         for (uint32_t f0 = 0; f0 < total; f0 += BLOCK * SPEC) {
             uint64_t v[SPEC];
 #pragma unroll
             for (int q = 0; q < SPEC; ++q) v[q] = fetch(f0 + q * BLOCK + tid);
 #pragma unroll
-            for (int q = 0; q < SPEC; ++q)
-                wave_append(v[q] != 0 && (uint32_t)(v[q] >> 32) >= L, v[q], s_list, &s_count, CAP);
+            for (int q = 0; q < SPEC; ++q) {
+                const bool in = v[q] != 0 && comp_key(v[q]) >= L;
+                if (in) kmax = comp_key(v[q]) > kmax ? comp_key(v[q]) : kmax;
+                wave_append(in, v[q], s_big, &s_count, CAP);
+            }
+        }
+        for (int i = tid; i < NBINS; i += BLOCK) s_bins[i] = 0u;
+        uint32_t kmin = L;
+        block_minmax_u32(kmin, kmax, red);
+        const uint32_t n = s_count;
+        const bool in_lds = n <= (uint32_t)CAP;
+        // T1: tight threshold from a histogram of the candidates' keys over [L, kmax]
+        const int sh = range_shift(L, kmax);
+        if (in_lds) {
+            for (uint32_t i = tid; i < n; i += BLOCK) atomicAdd(&s_bins[(comp_key(s_big[i]) - L) >> sh], 1u);
+        } else {
+            for (uint32_t f = tid; f < total; f += BLOCK) {
+                const uint64_t c = fetch(f);
+                if (c != 0 && comp_key(c) >= L) atomicAdd(&s_bins[(comp_key(c) - L) >> sh], 1u);
+            }
         }
         __syncthreads();
-        uint32_t n = s_count;
-        if (n > (uint32_t)CAP) {
-            // too many candidates at L (ties across chunks): exact k-th over the flat list, then gather >= X
-            auto each = [&](auto&& f) {
-                for (uint32_t f0 = tid; f0 < total; f0 += BLOCK) {
-                    const uint64_t c = fetch(f0);
-                    f((uint32_t)(c >> 32) >= L ? c : 0ull);
+        uint32_t c1;
+        const uint32_t T1 = hist_threshold(s_bins, L, sh, k, &c1, s_wsum, red);
+        // the c1 >= k candidates with key >= T1 contain the top k: sort them
+        uint64_t* top;
+        uint64_t* small_in = reinterpret_cast<uint64_t*>(s_bins);
+        uint64_t* small_out = small_in + SMALL;
+        if (tid == 0) s_count = 0u;
+        __syncthreads();
+        if (c1 <= (uint32_t)SMALL) {
+            if (in_lds) {
+                for (uint32_t i0 = 0; i0 < n; i0 += BLOCK) {
+                    const uint32_t i = i0 + tid;
+                    const uint64_t c = i < n ? s_big[i] : 0ull;
+                    wave_append(c != 0 && comp_key(c) >= T1, c, small_in, &s_count, SMALL);
                 }
-            };
-            const uint64_t X = radix_kth(each, k, s_bins, s_wsum, red);
-            if (tid == 0) s_count = 0u;
-            __syncthreads();
-            each([&](uint64_t c) { wave_append(c != 0 && c >= X, c, s_list, &s_count, CAP); });
-            __syncthreads();
-            n = s_count;
-        }
-        // ---- sort the n >= k candidates, descending; the first k are ferro's cand_ (sampler.cpp:25-35)
-        if (n < (uint32_t)k) {                       // impossible by construction; never read past the list
-            if (tid == 0) atomicOr(a.err, FS_DEVERR_INTERNAL);
-            k = (int)n;
-        }
-        uint64_t* top = s_list;
-        if (n <= 512) {
-            // rank by counting (candidates are distinct), ranks < k land in order
-            uint64_t* out = reinterpret_cast<uint64_t*>(s_bins);
-            for (uint32_t i = tid; i < n; i += BLOCK) {
-                const uint64_t c = s_list[i];
-                uint32_t rank = 0;
-                for (uint32_t m = 0; m < n; ++m) rank += s_list[m] > c ? 1u : 0u;
-                if (rank < (uint32_t)k) out[rank] = c;
+            } else {
+                for (uint32_t f0 = 0; f0 < total; f0 += BLOCK) {
+                    const uint64_t c = fetch(f0 + tid);
+                    wave_append(c != 0 && comp_key(c) >= T1, c, small_in, &s_count, SMALL);
+                }
             }
             __syncthreads();
-            top = out;
-        } else {
+            rank_sort(small_in, (int)c1, small_out, k);
+            top = small_out;
+        } else if (in_lds) {
             int np = 1;
             while (np < (int)n) np <<= 1;
-            for (int i = (int)n + tid; i < np; i += BLOCK) s_list[i] = 0ull;
+            for (int i = (int)n + tid; i < np; i += BLOCK) s_big[i] = 0ull;
             __syncthreads();
-            bitonic_desc(s_list, np);
+            bitonic_desc(s_big, np);
+            top = s_big;
+        } else {
+            uint64_t X = 0;                             // threshold for an exact gather of <= CAP entries
+            if (c1 > (uint32_t)CAP) {
+                X = radix_kth(
+                    [&](auto&& f) {
+                        for (uint32_t f0 = tid; f0 < total; f0 += BLOCK) {
+                            const uint64_t c = fetch(f0);
+                            f(c != 0 && comp_key(c) >= L ? c : 0ull);
+                        }
+                    },
+                    k, s_bins, s_wsum, red);
+            }
+            if (tid == 0) s_count = 0u;
+            __syncthreads();
+            for (uint32_t f0 = 0; f0 < total; f0 += BLOCK) {
+                const uint64_t c = fetch(f0 + tid);
+                wave_append(c != 0 && comp_key(c) >= T1 && c >= X, c, s_big, &s_count, CAP);
+            }
+            __syncthreads();
+            const int m = (int)s_count;
+            int np = 1;
+            while (np < m) np <<= 1;
+            for (int i = m + tid; i < np; i += BLOCK) s_big[i] = 0ull;
+            __syncthreads();
+            bitonic_desc(s_big, np);
+            top = s_big;
+        }
+        if (c1 < (uint32_t)k) {                       // impossible by construction; never read past the list
+            if (tid == 0) atomicOr(a.err, FS_DEVERR_INTERNAL);
+            k = (int)c1;
         }
 
         // ---- softmax at temperature, min-p, top-p, draw (sampler.cpp:37-49), k <= KMAX
-        constexpr int KPT = KMAX / BLOCK;            // candidates per thread, contiguous
         const int i0 = tid * KPT;
-        const float mx = val_of((uint32_t)(top[0] >> 32));
+        const float mx = val_of(comp_key(top[0]));
         const double Td = (double)p.temperature;
         double e[KPT];
         double part = 0.0;
@@ -618,7 +835,7 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
             const int i = i0 + q;
             e[q] = 0.0;
             if (i < k) {
-                const float d = val_of((uint32_t)(top[i] >> 32)) - mx;   // fp32 subtraction, as ferro
+                const float d = val_of(comp_key(top[i])) - mx;   // fp32 subtraction, as ferro
                 e[q] = exp((double)d / Td);
                 part += e[q];
             }
@@ -683,26 +900,27 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
             }
         }
     }
-    if (tid == 0) {
-        a.tok[row] = tok;
-        if (a.keep && a.mode != MODE_VERIFY) a.keep[row] = keep;
+    if (a.mode != MODE_VERIFY) {
+        if (tid == 0) {
+            a.tok[row] = tok;
+            if (a.keep) a.keep[row] = keep;
+        }
+        return;
     }
-    if (a.mode != MODE_VERIFY) return;
 
     // ---- verify: the last row of a stream to finish computes the accepted prefix (server.cpp:627-637)
-    __threadfence();
-    __syncthreads();
     if (tid == 0) {
+        st_agent(&a.tok[row], (int32_t)tok);
+        vm_drain();
         const int s = pidx;
         const int64_t r0 = a.row_off[s];
         const int m = (int)(a.row_off[s + 1] - r0);
-        const uint32_t old = atomicAdd(&a.stream_cnt[s], 1u);
+        const uint32_t old = __hip_atomic_fetch_add(&a.stream_cnt[s], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (old == (uint32_t)m - 1u) {
-            __threadfence();
-            a.stream_cnt[s] = 0u;
+            st_agent(&a.stream_cnt[s], 0u);
             int acc = 0;
             for (int r = 0; r < m; ++r) {
-                const int t = __hip_atomic_load(&a.tok[r0 + r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const int t = ld_agent(&a.tok[r0 + r]);
                 acc = r + 1;
                 if (a.eos >= 0 && t == a.eos) break;
                 if (r + 1 < m && t == a.rows[r0 + r + 1]) continue;
@@ -761,14 +979,19 @@ int grow(fs_context* c, size_t slots, size_t rows, size_t streams) {
     return FS_OK;
 }
 
-// Chunk size: 8192 elements per workgroup when the grid is large enough to fill 256 CUs, else 4096.
+// Chunk size: the largest of 16384 / 8192 / 2048 elements per workgroup that still puts >= 256 workgroups on the
+// chip (one per CU); fewer, longer chunks mean fewer candidates to merge per row.
 int choose_ept(int64_t rows, int V) {
-    const int64_t big = rows * ((V + 256 * 32 - 1) / (256 * 32));
-    return big >= 512 ? 32 : 16;
+    for (int ept : {32, 16}) {
+        const int64_t nch = (V + fs::BLOCK * ept - 1) / (fs::BLOCK * ept);
+        if (rows * nch >= 256) return ept;
+    }
+    return 4;
 }
 
 int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream_t st) {
-    const int ept = choose_ept(rows, a.V);
+    int ept = choose_ept(rows, a.V);
+    while (ept < 32 && (a.V + fs::BLOCK * ept - 1) / (fs::BLOCK * ept) > fs::MAX_CHUNKS) ept *= 4;
     const int chunk = fs::BLOCK * ept;
     a.nchunks = (a.V + chunk - 1) / chunk;
     if (a.nchunks > fs::MAX_CHUNKS) return FS_E_INVALID;
@@ -779,9 +1002,9 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
     int rc = grow(ctx, (size_t)grid, (size_t)rows, (size_t)(streams > 0 ? streams : 1));
     if (rc != FS_OK) return rc;
     a.cand = ctx->cand; a.meta = ctx->meta; a.row_cnt = ctx->row_cnt; a.stream_cnt = ctx->stream_cnt; a.err = ctx->err;
-    a.xcd_remap = (grid % 8 == 0) ? 1 : 0;
     if (ept == 32) hipLaunchKernelGGL(fs::sample_kernel<32>, dim3((unsigned)grid), dim3(fs::BLOCK), 0, st, a);
-    else hipLaunchKernelGGL(fs::sample_kernel<16>, dim3((unsigned)grid), dim3(fs::BLOCK), 0, st, a);
+    else if (ept == 16) hipLaunchKernelGGL(fs::sample_kernel<16>, dim3((unsigned)grid), dim3(fs::BLOCK), 0, st, a);
+    else hipLaunchKernelGGL(fs::sample_kernel<4>, dim3((unsigned)grid), dim3(fs::BLOCK), 0, st, a);
     return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
 }
 
