@@ -17,6 +17,8 @@ FLAGS = [
     "-ffp-contract=off",
     # packed-FP32 instructions are kept out of the device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # the persistent kernel's loop would otherwise hoist exp()'s constants and lane masks out of it and spill them
+    "-mllvm", "-disable-machine-licm",
     "-I" + os.path.join(ROOT, "include"),
 ]
 

@@ -1,25 +1,29 @@
 // sampler_kernels.hip - gfx950 (CDNA4) kernels of the token sampler and the C ABI of include/ferro_sampler.h.
 //
-// One fused kernel per call. A row of V fp32 logits is split into chunks of BLOCK*EPT elements, one 512-thread
-// workgroup per chunk (grid = B * nchunks, rows in order so early rows merge while later rows stream).
-// Each chunk workgroup:
-//   1. issues all of its 16-byte loads first (EPT/4 per thread, the chunk's only pass over HBM);
-//   2. applies the penalty pass on the fly: the row's history window is scattered into an LDS table of 16-bit
-//      counts over the chunk's ids and each thread patches the few penalised elements it holds
-//      (reference src/sampler.cpp:11-18, plus the frequency/presence extension);
-//   3. maps each logit to an order-preserving 32-bit key (-0 folded onto +0); for a top-k row it histograms the
-//      maxima of >= 2k disjoint groups of its elements over their [min, max] key range and takes the floor T0 of
-//      the bin where the count from the top reaches k - at least k of the chunk's elements reach T0;
-//   4. compacts the elements with key >= T0 (a little over k) into LDS with wave ballots and publishes them as
-//      64-bit composites (key << 32 | ~id: larger = earlier in ferro's candidate order, sampler.cpp:30); a chunk
-//      with too many ties at T0 falls back to an exact radix select over its registers.
-// Hand-off without an L2 write-back: the lists are written with agent-scope (sc1, write-through) stores, each wave
-// drains its stores (s_waitcnt vmcnt(0)), then one agent-scope counter add per workgroup; the last workgroup of a
-// row reads the lists with agent-scope loads and merges: L = max T0 bounds the row's k-th key from below, a
-// histogram of the candidates >= L over [L, max] gives a tight T1, the ~k candidates >= T1 are rank-sorted in LDS,
-// and the first k feed the double-precision softmax / min-p / top-p / draw (sampler.cpp:37-49), with block scans
-// in place of the sequential sums. Greedy rows (temperature <= 0 or top_k == 1, sampler.cpp:19) publish one
-// (key, lowest id) maximum per chunk.
+// Two kernels per call on the caller's stream.
+//
+// segment_kernel (persistent, two 512-thread workgroups per CU): a row of V fp32 logits is split into nseg
+// segments of seg_tiles tiles (TILE = 4096 logits); workgroup g handles items g, g+G, ... (item = row*nseg + seg,
+// row-major). A segment is streamed from HBM with PF tiles in flight (16-byte loads, the only pass over the
+// logits). Per tile:
+//   - penalty pass on the fly (reference src/sampler.cpp:11-18, plus the frequency/presence extension): the row's
+//     history window ids that fall in the tile are counted in a 16-bit LDS table and each thread patches the few
+//     penalised logits it holds;
+//   - greedy rows (temperature <= 0 or top_k == 1, sampler.cpp:19): each lane keeps its first maximum
+//     (order-preserving 32-bit keys, -0 folded onto +0, so ties go to the lowest id);
+//   - top-k rows: every logit is compared with a running fp32 threshold tf; the few that pass are checked against
+//     the exact 64-bit composite threshold X (key << 32 | ~id: integer order = ferro's candidate order, value desc
+//     then id asc, sampler.cpp:30) and appended to an LDS buffer with one LDS atomic per wave per tile.
+// The initial threshold comes from tile 0 (the maxima of >= 2k groups, histogrammed over their [min, max]: at least
+// k logits reach it); the buffer is compacted to the exact k-th composite when another tile could overflow it,
+// and at the end of the segment, so each segment publishes exactly its top k (or everything, if fewer).
+//
+// merge_kernel (one workgroup per row): gathers the segments' lists in one memory round trip, L = max of the
+// segments' k-th keys bounds the row's k-th key from below, a histogram over [L, max] gives a tight T1, the ~k
+// candidates >= T1 are rank-sorted in LDS (ferro's cand_, sampler.cpp:25-35), then the double-precision softmax
+// at temperature, min-p, top-p and the draw r = u * tot (sampler.cpp:37-49), with block scans in place of the
+// sequential sums. Verify windows (server.cpp:627-637): the last row of a stream to finish (agent-scope sc1
+// stores, a vmcnt drain and an agent-scope counter, no L2 write-back) computes the accepted prefix.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -38,14 +42,19 @@ namespace fs {
 constexpr int BLOCK = 512;                // threads per workgroup: 8 wave64s, two workgroups per CU
 constexpr int WAVE = 64;
 constexpr int NWAVES = BLOCK / WAVE;
+constexpr int TPT = 8;                    // logits per thread per tile
+constexpr int NV = TPT / 4;               // float4 loads per thread per tile
+constexpr int TILE = BLOCK * TPT;         // 4096 logits per tile
+constexpr int PF = 2;                     // tiles in flight per workgroup
 constexpr int KMAX = 2048;                // largest k on the fused select path
 constexpr int KPT = KMAX / BLOCK;         // candidates per thread in the softmax / draw phase
-constexpr int CAP = 8192;                 // candidates per chunk in the workspace; merge gather capacity in LDS
+constexpr int CAP = KMAX + TILE;          // candidate buffer (LDS), per-segment list in the workspace, merge gather
 constexpr int HBITS = 11;
 constexpr int NBINS = 1 << HBITS;         // threshold histograms
 constexpr int SMALL = 512;                // rank-sort capacity of the merge
-constexpr int MAX_CHUNKS = 1024;
-constexpr int SPEC = 4;                   // merge gather: loads in flight per thread per round
+constexpr int MAX_SEGS = 1024;            // segments per row
+constexpr int SPEC = 8;                   // merge gather: loads in flight per thread per round
+constexpr int HPF = 2;                    // history-window ids per thread fetched with a segment's first tiles
 
 enum Mode : int { MODE_SAMPLE = 0, MODE_ARGMAX = 1, MODE_VERIFY = 2 };
 
@@ -69,10 +78,11 @@ struct Args {
     int eos;
     int32_t* accepted;
     int mode;
-    int nchunks;
-    uint64_t* cand;                // [B*nchunks][CAP]
-    uint32_t* meta;                // [B*nchunks][2]: T0, count
-    uint32_t* row_cnt;             // [B] chunk completion counters, left at 0
+    int nseg;                      // segments per row
+    int seg_tiles;                 // tiles per segment
+    uint64_t* cand;                // [B*nseg][CAP]
+    uint32_t* meta;                // [B*nseg][2]: lower bound of the k-th key, count
+    uint32_t* row_cnt;             // [B] segment completion counters, left at 0
     uint32_t* stream_cnt;          // [n_streams] verify completion counters, left at 0
     int32_t* err;                  // device error bits
 };
@@ -395,429 +405,376 @@ __device__ __forceinline__ int64_t window_begin(int64_t len, const fs_row_params
 }
 
 // ------------------------------------------------------------------------------------------------ kernel
-template <int EPT>
-__global__ __launch_bounds__(BLOCK, 4) void sample_kernel(Args a) {
-    constexpr int NV = EPT / 4;                 // float4 loads per thread
-    constexpr int CHUNK = BLOCK * EPT;
-    static_assert(CHUNK * 2 <= CAP * 8, "the 16-bit count table must fit the candidate storage");
-    static_assert(2 * SMALL * 8 <= NBINS * 4, "rank-sort buffers alias the histogram");
+struct Shared {
+    uint64_t cand[CAP];                // candidate buffer / merge gather
+    uint32_t scr[TILE / 2 + NBINS];    // per-tile 16-bit penalty counts, then histograms; or a 64-bit stage
+    uint32_t off[MAX_SEGS + 1];        // merge: flat offsets of the segment lists
+    uint32_t wsum[NWAVES];
+    uint32_t count;
+    uint32_t flag;
+    Red red;
+    __device__ __forceinline__ uint32_t* cnt() { return scr; }
+    __device__ __forceinline__ uint32_t* bins() { return scr + TILE / 2; }
+    __device__ __forceinline__ uint64_t* stage() { return reinterpret_cast<uint64_t*>(scr); }   // KMAX entries
+};
+static_assert((TILE / 2 + NBINS) / 2 >= KMAX, "the stage holds a compacted top k");
 
-    __shared__ __align__(16) uint64_t s_big[CAP];    // counts (chunk phase) / chunk candidates / merge gather
-    __shared__ __align__(16) uint32_t s_bins[NBINS]; // histograms; merge: rank-sort input and output
-    __shared__ uint32_t s_off[MAX_CHUNKS + 1];       // merge: flat offsets of the chunk lists
-    __shared__ uint32_t s_wsum[NWAVES];
-    __shared__ uint32_t s_count;
-    __shared__ Red red;
+// Per-row view of the arguments: params, greedy/k, and the two history segments (a verify row sees its stream's
+// base history followed by the drafts fed before it).
+struct RowCtx {
+    int row, pidx;
+    fs_row_params p;
+    bool greedy, large, pen, rep_on, fp_on;
+    int k;
+    int64_t hA0, lenA, lenB, b, len;     // window [b, len) over the concatenated history
+    const int32_t* segB;
+};
 
-    const int tid = threadIdx.x;
-    const int row = blockIdx.x / a.nchunks;
-    const int chunk = blockIdx.x - row * a.nchunks;
-    const int V = a.V;
-    const int lo = chunk * CHUNK;
-    const float* rowp = a.logits + (int64_t)row * a.ld;
+// Inputs that no kernel writes (params, history offsets, verify row offsets) are read through the constant address
+// space, so uniform indices become scalar loads (lgkmcnt) and never wait behind the vector loads in flight.
+template <class T>
+__device__ __forceinline__ T ld_const(const T* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return *(const __attribute__((address_space(4))) T*)(p);
+#else
+    return *p;                                  // the host pass never runs device code
+#endif
+}
 
-    // ---- 1. stream the chunk: every load is issued before anything waits
-    float x[NV][4];
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const int e = lo + (j * BLOCK + tid) * 4;
-        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (e + 4 <= V) t = *reinterpret_cast<const float4*>(rowp + e);
-        else if (e < V) {                            // row tail: never read past element V-1
-            t.x = rowp[e];
-            if (e + 1 < V) t.y = rowp[e + 1];
-            if (e + 2 < V) t.z = rowp[e + 2];
-        }
-        x[j][0] = t.x; x[j][1] = t.y; x[j][2] = t.z; x[j][3] = t.w;
-    }
-
-    // ---- 2. row descriptor: params, history segments (verify rows see base history + earlier drafts)
-    int pidx = row;
-    int64_t hA0 = 0, lenA = 0, lenB = 0;
-    const int32_t* segB = nullptr;
+__device__ __forceinline__ RowCtx row_ctx(const Args& a, int row) {
+    RowCtx rc;
+    rc.row = row;
+    rc.pidx = row;
+    rc.hA0 = 0; rc.lenA = 0; rc.lenB = 0;
+    rc.segB = nullptr;
     if (a.mode == MODE_VERIFY) {
         int s0 = 0, s1 = a.n_streams;           // largest s with row_off[s] <= row
         while (s1 - s0 > 1) {
             const int m = (s0 + s1) >> 1;
-            if (a.row_off[m] <= row) s0 = m; else s1 = m;
+            if (ld_const(a.row_off + m) <= row) s0 = m; else s1 = m;
         }
-        pidx = s0;
-        const int64_t r0 = a.row_off[s0];
-        segB = a.rows + r0 + 1;
-        lenB = row - r0;
+        rc.pidx = s0;
+        const int64_t r0 = ld_const(a.row_off + s0);
+        rc.segB = a.rows + r0 + 1;
+        rc.lenB = row - r0;
     }
     if (a.hist_off && a.hist) {
-        hA0 = a.hist_off[pidx];
-        lenA = a.hist_off[pidx + 1] - hA0;
+        rc.hA0 = ld_const(a.hist_off + rc.pidx);
+        rc.lenA = ld_const(a.hist_off + rc.pidx + 1) - rc.hA0;
     }
-    fs_row_params p;
-    if (a.params) p = a.params[pidx];
+    if (a.params) rc.p = ld_const(a.params + rc.pidx);
     else {
-        p.temperature = 0.f; p.top_k = 1; p.top_p = 1.f; p.min_p = 0.f; p.repetition_penalty = 1.f;
-        p.frequency_penalty = 0.f; p.presence_penalty = 0.f; p.repeat_last_n = 0; p.penalty_from = 0;
-        p.reserved = 0;
+        rc.p.temperature = 0.f; rc.p.top_k = 1; rc.p.top_p = 1.f; rc.p.min_p = 0.f; rc.p.repetition_penalty = 1.f;
+        rc.p.frequency_penalty = 0.f; rc.p.presence_penalty = 0.f; rc.p.repeat_last_n = 0; rc.p.penalty_from = 0;
+        rc.p.reserved = 0;
     }
-    const bool greedy = a.mode == MODE_ARGMAX || p.temperature <= 0.0f || p.top_k == 1;
-    int k = greedy ? 1 : ((p.top_k > 0 && p.top_k < V) ? p.top_k : V);
-    const bool large = k > KMAX;                 // not on the fused select path: reported, token -1
+    const int V = a.V;
+    rc.greedy = a.mode == MODE_ARGMAX || rc.p.temperature <= 0.0f || rc.p.top_k == 1;
+    rc.k = rc.greedy ? 1 : ((rc.p.top_k > 0 && rc.p.top_k < V) ? rc.p.top_k : V);
+    rc.large = rc.k > KMAX;                 // not on the fused select path: reported, token -1
+    rc.rep_on = rc.p.repetition_penalty != 1.0f;
+    rc.fp_on = rc.p.frequency_penalty != 0.0f || rc.p.presence_penalty != 0.0f;
+    rc.len = rc.lenA + rc.lenB;
+    rc.pen = !rc.large && (rc.rep_on || rc.fp_on) && rc.p.repeat_last_n != 0 && rc.len > 0;
+    rc.b = rc.pen ? window_begin(rc.len, rc.p) : rc.len;
+    if (rc.b >= rc.len) rc.pen = false;
+    return rc;
+}
 
-    // ---- 3. penalties (sampler.cpp:11-18; frequency/presence extension)
-    const bool rep_on = p.repetition_penalty != 1.0f;
-    const bool fp_on = p.frequency_penalty != 0.0f || p.presence_penalty != 0.0f;
-    const int64_t len = lenA + lenB;
-    const bool pen = !large && (rep_on || fp_on) && p.repeat_last_n != 0 && len > 0;
-    if (pen) {
-        uint32_t* cnt = reinterpret_cast<uint32_t*>(s_big);   // CHUNK 16-bit counters, two per word
-        for (int i = tid; i < CHUNK / 8; i += BLOCK) reinterpret_cast<uint4*>(cnt)[i] = make_uint4(0u, 0u, 0u, 0u);
-        __syncthreads();
-        const int64_t b = window_begin(len, p);
-        bool ovf = false;
-        for (int64_t i = b + tid; i < len; i += BLOCK) {
-            const int id = i < lenA ? a.hist[hA0 + i] : segB[i - lenA];
-            const uint32_t rel = (uint32_t)(id - lo);
-            if (id >= 0 && id < V && rel < (uint32_t)CHUNK) {
-                const uint32_t sh = (rel & 1u) * 16u;
-                const uint32_t old = atomicAdd(&cnt[rel >> 1], 1u << sh);
-                ovf |= ((old >> sh) & 0xFFFFu) == 0xFFFFu;
-            }
-        }
-        if (ovf) atomicOr(a.err, FS_DEVERR_COUNT_OVERFLOW);
-        __syncthreads();
-        const float rp = p.repetition_penalty, fq = p.frequency_penalty, pr = p.presence_penalty;
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const int local = (j * BLOCK + tid) * 4;
-            const uint2 c2 = *reinterpret_cast<const uint2*>(&cnt[local >> 1]);
-            if ((c2.x | c2.y) != 0u) {
-                const uint32_t cc[4] = {c2.x & 0xFFFFu, c2.x >> 16, c2.y & 0xFFFFu, c2.y >> 16};
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    if (cc[q] != 0u) {
-                        float l = x[j][q];
-                        if (rep_on) l = l > 0.0f ? __fdiv_rn(l, rp) : __fmul_rn(l, rp);
-                        if (fp_on) l = __fsub_rn(l, __fadd_rn(__fmul_rn((float)cc[q], fq), pr));
-                        x[j][q] = l;
-                    }
-                }
-            }
-        }
-        __syncthreads();                                     // the count table's storage is reused below
-    }
+__device__ __forceinline__ int hist_at(const Args& a, const RowCtx& rc, int64_t i) {
+    return i < rc.lenA ? a.hist[rc.hA0 + i] : rc.segB[i - rc.lenA];
+}
 
-    // ---- 4. keys (0 marks an element past V)
-    uint32_t key[NV][4];
+// Issue the loads of one tile (TPT logits per thread: float4 j at element lo + (j*BLOCK + t)*4) without waiting.
+// Lanes past the row's end read a clamped in-bounds address and are zeroed. The float4 holding element V-1 may
+// extend up to 12 bytes past it, inside the same 16-byte-aligned block (never into another page); masked too.
+__device__ __forceinline__ void load_tile(float (&x)[TPT], const float* rowp, int lo, int V) {
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int e = lo + (j * BLOCK + tid) * 4;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) key[j][q] = e + q < V ? key_of(x[j][q]) : 0u;
+        const int e = lo + (j * BLOCK + (int)threadIdx.x) * 4;
+        const float4 t = *reinterpret_cast<const float4*>(rowp + (e < V ? e : 0));
+        x[4 * j + 0] = e + 0 < V ? t.x : 0.f;
+        x[4 * j + 1] = e + 1 < V ? t.y : 0.f;
+        x[4 * j + 2] = e + 2 < V ? t.z : 0.f;
+        x[4 * j + 3] = e + 3 < V ? t.w : 0.f;
     }
-    auto comp_at = [&](int j, int q) -> uint64_t {
-        const int e = lo + (j * BLOCK + tid) * 4 + q;
-        return e < V ? comp_of(key[j][q], (uint32_t)e) : 0ull;
-    };
+}
+// element id of this thread's i-th logit of the tile starting at lo
+__device__ __forceinline__ int elem_id(int lo, int i) { return lo + ((i >> 2) * BLOCK + (int)threadIdx.x) * 4 + (i & 3); }
 
-    // ---- 5. chunk selection, published with agent-scope stores
-    const int slot = row * a.nchunks + chunk;
-    uint64_t* gout = a.cand + (int64_t)slot * CAP;
-    if (large) {
-        if (tid == 0) { st_agent(&a.meta[2 * slot], 0u); st_agent(&a.meta[2 * slot + 1], 0u); }
-    } else if (greedy) {
-        uint64_t best = 0;
-#pragma unroll
-        for (int j = 0; j < NV; ++j)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) { const uint64_t c = comp_at(j, q); best = c > best ? c : best; }
-        best = block_max_u64(best, red);
-        if (tid == 0) {
-            st_agent(gout, best);
-            st_agent(&a.meta[2 * slot], comp_key(best));
-            st_agent(&a.meta[2 * slot + 1], 1u);
+// Penalty pass on one tile in registers (sampler.cpp:11-18; frequency/presence extension): the window's ids that
+// fall in [lo, lo + TILE) are counted in a 16-bit LDS table, then each thread patches its counted logits.
+// Entry: the table may still be read by the previous tile's patching, so the caller has passed a barrier.
+__device__ __forceinline__ void apply_penalties(float (&x)[TPT], const int (&hv)[HPF], const Args& a,
+                                                const RowCtx& rc, int lo, Shared& s) {
+    const int tid = threadIdx.x;
+    const int V = a.V;
+    for (int i = tid; i < TILE / 8; i += BLOCK) reinterpret_cast<uint4*>(s.cnt())[i] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+    bool ovf = false;
+    auto count_id = [&](int id) {
+        const uint32_t rel = (uint32_t)(id - lo);
+        if (id >= 0 && id < V && rel < (uint32_t)TILE) {
+            const uint32_t sh = (rel & 1u) * 16u;
+            const uint32_t old = atomicAdd(&s.cnt()[rel >> 1], 1u << sh);
+            ovf |= ((old >> sh) & 0xFFFFu) == 0xFFFFu;
         }
-    } else {
-        const int nvalid = min(CHUNK, V - lo);
-        uint32_t T0 = 0;
-        if (k < nvalid) {
-            // maxima of G groups per thread, BLOCK*G >= 2k groups in all (G <= EPT)
-            int G = 1;
-            while (G * BLOCK < 2 * k && G < EPT) G <<= 1;
-            const int per = EPT / G;                 // elements per group, in thread-local order j*4+q
-            uint32_t gmin = 0xFFFFFFFFu, gmax = 0u;
-            {
-                uint32_t gm = 0;
-                bool any = false;
+    };
 #pragma unroll
-                for (int j = 0; j < NV; ++j)
+    for (int q = 0; q < HPF; ++q) count_id(hv[q]);
+    for (int64_t i = rc.b + HPF * BLOCK + tid; i < rc.len; i += BLOCK) count_id(hist_at(a, rc, i));
+    if (ovf) atomicOr(a.err, FS_DEVERR_COUNT_OVERFLOW);
+    __syncthreads();
+    const float rp = rc.p.repetition_penalty, fq = rc.p.frequency_penalty, pr = rc.p.presence_penalty;
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        if (lo + (j * BLOCK + tid) * 4 + q < V) { gm = key[j][q] > gm ? key[j][q] : gm; any = true; }
-                        if ((j * 4 + q + 1) % per == 0) {
-                            if (any) { gmin = gm < gmin ? gm : gmin; gmax = gm > gmax ? gm : gmax; }
-                            gm = 0;
-                            any = false;
-                        }
-                    }
-            }
-            for (int i = tid; i < NBINS; i += BLOCK) s_bins[i] = 0u;
-            block_minmax_u32(gmin, gmax, red);
-            const int sh = range_shift(gmin, gmax);
-            {
-                uint32_t gm = 0;
-                bool any = false;
-#pragma unroll
-                for (int j = 0; j < NV; ++j)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        if (lo + (j * BLOCK + tid) * 4 + q < V) { gm = key[j][q] > gm ? key[j][q] : gm; any = true; }
-                        if ((j * 4 + q + 1) % per == 0) {
-                            if (any) atomicAdd(&s_bins[(gm - gmin) >> sh], 1u);
-                            gm = 0;
-                            any = false;
-                        }
-                    }
-            }
-            __syncthreads();
-            uint32_t c0;
-            T0 = hist_threshold(s_bins, gmin, sh, k, &c0, s_wsum, red);   // 0: groups could not certify k
-        }
-        // compaction of keys >= T0
-        if (tid == 0) s_count = 0u;
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < NV; ++j)
+    for (int j = 0; j < NV; ++j) {
+        const int local = (j * BLOCK + tid) * 4;
+        const uint2 c2 = *reinterpret_cast<const uint2*>(&s.cnt()[local >> 1]);
+        if ((c2.x | c2.y) != 0u) {
+            const uint32_t cc[4] = {c2.x & 0xFFFFu, c2.x >> 16, c2.y & 0xFFFFu, c2.y >> 16};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int e = lo + (j * BLOCK + tid) * 4 + q;
-                wave_append_kv(e < V && key[j][q] >= T0, key[j][q], (uint32_t)e, s_big, &s_count, CAP);
-            }
-        __syncthreads();
-        uint32_t n = s_count;
-        if (n > (uint32_t)CAP) {
-            // Too many keys >= T0 (a flat distribution or ties): narrow [rlo, rhi] onto the exact k-th key with
-            // histogram levels over the registers (2048x per level, 4 levels reach a single key value).
-            // Invariant: count(key > rhi) == above < k <= count(key >= rlo).
-            uint32_t rlo = T0, rhi = 0u, above = 0u, cnt_ge = n;
-#pragma unroll
-            for (int j = 0; j < NV; ++j)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) rhi = key[j][q] > rhi ? key[j][q] : rhi;   // invalid keys are 0
-            {
-                uint32_t dummy = 0u;
-                block_minmax_u32(dummy, rhi, red);
-            }
-            for (int level = 0; level < 4 && cnt_ge > (uint32_t)CAP && rlo != rhi; ++level) {
-                const int sh = range_shift(rlo, rhi);
-                for (int i = tid; i < NBINS; i += BLOCK) s_bins[i] = 0u;
-                __syncthreads();
-#pragma unroll
-                for (int j = 0; j < NV; ++j)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const uint32_t kq = key[j][q];
-                        if (lo + (j * BLOCK + tid) * 4 + q < V && kq >= rlo && kq <= rhi)
-                            atomicAdd(&s_bins[(kq - rlo) >> sh], 1u);
-                    }
-                __syncthreads();
-                uint32_t ab, atb;
-                const int bsel = hist_locate(s_bins, k - (int)above, &ab, &atb, s_wsum, red);
-                const uint64_t nlo = (uint64_t)rlo + ((uint64_t)bsel << sh);
-                const uint64_t nhi = (uint64_t)rlo + (((uint64_t)bsel + 1) << sh) - 1;
-                rlo = (uint32_t)nlo;
-                rhi = nhi < rhi ? (uint32_t)nhi : rhi;
-                above += ab;
-                cnt_ge = above + atb;
-            }
-            if (tid == 0) s_count = 0u;
-            __syncthreads();
-            if (cnt_ge <= (uint32_t)CAP) {
-#pragma unroll
-                for (int j = 0; j < NV; ++j)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int e = lo + (j * BLOCK + tid) * 4 + q;
-                        wave_append_kv(e < V && key[j][q] >= rlo, key[j][q], (uint32_t)e, s_big, &s_count, CAP);
-                    }
-            } else {
-                // rlo == rhi is the k-th key t and it is tied: keep every key > t and the (k - above) lowest ids
-                // with key == t; ids run in (j, thread, q) order, so one block scan per j ranks the ties
-                const uint32_t t = rlo;
-                const uint32_t need = (uint32_t)k - above;
-                uint32_t run = 0u;
-#pragma unroll
-                for (int j = 0; j < NV; ++j) {
-                    uint32_t mine = 0u;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        mine += (lo + (j * BLOCK + tid) * 4 + q < V && key[j][q] == t) ? 1u : 0u;
-                    uint32_t tot;
-                    uint32_t pos = run + block_excl_scan<uint32_t>(mine, s_wsum, &tot);
-                    run += tot;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int e = lo + (j * BLOCK + tid) * 4 + q;
-                        const bool valid = e < V;
-                        const bool tie = valid && key[j][q] == t;
-                        const bool take = (valid && key[j][q] > t) || (tie && pos < need);
-                        pos += tie ? 1u : 0u;
-                        wave_append_kv(take, key[j][q], (uint32_t)e, s_big, &s_count, CAP);
-                    }
+                if (cc[q] != 0u) {
+                    float l = x[4 * j + q];
+                    if (rc.rep_on) l = l > 0.0f ? __fdiv_rn(l, rp) : __fmul_rn(l, rp);
+                    if (rc.fp_on) l = __fsub_rn(l, __fadd_rn(__fmul_rn((float)cc[q], fq), pr));
+                    x[4 * j + q] = l;
                 }
             }
-            __syncthreads();
-            n = s_count;
-            T0 = rlo;
-        }
-        for (uint32_t i = tid; i < n; i += BLOCK) st_agent(gout + i, s_big[i]);
-        if (tid == 0) {
-            st_agent(&a.meta[2 * slot], T0);
-            st_agent(&a.meta[2 * slot + 1], n);
         }
     }
+}
 
-    // ---- 6. hand-off: drain this wave's stores, then one agent-scope count per chunk; the last one merges
-    vm_drain();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(&a.row_cnt[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        red.misc[3] = (old == (uint32_t)a.nchunks - 1u) ? 1u : 0u;
+// Narrow [rlo, rhi] onto the kk-th largest value among the entries a visitor yields (32-bit values, entries
+// outside [rlo, rhi] ignored; count(value > rhi) == *above < kk <= count(value >= rlo) on entry). On return
+// rlo == rhi is that value, *above = count(value > it), *at = count(value >= it).
+template <class Each>
+__device__ void narrow32(Each each, int kk, uint32_t& rlo, uint32_t& rhi, uint32_t* above, uint32_t* at, Shared& s) {
+    const int tid = threadIdx.x;
+    for (int level = 0; level < 4 && rlo != rhi; ++level) {
+        const int sh = range_shift(rlo, rhi);
+        for (int i = tid; i < NBINS; i += BLOCK) s.bins()[i] = 0u;
+        __syncthreads();
+        const uint32_t lo = rlo, hi = rhi;
+        each([&](uint32_t v) { if (v >= lo && v <= hi) atomicAdd(&s.bins()[(v - lo) >> sh], 1u); });
+        __syncthreads();
+        uint32_t ab, atb;
+        const int bsel = hist_locate(s.bins(), kk - (int)*above, &ab, &atb, s.wsum, s.red);
+        const uint64_t nlo = (uint64_t)rlo + ((uint64_t)bsel << sh);
+        const uint64_t nhi = (uint64_t)rlo + (((uint64_t)bsel + 1) << sh) - 1;
+        rlo = (uint32_t)nlo;
+        rhi = nhi < rhi ? (uint32_t)nhi : rhi;
+        *above += ab;
+        *at = *above + (atb - ab);
+    }
+}
+
+// Exact k-th largest composite X among the n > k candidates in s.cand, then keep exactly the k entries >= X.
+// Returns X. Keys first (histogram levels over [min, max]), then, if the k-th key is tied, the ids among the ties.
+__device__ __forceinline__ uint64_t compact_exact(int n, int k, Shared& s) {
+    const int tid = threadIdx.x;
+    uint32_t kmn = 0xFFFFFFFFu, kmx = 0u;
+    for (int i = tid; i < n; i += BLOCK) {
+        const uint32_t kk = comp_key(s.cand[i]);
+        kmn = kk < kmn ? kk : kmn;
+        kmx = kk > kmx ? kk : kmx;
+    }
+    block_minmax_u32(kmn, kmx, s.red);
+    uint32_t rlo = kmn, rhi = kmx, above = 0u, at = (uint32_t)n;
+    narrow32([&](auto&& f) { for (int i = tid; i < n; i += BLOCK) f(comp_key(s.cand[i])); }, k, rlo, rhi, &above, &at,
+             s);
+    const uint32_t t = rlo;                                   // the k-th key
+    const uint32_t need = (uint32_t)k - above;                // ties at t that belong to the top k
+    uint64_t X = (uint64_t)t << 32;
+    if (at - above != need) {
+        // the need-th largest low word (the need-th smallest id) among the entries with key t
+        uint32_t lmn = 0xFFFFFFFFu, lmx = 0u;
+        for (int i = tid; i < n; i += BLOCK) {
+            const uint64_t c = s.cand[i];
+            if (comp_key(c) == t) {
+                const uint32_t lw = (uint32_t)c;
+                lmn = lw < lmn ? lw : lmn;
+                lmx = lw > lmx ? lw : lmx;
+            }
+        }
+        block_minmax_u32(lmn, lmx, s.red);
+        uint32_t ab2 = 0u, at2 = 0u;
+        narrow32(
+            [&](auto&& f) {
+                for (int i = tid; i < n; i += BLOCK) {
+                    const uint64_t c = s.cand[i];
+                    if (comp_key(c) == t) f((uint32_t)c);
+                }
+            },
+            (int)need, lmn, lmx, &ab2, &at2, s);
+        X |= lmn;
+    }
+    // keep the entries >= X (exactly k): compact into the stage, then copy back to the front of the buffer
+    uint32_t mine = 0u;
+    for (int i = tid; i < n; i += BLOCK) mine += s.cand[i] >= X ? 1u : 0u;
+    uint32_t tot;
+    uint32_t pos = block_excl_scan<uint32_t>(mine, s.wsum, &tot);
+    uint64_t* st = s.stage();
+    for (int i = tid; i < n; i += BLOCK) {
+        const uint64_t c = s.cand[i];
+        if (c >= X) st[pos++] = c;
     }
     __syncthreads();
-    if (red.misc[3] == 0u) return;
-    if (tid == 0) st_agent(&a.row_cnt[row], 0u);
+    for (uint32_t i = tid; i < tot; i += BLOCK) s.cand[i] = st[i];
+    if (tid == 0) s.count = tot;
+    __syncthreads();
+    return X;
+}
 
-    // ---- 7. merge
-    const int nch = a.nchunks;
+// The merge of one row: gathers the segments' candidates, selects and sorts the row's top k, then softmax / min-p / top-p / draw (sampler.cpp:25-49).
+__device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Shared& s) {
+    const int tid = threadIdx.x;
+    const int row = rc.row;
+    const int nch = a.nseg;
     const int slot0 = row * nch;
+    int k = rc.k;
     int tok = 0, keep = 1;
-    if (large) {
+    if (rc.large) {
         tok = -1;
         keep = 0;
         if (tid == 0) atomicOr(a.err, FS_DEVERR_LARGE_K);
-    } else if (greedy) {
+    } else if (rc.greedy) {
         uint64_t best = 0;
         for (int c = tid; c < nch; c += BLOCK) {
-            const uint64_t v = ld_agent(a.cand + (int64_t)(slot0 + c) * CAP);
+            const uint64_t v = *(a.cand + (int64_t)(slot0 + c) * CAP);
             best = v > best ? v : best;
         }
-        best = block_max_u64(best, red);
+        best = block_max_u64(best, s.red);
         tok = (int)comp_id(best);
-        const float l0 = rowp[0];
+        const float l0 = a.logits[(int64_t)row * a.ld];
         if (l0 != l0) tok = 0;                         // ferro's scan never moves off a NaN at index 0
         if (tid == 0 && a.mode != MODE_VERIFY) {
             if (a.cand_ids && a.kcap > 0) a.cand_ids[(int64_t)row * a.kcap] = tok;
             if (a.cand_probs && a.kcap > 0) a.cand_probs[(int64_t)row * a.kcap] = 1.0;
         }
     } else {
-        // metas: L = max T0 (a lower bound of the row's k-th key), flat offsets of the chunk lists
-        uint32_t Lloc = 0, nmine = 0;
-        for (int c = 2 * tid; c < 2 * tid + 2 && c < nch; ++c) {
-            const uint32_t t0 = ld_agent(&a.meta[2 * (slot0 + c)]);
-            const uint32_t cn = ld_agent(&a.meta[2 * (slot0 + c) + 1]);
-            Lloc = t0 > Lloc ? t0 : Lloc;
-            s_off[c] = cn;
-            nmine += cn;
-        }
-        const uint32_t L = (uint32_t)block_max_u64(Lloc, red);
+        // One memory round trip: every segment's meta and the first SPEC*tps entries of its list, tps threads
+        // per segment (entries past a list's count are stale and masked once the counts are in).
+        const int tps = BLOCK / nch;                 // >= 1: the host keeps nseg <= BLOCK
+        const int c_me = tid % nch;
+        const int r_me = tid / nch;
+        const bool act = r_me < tps;
+        const uint64_t* lst = a.cand + (int64_t)(slot0 + c_me) * CAP;
+        const uint32_t t0m = *(&a.meta[2 * (slot0 + c_me)]);
+        const uint32_t cnm = *(&a.meta[2 * (slot0 + c_me) + 1]);
+        uint64_t v[SPEC];
+#pragma unroll
+        for (int q = 0; q < SPEC; ++q) v[q] = *(lst + (act ? r_me + q * tps : 0));
+        if (act && r_me == 0) s.off[c_me] = cnm;
+        const uint32_t L = (uint32_t)block_max_u64(act ? t0m : 0u, s.red);   // a lower bound of the k-th key
+        // flat offsets of the segment lists (used when the candidates >= L overflow LDS)
         uint32_t total;
-        uint32_t o = block_excl_scan<uint32_t>(nmine, s_wsum, &total);
-        for (int c = 2 * tid; c < 2 * tid + 2 && c < nch; ++c) { const uint32_t cn = s_off[c]; s_off[c] = o; o += cn; }
-        if (tid == 0) { s_off[nch] = total; s_count = 0u; }
-        __syncthreads();
+        {
+            const uint32_t mine = tid < nch ? s.off[tid] : 0u;
+            const uint32_t o = block_excl_scan<uint32_t>(mine, s.wsum, &total);
+            if (tid < nch) s.off[tid] = o;
+            if (tid == 0) { s.off[nch] = total; s.count = 0u; }
+            __syncthreads();
+        }
         auto fetch = [&](uint32_t f) -> uint64_t {          // flat index -> candidate (0 past the end)
-            if (f >= total) return 0ull;
-            int c0 = 0, c1 = nch;                            // largest c with s_off[c] <= f
+            const uint32_t g = f < total ? f : total - 1u;  // branch-free: the load is always issued in bounds
+            int c0 = 0, c1 = nch;                            // largest c with off[c] <= g
             while (c1 - c0 > 1) {
                 const int m = (c0 + c1) >> 1;
-                if (s_off[m] <= f) c0 = m; else c1 = m;
+                if (s.off[m] <= g) c0 = m; else c1 = m;
             }
-            return ld_agent(a.cand + (int64_t)(slot0 + c0) * CAP + (f - s_off[c0]));
+            const uint64_t w = *(a.cand + (int64_t)(slot0 + c0) * CAP + (g - s.off[c0]));
+            return f < total ? w : 0ull;
         };
         // gather the candidates >= L into LDS (counted past CAP), tracking their max key
         uint32_t kmax = L;
-        for (uint32_t f0 = 0; f0 < total; f0 += BLOCK * SPEC) {
-            uint64_t v[SPEC];
 #pragma unroll
-            for (int q = 0; q < SPEC; ++q) v[q] = fetch(f0 + q * BLOCK + tid);
-#pragma unroll
-            for (int q = 0; q < SPEC; ++q) {
-                const bool in = v[q] != 0 && comp_key(v[q]) >= L;
-                if (in) kmax = comp_key(v[q]) > kmax ? comp_key(v[q]) : kmax;
-                wave_append(in, v[q], s_big, &s_count, CAP);
-            }
+        for (int q = 0; q < SPEC; ++q) {
+            const bool in = act && (uint32_t)(r_me + q * tps) < cnm && v[q] != 0 && comp_key(v[q]) >= L;
+            if (in) kmax = comp_key(v[q]) > kmax ? comp_key(v[q]) : kmax;
+            wave_append(in, v[q], s.cand, &s.count, CAP);
         }
-        for (int i = tid; i < NBINS; i += BLOCK) s_bins[i] = 0u;
+        for (uint32_t i = (uint32_t)(r_me + SPEC * tps); act && i < cnm; i += (uint32_t)tps) {   // long lists
+            const uint64_t w = *(lst + i);
+            const bool in = w != 0 && comp_key(w) >= L;
+            if (in) kmax = comp_key(w) > kmax ? comp_key(w) : kmax;
+            wave_append(in, w, s.cand, &s.count, CAP);
+        }
+        for (int i = tid; i < NBINS; i += BLOCK) s.bins()[i] = 0u;
         uint32_t kmin = L;
-        block_minmax_u32(kmin, kmax, red);
-        const uint32_t n = s_count;
+        block_minmax_u32(kmin, kmax, s.red);
+        const uint32_t n = s.count;
         const bool in_lds = n <= (uint32_t)CAP;
         // T1: tight threshold from a histogram of the candidates' keys over [L, kmax]
         const int sh = range_shift(L, kmax);
         if (in_lds) {
-            for (uint32_t i = tid; i < n; i += BLOCK) atomicAdd(&s_bins[(comp_key(s_big[i]) - L) >> sh], 1u);
+            for (uint32_t i = tid; i < n; i += BLOCK) atomicAdd(&s.bins()[(comp_key(s.cand[i]) - L) >> sh], 1u);
         } else {
             for (uint32_t f = tid; f < total; f += BLOCK) {
                 const uint64_t c = fetch(f);
-                if (c != 0 && comp_key(c) >= L) atomicAdd(&s_bins[(comp_key(c) - L) >> sh], 1u);
+                if (c != 0 && comp_key(c) >= L) atomicAdd(&s.bins()[(comp_key(c) - L) >> sh], 1u);
             }
         }
         __syncthreads();
         uint32_t c1;
-        const uint32_t T1 = hist_threshold(s_bins, L, sh, k, &c1, s_wsum, red);
+        const uint32_t T1 = hist_threshold(s.bins(), L, sh, k, &c1, s.wsum, s.red);
         // the c1 >= k candidates with key >= T1 contain the top k: sort them
         uint64_t* top;
-        uint64_t* small_in = reinterpret_cast<uint64_t*>(s_bins);
+        uint64_t* small_in = reinterpret_cast<uint64_t*>(s.bins());
         uint64_t* small_out = small_in + SMALL;
-        if (tid == 0) s_count = 0u;
+        if (tid == 0) s.count = 0u;
         __syncthreads();
         if (c1 <= (uint32_t)SMALL) {
             if (in_lds) {
                 for (uint32_t i0 = 0; i0 < n; i0 += BLOCK) {
                     const uint32_t i = i0 + tid;
-                    const uint64_t c = i < n ? s_big[i] : 0ull;
-                    wave_append(c != 0 && comp_key(c) >= T1, c, small_in, &s_count, SMALL);
+                    const uint64_t c = i < n ? s.cand[i] : 0ull;
+                    wave_append(c != 0 && comp_key(c) >= T1, c, small_in, &s.count, SMALL);
                 }
             } else {
                 for (uint32_t f0 = 0; f0 < total; f0 += BLOCK) {
                     const uint64_t c = fetch(f0 + tid);
-                    wave_append(c != 0 && comp_key(c) >= T1, c, small_in, &s_count, SMALL);
+                    wave_append(c != 0 && comp_key(c) >= T1, c, small_in, &s.count, SMALL);
                 }
             }
             __syncthreads();
             rank_sort(small_in, (int)c1, small_out, k);
             top = small_out;
-        } else if (in_lds) {
-            int np = 1;
-            while (np < (int)n) np <<= 1;
-            for (int i = (int)n + tid; i < np; i += BLOCK) s_big[i] = 0ull;
-            __syncthreads();
-            bitonic_desc(s_big, np);
-            top = s_big;
         } else {
-            uint64_t X = 0;                             // threshold for an exact gather of <= CAP entries
-            if (c1 > (uint32_t)CAP) {
-                X = radix_kth(
-                    [&](auto&& f) {
-                        for (uint32_t f0 = tid; f0 < total; f0 += BLOCK) {
-                            const uint64_t c = fetch(f0);
-                            f(c != 0 && comp_key(c) >= L ? c : 0ull);
-                        }
-                    },
-                    k, s_bins, s_wsum, red);
+            // more than SMALL candidates reach T1: reduce to exactly the k >= X in LDS, then sort those
+            int m = (int)n;
+            if (!in_lds) {
+                uint64_t X = 0;                         // threshold for a gather of <= CAP entries
+                if (c1 > (uint32_t)CAP) {
+                    X = radix_kth(
+                        [&](auto&& f) {
+                            for (uint32_t f0 = tid; f0 < total; f0 += BLOCK) {
+                                const uint64_t c = fetch(f0);
+                                f(c != 0 && comp_key(c) >= L ? c : 0ull);
+                            }
+                        },
+                        k, s.bins(), s.wsum, s.red);
+                }
+                if (tid == 0) s.count = 0u;
+                __syncthreads();
+                for (uint32_t f0 = 0; f0 < total; f0 += BLOCK) {
+                    const uint64_t c = fetch(f0 + tid);
+                    wave_append(c != 0 && comp_key(c) >= T1 && c >= X, c, s.cand, &s.count, CAP);
+                }
+                __syncthreads();
+                m = (int)s.count;
             }
-            if (tid == 0) s_count = 0u;
-            __syncthreads();
-            for (uint32_t f0 = 0; f0 < total; f0 += BLOCK) {
-                const uint64_t c = fetch(f0 + tid);
-                wave_append(c != 0 && comp_key(c) >= T1 && c >= X, c, s_big, &s_count, CAP);
+            if (m > k) {
+                compact_exact(m, k, s);
+                m = k;
             }
-            __syncthreads();
-            const int m = (int)s_count;
             int np = 1;
-            while (np < m) np <<= 1;
-            for (int i = m + tid; i < np; i += BLOCK) s_big[i] = 0ull;
+            while (np < m) np <<= 1;                    // <= KMAX
+            for (int i = m + tid; i < np; i += BLOCK) s.cand[i] = 0ull;
             __syncthreads();
-            bitonic_desc(s_big, np);
-            top = s_big;
+            bitonic_desc(s.cand, np);
+            top = s.cand;
+            c1 = (uint32_t)m;
         }
         if (c1 < (uint32_t)k) {                       // impossible by construction; never read past the list
             if (tid == 0) atomicOr(a.err, FS_DEVERR_INTERNAL);
@@ -825,6 +782,7 @@ __global__ __launch_bounds__(BLOCK, 4) void sample_kernel(Args a) {
         }
 
         // ---- softmax at temperature, min-p, top-p, draw (sampler.cpp:37-49), k <= KMAX
+        const fs_row_params& p = rc.p;
         const int i0 = tid * KPT;
         const float mx = val_of(comp_key(top[0]));
         const double Td = (double)p.temperature;
@@ -840,7 +798,7 @@ __global__ __launch_bounds__(BLOCK, 4) void sample_kernel(Args a) {
                 part += e[q];
             }
         }
-        const double sum = block_sum_f64(part, red);
+        const double sum = block_sum_f64(part, s.red);
         double pr[KPT];
 #pragma unroll
         for (int q = 0; q < KPT; ++q) pr[q] = e[q] / sum;
@@ -852,7 +810,7 @@ __global__ __launch_bounds__(BLOCK, 4) void sample_kernel(Args a) {
 #pragma unroll
             for (int q = 0; q < KPT; ++q)
                 if (i0 + q < k && pr[q] >= thr) last = i0 + q;
-            last = block_max_i32(last, red);
+            last = block_max_i32(last, s.red);
             keep_m = last + 1 > 1 ? last + 1 : 1;
         }
         // inclusive prefix of pr in candidate order
@@ -861,7 +819,7 @@ __global__ __launch_bounds__(BLOCK, 4) void sample_kernel(Args a) {
 #pragma unroll
         for (int q = 0; q < KPT; ++q) { run += pr[q]; c[q] = run; }
         double tot_all;
-        const double off = block_excl_scan<double>(run, red.f64, &tot_all);
+        const double off = block_excl_scan<double>(run, s.red.f64, &tot_all);
 #pragma unroll
         for (int q = 0; q < KPT; ++q) c[q] += off;
         keep = keep_m;
@@ -870,23 +828,23 @@ __global__ __launch_bounds__(BLOCK, 4) void sample_kernel(Args a) {
 #pragma unroll
             for (int q = 0; q < KPT; ++q)
                 if (i0 + q < keep_m && c[q] >= (double)p.top_p && first == 0x7fffffff) first = i0 + q;
-            first = block_min_i32(first, red);
+            first = block_min_i32(first, s.red);
             if (first != 0x7fffffff) keep = first + 1 < keep_m ? first + 1 : keep_m;
             if (keep < 1) keep = 1;
         }
         // tot = sum of the kept prefix; r = u * tot; the first i with r <= c_i
 #pragma unroll
         for (int q = 0; q < KPT; ++q)
-            if (i0 + q == keep - 1) red.dmisc[0] = c[q];
+            if (i0 + q == keep - 1) s.red.dmisc[0] = c[q];
         __syncthreads();
-        const double tot = red.dmisc[0];
+        const double tot = s.red.dmisc[0];
         const double u = a.u ? a.u[row] : 0.0;
         const double rr = u * tot + 0.0;
         int hit = 0x7fffffff;
 #pragma unroll
         for (int q = 0; q < KPT; ++q)
             if (i0 + q < keep && rr <= c[q] && hit == 0x7fffffff) hit = i0 + q;
-        hit = block_min_i32(hit, red);
+        hit = block_min_i32(hit, s.red);
         const int pos = hit == 0x7fffffff ? keep - 1 : hit;
         tok = (int)comp_id(top[pos]);
         if (a.mode != MODE_VERIFY) {
@@ -905,19 +863,16 @@ __global__ __launch_bounds__(BLOCK, 4) void sample_kernel(Args a) {
             a.tok[row] = tok;
             if (a.keep) a.keep[row] = keep;
         }
-        return;
-    }
-
-    // ---- verify: the last row of a stream to finish computes the accepted prefix (server.cpp:627-637)
-    if (tid == 0) {
+    } else if (tid == 0) {
+        // verify: the last row of a stream to finish computes the accepted prefix (server.cpp:627-637)
         st_agent(&a.tok[row], (int32_t)tok);
         vm_drain();
-        const int s = pidx;
-        const int64_t r0 = a.row_off[s];
-        const int m = (int)(a.row_off[s + 1] - r0);
-        const uint32_t old = __hip_atomic_fetch_add(&a.stream_cnt[s], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int st = rc.pidx;
+        const int64_t r0 = a.row_off[st];
+        const int m = (int)(a.row_off[st + 1] - r0);
+        const uint32_t old = __hip_atomic_fetch_add(&a.stream_cnt[st], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (old == (uint32_t)m - 1u) {
-            st_agent(&a.stream_cnt[s], 0u);
+            st_agent(&a.stream_cnt[st], 0u);
             int acc = 0;
             for (int r = 0; r < m; ++r) {
                 const int t = ld_agent(&a.tok[r0 + r]);
@@ -926,9 +881,238 @@ __global__ __launch_bounds__(BLOCK, 4) void sample_kernel(Args a) {
                 if (r + 1 < m && t == a.rows[r0 + r + 1]) continue;
                 break;
             }
-            a.accepted[s] = acc;
+            a.accepted[st] = acc;
         }
     }
+    __syncthreads();                                   // LDS is reused by the caller's next chunk
+}
+
+// One (row, segment) item: stream the segment's tiles with PF tiles in flight, apply penalties, keep the running
+// candidates (greedy: this lane's first maximum; top-k: every logit whose composite reaches the running exact
+// threshold X, with an fp32 compare as the common-path filter), publish them with agent-scope stores, count the
+// segment done, and merge the row if it was the last.
+__device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc, int seg, Shared& s) {
+    const int tid = threadIdx.x;
+    const int V = a.V;
+    const int seg_lo = seg * a.seg_tiles * TILE;
+    const int left = (V - seg_lo + TILE - 1) / TILE;
+    const int ntiles = left < a.seg_tiles ? left : a.seg_tiles;    // >= 1
+    const float* rowp = a.logits + (int64_t)rc.row * a.ld;
+
+    float buf[PF][TPT];
+#pragma unroll
+    for (int p = 0; p < PF; ++p) load_tile(buf[p], rowp, seg_lo + (p < ntiles ? p : 0) * TILE, V);
+    int hv[HPF];
+#pragma unroll
+    for (int q = 0; q < HPF; ++q) {
+        const int64_t i = rc.b + q * BLOCK + tid;
+        const bool in = rc.pen && i < rc.len;
+        const int32_t* src = !in ? reinterpret_cast<const int32_t*>(rowp)
+                                 : (i < rc.lenA ? a.hist + rc.hA0 + i : rc.segB + (i - rc.lenA));
+        const int v = *src;
+        hv[q] = in ? v : -1;
+    }
+
+    const int k = rc.k;
+    const bool topk = !rc.greedy && !rc.large;
+    uint32_t bk = 0u;                  // greedy: this lane's best key and its (first) id
+    int bi = -1;
+    uint64_t X = 1ull;                 // top-k: candidates are the composites >= X (1: every valid logit)
+    float tf = -__builtin_huge_valf(); // fp32 superset filter of X: key(x) >= key(X) <=> x >= tf
+    if (tid == 0) s.count = 0u;
+    __syncthreads();
+
+    // Top-k buffer discipline: after tile 0 the buffer is checked (barrier) only every R tiles, R sized so the
+    // expected appends fill at most half the headroom; an overflow (appends past CAP are dropped) is detected at
+    // the next check and the segment is streamed again in safe mode (a check after every tile).
+    auto greedy_update = [&](const float (&x)[TPT], int lo) {
+#pragma unroll
+        for (int i = 0; i < TPT; ++i) {
+            const int e = elem_id(lo, i);
+            const uint32_t kq = key_of(x[i]);
+            if (e < V && kq > bk) { bk = kq; bi = e; }
+        }
+    };
+    // appends of one tile: per-element wave ballots, one LDS atomic per wave for the whole tile
+    auto topk_append = [&](const float (&x)[TPT], int lo) {
+        uint64_t bal[TPT];
+        uint32_t tot = 0u;
+#pragma unroll
+        for (int i = 0; i < TPT; ++i) {
+            const int e = elem_id(lo, i);
+            bool take = e < V && x[i] >= tf;
+            if (take) take = comp_of(key_of(x[i]), (uint32_t)e) >= X;
+            bal[i] = __ballot(take);
+            tot += (uint32_t)__popcll(bal[i]);
+        }
+        if (tot == 0u) return;                       // wave-uniform
+        uint32_t base = 0u;
+        if (lane_id() == 0) base = atomicAdd(&s.count, tot);
+        base = __shfl(base, 0);
+#pragma unroll
+        for (int i = 0; i < TPT; ++i) {
+            if ((bal[i] >> lane_id()) & 1ull) {
+                const uint32_t pos = base + mbcnt(bal[i]);
+                if (pos < (uint32_t)CAP) s.cand[pos] = comp_of(key_of(x[i]), (uint32_t)elem_id(lo, i));
+            }
+            base += (uint32_t)__popcll(bal[i]);
+        }
+    };
+    // barrier + count; compacts when another tile could overflow; returns the count (> CAP: overflowed)
+    auto check = [&]() -> int {
+        __syncthreads();
+        int n = (int)s.count;
+        if (n <= CAP && n > CAP - TILE && n > k) {
+            X = compact_exact(n, k, s);
+            tf = val_of(comp_key(X));
+            n = k;
+        }
+        return n;
+    };
+    for (int pass = 0; pass < 2; ++pass) {
+        const bool safe = pass == 1;
+        bool overflow = false;
+        int R = 1;
+        // ---- tile 0 (peeled: the initial threshold is computed here)
+        {
+            float (&x)[TPT] = buf[0];
+            const int lo = seg_lo;
+            if (rc.pen) apply_penalties(x, hv, a, rc, lo, s);
+            if (rc.greedy) {
+                greedy_update(x, lo);
+            } else if (topk) {
+                if (!safe && k < min(TILE, V - seg_lo)) {
+                    // maxima of >= 2k groups of tile 0 (G per thread), histogrammed over their [min, max]:
+                    // at least k of the tile's logits reach T0
+                    int G = 1;
+                    while (G * BLOCK < 2 * k && G < TPT) G <<= 1;
+                    const int per = TPT / G;
+                    uint32_t gmin = 0xFFFFFFFFu, gmax = 0u;
+                    uint32_t gm = 0u;
+                    bool any = false;
+#pragma unroll
+                    for (int i = 0; i < TPT; ++i) {
+                        if (elem_id(lo, i) < V) { const uint32_t kq = key_of(x[i]); gm = kq > gm ? kq : gm; any = true; }
+                        if ((i + 1) % per == 0) {
+                            if (any) { gmin = gm < gmin ? gm : gmin; gmax = gm > gmax ? gm : gmax; }
+                            gm = 0u;
+                            any = false;
+                        }
+                    }
+                    for (int i = tid; i < NBINS; i += BLOCK) s.bins()[i] = 0u;
+                    block_minmax_u32(gmin, gmax, s.red);
+                    const int sh = range_shift(gmin, gmax);
+#pragma unroll
+                    for (int i = 0; i < TPT; ++i) {
+                        if (elem_id(lo, i) < V) { const uint32_t kq = key_of(x[i]); gm = kq > gm ? kq : gm; any = true; }
+                        if ((i + 1) % per == 0) {
+                            if (any) atomicAdd(&s.bins()[(gm - gmin) >> sh], 1u);
+                            gm = 0u;
+                            any = false;
+                        }
+                    }
+                    __syncthreads();
+                    uint32_t c0;
+                    const uint32_t T0 = hist_threshold(s.bins(), gmin, sh, k, &c0, s.wsum, s.red);
+                    if (T0 != 0u) {
+                        X = (uint64_t)T0 << 32;
+                        tf = val_of(T0);
+                    }
+                }
+                topk_append(x, lo);
+            }
+            if (PF < ntiles) load_tile(x, rowp, lo + PF * TILE, V);
+            if (topk) {
+                const int n = check();
+                overflow = n > CAP;
+                const int per_tile = n > 32 ? n : 32;
+                R = safe ? 1 : (CAP - n) / (2 * per_tile);
+                if (R < 1) R = 1;
+            } else if (rc.pen) {
+                __syncthreads();                         // penalty-table reads of this tile are done
+            }
+        }
+        // ---- tiles 1.. (PF in flight; buffer p holds tiles p, p+PF, ...)
+        int since = 0;
+        for (int t0 = 0; t0 < ntiles && !overflow; t0 += PF) {
+#pragma unroll
+            for (int p = 0; p < PF; ++p) {
+                const int tt = t0 + p;
+                if (tt >= 1 && tt < ntiles && !overflow) {
+                    const int lo = seg_lo + tt * TILE;
+                    float (&x)[TPT] = buf[p];
+                    if (rc.pen) apply_penalties(x, hv, a, rc, lo, s);
+                    if (rc.greedy) greedy_update(x, lo);
+                    else if (topk) topk_append(x, lo);
+                    if (tt + PF < ntiles) load_tile(x, rowp, lo + PF * TILE, V);
+                    if (topk) {
+                        if (++since >= R || rc.pen) {
+                            since = 0;
+                            overflow = check() > CAP;   // uniform: every thread read the same count
+                        }
+                    } else if (rc.pen) {
+                        __syncthreads();                 // penalty-table reads of this tile are done
+                    }
+                }
+            }
+        }
+        if (!topk) break;
+        if (!overflow) overflow = check() > CAP;
+        if (!overflow) break;
+        // overflow: the buffer lost candidates. X is still a valid bound; stream the segment again in safe mode.
+        __syncthreads();
+        if (tid == 0) s.count = 0u;
+#pragma unroll
+        for (int p = 0; p < PF; ++p) load_tile(buf[p], rowp, seg_lo + (p < ntiles ? p : 0) * TILE, V);
+        __syncthreads();
+    }
+    if (topk) {
+        // the segment's exact top k (fewer candidates to merge)
+        const int n = (int)s.count;
+        if (n > k) X = compact_exact(n, k, s);
+    }
+
+    // ---- publish this segment's candidates (read by the merge kernel after this kernel completes)
+    const int nseg = a.nseg;
+    const int slot = rc.row * nseg + seg;
+    uint64_t* gout = a.cand + (int64_t)slot * CAP;
+    if (rc.large) {
+        if (tid == 0) { a.meta[2 * slot] = 0u; a.meta[2 * slot + 1] = 0u; }
+    } else if (rc.greedy) {
+        uint64_t best = bi >= 0 ? comp_of(bk, (uint32_t)bi) : 0ull;
+        best = block_max_u64(best, s.red);
+        if (tid == 0) {
+            gout[0] = best;
+            a.meta[2 * slot] = comp_key(best);
+            a.meta[2 * slot + 1] = 1u;
+        }
+    } else {
+        const uint32_t n = s.count;
+        for (uint32_t i = tid; i < n; i += BLOCK) gout[i] = s.cand[i];
+        if (tid == 0) {
+            a.meta[2 * slot] = comp_key(X);        // X's key: at least k of this segment's keys reach it
+            a.meta[2 * slot + 1] = n;
+        }
+    }
+    __syncthreads();                               // LDS is reused by the next item
+}
+
+// Segment kernel (persistent): workgroup g handles items g, g+G, ... (item = row*nseg + segment, row-major).
+__global__ __launch_bounds__(BLOCK, 4) void segment_kernel(Args a) {
+    static_assert(KMAX + TILE <= CAP, "a compacted buffer plus one tile must fit the candidate buffer");
+    __shared__ __align__(16) Shared s;
+    const int total = a.B * a.nseg;
+    for (int item = (int)blockIdx.x; item < total; item += (int)gridDim.x) {
+        const int row = item / a.nseg;
+        process_segment(a, row_ctx(a, row), item - row * a.nseg, s);
+    }
+}
+
+// Merge kernel: one workgroup per row, after the segment kernel has published every segment's candidates.
+__global__ __launch_bounds__(BLOCK) void merge_kernel(Args a) {
+    static_assert(2 * SMALL * 8 <= NBINS * 4, "rank-sort buffers alias the histogram");
+    __shared__ __align__(16) Shared s;
+    merge_row(a, row_ctx(a, (int)blockIdx.x), s);
 }
 
 }  // namespace fs
@@ -937,6 +1121,7 @@ __global__ __launch_bounds__(BLOCK, 4) void sample_kernel(Args a) {
 struct fs_context {
     std::mutex mu;
     int device = -1;
+    int cus = 0;               // compute units of the device
     uint64_t* cand = nullptr;
     size_t cand_slots = 0;     // chunk slots of CAP entries
     uint32_t* meta = nullptr;
@@ -979,32 +1164,31 @@ int grow(fs_context* c, size_t slots, size_t rows, size_t streams) {
     return FS_OK;
 }
 
-// Chunk size: the largest of 16384 / 8192 / 2048 elements per workgroup that still puts >= 256 workgroups on the
-// chip (one per CU); fewer, longer chunks mean fewer candidates to merge per row.
-int choose_ept(int64_t rows, int V) {
-    for (int ept : {32, 16}) {
-        const int64_t nch = (V + fs::BLOCK * ept - 1) / (fs::BLOCK * ept);
-        if (rows * nch >= 256) return ept;
-    }
-    return 4;
-}
-
 int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream_t st) {
-    int ept = choose_ept(rows, a.V);
-    while (ept < 32 && (a.V + fs::BLOCK * ept - 1) / (fs::BLOCK * ept) > fs::MAX_CHUNKS) ept *= 4;
-    const int chunk = fs::BLOCK * ept;
-    a.nchunks = (a.V + chunk - 1) / chunk;
-    if (a.nchunks > fs::MAX_CHUNKS) return FS_E_INVALID;
-    const int64_t grid = rows * a.nchunks;
-    if (grid > 0x7fffffff) return FS_E_INVALID;
     std::lock_guard<std::mutex> g(ctx->mu);
-    if (ctx->device < 0) { if (hipGetDevice(&ctx->device) != hipSuccess) return FS_E_HIP; }
-    int rc = grow(ctx, (size_t)grid, (size_t)rows, (size_t)(streams > 0 ? streams : 1));
+    if (ctx->device < 0) {
+        if (hipGetDevice(&ctx->device) != hipSuccess) return FS_E_HIP;
+        if (hipDeviceGetAttribute(&ctx->cus, hipDeviceAttributeMultiprocessorCount, ctx->device) != hipSuccess)
+            return FS_E_HIP;
+    }
+    // Segments: about two per CU over the whole batch (each streams >= 1 tile), the rest of a row per segment.
+    const int64_t tiles_row = (a.V + fs::TILE - 1) / fs::TILE;
+    int64_t want = (2 * (int64_t)ctx->cus + rows - 1) / rows;
+    if (want < 1) want = 1;
+    if (want > tiles_row) want = tiles_row;
+    if (want > fs::BLOCK) want = fs::BLOCK;        // the merge gives each segment >= 1 thread
+    a.seg_tiles = (int)((tiles_row + want - 1) / want);
+    a.nseg = (int)((tiles_row + a.seg_tiles - 1) / a.seg_tiles);
+    if (a.nseg > fs::MAX_SEGS) return FS_E_INVALID;
+    const int64_t items = rows * a.nseg;
+    if (items > 0x7fffffff) return FS_E_INVALID;
+    const int64_t grid = items < 2 * (int64_t)ctx->cus ? items : 2 * (int64_t)ctx->cus;
+    int rc = grow(ctx, (size_t)items, (size_t)rows, (size_t)(streams > 0 ? streams : 1));
     if (rc != FS_OK) return rc;
     a.cand = ctx->cand; a.meta = ctx->meta; a.row_cnt = ctx->row_cnt; a.stream_cnt = ctx->stream_cnt; a.err = ctx->err;
-    if (ept == 32) hipLaunchKernelGGL(fs::sample_kernel<32>, dim3((unsigned)grid), dim3(fs::BLOCK), 0, st, a);
-    else if (ept == 16) hipLaunchKernelGGL(fs::sample_kernel<16>, dim3((unsigned)grid), dim3(fs::BLOCK), 0, st, a);
-    else hipLaunchKernelGGL(fs::sample_kernel<4>, dim3((unsigned)grid), dim3(fs::BLOCK), 0, st, a);
+    hipLaunchKernelGGL(fs::segment_kernel, dim3((unsigned)grid), dim3(fs::BLOCK), 0, st, a);
+    if (hipGetLastError() != hipSuccess) return FS_E_HIP;
+    hipLaunchKernelGGL(fs::merge_kernel, dim3((unsigned)rows), dim3(fs::BLOCK), 0, st, a);
     return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
 }
 
