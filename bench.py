@@ -76,6 +76,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="after the timed steps, run plain 256 MiB device copies (counter calibration for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the sampler path is built and measured on a single MI355X "
@@ -155,8 +157,16 @@ def main():
                    "logit_copies_rotated": nrot},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "fs::sample_kernel<32>", "kernel_ms": kern_ms, "algorithmic_bytes": alg_bytes},
+                     "kernel": "fs_sample_batch: fs::segment_kernel + fs::merge_kernel", "kernel_ms": kern_ms,
+                     "algorithmic_bytes": alg_bytes},
     }
+    if args.copy_calib:
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev)   # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy calibration: 5 copies of 268435456 bytes")
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(w, gpu_tok, args.cpu_seconds)
     print(json.dumps(out), flush=True)
