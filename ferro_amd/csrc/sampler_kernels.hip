@@ -54,7 +54,7 @@ constexpr int NBINS = 1 << HBITS;         // threshold histograms
 constexpr int SMALL = 512;                // rank-sort capacity of the merge
 constexpr int MAX_SEGS = 1024;            // segments per row
 constexpr int SPEC = 8;                   // merge gather: loads in flight per thread per round
-constexpr int HPF = 2;                    // history-window ids per thread fetched with a segment's first tiles
+constexpr int WIDS = 2048;                // penalty-window ids of one segment kept in LDS (longer: rescanned per tile)
 
 enum Mode : int { MODE_SAMPLE = 0, MODE_ARGMAX = 1, MODE_VERIFY = 2 };
 
@@ -409,9 +409,11 @@ struct Shared {
     uint64_t cand[CAP];                // candidate buffer / merge gather
     uint32_t scr[TILE / 2 + NBINS];    // per-tile 16-bit penalty counts, then histograms; or a 64-bit stage
     uint32_t off[MAX_SEGS + 1];        // merge: flat offsets of the segment lists
+    int32_t ids[WIDS];                 // the penalty window's ids that fall in the current segment
     uint32_t wsum[NWAVES];
     uint32_t count;
     uint32_t flag;
+    uint32_t nids;
     Red red;
     __device__ __forceinline__ uint32_t* cnt() { return scr; }
     __device__ __forceinline__ uint32_t* bins() { return scr + TILE / 2; }
@@ -488,15 +490,13 @@ __device__ __forceinline__ int hist_at(const Args& a, const RowCtx& rc, int64_t 
 // Issue the loads of one tile (TPT logits per thread: float4 j at element lo + (j*BLOCK + t)*4) without waiting.
 // Lanes past the row's end read a clamped in-bounds address and are zeroed. The float4 holding element V-1 may
 // extend up to 12 bytes past it, inside the same 16-byte-aligned block (never into another page); masked too.
-__device__ __forceinline__ void load_tile(float (&x)[TPT], const float* rowp, int lo, int V) {
+// The segment kernel only streams full tiles (a row's partial last tile is handled by the merge kernel).
+__device__ __forceinline__ void load_tile(float (&x)[TPT], const float* rowp, int lo) {
+    const float4* p = reinterpret_cast<const float4*>(rowp + lo) + threadIdx.x;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int e = lo + (j * BLOCK + (int)threadIdx.x) * 4;
-        const float4 t = *reinterpret_cast<const float4*>(rowp + (e < V ? e : 0));
-        x[4 * j + 0] = e + 0 < V ? t.x : 0.f;
-        x[4 * j + 1] = e + 1 < V ? t.y : 0.f;
-        x[4 * j + 2] = e + 2 < V ? t.z : 0.f;
-        x[4 * j + 3] = e + 3 < V ? t.w : 0.f;
+        const float4 t = p[j * BLOCK];
+        x[4 * j + 0] = t.x; x[4 * j + 1] = t.y; x[4 * j + 2] = t.z; x[4 * j + 3] = t.w;
     }
 }
 // element id of this thread's i-th logit of the tile starting at lo
@@ -505,24 +505,26 @@ __device__ __forceinline__ int elem_id(int lo, int i) { return lo + ((i >> 2) * 
 // Penalty pass on one tile in registers (sampler.cpp:11-18; frequency/presence extension): the window's ids that
 // fall in [lo, lo + TILE) are counted in a 16-bit LDS table, then each thread patches its counted logits.
 // Entry: the table may still be read by the previous tile's patching, so the caller has passed a barrier.
-__device__ __forceinline__ void apply_penalties(float (&x)[TPT], const int (&hv)[HPF], const Args& a,
-                                                const RowCtx& rc, int lo, Shared& s) {
+__device__ __forceinline__ void apply_penalties(float (&x)[TPT], const Args& a, const RowCtx& rc, int lo, Shared& s) {
     const int tid = threadIdx.x;
-    const int V = a.V;
     for (int i = tid; i < TILE / 8; i += BLOCK) reinterpret_cast<uint4*>(s.cnt())[i] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
     bool ovf = false;
     auto count_id = [&](int id) {
         const uint32_t rel = (uint32_t)(id - lo);
-        if (id >= 0 && id < V && rel < (uint32_t)TILE) {
+        if (rel < (uint32_t)TILE) {
             const uint32_t sh = (rel & 1u) * 16u;
             const uint32_t old = atomicAdd(&s.cnt()[rel >> 1], 1u << sh);
             ovf |= ((old >> sh) & 0xFFFFu) == 0xFFFFu;
         }
     };
-#pragma unroll
-    for (int q = 0; q < HPF; ++q) count_id(hv[q]);
-    for (int64_t i = rc.b + HPF * BLOCK + tid; i < rc.len; i += BLOCK) count_id(hist_at(a, rc, i));
+    const int nids = (int)s.nids;
+    for (int i = tid; i < nids && i < WIDS; i += BLOCK) count_id(s.ids[i]);
+    if (nids > WIDS)                                  // long window: rescan it from memory
+        for (int64_t i = rc.b + tid; i < rc.len; i += BLOCK) {
+            const int id = hist_at(a, rc, i);
+            if (id >= 0 && id < a.V) count_id(id);
+        }
     if (ovf) atomicOr(a.err, FS_DEVERR_COUNT_OVERFLOW);
     __syncthreads();
     const float rp = rc.p.repetition_penalty, fq = rc.p.frequency_penalty, pr = rc.p.presence_penalty;
@@ -543,6 +545,29 @@ __device__ __forceinline__ void apply_penalties(float (&x)[TPT], const int (&hv)
             }
         }
     }
+}
+
+// The penalty window's ids in [seg_lo, seg_hi) into s.ids (s.nids counts past WIDS). Called with the segment's
+// first tiles in flight; ends with a barrier.
+__device__ __forceinline__ void gather_window(const Args& a, const RowCtx& rc, int seg_lo, int seg_hi, Shared& s) {
+    const int tid = threadIdx.x;
+    if (tid == 0) s.nids = 0u;
+    __syncthreads();
+    for (int64_t i0 = rc.b; i0 < rc.len; i0 += BLOCK) {
+        const int64_t i = i0 + tid;
+        int id = -1;
+        if (i < rc.len) id = hist_at(a, rc, i);
+        const bool in = id >= seg_lo && id < seg_hi;
+        const uint64_t m = __ballot(in);
+        if (m != 0ull) {
+            uint32_t base = 0u;
+            if (lane_id() == 0) base = atomicAdd(&s.nids, (uint32_t)__popcll(m));
+            base = __shfl(base, 0);
+            const uint32_t pos = base + mbcnt(m);
+            if (in && pos < (uint32_t)WIDS) s.ids[pos] = id;
+        }
+    }
+    __syncthreads();
 }
 
 // Narrow [rlo, rhi] onto the kk-th largest value among the entries a visitor yields (32-bit values, entries
@@ -630,44 +655,124 @@ __device__ __forceinline__ uint64_t compact_exact(int n, int k, Shared& s) {
 __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Shared& s) {
     const int tid = threadIdx.x;
     const int row = rc.row;
-    const int nch = a.nseg;
-    const int slot0 = row * nch;
+    const int V = a.V;
+    const int nseg = a.nseg;
+    const int tail_lo = (V / TILE) * TILE;            // the segment kernel streamed [0, tail_lo)
+    const int ntail = V - tail_lo;                    // < TILE logits left for this kernel
+    const int tslot = a.B * nseg + row;               // workspace slot of this row's tail list
     int k = rc.k;
     int tok = 0, keep = 1;
+
+    // ---- the row's tail: loads first, then its penalty pass (the same arithmetic as the segment kernel)
+    constexpr int TT = TILE / BLOCK;                  // tail logits per thread: element tail_lo + r*BLOCK + tid
+    float tx[TT];
+    const float* rowp = a.logits + (int64_t)row * a.ld;
+#pragma unroll
+    for (int r = 0; r < TT; ++r) {
+        const int e = tail_lo + r * BLOCK + tid;
+        tx[r] = e < V ? rowp[e] : 0.f;
+    }
+    if (ntail > 0 && rc.pen) {
+        for (int i = tid; i < TILE / 8; i += BLOCK) reinterpret_cast<uint4*>(s.cnt())[i] = make_uint4(0u, 0u, 0u, 0u);
+        __syncthreads();
+        bool ovf = false;
+        for (int64_t i = rc.b + tid; i < rc.len; i += BLOCK) {
+            const int id = hist_at(a, rc, i);
+            const uint32_t rel = (uint32_t)(id - tail_lo);
+            if (id >= 0 && id < V && rel < (uint32_t)TILE) {
+                const uint32_t sh = (rel & 1u) * 16u;
+                const uint32_t old = atomicAdd(&s.cnt()[rel >> 1], 1u << sh);
+                ovf |= ((old >> sh) & 0xFFFFu) == 0xFFFFu;
+            }
+        }
+        if (ovf) atomicOr(a.err, FS_DEVERR_COUNT_OVERFLOW);
+        __syncthreads();
+        const float rp = rc.p.repetition_penalty, fq = rc.p.frequency_penalty, pr = rc.p.presence_penalty;
+#pragma unroll
+        for (int r = 0; r < TT; ++r) {
+            const int rel = r * BLOCK + tid;
+            const uint32_t cc = (s.cnt()[rel >> 1] >> ((rel & 1) * 16)) & 0xFFFFu;
+            if (cc != 0u && tail_lo + rel < V) {
+                float l = tx[r];
+                if (rc.rep_on) l = l > 0.0f ? __fdiv_rn(l, rp) : __fmul_rn(l, rp);
+                if (rc.fp_on) l = __fsub_rn(l, __fadd_rn(__fmul_rn((float)cc, fq), pr));
+                tx[r] = l;
+            }
+        }
+        __syncthreads();
+    }
+
     if (rc.large) {
         tok = -1;
         keep = 0;
         if (tid == 0) atomicOr(a.err, FS_DEVERR_LARGE_K);
     } else if (rc.greedy) {
         uint64_t best = 0;
-        for (int c = tid; c < nch; c += BLOCK) {
-            const uint64_t v = *(a.cand + (int64_t)(slot0 + c) * CAP);
+        for (int c = tid; c < nseg; c += BLOCK) {
+            const uint64_t v = *(a.cand + (int64_t)(row * nseg + c) * CAP);
             best = v > best ? v : best;
         }
+#pragma unroll
+        for (int r = 0; r < TT; ++r) {                // > -inf, as the segment kernel's IEEE compare from -inf:
+            const int e = tail_lo + r * BLOCK + tid;  // NaN and -inf are never taken
+            if (e < V && tx[r] > -__builtin_huge_valf()) {
+                const uint64_t c = comp_of(key_of(tx[r]), (uint32_t)e);
+                best = c > best ? c : best;
+            }
+        }
         best = block_max_u64(best, s.red);
-        tok = (int)comp_id(best);
-        const float l0 = a.logits[(int64_t)row * a.ld];
+        tok = best != 0 ? (int)comp_id(best) : 0;      // nothing above -inf / NaN: ferro's scan stays at 0
+        const float l0 = rowp[0];
         if (l0 != l0) tok = 0;                         // ferro's scan never moves off a NaN at index 0
         if (tid == 0 && a.mode != MODE_VERIFY) {
             if (a.cand_ids && a.kcap > 0) a.cand_ids[(int64_t)row * a.kcap] = tok;
             if (a.cand_probs && a.kcap > 0) a.cand_probs[(int64_t)row * a.kcap] = 1.0;
         }
     } else {
-        // One memory round trip: every segment's meta and the first SPEC*tps entries of its list, tps threads
-        // per segment (entries past a list's count are stale and masked once the counts are in).
-        const int tps = BLOCK / nch;                 // >= 1: the host keeps nseg <= BLOCK
+        // ---- the tail's own top k becomes one more list (agent-scope stores, drained, then read back below)
+        if (ntail > 0) {
+            if (tid == 0) s.count = 0u;
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < TT; ++r) {
+                const int e = tail_lo + r * BLOCK + tid;
+                const bool in = e < V && tx[r] == tx[r];
+                wave_append(in, in ? comp_of(key_of(tx[r]), (uint32_t)e) : 0ull, s.cand, &s.count, CAP);
+            }
+            __syncthreads();
+            int nt = (int)s.count;
+            uint32_t tkey = 0u;                       // fewer than k: 0 bounds nothing
+            if (nt > k) {
+                tkey = comp_key(compact_exact(nt, k, s));
+                nt = k;
+            }
+            uint64_t* tout = a.cand + (int64_t)tslot * CAP;
+            for (int i = tid; i < nt; i += BLOCK) st_agent(tout + i, s.cand[i]);
+            if (tid == 0) {
+                st_agent(&a.meta[2 * tslot], tkey);
+                st_agent(&a.meta[2 * tslot + 1], (uint32_t)nt);
+            }
+            vm_drain();
+            __syncthreads();
+        }
+        // One memory round trip: every list's meta and the first SPEC*tps entries of it, tps threads per list
+        // (entries past a list's count are stale and masked once the counts are in). Lists 0..nseg-1 are the
+        // segments', list nseg (if any) the tail's.
+        const int nch = nseg + (ntail > 0 ? 1 : 0);  // >= 1
+        auto slot_of = [&](int c) -> int64_t { return c < nseg ? (int64_t)row * nseg + c : (int64_t)tslot; };
+        const int tps = BLOCK / nch;                 // >= 1: the host keeps nseg < BLOCK
         const int c_me = tid % nch;
         const int r_me = tid / nch;
         const bool act = r_me < tps;
-        const uint64_t* lst = a.cand + (int64_t)(slot0 + c_me) * CAP;
-        const uint32_t t0m = *(&a.meta[2 * (slot0 + c_me)]);
-        const uint32_t cnm = *(&a.meta[2 * (slot0 + c_me) + 1]);
+        const uint64_t* lst = a.cand + slot_of(c_me) * CAP;
+        const uint32_t t0m = ld_agent(&a.meta[2 * slot_of(c_me)]);
+        const uint32_t cnm = ld_agent(&a.meta[2 * slot_of(c_me) + 1]);
         uint64_t v[SPEC];
 #pragma unroll
-        for (int q = 0; q < SPEC; ++q) v[q] = *(lst + (act ? r_me + q * tps : 0));
+        for (int q = 0; q < SPEC; ++q) v[q] = ld_agent(lst + (act ? r_me + q * tps : 0));
         if (act && r_me == 0) s.off[c_me] = cnm;
         const uint32_t L = (uint32_t)block_max_u64(act ? t0m : 0u, s.red);   // a lower bound of the k-th key
-        // flat offsets of the segment lists (used when the candidates >= L overflow LDS)
+        // flat offsets of the lists (used when the candidates >= L overflow LDS)
         uint32_t total;
         {
             const uint32_t mine = tid < nch ? s.off[tid] : 0u;
@@ -683,7 +788,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 const int m = (c0 + c1) >> 1;
                 if (s.off[m] <= g) c0 = m; else c1 = m;
             }
-            const uint64_t w = *(a.cand + (int64_t)(slot0 + c0) * CAP + (g - s.off[c0]));
+            const uint64_t w = ld_agent(a.cand + slot_of(c0) * CAP + (g - s.off[c0]));
             return f < total ? w : 0ull;
         };
         // gather the candidates >= L into LDS (counted past CAP), tracking their max key
@@ -695,7 +800,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             wave_append(in, v[q], s.cand, &s.count, CAP);
         }
         for (uint32_t i = (uint32_t)(r_me + SPEC * tps); act && i < cnm; i += (uint32_t)tps) {   // long lists
-            const uint64_t w = *(lst + i);
+            const uint64_t w = ld_agent(lst + i);
             const bool in = w != 0 && comp_key(w) >= L;
             if (in) kmax = comp_key(w) > kmax ? comp_key(w) : kmax;
             wave_append(in, w, s.cand, &s.count, CAP);
@@ -895,67 +1000,71 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     const int tid = threadIdx.x;
     const int V = a.V;
     const int seg_lo = seg * a.seg_tiles * TILE;
-    const int left = (V - seg_lo + TILE - 1) / TILE;
+    const int left = V / TILE - seg * a.seg_tiles;                 // full tiles left in the row
     const int ntiles = left < a.seg_tiles ? left : a.seg_tiles;    // >= 1
     const float* rowp = a.logits + (int64_t)rc.row * a.ld;
 
     float buf[PF][TPT];
 #pragma unroll
-    for (int p = 0; p < PF; ++p) load_tile(buf[p], rowp, seg_lo + (p < ntiles ? p : 0) * TILE, V);
-    int hv[HPF];
-#pragma unroll
-    for (int q = 0; q < HPF; ++q) {
-        const int64_t i = rc.b + q * BLOCK + tid;
-        const bool in = rc.pen && i < rc.len;
-        const int32_t* src = !in ? reinterpret_cast<const int32_t*>(rowp)
-                                 : (i < rc.lenA ? a.hist + rc.hA0 + i : rc.segB + (i - rc.lenA));
-        const int v = *src;
-        hv[q] = in ? v : -1;
+    for (int p = 0; p < PF; ++p) load_tile(buf[p], rowp, seg_lo + (p < ntiles ? p : 0) * TILE);
+    if (rc.pen) {
+        const int seg_hi = seg_lo + ntiles * TILE;
+        gather_window(a, rc, seg_lo, seg_hi, s);
     }
 
     const int k = rc.k;
     const bool topk = !rc.greedy && !rc.large;
-    uint32_t bk = 0u;                  // greedy: this lane's best key and its (first) id
-    int bi = -1;
+    float bv = -__builtin_huge_valf(); // greedy: this lane's first maximum (IEEE >: NaN never taken, -0 == +0)
+    int bs = -1;                       //         and its slot tile*TPT + i (-1: none)
     uint64_t X = 1ull;                 // top-k: candidates are the composites >= X (1: every valid logit)
-    float tf = -__builtin_huge_valf(); // fp32 superset filter of X: key(x) >= key(X) <=> x >= tf
+    float tf = -__builtin_huge_valf(); // fp32 form of X's key: composite >= X <=> x > tf, or x == tf and id <= idX
     if (tid == 0) s.count = 0u;
     __syncthreads();
 
     // Top-k buffer discipline: after tile 0 the buffer is checked (barrier) only every R tiles, R sized so the
     // expected appends fill at most half the headroom; an overflow (appends past CAP are dropped) is detected at
     // the next check and the segment is streamed again in safe mode (a check after every tile).
-    auto greedy_update = [&](const float (&x)[TPT], int lo) {
+    auto greedy_update = [&](const float (&x)[TPT], int tt) {
+        const int sb = tt * TPT;
 #pragma unroll
-        for (int i = 0; i < TPT; ++i) {
-            const int e = elem_id(lo, i);
-            const uint32_t kq = key_of(x[i]);
-            if (e < V && kq > bk) { bk = kq; bi = e; }
-        }
+        for (int i = 0; i < TPT; ++i)
+            if (x[i] > bv) { bv = x[i]; bs = sb + i; }
     };
-    // appends of one tile: per-element wave ballots, one LDS atomic per wave for the whole tile
+    // appends of one tile: the common path is one fp32 compare per logit folded into a wave ballot; ties with the
+    // threshold key are resolved by id and the composites are formed only in slots where some lane passed
     auto topk_append = [&](const float (&x)[TPT], int lo) {
         uint64_t bal[TPT];
+        uint64_t any = 0ull;
+#pragma unroll
+        for (int i = 0; i < TPT; ++i) {
+            bal[i] = __ballot(x[i] >= tf);
+            any |= bal[i];
+        }
+        if (any == 0ull) return;                     // wave-uniform
+        const uint32_t idX = comp_id(X);
+        const int lane = lane_id();
         uint32_t tot = 0u;
 #pragma unroll
         for (int i = 0; i < TPT; ++i) {
-            const int e = elem_id(lo, i);
-            bool take = e < V && x[i] >= tf;
-            if (take) take = comp_of(key_of(x[i]), (uint32_t)e) >= X;
-            bal[i] = __ballot(take);
-            tot += (uint32_t)__popcll(bal[i]);
+            if (bal[i] != 0ull) {
+                const bool take = ((bal[i] >> lane) & 1ull) && (x[i] > tf || (uint32_t)elem_id(lo, i) <= idX);
+                bal[i] = __ballot(take);
+                tot += (uint32_t)__popcll(bal[i]);
+            }
         }
-        if (tot == 0u) return;                       // wave-uniform
+        if (tot == 0u) return;
         uint32_t base = 0u;
-        if (lane_id() == 0) base = atomicAdd(&s.count, tot);
+        if (lane == 0) base = atomicAdd(&s.count, tot);
         base = __shfl(base, 0);
 #pragma unroll
         for (int i = 0; i < TPT; ++i) {
-            if ((bal[i] >> lane_id()) & 1ull) {
-                const uint32_t pos = base + mbcnt(bal[i]);
-                if (pos < (uint32_t)CAP) s.cand[pos] = comp_of(key_of(x[i]), (uint32_t)elem_id(lo, i));
+            if (bal[i] != 0ull) {
+                if ((bal[i] >> lane) & 1ull) {
+                    const uint32_t pos = base + mbcnt(bal[i]);
+                    if (pos < (uint32_t)CAP) s.cand[pos] = comp_of(key_of(x[i]), (uint32_t)elem_id(lo, i));
+                }
+                base += (uint32_t)__popcll(bal[i]);
             }
-            base += (uint32_t)__popcll(bal[i]);
         }
     };
     // barrier + count; compacts when another tile could overflow; returns the count (> CAP: overflowed)
@@ -977,11 +1086,11 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         {
             float (&x)[TPT] = buf[0];
             const int lo = seg_lo;
-            if (rc.pen) apply_penalties(x, hv, a, rc, lo, s);
+            if (rc.pen) apply_penalties(x, a, rc, lo, s);
             if (rc.greedy) {
-                greedy_update(x, lo);
+                greedy_update(x, 0);
             } else if (topk) {
-                if (!safe && k < min(TILE, V - seg_lo)) {
+                if (!safe) {                             // k <= KMAX < TILE
                     // maxima of >= 2k groups of tile 0 (G per thread), histogrammed over their [min, max]:
                     // at least k of the tile's logits reach T0
                     int G = 1;
@@ -992,7 +1101,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     bool any = false;
 #pragma unroll
                     for (int i = 0; i < TPT; ++i) {
-                        if (elem_id(lo, i) < V) { const uint32_t kq = key_of(x[i]); gm = kq > gm ? kq : gm; any = true; }
+                        { const uint32_t kq = key_of(x[i]); gm = kq > gm ? kq : gm; any = true; }
                         if ((i + 1) % per == 0) {
                             if (any) { gmin = gm < gmin ? gm : gmin; gmax = gm > gmax ? gm : gmax; }
                             gm = 0u;
@@ -1004,7 +1113,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     const int sh = range_shift(gmin, gmax);
 #pragma unroll
                     for (int i = 0; i < TPT; ++i) {
-                        if (elem_id(lo, i) < V) { const uint32_t kq = key_of(x[i]); gm = kq > gm ? kq : gm; any = true; }
+                        { const uint32_t kq = key_of(x[i]); gm = kq > gm ? kq : gm; any = true; }
                         if ((i + 1) % per == 0) {
                             if (any) atomicAdd(&s.bins()[(gm - gmin) >> sh], 1u);
                             gm = 0u;
@@ -1021,7 +1130,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 }
                 topk_append(x, lo);
             }
-            if (PF < ntiles) load_tile(x, rowp, lo + PF * TILE, V);
+            if (PF < ntiles) load_tile(x, rowp, lo + PF * TILE);
             if (topk) {
                 const int n = check();
                 overflow = n > CAP;
@@ -1041,10 +1150,10 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 if (tt >= 1 && tt < ntiles && !overflow) {
                     const int lo = seg_lo + tt * TILE;
                     float (&x)[TPT] = buf[p];
-                    if (rc.pen) apply_penalties(x, hv, a, rc, lo, s);
-                    if (rc.greedy) greedy_update(x, lo);
+                    if (rc.pen) apply_penalties(x, a, rc, lo, s);
+                    if (rc.greedy) greedy_update(x, tt);
                     else if (topk) topk_append(x, lo);
-                    if (tt + PF < ntiles) load_tile(x, rowp, lo + PF * TILE, V);
+                    if (tt + PF < ntiles) load_tile(x, rowp, lo + PF * TILE);
                     if (topk) {
                         if (++since >= R || rc.pen) {
                             since = 0;
@@ -1063,7 +1172,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         __syncthreads();
         if (tid == 0) s.count = 0u;
 #pragma unroll
-        for (int p = 0; p < PF; ++p) load_tile(buf[p], rowp, seg_lo + (p < ntiles ? p : 0) * TILE, V);
+        for (int p = 0; p < PF; ++p) load_tile(buf[p], rowp, seg_lo + (p < ntiles ? p : 0) * TILE);
         __syncthreads();
     }
     if (topk) {
@@ -1079,7 +1188,8 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     if (rc.large) {
         if (tid == 0) { a.meta[2 * slot] = 0u; a.meta[2 * slot + 1] = 0u; }
     } else if (rc.greedy) {
-        uint64_t best = bi >= 0 ? comp_of(bk, (uint32_t)bi) : 0ull;
+        uint64_t best = 0ull;
+        if (bs >= 0) best = comp_of(key_of(bv), (uint32_t)elem_id(seg_lo + (bs / TPT) * TILE, bs % TPT));
         best = block_max_u64(best, s.red);
         if (tid == 0) {
             gout[0] = best;
@@ -1171,23 +1281,30 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
         if (hipDeviceGetAttribute(&ctx->cus, hipDeviceAttributeMultiprocessorCount, ctx->device) != hipSuccess)
             return FS_E_HIP;
     }
-    // Segments: about two per CU over the whole batch (each streams >= 1 tile), the rest of a row per segment.
-    const int64_t tiles_row = (a.V + fs::TILE - 1) / fs::TILE;
-    int64_t want = (2 * (int64_t)ctx->cus + rows - 1) / rows;
-    if (want < 1) want = 1;
-    if (want > tiles_row) want = tiles_row;
-    if (want > fs::BLOCK) want = fs::BLOCK;        // the merge gives each segment >= 1 thread
-    a.seg_tiles = (int)((tiles_row + want - 1) / want);
-    a.nseg = (int)((tiles_row + a.seg_tiles - 1) / a.seg_tiles);
+    // Segments: about two per CU over the whole batch; a segment streams >= 1 full tile of 4096 logits. The
+    // merge kernel handles each row's partial last tile (all of a row shorter than one tile).
+    const int64_t tiles_row = a.V / fs::TILE;
+    a.nseg = 0;
+    a.seg_tiles = 1;
+    if (tiles_row > 0) {
+        int64_t want = (2 * (int64_t)ctx->cus + rows - 1) / rows;
+        if (want < 1) want = 1;
+        if (want > tiles_row) want = tiles_row;
+        if (want > fs::BLOCK - 1) want = fs::BLOCK - 1;   // the merge gives each list (segments + tail) a thread
+        a.seg_tiles = (int)((tiles_row + want - 1) / want);
+        a.nseg = (int)((tiles_row + a.seg_tiles - 1) / a.seg_tiles);
+    }
     if (a.nseg > fs::MAX_SEGS) return FS_E_INVALID;
     const int64_t items = rows * a.nseg;
     if (items > 0x7fffffff) return FS_E_INVALID;
     const int64_t grid = items < 2 * (int64_t)ctx->cus ? items : 2 * (int64_t)ctx->cus;
-    int rc = grow(ctx, (size_t)items, (size_t)rows, (size_t)(streams > 0 ? streams : 1));
+    int rc = grow(ctx, (size_t)(items + rows), (size_t)rows, (size_t)(streams > 0 ? streams : 1));
     if (rc != FS_OK) return rc;
     a.cand = ctx->cand; a.meta = ctx->meta; a.row_cnt = ctx->row_cnt; a.stream_cnt = ctx->stream_cnt; a.err = ctx->err;
-    hipLaunchKernelGGL(fs::segment_kernel, dim3((unsigned)grid), dim3(fs::BLOCK), 0, st, a);
-    if (hipGetLastError() != hipSuccess) return FS_E_HIP;
+    if (grid > 0) {
+        hipLaunchKernelGGL(fs::segment_kernel, dim3((unsigned)grid), dim3(fs::BLOCK), 0, st, a);
+        if (hipGetLastError() != hipSuccess) return FS_E_HIP;
+    }
     hipLaunchKernelGGL(fs::merge_kernel, dim3((unsigned)rows), dim3(fs::BLOCK), 0, st, a);
     return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
 }

@@ -273,3 +273,18 @@ def test_sampler_shim_reproduces_reference_streams():
             t = smp.sample(torch.from_numpy(row).cuda(), row.size, hist)
             assert t == gold["stream_tok"][s][i], (s, i)
             hist.append(t)
+
+
+def test_greedy_infinities_and_nan_rows():
+    """ferro's scan (sampler.cpp:21): the first index strictly above logits[0]'s running best; -inf / NaN rows."""
+    V = 3 * 4096 + 77                                   # full tiles plus a partial tail
+    rows = []
+    r = np.full(V, -np.inf, np.float32); rows.append(r)                      # all -inf -> 0
+    r = np.full(V, -np.inf, np.float32); r[V - 5] = np.nan; rows.append(r)   # -inf and NaN -> 0
+    r = np.full(V, np.nan, np.float32); r[4100] = -np.inf; rows.append(r)    # NaN at 0 -> 0
+    r = np.full(V, -np.inf, np.float32); r[V - 3] = -1.0; rows.append(r)     # max in the tail
+    r = np.full(V, -np.inf, np.float32); r[5000] = np.inf; r[V - 2] = np.inf; rows.append(r)   # +inf tie
+    x = np.stack(rows)
+    tok = F.argmax_batch(torch.from_numpy(x).cuda()).cpu().numpy()
+    want = [O.sample(row, [], O.make_params(temperature=0.0, repetition_penalty=1.0))[0] for row in rows]
+    assert list(tok) == want == [0, 0, 0, V - 3, 5000]
