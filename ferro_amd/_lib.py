@@ -39,6 +39,7 @@ SIGNATURES = {
     "fs_sample_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P]),
     "fs_argmax_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P]),
     "fs_verify": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P]),
+    "fs_penalize_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P]),
     "fs_device_error": (ctypes.c_int, [_P, _P, _P]),
     "fs_rng_create": (ctypes.c_int, [ctypes.c_uint64, _P]),
     "fs_rng_destroy": (ctypes.c_int, [_P]),

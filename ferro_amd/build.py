@@ -9,6 +9,10 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 SRC = os.path.join(PKG, "csrc", "sampler_kernels.hip")
 LIB = os.path.join(PKG, "libferro_sampler.so")
+# C++ drop-in test driver (tests/cpp): host code over include/ferro_sampler.hpp, linked against LIB
+SHIM_SRC = os.path.join(ROOT, "tests", "cpp", "shim_replay.cpp")
+SHIM_BIN = os.path.join(ROOT, "tests", "cpp", "shim_replay")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -23,14 +27,22 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
-    cmd = [HIPCC, *FLAGS, "-o", LIB, SRC]
+def _run(cmd, what, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
-        raise RuntimeError(f"hipcc failed ({r.returncode}) building {LIB}")
+        raise RuntimeError(f"{cmd[0]} failed ({r.returncode}) building {what}")
+
+
+def build(verbose: bool = False) -> str:
+    _run([HIPCC, *FLAGS, "-o", LIB, SRC], LIB, verbose)
+    if os.path.exists(SHIM_SRC):
+        _run(["g++", "-O2", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROOT, "include"),
+              "-I" + os.path.join(ROCM, "include"), SHIM_SRC, "-o", SHIM_BIN, "-L" + PKG, "-lferro_sampler",
+              "-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,-rpath,$ORIGIN/../../ferro_amd",
+              "-Wl,-rpath," + os.path.join(ROCM, "lib")], SHIM_BIN, verbose)
     return LIB
 
 

@@ -1225,6 +1225,59 @@ __global__ __launch_bounds__(BLOCK) void merge_kernel(Args a) {
     merge_row(a, row_ctx(a, (int)blockIdx.x), s);
 }
 
+// In-place penalty pass (fs_penalize_batch): ferro's sample() leaves its host row penalised (sampler.cpp:11-18),
+// and a caller that reads the row back afterwards (lm_cli.cpp:353) sees those values. One workgroup per
+// (row, 8192-id chunk): the window's ids that fall in the chunk are counted in a 16-bit LDS table, then every
+// counted logit is rewritten once with the same arithmetic as the sampling kernels.
+constexpr int PEN_BLOCK = 256;
+constexpr int PEN_CHUNK = 8192;
+
+__global__ __launch_bounds__(PEN_BLOCK) void penalize_kernel(float* logits, int64_t ld, int V, const int32_t* hist,
+                                                            const int64_t* hist_off, const fs_row_params* params,
+                                                            int nchunk, int32_t* err) {
+    __shared__ uint32_t cnt[PEN_CHUNK / 2];
+    const int tid = threadIdx.x;
+    const int row = (int)blockIdx.x / nchunk;
+    const int lo = ((int)blockIdx.x - row * nchunk) * PEN_CHUNK;
+    const fs_row_params p = ld_const(params + row);
+    const bool rep_on = p.repetition_penalty != 1.0f;
+    const bool fp_on = p.frequency_penalty != 0.0f || p.presence_penalty != 0.0f;
+    if (!(rep_on || fp_on) || p.repeat_last_n == 0 || !hist || !hist_off) return;
+    const int64_t h0 = ld_const(hist_off + row);
+    const int64_t len = ld_const(hist_off + row + 1) - h0;
+    const int64_t b = window_begin(len, p);
+    if (b >= len) return;
+    for (int i = tid; i < PEN_CHUNK / 2; i += PEN_BLOCK) cnt[i] = 0u;
+    __syncthreads();
+    bool ovf = false;
+    for (int64_t i = b + tid; i < len; i += PEN_BLOCK) {
+        const int id = hist[h0 + i];
+        const uint32_t rel = (uint32_t)(id - lo);
+        if (id >= 0 && id < V && rel < (uint32_t)PEN_CHUNK) {
+            const uint32_t sh = (rel & 1u) * 16u;
+            const uint32_t old = atomicAdd(&cnt[rel >> 1], 1u << sh);
+            ovf |= ((old >> sh) & 0xFFFFu) == 0xFFFFu;
+        }
+    }
+    if (ovf) atomicOr(err, FS_DEVERR_COUNT_OVERFLOW);
+    __syncthreads();
+    float* rowp = logits + (int64_t)row * ld + lo;
+    for (int i = tid; i < PEN_CHUNK / 2; i += PEN_BLOCK) {
+        const uint32_t c2 = cnt[i];
+        if (c2 == 0u) continue;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t c = (c2 >> (16 * q)) & 0xFFFFu;
+            if (c != 0u) {                                  // a counted id is < V
+                float l = rowp[2 * i + q];
+                if (rep_on) l = l > 0.0f ? __fdiv_rn(l, p.repetition_penalty) : __fmul_rn(l, p.repetition_penalty);
+                if (fp_on) l = __fsub_rn(l, __fadd_rn(__fmul_rn((float)c, p.frequency_penalty), p.presence_penalty));
+                rowp[2 * i + q] = l;
+            }
+        }
+    }
+}
+
 }  // namespace fs
 
 // ================================================================================================ host side
@@ -1378,6 +1431,24 @@ int fs_verify(fs_context* ctx, const float* d_logits, int64_t ld, int32_t n_stre
     a.params = d_params; a.u = d_u; a.tok = d_tok; a.rows = d_rows; a.row_off = d_row_off; a.n_streams = n_streams;
     a.eos = eos_id; a.accepted = d_accepted; a.mode = fs::MODE_VERIFY;
     return launch(ctx, a, total_rows, n_streams, (hipStream_t)stream);
+}
+
+int fs_penalize_batch(fs_context* ctx, float* d_logits, int64_t ld, int32_t B, int32_t V, const int32_t* d_hist,
+                      const int64_t* d_hist_off, const fs_row_params* d_params, void* stream) {
+    if (!ctx || !d_params) return FS_E_INVALID;
+    int rc = check_rows(d_logits, ld, B, V);
+    if (rc != FS_OK) return rc;
+    if (B == 0 || !d_hist || !d_hist_off) return FS_OK;
+    const int64_t nchunk = ((int64_t)V + fs::PEN_CHUNK - 1) / fs::PEN_CHUNK;
+    if ((int64_t)B * nchunk > 0x7fffffff) return FS_E_INVALID;
+    {
+        std::lock_guard<std::mutex> g(ctx->mu);
+        rc = grow(ctx, 0, 0, 0);
+        if (rc != FS_OK) return rc;
+    }
+    hipLaunchKernelGGL(fs::penalize_kernel, dim3((unsigned)(B * nchunk)), dim3(fs::PEN_BLOCK), 0, (hipStream_t)stream,
+                       d_logits, ld, V, d_hist, d_hist_off, d_params, (int)nchunk, ctx->err);
+    return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
 }
 
 int fs_device_error(fs_context* ctx, void* stream, int32_t* bits) {

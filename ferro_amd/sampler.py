@@ -226,6 +226,27 @@ def verify(logits, rows, row_off, params, u=None, hist=None, hist_off=None, eos_
     return tok, acc
 
 
+def penalize_batch(logits, params, hist=None, hist_off=None, V=None, ctx=None, stream=None):
+    """fs_penalize_batch: leave each row penalised in place, as ferro's sample() leaves its host row
+    (sampler.cpp:11-18). logits must be a writable [B, ld] fp32 CUDA tensor; returns it."""
+    target = logits
+    logits, ld, n = _check_logits(logits, V)
+    B = logits.shape[0]
+    dev = logits.device
+    p = _dev_params(params, dev)
+    if p.numel() != B * PARAMS_DTYPE.itemsize:
+        raise SamplerError("one params record per row")
+    hist, hist_off = _hist_tensors(hist, hist_off, B, dev)
+    ctx = ctx or Context.default(dev)
+    with ctx.lock:
+        check(lib().fs_penalize_batch(ctx.h, _ptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p),
+                                      _stream(stream)), "fs_penalize_batch")
+    t2 = target if target.dim() == 2 else target.unsqueeze(0)
+    if logits.data_ptr() != t2.data_ptr():            # repacked into an aligned copy: write the rows back
+        t2[:, :n].copy_(logits[:, :n])
+    return target
+
+
 def device_error(ctx=None, stream=None) -> int:
     ctx = ctx or Context.default()
     bits = ctypes.c_int32(0)
@@ -237,25 +258,38 @@ class Sampler:
     """Mirror of ferro::Sampler (src/sampler.h:23-34) running on the GPU.
 
     sample(logits, n_vocab, history) -> int, with logits a CUDA float32 tensor (device-resident, the intended
-    use) or a host array/tensor (copied to the device). Unlike ferro, the logits are not modified in place: the
-    penalty is applied on the fly inside the kernel."""
+    use), a CPU tensor or a numpy float32 array (copied to the device). As in ferro (sampler.cpp:11-18) the row is
+    left penalised in place, on whichever side it lives, unless the sampler was made with write_back=False (the
+    token is the same either way: the kernels penalise on the fly)."""
 
-    def __init__(self, p: SamplerParams, device=None):
+    def __init__(self, p: SamplerParams, device=None, write_back: bool = True):
         self._p = p
         self._rng = Rng(int(p.seed))
         self._dev = torch.device("cuda" if device is None else device)
         self._rec = torch.from_numpy(params_array(p).view(np.uint8).copy()).to(self._dev)
         self._ctx = Context.default(self._dev)
+        self._write_back = write_back
 
     def params(self) -> SamplerParams:
         return self._p
 
     def sample(self, logits, n_vocab: int, history) -> int:
-        if not (isinstance(logits, torch.Tensor) and logits.is_cuda):
+        host = logits
+        on_dev = isinstance(logits, torch.Tensor) and logits.is_cuda
+        if not on_dev:
             logits = torch.as_tensor(np.asarray(logits, np.float32)).to(self._dev)
-        row = logits.reshape(-1)[:n_vocab]
+        row = logits.reshape(-1)[:n_vocab].reshape(1, -1)
         h = np.asarray(history, np.int32).reshape(-1)
         u = np.zeros(1) if self._p.is_greedy() else self._rng.next_u(1)
-        out = sample_batch(row.reshape(1, -1), self._rec, u, hist=h, hist_off=[0, h.size], V=n_vocab,
-                           ctx=self._ctx)
-        return int(out["tok"].item())
+        hist_off = [0, h.size]
+        out = sample_batch(row, self._rec, u, hist=h, hist_off=hist_off, V=n_vocab, ctx=self._ctx)
+        tok = int(out["tok"].item())
+        if self._write_back and h.size:
+            penalize_batch(row, self._rec, hist=h, hist_off=hist_off, V=n_vocab, ctx=self._ctx)
+            if not on_dev:
+                pen = row.reshape(-1).cpu()
+                if isinstance(host, torch.Tensor):
+                    host.reshape(-1)[:n_vocab].copy_(pen)
+                elif isinstance(host, np.ndarray) and host.dtype == np.float32:
+                    host.reshape(-1)[:n_vocab] = pen.numpy()
+        return tok

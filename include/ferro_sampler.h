@@ -103,6 +103,14 @@ int fs_rng_destroy(fs_rng* r);
 int fs_rng_next_u(fs_rng* r, double* u, int32_t n);
 int fs_rng_copy(const fs_rng* src, fs_rng* dst);
 
+/* The penalty stage alone, in place: row b of d_logits is left exactly as ferro's sample() leaves its host row
+ * (sampler.cpp:11-18: each distinct window id in [0, V) once, l > 0 ? l/rep : l*rep, then the frequency/presence
+ * extension). For callers that read the penalised row back (lm_cli.cpp:353); fs_sample_batch does not need it (it
+ * penalises on the fly). Rows without an active penalty, and every row when d_hist or d_hist_off is NULL, are
+ * left untouched. Same row layout rules as fs_sample_batch. */
+int fs_penalize_batch(fs_context* ctx, float* d_logits, int64_t ld, int32_t B, int32_t V, const int32_t* d_hist,
+                      const int64_t* d_hist_off, const fs_row_params* d_params, void* stream);
+
 /* Waits for `stream`, then returns and clears the device error bits (FS_DEVERR_*) kernels of this context set. */
 int fs_device_error(fs_context* ctx, void* stream, int32_t* bits);
 

@@ -1,0 +1,167 @@
+// ferro_sampler.hpp - header-only C++ drop-in for ferro::Sampler (reference src/sampler.h:23-34) over the C ABI of
+// ferro_sampler.h. Replace `ferro::Sampler` with `ferro_amd::Sampler` at the call sites
+// (src/server.cpp:546,605,631; src/lm_cli.cpp:129,324,344); link libferro_sampler.so and libamdhip64.
+//
+//   ferro_amd::Sampler s(params);                    // params: ferro's SamplerParams fields (+ freq/presence)
+//   int tok = s.sample(host_row, n_vocab, history);  // as ferro: the host row is left penalised in place
+//   int tok = s.sample_device(d_row, n_vocab, history);  // device-resident row (no PCIe copy of the logits)
+//
+// Semantics match ferro::Sampler::sample token for token: the same std::mt19937_64 seeded the same way
+// (sampler.h:25), one generate_canonical draw per sampled (non-greedy) call and none for greedy calls
+// (sampler.cpp:19-23,45-46). Unlike ferro, failures of the device path throw std::runtime_error (ferro's
+// sample cannot fail). One instance per stream and caller thread, as ferro's.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "ferro_sampler.h"
+
+namespace ferro_amd {
+
+// ferro::SamplerParams (src/sampler.h:12-21), same defaults, plus the frequency/presence extension (0 = off).
+struct SamplerParams {
+    float temperature = 0.05f;
+    int top_k = 50;
+    float top_p = 1.0f;
+    float min_p = 0.0f;
+    float repetition_penalty = 1.05f;
+    int repeat_last_n = -1;
+    int penalty_from = 0;
+    uint64_t seed = 0;
+    float frequency_penalty = 0.0f;
+    float presence_penalty = 0.0f;
+};
+
+class Sampler {
+public:
+    // write_back = true leaves the host row penalised like ferro's (one extra device->host copy of the row when
+    // a penalty is active); false skips it (the token is the same).
+    explicit Sampler(const SamplerParams& p, hipStream_t stream = nullptr, bool write_back = true)
+        : p_(p), stream_(stream), write_back_(write_back) {
+        check(fs_create(&ctx_), "fs_create");
+        check(fs_rng_create(p.seed, &rng_), "fs_rng_create");
+        rec_.temperature = p.temperature;
+        rec_.top_k = p.top_k;
+        rec_.top_p = p.top_p;
+        rec_.min_p = p.min_p;
+        rec_.repetition_penalty = p.repetition_penalty;
+        rec_.frequency_penalty = p.frequency_penalty;
+        rec_.presence_penalty = p.presence_penalty;
+        rec_.repeat_last_n = p.repeat_last_n;
+        rec_.penalty_from = p.penalty_from;
+        rec_.reserved = 0;
+        hip(hipMalloc(&d_small_, sizeof(Small)), "hipMalloc");
+        hip(hipMemcpy(&d_small_->rec, &rec_, sizeof(rec_), hipMemcpyHostToDevice), "hipMemcpy");
+    }
+    ~Sampler() {
+        (void)hipFree(d_row_);
+        (void)hipFree(d_hist_);
+        (void)hipFree(d_small_);
+        fs_rng_destroy(rng_);
+        fs_destroy(ctx_);
+    }
+    Sampler(const Sampler&) = delete;
+    Sampler& operator=(const Sampler&) = delete;
+
+    // ferro::Sampler::sample (sampler.cpp:10): host row, penalised in place (when write_back).
+    int sample(float* logits, int n_vocab, const std::vector<int>& history) {
+        if (!logits || n_vocab < 1) throw std::runtime_error("ferro_amd::Sampler: bad row");
+        const int64_t ld = ((int64_t)n_vocab + 3) & ~(int64_t)3;
+        if (ld > row_cap_) {
+            (void)hipFree(d_row_);
+            d_row_ = nullptr;
+            row_cap_ = 0;
+            hip(hipMalloc(&d_row_, (size_t)ld * sizeof(float)), "hipMalloc");
+            row_cap_ = ld;
+        }
+        hip(hipMemcpyAsync(d_row_, logits, (size_t)n_vocab * sizeof(float), hipMemcpyHostToDevice, stream_),
+            "hipMemcpyAsync");
+        const int tok = run(d_row_, n_vocab, history);
+        if (write_back_ && penalised_) {
+            check(fs_penalize_batch(ctx_, d_row_, ld, 1, n_vocab, d_hist_, &d_small_->off[0], &d_small_->rec, stream_),
+                  "fs_penalize_batch");
+            hip(hipMemcpyAsync(logits, d_row_, (size_t)n_vocab * sizeof(float), hipMemcpyDeviceToHost, stream_),
+                "hipMemcpyAsync");
+            hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+        }
+        return tok;
+    }
+
+    // Device-resident row (16-byte aligned): read only; use fs_penalize_batch where the penalised row is wanted.
+    int sample_device(const float* d_logits, int n_vocab, const std::vector<int>& history) {
+        return run(d_logits, n_vocab, history);
+    }
+
+    const SamplerParams& params() const { return p_; }
+
+private:
+    struct Small {
+        fs_row_params rec;
+        int64_t off[2];
+        double u;
+        int32_t tok;
+    };
+
+    static void check(int rc, const char* what) {
+        if (rc != FS_OK) throw std::runtime_error(std::string("ferro_amd::Sampler: ") + what + ": " + fs_strerror(rc));
+    }
+    static void hip(hipError_t e, const char* what) {
+        if (e != hipSuccess)
+            throw std::runtime_error(std::string("ferro_amd::Sampler: ") + what + ": " + hipGetErrorString(e));
+    }
+
+    int run(const float* d_logits, int n_vocab, const std::vector<int>& history) {
+        const bool greedy = p_.temperature <= 0.0f || p_.top_k == 1;      // sampler.cpp:19: no draw
+        double u = 0.0;
+        if (!greedy) check(fs_rng_next_u(rng_, &u, 1), "fs_rng_next_u");
+        const int64_t h = (int64_t)history.size();
+        if (h > hist_cap_) {
+            (void)hipFree(d_hist_);
+            d_hist_ = nullptr;
+            hist_cap_ = 0;
+            hip(hipMalloc(&d_hist_, (size_t)h * sizeof(int32_t)), "hipMalloc");
+            hist_cap_ = h;
+        }
+        if (h) hip(hipMemcpyAsync(d_hist_, history.data(), (size_t)h * sizeof(int32_t), hipMemcpyHostToDevice, stream_),
+                   "hipMemcpyAsync");
+        host_.off[0] = 0;
+        host_.off[1] = h;
+        host_.u = u;
+        hip(hipMemcpyAsync(&d_small_->off[0], &host_.off[0], 2 * sizeof(int64_t) + sizeof(double),
+                           hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
+        const int64_t ld = ((int64_t)n_vocab + 3) & ~(int64_t)3;
+        check(fs_sample_batch(ctx_, d_logits, ld, 1, n_vocab, h ? d_hist_ : nullptr, &d_small_->off[0], &d_small_->rec,
+                              &d_small_->u, &d_small_->tok, 0, nullptr, nullptr, nullptr, stream_),
+              "fs_sample_batch");
+        int32_t tok = -1;
+        hip(hipMemcpyAsync(&tok, &d_small_->tok, sizeof(tok), hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
+        hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+        int32_t bits = 0;
+        check(fs_device_error(ctx_, stream_, &bits), "fs_device_error");
+        if (bits) throw std::runtime_error("ferro_amd::Sampler: device error bits " + std::to_string(bits));
+        penalised_ = h > 0 && p_.repeat_last_n != 0 &&
+                     (p_.repetition_penalty != 1.0f || p_.frequency_penalty != 0.0f || p_.presence_penalty != 0.0f);
+        return tok;
+    }
+
+    SamplerParams p_;
+    hipStream_t stream_;
+    bool write_back_;
+    bool penalised_ = false;
+    fs_context* ctx_ = nullptr;
+    fs_rng* rng_ = nullptr;
+    fs_row_params rec_{};
+    Small host_{};
+    Small* d_small_ = nullptr;
+    float* d_row_ = nullptr;
+    int64_t row_cap_ = 0;
+    int32_t* d_hist_ = nullptr;
+    int64_t hist_cap_ = 0;
+};
+
+}  // namespace ferro_amd

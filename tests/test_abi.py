@@ -46,6 +46,7 @@ def test_invalid_arguments_rejected_without_device():
     assert L.fs_verify(None, None, 0, 0, 0, 0, None, None, None, None, None, None, -1, None, None, None) \
         == _lib.FS_E_INVALID
     assert L.fs_argmax_batch(None, None, 0, 0, 0, None, None, None, None, None) == _lib.FS_E_INVALID
+    assert L.fs_penalize_batch(None, None, 0, 0, 0, None, None, None, None) == _lib.FS_E_INVALID
     assert L.fs_rng_create(1, None) == _lib.FS_E_INVALID
     h = P()
     assert L.fs_create(ctypes.byref(h)) == _lib.FS_OK

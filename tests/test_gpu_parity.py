@@ -288,3 +288,82 @@ def test_greedy_infinities_and_nan_rows():
     tok = F.argmax_batch(torch.from_numpy(x).cuda()).cpu().numpy()
     want = [O.sample(row, [], O.make_params(temperature=0.0, repetition_penalty=1.0))[0] for row in rows]
     assert list(tok) == want == [0, 0, 0, V - 3, 5000]
+
+
+def test_penalize_in_place_matches_oracle():
+    """fs_penalize_batch leaves each row exactly as ferro's sample() leaves its host row (sampler.cpp:11-18), with
+    the frequency/presence extension, per-row windows and scopes (cfg5 rows: V=262144, H=1024)."""
+    w = W.config5()
+    B = 48
+    x = torch.from_numpy(w.logits[:B].copy()).cuda()
+    p = w.params[:B].copy()
+    p["repeat_last_n"][:8] = [-1, 0, 1, 7, 100, 5000, -1, 64]
+    p["penalty_from"][8:12] = [0, 3, 1000, 2000]
+    off = w.hist_off[:B + 1]
+    F.penalize_batch(x, p, hist=w.hist[:off[-1]], hist_off=off)
+    got = x.cpu().numpy()
+    changed = 0
+    for b in range(B):
+        want = O.penalize(w.logits[b], w.hist[off[b]:off[b + 1]], p[b])
+        changed += int((want != w.logits[b]).sum())
+        np.testing.assert_array_equal(got[b].view(np.uint32), want.view(np.uint32), err_msg=f"row {b}")
+    assert changed > 1000
+    assert F.device_error() == 0
+
+
+def test_sampler_shim_writes_penalised_row_back():
+    """Like ferro::Sampler::sample, the mirror leaves a host (numpy) or device row penalised in place."""
+    rng = np.random.default_rng(3)
+    V = 70000
+    row = (rng.standard_normal(V) * 2).astype(np.float32)
+    hist = list(rng.integers(0, V, 300)) + [5, 5, 5]
+    sp = F.SamplerParams(temperature=0.7, top_k=40, repetition_penalty=1.3, frequency_penalty=0.25, seed=9)
+    want = O.penalize(row, np.asarray(hist, np.int32), F.params_array(sp)[0])
+    assert (want != row).sum() > 250
+    host = row.copy()
+    F.Sampler(sp).sample(host, V, hist)
+    np.testing.assert_array_equal(host, want)
+    dev = torch.from_numpy(row.copy()).cuda()
+    F.Sampler(sp).sample(dev, V, hist)
+    np.testing.assert_array_equal(dev.cpu().numpy(), want)
+    kept = row.copy()
+    F.Sampler(sp, write_back=False).sample(kept, V, hist)
+    np.testing.assert_array_equal(kept, row)
+
+
+def test_cpp_dropin_shim_replays_reference_streams(tmp_path):
+    """include/ferro_sampler.hpp's ferro_amd::Sampler, driven from C++ like lm_cli.cpp:129-130, reproduces the
+    reference's own seeded 40-call streams and leaves every host row penalised in place as ferro does."""
+    import subprocess
+    exe = os.path.join(os.path.dirname(__file__), "cpp", "shim_replay")
+    if not os.path.exists(exe):
+        pytest.fail("tests/cpp/shim_replay is not built (run __graft_entry__.build())")
+    gold = np.load(os.path.join(os.path.dirname(__file__), "golden", "sampler_golden.npz"), allow_pickle=False)
+    params = gold["stream_params"].view(F.PARAMS_DTYPE)
+    X = gold["stream_x"]
+    S, steps, V = X.shape
+    inp, outp = tmp_path / "in.bin", tmp_path / "out.bin"
+    with open(inp, "wb") as f:
+        f.write(np.int64(S).tobytes())
+        for s in range(S):
+            h0 = gold["stream_h0"][s].astype(np.int32)
+            f.write(params[s:s + 1].tobytes())
+            f.write(np.array([gold["stream_seed"][s]], np.uint64).tobytes())
+            f.write(np.array([V, steps, h0.size], np.int64).tobytes())
+            f.write(h0.tobytes())
+            f.write(np.ascontiguousarray(X[s], np.float32).tobytes())
+    say(f"case cpp shim: S={S} steps={steps} V={V}")
+    r = subprocess.run([exe, str(inp), str(outp)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    buf = np.fromfile(outp, np.uint8)
+    pos = 0
+    for s in range(S):
+        tok = buf[pos:pos + 4 * steps].view(np.int32); pos += 4 * steps
+        rows = buf[pos:pos + 4 * steps * V].view(np.float32).reshape(steps, V); pos += 4 * steps * V
+        np.testing.assert_array_equal(tok, gold["stream_tok"][s])
+        hist = list(gold["stream_h0"][s])
+        for i in range(steps):
+            want = O.penalize(X[s, i], np.asarray(hist, np.int32), params[s])
+            np.testing.assert_array_equal(rows[i], want, err_msg=f"stream {s} step {i}")
+            hist.append(int(tok[i]))
+    assert pos == buf.size
