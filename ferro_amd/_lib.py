@@ -19,7 +19,6 @@ FS_E_HIP = -2
 FS_E_NOMEM = -3
 FS_E_DEVICE = -4
 FS_DEVERR_COUNT_OVERFLOW = 1
-FS_DEVERR_LARGE_K = 4
 
 # fs_row_params (include/ferro_sampler.h); field order follows ferro's SamplerParams (src/sampler.h:12-21).
 PARAMS_DTYPE = np.dtype([

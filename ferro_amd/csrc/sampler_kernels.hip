@@ -175,6 +175,16 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, Red& r) {
     __syncthreads();
     return m;
 }
+__device__ __forceinline__ uint64_t block_min_u64(uint64_t v, Red& r) {
+    v = wave_min(v);
+    if (lane_id() == 0) r.u64[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    uint64_t m = r.u64[0];
+#pragma unroll
+    for (int w = 1; w < NWAVES; ++w) m = r.u64[w] < m ? r.u64[w] : m;
+    __syncthreads();
+    return m;
+}
 // max and min in one round
 __device__ __forceinline__ void block_minmax_u32(uint32_t& mn, uint32_t& mx, Red& r) {
     uint32_t a = wave_max(mx), b = wave_min(mn);
@@ -285,7 +295,7 @@ __device__ __forceinline__ int range_shift(uint32_t lo, uint32_t hi) {
 }
 // From a filled histogram, the bin b holding the kk-th largest entry: count(bins > b) < kk <= count(bins >= b).
 // *above = count(bins > b), *atb = count(bins >= b). Requires 1 <= kk <= total.
-__device__ int hist_locate(const uint32_t* bins, int kk, uint32_t* above_out, uint32_t* atb_out, uint32_t* wsum,
+__device__ __forceinline__ int hist_locate(const uint32_t* bins, int kk, uint32_t* above_out, uint32_t* atb_out, uint32_t* wsum,
                            Red& r) {
     constexpr int BPT = NBINS / BLOCK;
     const int tid = threadIdx.x;
@@ -313,7 +323,7 @@ __device__ int hist_locate(const uint32_t* bins, int kk, uint32_t* above_out, ui
 
 // From a filled histogram: the largest bin b such that count(bins >= b) >= k. Returns T = base + (b << shift) and
 // *cnt = count(bins >= b); T = 0 and *cnt = total when the histogram holds fewer than k entries.
-__device__ uint32_t hist_threshold(const uint32_t* bins, uint32_t base, int shift, int k, uint32_t* cnt,
+__device__ __forceinline__ uint32_t hist_threshold(const uint32_t* bins, uint32_t base, int shift, int k, uint32_t* cnt,
                                    uint32_t* wsum, Red& r) {
     constexpr int BPT = NBINS / BLOCK;
     const int tid = threadIdx.x;
@@ -343,7 +353,7 @@ __device__ uint32_t hist_threshold(const uint32_t* bins, uint32_t base, int shif
 // Radix select from the top byte: 8 passes of a 256-bin LDS histogram. each(f) calls f(c) for every candidate the
 // calling thread holds.
 template <class Each>
-__device__ uint64_t radix_kth(Each each, int k, uint32_t* hist256, uint32_t* wsum, Red& r) {
+__device__ __forceinline__ uint64_t radix_kth(Each each, int k, uint32_t* hist256, uint32_t* wsum, Red& r) {
     uint64_t prefix = 0, mask = 0;
     int kk = k;
     const int tid = threadIdx.x;
@@ -372,7 +382,7 @@ __device__ uint64_t radix_kth(Each each, int k, uint32_t* hist256, uint32_t* wsu
 }
 
 // Descending bitonic sort of n (power of two) composites in LDS.
-__device__ void bitonic_desc(uint64_t* a, int n) {
+__device__ __forceinline__ void bitonic_desc(uint64_t* a, int n) {
     for (int size = 2; size <= n; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
             for (int t = threadIdx.x; t < n / 2; t += BLOCK) {
@@ -388,7 +398,7 @@ __device__ void bitonic_desc(uint64_t* a, int n) {
 }
 
 // Rank sort of n <= SMALL distinct composites: out[rank] = in[i] for ranks < k.
-__device__ void rank_sort(const uint64_t* in, int n, uint64_t* out, int k) {
+__device__ __forceinline__ void rank_sort(const uint64_t* in, int n, uint64_t* out, int k) {
     for (int i = threadIdx.x; i < n; i += BLOCK) {
         const uint64_t c = in[i];
         int rank = 0;
@@ -473,11 +483,11 @@ __device__ __forceinline__ RowCtx row_ctx(const Args& a, int row) {
     const int V = a.V;
     rc.greedy = a.mode == MODE_ARGMAX || rc.p.temperature <= 0.0f || rc.p.top_k == 1;
     rc.k = rc.greedy ? 1 : ((rc.p.top_k > 0 && rc.p.top_k < V) ? rc.p.top_k : V);
-    rc.large = rc.k > KMAX;                 // not on the fused select path: reported, token -1
+    rc.large = rc.k > KMAX;                 // not on the segment path: sampled by large_row in the merge kernel
     rc.rep_on = rc.p.repetition_penalty != 1.0f;
     rc.fp_on = rc.p.frequency_penalty != 0.0f || rc.p.presence_penalty != 0.0f;
     rc.len = rc.lenA + rc.lenB;
-    rc.pen = !rc.large && (rc.rep_on || rc.fp_on) && rc.p.repeat_last_n != 0 && rc.len > 0;
+    rc.pen = (rc.rep_on || rc.fp_on) && rc.p.repeat_last_n != 0 && rc.len > 0;
     rc.b = rc.pen ? window_begin(rc.len, rc.p) : rc.len;
     if (rc.b >= rc.len) rc.pen = false;
     return rc;
@@ -574,7 +584,7 @@ __device__ __forceinline__ void gather_window(const Args& a, const RowCtx& rc, i
 // outside [rlo, rhi] ignored; count(value > rhi) == *above < kk <= count(value >= rlo) on entry). On return
 // rlo == rhi is that value, *above = count(value > it), *at = count(value >= it).
 template <class Each>
-__device__ void narrow32(Each each, int kk, uint32_t& rlo, uint32_t& rhi, uint32_t* above, uint32_t* at, Shared& s) {
+__device__ __forceinline__ void narrow32(Each each, int kk, uint32_t& rlo, uint32_t& rhi, uint32_t* above, uint32_t* at, Shared& s) {
     const int tid = threadIdx.x;
     for (int level = 0; level < 4 && rlo != rhi; ++level) {
         const int sh = range_shift(rlo, rhi);
@@ -652,6 +662,317 @@ __device__ __forceinline__ uint64_t compact_exact(int n, int k, Shared& s) {
 }
 
 // The merge of one row: gathers the segments' candidates, selects and sorts the row's top k, then softmax / min-p / top-p / draw (sampler.cpp:25-49).
+// ------------------------------------------------------------------------------------------------ large k
+// Rows that sample with k > KMAX candidates (top_k = 0 or > 2048; ferro's k = n / top_k, sampler.cpp:26) are handled
+// by one workgroup with several streaming passes over the row (it stays in L2 / MALL after the first):
+//   1. the max / min composite and the count of ordered (non-NaN) logits;
+//   2. the k-th composite Xk (key histograms, then ids among ties), unless every logit is a candidate;
+//   3. S = sum of exp((double)(float)(v - mx) / T) over the candidates (sampler.cpp:37-41);
+//   4. min-p: pr = e / S is monotone in the logit, so the kept keys are found by a binary search over keys;
+//   5. top-p and the draw: the first candidate (candidate order) whose cumulative mass reaches a target, by a
+//      descent over fp64 mass histograms of the keys, then the j-th smallest id among the ties at the final key.
+// Sums run in a different order than ferro's sequential loop (probabilities agree to ~1e-15 relative).
+constexpr int LPF = 4;                    // tiles in flight per large-row pass
+constexpr int MB = 256;                   // mass histogram bins
+
+// Issue the loads of the tile at lo of a row that may end inside it (elements >= V read as 0, never used).
+__device__ __forceinline__ void load_tile_masked(float (&x)[TPT], const float* rowp, int lo, int V) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int e = lo + (j * BLOCK + (int)threadIdx.x) * 4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) x[4 * j + q] = e + q < V ? rowp[e + q] : 0.f;
+    }
+}
+
+// One pass over the whole row, LPF tiles in flight, penalties applied (the window ids are in s.ids): g(x, lo) per
+// tile, called by every thread (g may use barriers). Element i of a thread is elem_id(lo, i) when < V.
+template <class G>
+__device__ __forceinline__ void row_tiles(const Args& a, const RowCtx& rc, Shared& s, G g) {
+    const int V = a.V;
+    const float* rowp = a.logits + (int64_t)rc.row * a.ld;
+    const int ntile = (V + TILE - 1) / TILE;
+    const int full = V / TILE;
+    float buf[LPF][TPT];
+#pragma unroll
+    for (int p = 0; p < LPF; ++p) {
+        if (p < full) load_tile(buf[p], rowp, p * TILE);
+        else if (p < ntile) load_tile_masked(buf[p], rowp, p * TILE, V);
+    }
+    for (int t0 = 0; t0 < ntile; t0 += LPF) {
+#pragma unroll
+        for (int p = 0; p < LPF; ++p) {
+            const int t = t0 + p;
+            if (t < ntile) {
+                float x[TPT];
+#pragma unroll
+                for (int i = 0; i < TPT; ++i) x[i] = buf[p][i];
+                const int nt = t + LPF;
+                if (nt < full) load_tile(buf[p], rowp, nt * TILE);
+                else if (nt < ntile) load_tile_masked(buf[p], rowp, nt * TILE, V);
+                if (rc.pen) {
+                    __syncthreads();                 // the previous tile's table reads are done
+                    apply_penalties(x, a, rc, t * TILE, s);
+                }
+                g(x, t * TILE);
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// Per ordered element (non-NaN, id < V): f(x, key, composite).
+template <class F>
+__device__ __forceinline__ void row_elems(const Args& a, const RowCtx& rc, Shared& s, F f) {
+    const int V = a.V;
+    row_tiles(a, rc, s, [&](const float (&x)[TPT], int lo) {
+#pragma unroll
+        for (int i = 0; i < TPT; ++i) {
+            const int e = elem_id(lo, i);
+            if (e < V && x[i] == x[i]) {
+                const uint32_t kq = key_of(x[i]);
+                f(x[i], kq, comp_of(kq, (uint32_t)e));
+            }
+        }
+    });
+}
+
+__device__ __forceinline__ double mass_of(float x, float mx, double Td) {
+    const float d = x - mx;                    // fp32 subtraction, as ferro
+    return exp((double)d / Td);
+}
+
+// The kk-th largest composite among the ordered elements with composite in [lo_c, hi_c) (1 <= kk <= their count;
+// keys of that set span [klo, khi]).
+__device__ __forceinline__ uint64_t large_kth(const Args& a, const RowCtx& rc, Shared& s, int kk, uint64_t lo_c, uint64_t hi_c,
+                              uint32_t klo, uint32_t khi) {
+    uint32_t rlo = klo, rhi = khi, above = 0u, at = 0u;
+    narrow32([&](auto&& f) {
+                 row_elems(a, rc, s, [&](float, uint32_t kq, uint64_t c) { if (c >= lo_c && c < hi_c) f(kq); });
+             },
+             kk, rlo, rhi, &above, &at, s);
+    const uint32_t t = rlo;
+    const uint32_t need = (uint32_t)kk - above;
+    uint32_t lmn = 0xFFFFFFFFu - (uint32_t)(a.V - 1), lmx = 0xFFFFFFFFu;
+    uint32_t ab2 = 0u, at2 = 0u;
+    narrow32([&](auto&& f) {
+                 row_elems(a, rc, s, [&](float, uint32_t kq, uint64_t c) {
+                     if (kq == t && c >= lo_c && c < hi_c) f((uint32_t)c);
+                 });
+             },
+             (int)need, lmn, lmx, &ab2, &at2, s);
+    return ((uint64_t)t << 32) | lmn;
+}
+
+// The j-th smallest id among the ordered elements with key t and composite >= lo_c (their largest id if fewer
+// than j): one id-ordered pass. Returns its composite (0: none).
+__device__ __forceinline__ uint64_t large_pick(const Args& a, const RowCtx& rc, Shared& s, uint32_t t, uint64_t lo_c, uint32_t j) {
+    const int tid = threadIdx.x;
+    const int V = a.V;
+    uint32_t running = 0u;                     // flagged elements in earlier tiles (uniform)
+    uint64_t found = 0ull, last = ~0ull;
+    row_tiles(a, rc, s, [&](const float (&x)[TPT], int lo) {
+        bool f[TPT];
+        uint32_t c0 = 0u, c1 = 0u;
+#pragma unroll
+        for (int i = 0; i < TPT; ++i) {
+            const int e = elem_id(lo, i);
+            f[i] = e < V && x[i] == x[i] && key_of(x[i]) == t && comp_of(t, (uint32_t)e) >= lo_c;
+            if (f[i]) {
+                if (i < 4) ++c0; else ++c1;
+                const uint64_t c = comp_of(t, (uint32_t)e);
+                last = c < last ? c : last;
+            }
+        }
+        uint32_t tot;                          // ids in a tile: float4 0 of every thread, then float4 1
+        const uint32_t pre = block_excl_scan<uint32_t>(c0 | (c1 << 16), s.wsum, &tot);
+        uint32_t r0 = running + (pre & 0xFFFFu);
+        uint32_t r1 = running + (tot & 0xFFFFu) + (pre >> 16);
+#pragma unroll
+        for (int i = 0; i < TPT; ++i) {
+            if (f[i]) {
+                const uint32_t rank = i < 4 ? r0++ : r1++;
+                if (rank + 1u == j) found = comp_of(t, (uint32_t)elem_id(lo, i));
+            }
+        }
+        running += (tot & 0xFFFFu) + (tot >> 16);
+    });
+    found = block_max_u64(found, s.red);
+    last = block_min_u64(last, s.red);
+    (void)tid;
+    return found != 0ull ? found : (last != ~0ull ? last : 0ull);
+}
+
+// The first candidate, in candidate order among the ordered elements with composite >= lo_c, at which the
+// cumulative mass reaches target (0: the total stays below it). Keys of that set span [klo, khi].
+__device__ __forceinline__ uint64_t large_mass_select(const Args& a, const RowCtx& rc, Shared& s, double target, uint64_t lo_c,
+                                      uint32_t klo, uint32_t khi, float mx, double Td) {
+    const int tid = threadIdx.x;
+    const int w = tid / WAVE;
+    double* hd = reinterpret_cast<double*>(s.cand);          // [NWAVES][MB] per-wave masses
+    uint32_t* hc = s.bins();                                  // [MB] counts
+    double above = 0.0;
+    while (klo != khi) {
+        int sh = 0;
+        while (((khi - klo) >> sh) >= (uint32_t)MB) ++sh;
+        for (int i = tid; i < NWAVES * MB; i += BLOCK) hd[i] = 0.0;
+        for (int i = tid; i < MB; i += BLOCK) hc[i] = 0u;
+        __syncthreads();
+        const uint32_t lo = klo, hi = khi;
+        row_elems(a, rc, s, [&](float x, uint32_t kq, uint64_t c) {
+            if (c >= lo_c && kq >= lo && kq <= hi) {
+                const uint32_t b = (kq - lo) >> sh;
+                atomicAdd(&hd[w * MB + b], mass_of(x, mx, Td));
+                atomicAdd(&hc[b], 1u);
+            }
+        });
+        // thread t < MB owns bin MB-1-t: cumulative from the top in a fixed order
+        double m = 0.0;
+        uint32_t cnt = 0u;
+        if (tid < MB) {
+            const int b = MB - 1 - tid;
+#pragma unroll
+            for (int q = 0; q < NWAVES; ++q) m += hd[q * MB + b];
+            cnt = hc[b];
+        }
+        double tot;
+        const double ex = block_excl_scan<double>(m, s.red.f64, &tot);
+        const int hit = (tid < MB && cnt != 0u && above + ex + m >= target) ? tid : 0x7fffffff;
+        const int first = block_min_i32(hit, s.red);
+        if (first == 0x7fffffff) return 0ull;
+        if (tid == first) s.red.dmisc[1] = ex;
+        __syncthreads();
+        above += s.red.dmisc[1];
+        __syncthreads();
+        const uint32_t b = (uint32_t)(MB - 1 - first);
+        const uint64_t nlo = (uint64_t)klo + ((uint64_t)b << sh);
+        const uint64_t nhi = (uint64_t)klo + (((uint64_t)b + 1) << sh) - 1;
+        klo = (uint32_t)nlo;
+        khi = nhi < khi ? (uint32_t)nhi : khi;
+    }
+    const double et = mass_of(val_of(klo), mx, Td);
+    double jd = et > 0.0 ? ceil((target - above) / et) : 1.0;
+    if (!(jd >= 1.0)) jd = 1.0;
+    const uint32_t j = jd > 4294967295.0 ? 0xFFFFFFFFu : (uint32_t)jd;
+    return large_pick(a, rc, s, klo, lo_c, j);
+}
+
+// The whole large-k sample of one row: token, kept count, optional candidate outputs (in chunks of KMAX).
+__device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Shared& s, int& tok_out, int& keep_out) {
+    const int tid = threadIdx.x;
+    const int row = rc.row;
+    const fs_row_params& p = rc.p;
+    if (rc.pen) gather_window(a, rc, 0, a.V, s);
+    // 1. extremes and count of the ordered elements
+    uint64_t cmax = 0ull, cmin = ~0ull;
+    uint32_t nv = 0u;
+    row_elems(a, rc, s, [&](float, uint32_t, uint64_t c) {
+        cmax = c > cmax ? c : cmax;
+        cmin = c < cmin ? c : cmin;
+        ++nv;
+    });
+    cmax = block_max_u64(cmax, s.red);
+    cmin = block_min_u64(cmin, s.red);
+    uint32_t ntot;
+    (void)block_excl_scan<uint32_t>(nv, s.wsum, &ntot);
+    if (ntot == 0u) {                         // every logit NaN: no order to sample from
+        tok_out = 0;
+        keep_out = 0;
+        return;
+    }
+    const uint32_t kmax = comp_key(cmax);
+    const float mx = val_of(kmax);
+    const double Td = (double)p.temperature;
+    // 2. the candidates: composites >= Xk
+    const int keff = (uint32_t)rc.k < ntot ? rc.k : (int)ntot;
+    const uint64_t Xk = (uint32_t)keff == ntot ? cmin : large_kth(a, rc, s, keff, 1ull, ~0ull, comp_key(cmin), kmax);
+    const uint32_t kk = comp_key(Xk);
+    // 3. the softmax denominator
+    double part = 0.0;
+    row_elems(a, rc, s, [&](float x, uint32_t, uint64_t c) { if (c >= Xk) part += mass_of(x, mx, Td); });
+    const double S = block_sum_f64(part, s.red);
+    // 4. min-p: the smallest key whose pr reaches pr[0] * min_p (pr[0] = 1 / S)
+    uint64_t Xkeep = Xk;
+    if (p.min_p > 0.0f) {
+        const double thr = (1.0 / S) * (double)p.min_p;
+        auto ok = [&](uint32_t key) { return mass_of(val_of(key), mx, Td) / S >= thr; };
+        uint64_t Xm;
+        if (!ok(kmax)) {
+            Xm = cmax;                                  // keep >= 1
+        } else {
+            uint32_t lo = kk, hi = kmax;
+            while (lo < hi) {
+                const uint32_t mid = lo + ((hi - lo) >> 1);
+                if (ok(mid)) hi = mid; else lo = mid + 1u;
+            }
+            Xm = (uint64_t)lo << 32;
+        }
+        Xkeep = Xm > Xkeep ? Xm : Xkeep;
+    }
+    // 5. top-p: the crossing candidate is the last one kept (sampler.cpp:44)
+    if (p.top_p < 1.0f) {
+        const uint64_t Xc = large_mass_select(a, rc, s, (double)p.top_p * S, Xk, kk, kmax, mx, Td);
+        if (Xc != 0ull) Xkeep = Xc > Xkeep ? Xc : Xkeep;
+    }
+    // tot over the kept prefix, its size and its last candidate
+    double tpart = 0.0;
+    uint32_t kc = 0u;
+    uint64_t clast = ~0ull;
+    row_elems(a, rc, s, [&](float x, uint32_t, uint64_t c) {
+        if (c >= Xkeep) {
+            tpart += mass_of(x, mx, Td);
+            ++kc;
+            clast = c < clast ? c : clast;
+        }
+    });
+    const double tot = block_sum_f64(tpart, s.red);
+    uint32_t keep;
+    (void)block_excl_scan<uint32_t>(kc, s.wsum, &keep);
+    clast = block_min_u64(clast, s.red);
+    // 6. the draw r = u * tot (sampler.cpp:45-49), in mass units
+    const double u = a.u ? a.u[row] : 0.0;
+    uint64_t pick = large_mass_select(a, rc, s, u * tot + 0.0, Xkeep, comp_key(Xkeep), kmax, mx, Td);
+    if (pick == 0ull) pick = clast;
+    tok_out = (int)comp_id(pick);
+    keep_out = (int)keep;
+    // optional outputs: the first min(k, kcap) candidates in candidate order, KMAX at a time
+    if (a.mode != MODE_VERIFY && a.kcap > 0 && (a.cand_ids || a.cand_probs)) {
+        const int mtot = keff < a.kcap ? keff : a.kcap;
+        uint64_t hi_c = ~0ull;                          // this chunk: composites in [Xc, hi_c)
+        for (int done = 0; done < mtot;) {
+            const int m = mtot - done < KMAX ? mtot - done : KMAX;
+            const uint32_t khi = hi_c == ~0ull ? kmax : comp_key(hi_c - 1ull);
+            const uint64_t Xc = done + m == keff ? Xk : large_kth(a, rc, s, m, Xk, hi_c, kk, khi);
+            if (tid == 0) s.count = 0u;
+            __syncthreads();
+            const int V = a.V;
+            row_tiles(a, rc, s, [&](const float (&x)[TPT], int lo) {
+#pragma unroll
+                for (int i = 0; i < TPT; ++i) {
+                    const int e = elem_id(lo, i);
+                    const bool in = e < V && x[i] == x[i] && comp_of(key_of(x[i]), (uint32_t)e) >= Xc &&
+                                    comp_of(key_of(x[i]), (uint32_t)e) < hi_c;
+                    wave_append(in, in ? comp_of(key_of(x[i]), (uint32_t)e) : 0ull, s.cand, &s.count, CAP);
+                }
+            });
+            int np = 1;
+            while (np < m) np <<= 1;
+            for (int i = m + tid; i < np; i += BLOCK) s.cand[i] = 0ull;
+            __syncthreads();
+            bitonic_desc(s.cand, np);
+            for (int i = tid; i < m; i += BLOCK) {
+                const uint64_t c = s.cand[i];
+                const int64_t o = (int64_t)row * a.kcap + done + i;
+                if (a.cand_ids) a.cand_ids[o] = (int32_t)comp_id(c);
+                if (a.cand_probs) a.cand_probs[o] = mass_of(val_of(comp_key(c)), mx, Td) / S;
+            }
+            __syncthreads();
+            done += m;
+            hi_c = Xc;
+        }
+    }
+}
+
 __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Shared& s) {
     const int tid = threadIdx.x;
     const int row = rc.row;
@@ -663,6 +984,9 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
     int k = rc.k;
     int tok = 0, keep = 1;
 
+    if (rc.large) {
+        large_row(a, rc, s, tok, keep);
+    } else {
     // ---- the row's tail: loads first, then its penalty pass (the same arithmetic as the segment kernel)
     constexpr int TT = TILE / BLOCK;                  // tail logits per thread: element tail_lo + r*BLOCK + tid
     float tx[TT];
@@ -702,11 +1026,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
         __syncthreads();
     }
 
-    if (rc.large) {
-        tok = -1;
-        keep = 0;
-        if (tid == 0) atomicOr(a.err, FS_DEVERR_LARGE_K);
-    } else if (rc.greedy) {
+    if (rc.greedy) {
         uint64_t best = 0;
         for (int c = tid; c < nseg; c += BLOCK) {
             const uint64_t v = *(a.cand + (int64_t)(row * nseg + c) * CAP);
@@ -963,6 +1283,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             }
         }
     }
+    }
     if (a.mode != MODE_VERIFY) {
         if (tid == 0) {
             a.tok[row] = tok;
@@ -1214,7 +1535,9 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(Args a) {
     const int total = a.B * a.nseg;
     for (int item = (int)blockIdx.x; item < total; item += (int)gridDim.x) {
         const int row = item / a.nseg;
-        process_segment(a, row_ctx(a, row), item - row * a.nseg, s);
+        const RowCtx rc = row_ctx(a, row);
+        if (rc.large) continue;                    // the merge kernel samples the whole row
+        process_segment(a, rc, item - row * a.nseg, s);
     }
 }
 

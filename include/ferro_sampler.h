@@ -34,7 +34,6 @@ extern "C" {
 /* Device-side error bits (fs_device_error). */
 #define FS_DEVERR_COUNT_OVERFLOW 1   /* one token occurs > 65535 times in a penalty window */
 #define FS_DEVERR_INTERNAL 2         /* an internal invariant failed (a bug: please report) */
-#define FS_DEVERR_LARGE_K 4          /* a sampled row needs k > 2048 candidates (not yet on the device path): token -1 */
 
 /* Limits. */
 #define FS_MAX_VOCAB (1 << 30)

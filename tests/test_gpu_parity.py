@@ -228,17 +228,53 @@ def test_penalty_windows_and_out_of_range_ids():
     assert nb == 0
 
 
-def test_large_k_reported():
-    V = 10000
-    x = np.random.default_rng(1).standard_normal((2, V)).astype(np.float32)
-    p = W.make_params(2, temperature=1.0, top_k=0, repetition_penalty=1.0)
-    p["top_k"][1] = 40
-    out = F.sample_batch(torch.from_numpy(x).cuda(), p, [0.5, 0.5])
-    tok = out["tok"].cpu().numpy()
-    err = F.device_error()
-    assert tok[0] == -1 and err & F._lib.FS_DEVERR_LARGE_K
-    o = O.sample(x[1], [], p[1], 0.5)[0]
-    assert tok[1] == o
+def test_large_k_full_vocab():
+    """k > 2048 (top_k = 0 is ferro's k = n, sampler.cpp:26): the whole-row path, with every candidate's
+    probability compared (kcap = V) and the draw at the extremes of u."""
+    V = 65536
+    rng = np.random.default_rng(21)
+    B = 10
+    rows = [(rng.standard_normal(V) * 2).astype(np.float32) for _ in range(B)]
+    rows[6] = (np.round(rows[6] * 2) / 2).astype(np.float32)             # heavy ties
+    p = W.make_params(B, temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0)
+    p["temperature"][1], p["top_p"][1] = 0.7, 0.9
+    p["temperature"][2], p["min_p"][2] = 1.5, 0.05
+    p["top_k"][3], p["top_p"][3], p["repetition_penalty"][3] = 5000, 0.95, 1.3
+    p["top_k"][4], p["temperature"][4] = 2049, 0.8
+    p["temperature"][5], p["top_p"][5], p["min_p"][5] = 2.0, 0.5, 0.01
+    p["frequency_penalty"][5], p["presence_penalty"][5], p["repetition_penalty"][5] = 0.3, 0.2, 1.1
+    p["top_k"][7] = V - 1
+    hists = [rng.integers(0, V, 200) for _ in range(B)]
+    u = rng.random(B)
+    u[8], u[9] = 0.0, 1.0 - 2.0 ** -40
+    g, o, nb = check(_case(rows, p, hists, u, "large_k"), kcap=V)
+    say(f"large_k boundary rows: {nb}")
+    assert nb <= 1
+
+
+def test_large_k_serving_rows_mixed_with_topk():
+    """cfg5-shaped rows (V = 262144, H = 1024, frequency / presence) where some rows ask for top_k = 0."""
+    w = W.config5(B=12)
+    w.params["top_k"][::3] = 0
+    w.params["temperature"][::3] = np.maximum(w.params["temperature"][::3], 0.3)
+    g, o, nb = check(w, kcap=16)
+    assert nb == 0
+
+
+def test_verify_large_k():
+    rng = np.random.default_rng(8)
+    S, M, V = 3, 4, 3000
+    x = (rng.standard_normal((S * M, V)) * 3).astype(np.float32)
+    rows = rng.integers(0, V, S * M).astype(np.int32)
+    row_off = np.arange(0, S * M + 1, M, dtype=np.int64)
+    x[np.arange(S * M - 1), rows[1:]] += 30.0                        # drafts the model agrees with
+    p = W.make_params(S, temperature=0.5, top_k=0, top_p=0.9, repetition_penalty=1.0)
+    u = rng.random(S * M)
+    tok, acc = F.verify(torch.from_numpy(x).cuda(), rows, row_off, p, u=u)
+    otok, oacc = O.verify(x, rows, row_off, np.zeros(0, np.int32), np.zeros(S + 1, np.int64), p, u)
+    np.testing.assert_array_equal(tok.cpu().numpy(), otok)
+    np.testing.assert_array_equal(acc.cpu().numpy(), oacc)
+    assert F.device_error() == 0
 
 
 def test_batch_invariance_and_determinism():
