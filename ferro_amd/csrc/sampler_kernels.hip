@@ -54,6 +54,9 @@ constexpr int NBINS = 1 << HBITS;         // threshold histograms
 constexpr int SMALL = 512;                // rank-sort capacity of the merge
 constexpr int MAX_SEGS = 1024;            // segments per row
 constexpr int SPEC = 8;                   // merge gather: loads in flight per thread per round
+constexpr int RBITS = 12;                 // row histogram: bins of the top key bits, shared by a row's segments
+constexpr int RBINS = 1 << RBITS;
+constexpr int RSHIFT = 32 - RBITS;
 constexpr int WIDS = 2048;                // penalty-window ids of one segment kept in LDS (longer: rescanned per tile)
 
 enum Mode : int { MODE_SAMPLE = 0, MODE_ARGMAX = 1, MODE_VERIFY = 2 };
@@ -83,6 +86,7 @@ struct Args {
     uint64_t* cand;                // [B*nseg][CAP]
     uint32_t* meta;                // [B*nseg][2]: lower bound of the k-th key, count
     uint32_t* row_cnt;             // [B] segment completion counters, left at 0
+    uint32_t* rhist;               // [B][RBINS] row histograms of the segments' candidates, left at 0
     uint32_t* stream_cnt;          // [n_streams] verify completion counters, left at 0
     int32_t* err;                  // device error bits
 };
@@ -973,6 +977,78 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
     }
 }
 
+// ------------------------------------------------------------------------------------------------ one-wave finish
+// For k <= 64 once the block has narrowed the row to c1 <= 64 candidates (composites, all distinct, containing the
+// top k): wave 0 ranks them (lane i = candidate i in ferro's order) and runs the softmax / min-p / top-p / draw of
+// sampler.cpp:37-49 with every sum in candidate order, as ferro's sequential loops. LDS accesses of one wave are
+// ordered, so no block barrier is needed: the other waves go straight to the row's epilogue.
+
+__device__ __forceinline__ void wave_finish(const Args& a, const RowCtx& rc, uint64_t* in, int c1, int k,
+                                            double* wbuf, int& tok_out, int& keep_out) {
+    const int lane = lane_id();
+    const int row = rc.row;
+    // rank of this lane's candidate among the c1 (broadcast LDS reads, no cross-lane dependency chain). The loops
+    // below run a fixed 64 steps without conditions (entries past c1 / k are 0) so their loads batch up.
+    const uint64_t mine = lane < c1 ? in[lane] : 0ull;
+    in[lane] = mine;
+    int rank = 0;
+#pragma unroll 16
+    for (int j = 0; j < WAVE; ++j) rank += in[j] > mine ? 1 : 0;
+    uint64_t* sorted = reinterpret_cast<uint64_t*>(wbuf) + WAVE;     // [WAVE] after the [WAVE] doubles
+    if (lane < c1 && rank < k) sorted[rank] = mine;
+    const uint64_t v = lane < k ? sorted[lane] : 0ull;               // candidate `lane` in ferro's order
+    // softmax at temperature, min-p, top-p, draw (sampler.cpp:37-49). Every sum runs in candidate order, as
+    // ferro's loops: each lane reads the values of the lanes before it.
+    const fs_row_params& p = rc.p;
+    const float mx = val_of(comp_key(sorted[0]));
+    const double Td = (double)p.temperature;
+    double e = 0.0;
+    if (lane < k) {
+        const float d = val_of(comp_key(v)) - mx;        // fp32 subtraction, as ferro
+        e = exp((double)d / Td);
+    }
+    wbuf[lane] = e;                                       // lanes >= k hold 0
+    double sum = 0.0;
+#pragma unroll 16
+    for (int j = 0; j < WAVE; ++j) sum += wbuf[j];        // + 0.0 past k: the sum is unchanged
+    const double pr = e / sum;
+    wbuf[lane] = pr;
+    double cum = 0.0, run = 0.0;                          // ferro's running c (sampler.cpp:44,47): every lane
+#pragma unroll 16                                         // walks it and keeps the value at its own index
+    for (int j = 0; j < WAVE; ++j) {
+        run += wbuf[j];
+        cum = j == lane ? run : cum;
+    }
+    int keep_m = k;
+    if (p.min_p > 0.0f) {                                 // keep = 1 + the last index with pr >= pr[0]*min_p
+        const double thr = __shfl(pr, 0) * (double)p.min_p;
+        const uint64_t mm = __ballot(lane < k && pr >= thr);
+        keep_m = mm ? 64 - __clzll((long long)mm) : 1;
+    }
+    int keep = keep_m;
+    if (p.top_p < 1.0f) {
+        const uint64_t mm = __ballot(lane < keep_m && cum >= (double)p.top_p);
+        if (mm) {
+            const int first = __ffsll((unsigned long long)mm) - 1;
+            keep = first + 1 < keep_m ? first + 1 : keep_m;
+        }
+    }
+    const double tot = __shfl(cum, keep - 1);
+    const double u = a.u ? a.u[row] : 0.0;
+    const double rr = u * tot + 0.0;
+    const uint64_t hm = __ballot(lane < keep && rr <= cum);
+    const int at = hm ? __ffsll((unsigned long long)hm) - 1 : keep - 1;
+    tok_out = (int)comp_id(sorted[at]);
+    keep_out = keep;
+    if (a.mode != MODE_VERIFY) {
+        const int m = k < a.kcap ? k : a.kcap;
+        if (lane < m) {
+            if (a.cand_ids) a.cand_ids[(int64_t)row * a.kcap + lane] = (int32_t)comp_id(v);
+            if (a.cand_probs) a.cand_probs[(int64_t)row * a.kcap + lane] = pr;
+        }
+    }
+}
+
 __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Shared& s) {
     const int tid = threadIdx.x;
     const int row = rc.row;
@@ -1125,6 +1201,10 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             if (in) kmax = comp_key(w) > kmax ? comp_key(w) : kmax;
             wave_append(in, w, s.cand, &s.count, CAP);
         }
+        {                                           // the segments' row histogram is spent: leave it at 0
+            uint4* rz = reinterpret_cast<uint4*>(a.rhist + (int64_t)row * RBINS);
+            for (int i = tid; i < RBINS / 4; i += BLOCK) rz[i] = make_uint4(0u, 0u, 0u, 0u);
+        }
         for (int i = tid; i < NBINS; i += BLOCK) s.bins()[i] = 0u;
         uint32_t kmin = L;
         block_minmax_u32(kmin, kmax, s.red);
@@ -1145,6 +1225,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
         const uint32_t T1 = hist_threshold(s.bins(), L, sh, k, &c1, s.wsum, s.red);
         // the c1 >= k candidates with key >= T1 contain the top k: sort them
         uint64_t* top;
+        bool wave_done = false;                   // wave 0 finished the row (c1 <= 64)
         uint64_t* small_in = reinterpret_cast<uint64_t*>(s.bins());
         uint64_t* small_out = small_in + SMALL;
         if (tid == 0) s.count = 0u;
@@ -1163,7 +1244,12 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 }
             }
             __syncthreads();
-            rank_sort(small_in, (int)c1, small_out, k);
+            if (c1 <= (uint32_t)WAVE) {
+                if (tid < WAVE) wave_finish(a, rc, small_in, (int)c1, k, reinterpret_cast<double*>(small_out), tok, keep);
+                wave_done = true;
+            } else {
+                rank_sort(small_in, (int)c1, small_out, k);
+            }
             top = small_out;
         } else {
             // more than SMALL candidates reach T1: reduce to exactly the k >= X in LDS, then sort those
@@ -1201,85 +1287,87 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             top = s.cand;
             c1 = (uint32_t)m;
         }
-        if (c1 < (uint32_t)k) {                       // impossible by construction; never read past the list
-            if (tid == 0) atomicOr(a.err, FS_DEVERR_INTERNAL);
-            k = (int)c1;
-        }
-
-        // ---- softmax at temperature, min-p, top-p, draw (sampler.cpp:37-49), k <= KMAX
-        const fs_row_params& p = rc.p;
-        const int i0 = tid * KPT;
-        const float mx = val_of(comp_key(top[0]));
-        const double Td = (double)p.temperature;
-        double e[KPT];
-        double part = 0.0;
-#pragma unroll
-        for (int q = 0; q < KPT; ++q) {
-            const int i = i0 + q;
-            e[q] = 0.0;
-            if (i < k) {
-                const float d = val_of(comp_key(top[i])) - mx;   // fp32 subtraction, as ferro
-                e[q] = exp((double)d / Td);
-                part += e[q];
+        if (!wave_done) {
+            if (c1 < (uint32_t)k) {                       // impossible by construction; never read past the list
+                if (tid == 0) atomicOr(a.err, FS_DEVERR_INTERNAL);
+                k = (int)c1;
             }
-        }
-        const double sum = block_sum_f64(part, s.red);
-        double pr[KPT];
-#pragma unroll
-        for (int q = 0; q < KPT; ++q) pr[q] = e[q] / sum;
-        // min-p: keep = 1 + the last index with pr >= pr[0]*min_p (at least 1)
-        int keep_m = k;
-        if (p.min_p > 0.0f) {
-            const double thr = (1.0 / sum) * (double)p.min_p;
-            int last = -1;
-#pragma unroll
-            for (int q = 0; q < KPT; ++q)
-                if (i0 + q < k && pr[q] >= thr) last = i0 + q;
-            last = block_max_i32(last, s.red);
-            keep_m = last + 1 > 1 ? last + 1 : 1;
-        }
-        // inclusive prefix of pr in candidate order
-        double c[KPT];
-        double run = 0.0;
-#pragma unroll
-        for (int q = 0; q < KPT; ++q) { run += pr[q]; c[q] = run; }
-        double tot_all;
-        const double off = block_excl_scan<double>(run, s.red.f64, &tot_all);
-#pragma unroll
-        for (int q = 0; q < KPT; ++q) c[q] += off;
-        keep = keep_m;
-        if (p.top_p < 1.0f) {
-            int first = 0x7fffffff;
-#pragma unroll
-            for (int q = 0; q < KPT; ++q)
-                if (i0 + q < keep_m && c[q] >= (double)p.top_p && first == 0x7fffffff) first = i0 + q;
-            first = block_min_i32(first, s.red);
-            if (first != 0x7fffffff) keep = first + 1 < keep_m ? first + 1 : keep_m;
-            if (keep < 1) keep = 1;
-        }
-        // tot = sum of the kept prefix; r = u * tot; the first i with r <= c_i
-#pragma unroll
-        for (int q = 0; q < KPT; ++q)
-            if (i0 + q == keep - 1) s.red.dmisc[0] = c[q];
-        __syncthreads();
-        const double tot = s.red.dmisc[0];
-        const double u = a.u ? a.u[row] : 0.0;
-        const double rr = u * tot + 0.0;
-        int hit = 0x7fffffff;
-#pragma unroll
-        for (int q = 0; q < KPT; ++q)
-            if (i0 + q < keep && rr <= c[q] && hit == 0x7fffffff) hit = i0 + q;
-        hit = block_min_i32(hit, s.red);
-        const int pos = hit == 0x7fffffff ? keep - 1 : hit;
-        tok = (int)comp_id(top[pos]);
-        if (a.mode != MODE_VERIFY) {
-            const int m = k < a.kcap ? k : a.kcap;
-            if (a.cand_ids)
-                for (int i = tid; i < m; i += BLOCK) a.cand_ids[(int64_t)row * a.kcap + i] = (int32_t)comp_id(top[i]);
-            if (a.cand_probs) {
-#pragma unroll
+
+            // ---- softmax at temperature, min-p, top-p, draw (sampler.cpp:37-49), k <= KMAX
+            const fs_row_params& p = rc.p;
+            const int i0 = tid * KPT;
+            const float mx = val_of(comp_key(top[0]));
+            const double Td = (double)p.temperature;
+            double e[KPT];
+            double part = 0.0;
+    #pragma unroll
+            for (int q = 0; q < KPT; ++q) {
+                const int i = i0 + q;
+                e[q] = 0.0;
+                if (i < k) {
+                    const float d = val_of(comp_key(top[i])) - mx;   // fp32 subtraction, as ferro
+                    e[q] = exp((double)d / Td);
+                    part += e[q];
+                }
+            }
+            const double sum = block_sum_f64(part, s.red);
+            double pr[KPT];
+    #pragma unroll
+            for (int q = 0; q < KPT; ++q) pr[q] = e[q] / sum;
+            // min-p: keep = 1 + the last index with pr >= pr[0]*min_p (at least 1)
+            int keep_m = k;
+            if (p.min_p > 0.0f) {
+                const double thr = (1.0 / sum) * (double)p.min_p;
+                int last = -1;
+    #pragma unroll
                 for (int q = 0; q < KPT; ++q)
-                    if (i0 + q < m) a.cand_probs[(int64_t)row * a.kcap + i0 + q] = pr[q];
+                    if (i0 + q < k && pr[q] >= thr) last = i0 + q;
+                last = block_max_i32(last, s.red);
+                keep_m = last + 1 > 1 ? last + 1 : 1;
+            }
+            // inclusive prefix of pr in candidate order
+            double c[KPT];
+            double run = 0.0;
+    #pragma unroll
+            for (int q = 0; q < KPT; ++q) { run += pr[q]; c[q] = run; }
+            double tot_all;
+            const double off = block_excl_scan<double>(run, s.red.f64, &tot_all);
+    #pragma unroll
+            for (int q = 0; q < KPT; ++q) c[q] += off;
+            keep = keep_m;
+            if (p.top_p < 1.0f) {
+                int first = 0x7fffffff;
+    #pragma unroll
+                for (int q = 0; q < KPT; ++q)
+                    if (i0 + q < keep_m && c[q] >= (double)p.top_p && first == 0x7fffffff) first = i0 + q;
+                first = block_min_i32(first, s.red);
+                if (first != 0x7fffffff) keep = first + 1 < keep_m ? first + 1 : keep_m;
+                if (keep < 1) keep = 1;
+            }
+            // tot = sum of the kept prefix; r = u * tot; the first i with r <= c_i
+    #pragma unroll
+            for (int q = 0; q < KPT; ++q)
+                if (i0 + q == keep - 1) s.red.dmisc[0] = c[q];
+            __syncthreads();
+            const double tot = s.red.dmisc[0];
+            const double u = a.u ? a.u[row] : 0.0;
+            const double rr = u * tot + 0.0;
+            int hit = 0x7fffffff;
+    #pragma unroll
+            for (int q = 0; q < KPT; ++q)
+                if (i0 + q < keep && rr <= c[q] && hit == 0x7fffffff) hit = i0 + q;
+            hit = block_min_i32(hit, s.red);
+            const int pos = hit == 0x7fffffff ? keep - 1 : hit;
+            tok = (int)comp_id(top[pos]);
+            if (a.mode != MODE_VERIFY) {
+                const int m = k < a.kcap ? k : a.kcap;
+                if (a.cand_ids)
+                    for (int i = tid; i < m; i += BLOCK) a.cand_ids[(int64_t)row * a.kcap + i] = (int32_t)comp_id(top[i]);
+                if (a.cand_probs) {
+    #pragma unroll
+                    for (int q = 0; q < KPT; ++q)
+                        if (i0 + q < m) a.cand_probs[(int64_t)row * a.kcap + i0 + q] = pr[q];
+                }
             }
         }
     }
@@ -1313,10 +1401,17 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
     __syncthreads();                                   // LDS is reused by the caller's next chunk
 }
 
-// One (row, segment) item: stream the segment's tiles with PF tiles in flight, apply penalties, keep the running
-// candidates (greedy: this lane's first maximum; top-k: every logit whose composite reaches the running exact
-// threshold X, with an fp32 compare as the common-path filter), publish them with agent-scope stores, count the
-// segment done, and merge the row if it was the last.
+// One (row, segment) item: stream the segment's full tiles with PF tiles in flight, apply the penalties, and keep
+// the running candidates.
+//   - greedy rows: each lane's first maximum;
+//   - top-k rows: every logit with key >= tkey, a lower bound of the row's k-th key (at least k logits of the row
+//     reach it). tkey starts from tile 0 (the maxima of >= 2k groups: at least k of the tile's logits reach it) and
+//     is raised from the row histogram (a_rhist): every appended logit counts itself in its row's bin of the top
+//     key bits, every segment reads the counts back asynchronously and takes the highest bin with >= k counted
+//     logits at or above it. Counts only grow, so any snapshot gives a valid bound, and the bound combines the
+//     whole row's evidence instead of one segment's.
+// The segment publishes its candidates with key >= the final tkey (plain stores; the merge kernel runs after this
+// kernel). They include every logit of the row's top k that lies in this segment.
 __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc, int seg, Shared& s) {
     const int tid = threadIdx.x;
     const int V = a.V;
@@ -1334,13 +1429,60 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     }
 
     const int k = rc.k;
-    const bool topk = !rc.greedy && !rc.large;
+    const bool topk = !rc.greedy;      // large rows never reach this function
     float bv = -__builtin_huge_valf(); // greedy: this lane's first maximum (IEEE >: NaN never taken, -0 == +0)
     int bs = -1;                       //         and its slot tile*TPT + i (-1: none)
-    uint64_t X = 1ull;                 // top-k: candidates are the composites >= X (1: every valid logit)
-    float tf = -__builtin_huge_valf(); // fp32 form of X's key: composite >= X <=> x > tf, or x == tf and id <= idX
+    uint32_t tkey = 0u;                // top-k: candidates are the logits with key >= tkey
+    float tf = -__builtin_huge_valf(); //         in fp32: x >= tf (NaN never passes)
+    uint32_t* rh = a.rhist + (int64_t)rc.row * RBINS;
+    uint32_t rcnt = 0u;                // row histogram read in flight: thread t holds bin rb0 + BLOCK-1-t
+    uint32_t rb0 = 0u;
+    bool rpending = false;
     if (tid == 0) s.count = 0u;
     __syncthreads();
+
+    auto raise_key = [&](uint32_t kq) {
+        if (kq > tkey) {
+            tkey = kq;
+            tf = kq > 0x007FFFFFu ? val_of(kq) : -__builtin_huge_valf();   // keys below -inf's are NaN patterns
+        }
+    };
+    auto row_issue = [&]() {
+        rb0 = tkey >> RSHIFT;
+        const uint32_t b = rb0 + (uint32_t)(BLOCK - 1 - tid);
+        rcnt = ld_agent(rh + (b < (uint32_t)RBINS ? b : (uint32_t)RBINS - 1u));   // consumed a tile later
+        rpending = true;
+    };
+    // the highest bin b (>= rb0) with at least k counted logits in bins [b, rb0 + BLOCK - 1]: a row-wide bound
+    auto row_take = [&]() {
+        const uint32_t c = rb0 + (uint32_t)(BLOCK - 1 - tid) < (uint32_t)RBINS ? rcnt : 0u;
+        uint32_t tot;
+        const uint32_t above = block_excl_scan<uint32_t>(c, s.wsum, &tot);   // thread order = descending bins
+        const int hit = (c != 0u && above + c >= (uint32_t)k) ? tid : BLOCK;
+        const int first = block_min_i32(hit, s.red);
+        if (first < BLOCK) raise_key((rb0 + (uint32_t)(BLOCK - 1 - first)) << RSHIFT);
+        rpending = false;
+    };
+    // count the n buffered candidates (all >= tkey) into the row histogram: LDS bins relative to tkey's bin, then
+    // one global atomic per non-empty bin. A candidate beyond the LDS range is counted in a lower bin (still a
+    // valid count for every threshold at or below that bin).
+    auto row_count = [&](int n) {
+        const uint32_t rb = tkey >> RSHIFT;
+        for (int i = tid; i < NBINS; i += BLOCK) s.bins()[i] = 0u;
+        __syncthreads();
+        for (int i = tid; i < n; i += BLOCK) {
+            const uint32_t b = (comp_key(s.cand[i]) >> RSHIFT) - rb;
+            atomicAdd(&s.bins()[b < (uint32_t)NBINS ? b : (uint32_t)NBINS - 1u], 1u);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < NBINS / BLOCK; ++q) {
+            const uint32_t bi = (uint32_t)(q * BLOCK + tid);
+            const uint32_t c = s.bins()[bi];
+            const uint32_t g = rb + bi < (uint32_t)RBINS ? rb + bi : (uint32_t)RBINS - 1u;
+            if (c != 0u) __hip_atomic_fetch_add(rh + g, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    };
 
     // Top-k buffer discipline: after tile 0 the buffer is checked (barrier) only every R tiles, R sized so the
     // expected appends fill at most half the headroom; an overflow (appends past CAP are dropped) is detected at
@@ -1351,8 +1493,8 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         for (int i = 0; i < TPT; ++i)
             if (x[i] > bv) { bv = x[i]; bs = sb + i; }
     };
-    // appends of one tile: the common path is one fp32 compare per logit folded into a wave ballot; ties with the
-    // threshold key are resolved by id and the composites are formed only in slots where some lane passed
+    // appends of one tile: one fp32 compare per logit folded into a wave ballot; composites, LDS slots and row
+    // counts are formed only where some lane passed
     auto topk_append = [&](const float (&x)[TPT], int lo) {
         uint64_t bal[TPT];
         uint64_t any = 0ull;
@@ -1362,18 +1504,10 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
             any |= bal[i];
         }
         if (any == 0ull) return;                     // wave-uniform
-        const uint32_t idX = comp_id(X);
         const int lane = lane_id();
         uint32_t tot = 0u;
 #pragma unroll
-        for (int i = 0; i < TPT; ++i) {
-            if (bal[i] != 0ull) {
-                const bool take = ((bal[i] >> lane) & 1ull) && (x[i] > tf || (uint32_t)elem_id(lo, i) <= idX);
-                bal[i] = __ballot(take);
-                tot += (uint32_t)__popcll(bal[i]);
-            }
-        }
-        if (tot == 0u) return;
+        for (int i = 0; i < TPT; ++i) tot += (uint32_t)__popcll(bal[i]);
         uint32_t base = 0u;
         if (lane == 0) base = atomicAdd(&s.count, tot);
         base = __shfl(base, 0);
@@ -1381,8 +1515,9 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         for (int i = 0; i < TPT; ++i) {
             if (bal[i] != 0ull) {
                 if ((bal[i] >> lane) & 1ull) {
+                    const uint32_t kq = key_of(x[i]);
                     const uint32_t pos = base + mbcnt(bal[i]);
-                    if (pos < (uint32_t)CAP) s.cand[pos] = comp_of(key_of(x[i]), (uint32_t)elem_id(lo, i));
+                    if (pos < (uint32_t)CAP) s.cand[pos] = comp_of(kq, (uint32_t)elem_id(lo, i));
                 }
                 base += (uint32_t)__popcll(bal[i]);
             }
@@ -1393,8 +1528,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         __syncthreads();
         int n = (int)s.count;
         if (n <= CAP && n > CAP - TILE && n > k) {
-            X = compact_exact(n, k, s);
-            tf = val_of(comp_key(X));
+            raise_key(comp_key(compact_exact(n, k, s)));
             n = k;
         }
         return n;
@@ -1410,7 +1544,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
             if (rc.pen) apply_penalties(x, a, rc, lo, s);
             if (rc.greedy) {
                 greedy_update(x, 0);
-            } else if (topk) {
+            } else {
                 if (!safe) {                             // k <= KMAX < TILE
                     // maxima of >= 2k groups of tile 0 (G per thread), histogrammed over their [min, max]:
                     // at least k of the tile's logits reach T0
@@ -1419,14 +1553,14 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     const int per = TPT / G;
                     uint32_t gmin = 0xFFFFFFFFu, gmax = 0u;
                     uint32_t gm = 0u;
-                    bool any = false;
 #pragma unroll
                     for (int i = 0; i < TPT; ++i) {
-                        { const uint32_t kq = key_of(x[i]); gm = kq > gm ? kq : gm; any = true; }
+                        const uint32_t kq = key_of(x[i]);
+                        gm = kq > gm ? kq : gm;
                         if ((i + 1) % per == 0) {
-                            if (any) { gmin = gm < gmin ? gm : gmin; gmax = gm > gmax ? gm : gmax; }
+                            gmin = gm < gmin ? gm : gmin;
+                            gmax = gm > gmax ? gm : gmax;
                             gm = 0u;
-                            any = false;
                         }
                     }
                     for (int i = tid; i < NBINS; i += BLOCK) s.bins()[i] = 0u;
@@ -1434,20 +1568,16 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     const int sh = range_shift(gmin, gmax);
 #pragma unroll
                     for (int i = 0; i < TPT; ++i) {
-                        { const uint32_t kq = key_of(x[i]); gm = kq > gm ? kq : gm; any = true; }
+                        const uint32_t kq = key_of(x[i]);
+                        gm = kq > gm ? kq : gm;
                         if ((i + 1) % per == 0) {
-                            if (any) atomicAdd(&s.bins()[(gm - gmin) >> sh], 1u);
+                            atomicAdd(&s.bins()[(gm - gmin) >> sh], 1u);
                             gm = 0u;
-                            any = false;
                         }
                     }
                     __syncthreads();
                     uint32_t c0;
-                    const uint32_t T0 = hist_threshold(s.bins(), gmin, sh, k, &c0, s.wsum, s.red);
-                    if (T0 != 0u) {
-                        X = (uint64_t)T0 << 32;
-                        tf = val_of(T0);
-                    }
+                    raise_key(hist_threshold(s.bins(), gmin, sh, k, &c0, s.wsum, s.red));
                 }
                 topk_append(x, lo);
             }
@@ -1458,6 +1588,8 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 const int per_tile = n > 32 ? n : 32;
                 R = safe ? 1 : (CAP - n) / (2 * per_tile);
                 if (R < 1) R = 1;
+                if (!safe && !overflow) row_count(n);
+                if (!safe && ntiles < 3) row_issue();    // short segments: read once, taken at the end
             } else if (rc.pen) {
                 __syncthreads();                         // penalty-table reads of this tile are done
             }
@@ -1473,12 +1605,16 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     float (&x)[TPT] = buf[p];
                     if (rc.pen) apply_penalties(x, a, rc, lo, s);
                     if (rc.greedy) greedy_update(x, tt);
-                    else if (topk) topk_append(x, lo);
+                    else topk_append(x, lo);
                     if (tt + PF < ntiles) load_tile(x, rowp, lo + PF * TILE);
                     if (topk) {
                         if (++since >= R || rc.pen) {
                             since = 0;
                             overflow = check() > CAP;   // uniform: every thread read the same count
+                        }
+                        if (!safe && !overflow) {       // read the row bound at tile 1, use it at tile 3
+                            if (rpending && tt == 3) row_take();
+                            if (tt == 1 && !rpending) row_issue();
                         }
                     } else if (rc.pen) {
                         __syncthreads();                 // penalty-table reads of this tile are done
@@ -1489,26 +1625,22 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         if (!topk) break;
         if (!overflow) overflow = check() > CAP;
         if (!overflow) break;
-        // overflow: the buffer lost candidates. X is still a valid bound; stream the segment again in safe mode.
+        // overflow: the buffer lost candidates. tkey is still a valid bound; stream the segment again in safe mode
+        // (its logits are already counted in the row histogram).
         __syncthreads();
         if (tid == 0) s.count = 0u;
+        rpending = false;
 #pragma unroll
         for (int p = 0; p < PF; ++p) load_tile(buf[p], rowp, seg_lo + (p < ntiles ? p : 0) * TILE);
         __syncthreads();
     }
-    if (topk) {
-        // the segment's exact top k (fewer candidates to merge)
-        const int n = (int)s.count;
-        if (n > k) X = compact_exact(n, k, s);
-    }
+    if (topk && rpending) row_take();
 
     // ---- publish this segment's candidates (read by the merge kernel after this kernel completes)
     const int nseg = a.nseg;
     const int slot = rc.row * nseg + seg;
     uint64_t* gout = a.cand + (int64_t)slot * CAP;
-    if (rc.large) {
-        if (tid == 0) { a.meta[2 * slot] = 0u; a.meta[2 * slot + 1] = 0u; }
-    } else if (rc.greedy) {
+    if (rc.greedy) {
         uint64_t best = 0ull;
         if (bs >= 0) best = comp_of(key_of(bv), (uint32_t)elem_id(seg_lo + (bs / TPT) * TILE, bs % TPT));
         best = block_max_u64(best, s.red);
@@ -1518,11 +1650,28 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
             a.meta[2 * slot + 1] = 1u;
         }
     } else {
-        const uint32_t n = s.count;
-        for (uint32_t i = tid; i < n; i += BLOCK) gout[i] = s.cand[i];
+        // the buffered candidates with key >= tkey, in buffer order
+        constexpr int RPT = (CAP + BLOCK - 1) / BLOCK;
+        const int n = (int)s.count;              // <= CAP: no overflow past the checks above
+        uint32_t mine = 0u;
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+            const int i = r * BLOCK + tid;
+            if (i < n && comp_key(s.cand[i]) >= tkey) ++mine;
+        }
+        uint32_t tot;
+        uint32_t pos = block_excl_scan<uint32_t>(mine, s.wsum, &tot);
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+            const int i = r * BLOCK + tid;
+            if (i < n) {
+                const uint64_t c = s.cand[i];
+                if (comp_key(c) >= tkey) gout[pos++] = c;
+            }
+        }
         if (tid == 0) {
-            a.meta[2 * slot] = comp_key(X);        // X's key: at least k of this segment's keys reach it
-            a.meta[2 * slot + 1] = n;
+            a.meta[2 * slot] = tkey;              // at least k of the row's logits reach it
+            a.meta[2 * slot + 1] = tot;
         }
     }
     __syncthreads();                               // LDS is reused by the next item
@@ -1612,6 +1761,7 @@ struct fs_context {
     size_t cand_slots = 0;     // chunk slots of CAP entries
     uint32_t* meta = nullptr;
     uint32_t* row_cnt = nullptr;
+    uint32_t* rhist = nullptr;  // [row_cap][RBINS]
     size_t row_cap = 0;
     uint32_t* stream_cnt = nullptr;
     size_t stream_cap = 0;
@@ -1631,9 +1781,12 @@ int grow(fs_context* c, size_t slots, size_t rows, size_t streams) {
     }
     if (rows > c->row_cap) {
         if (c->row_cnt) (void)hipFree(c->row_cnt);
-        c->row_cnt = nullptr; c->row_cap = 0;
+        if (c->rhist) (void)hipFree(c->rhist);
+        c->row_cnt = nullptr; c->rhist = nullptr; c->row_cap = 0;
         if (hipMalloc(&c->row_cnt, rows * sizeof(uint32_t)) != hipSuccess) return FS_E_NOMEM;
         if (hipMemset(c->row_cnt, 0, rows * sizeof(uint32_t)) != hipSuccess) return FS_E_HIP;
+        if (hipMalloc(&c->rhist, rows * fs::RBINS * sizeof(uint32_t)) != hipSuccess) return FS_E_NOMEM;
+        if (hipMemset(c->rhist, 0, rows * fs::RBINS * sizeof(uint32_t)) != hipSuccess) return FS_E_HIP;
         c->row_cap = rows;
     }
     if (streams > c->stream_cap) {
@@ -1676,7 +1829,8 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
     const int64_t grid = items < 2 * (int64_t)ctx->cus ? items : 2 * (int64_t)ctx->cus;
     int rc = grow(ctx, (size_t)(items + rows), (size_t)rows, (size_t)(streams > 0 ? streams : 1));
     if (rc != FS_OK) return rc;
-    a.cand = ctx->cand; a.meta = ctx->meta; a.row_cnt = ctx->row_cnt; a.stream_cnt = ctx->stream_cnt; a.err = ctx->err;
+    a.cand = ctx->cand; a.meta = ctx->meta; a.row_cnt = ctx->row_cnt; a.rhist = ctx->rhist;
+    a.stream_cnt = ctx->stream_cnt; a.err = ctx->err;
     if (grid > 0) {
         hipLaunchKernelGGL(fs::segment_kernel, dim3((unsigned)grid), dim3(fs::BLOCK), 0, st, a);
         if (hipGetLastError() != hipSuccess) return FS_E_HIP;
@@ -1708,6 +1862,7 @@ int fs_destroy(fs_context* c) {
     (void)hipFree(c->cand);
     (void)hipFree(c->meta);
     (void)hipFree(c->row_cnt);
+    (void)hipFree(c->rhist);
     (void)hipFree(c->stream_cnt);
     (void)hipFree(c->err);
     delete c;
