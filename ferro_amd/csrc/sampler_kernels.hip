@@ -83,6 +83,7 @@ struct Args {
     int mode;
     int nseg;                      // segments per row
     int seg_tiles;                 // tiles per segment
+    int seg_grid;                  // segment workgroups (the merge workgroups follow, one per row)
     uint64_t* cand;                // [B*nseg][CAP]
     uint32_t* meta;                // [B*nseg][2]: lower bound of the k-th key, count
     uint32_t* row_cnt;             // [B] segment completion counters, left at 0
@@ -676,7 +677,7 @@ __device__ __forceinline__ uint64_t compact_exact(int n, int k, Shared& s) {
 //   5. top-p and the draw: the first candidate (candidate order) whose cumulative mass reaches a target, by a
 //      descent over fp64 mass histograms of the keys, then the j-th smallest id among the ties at the final key.
 // Sums run in a different order than ferro's sequential loop (probabilities agree to ~1e-15 relative).
-constexpr int LPF = 4;                    // tiles in flight per large-row pass
+constexpr int LPF = 2;                    // tiles in flight per large-row pass
 constexpr int MB = 256;                   // mass histogram bins
 
 // Issue the loads of the tile at lo of a row that may end inside it (elements >= V read as 0, never used).
@@ -978,10 +979,35 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
 }
 
 // ------------------------------------------------------------------------------------------------ one-wave finish
-// For k <= 64 once the block has narrowed the row to c1 <= 64 candidates (composites, all distinct, containing the
+// For k <= 64 once the block has narrowed the row to c1 <= 128 candidates (composites, all distinct, containing the
 // top k): wave 0 ranks them (lane i = candidate i in ferro's order) and runs the softmax / min-p / top-p / draw of
-// sampler.cpp:37-49 with every sum in candidate order, as ferro's sequential loops. LDS accesses of one wave are
-// ordered, so no block barrier is needed: the other waves go straight to the row's epilogue.
+// sampler.cpp:37-49, the sums as DPP wave scans in candidate order. LDS accesses of one wave are ordered, so no
+// block barrier is needed: the other waves go straight to the row's epilogue.
+
+// DPP moves of a double (two 32-bit halves); lanes without a source read 0 (bound_ctrl off, old = 0).
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROWMASK, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROWMASK, 0xF, false);
+    return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint64_t)(uint32_t)lo));
+}
+// Inclusive wave scan: row_shr 1, 2, 4, 8 inside each 16-lane row, then row_bcast 15 / 31 across rows.
+__device__ __forceinline__ double wave_scan_f64(double v) {
+    v += dpp_f64<0x111, 0xF>(v);
+    v += dpp_f64<0x112, 0xF>(v);
+    v += dpp_f64<0x114, 0xF>(v);
+    v += dpp_f64<0x118, 0xF>(v);
+    v += dpp_f64<0x142, 0xA>(v);
+    v += dpp_f64<0x143, 0xC>(v);
+    return v;
+}
+__device__ __forceinline__ double lane_f64(double v, int lane) {   // lane: wave-uniform
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
 
 __device__ __forceinline__ void wave_finish(const Args& a, const RowCtx& rc, uint64_t* in, int c1, int k,
                                             double* wbuf, int& tok_out, int& keep_out) {
@@ -989,16 +1015,27 @@ __device__ __forceinline__ void wave_finish(const Args& a, const RowCtx& rc, uin
     const int row = rc.row;
     // rank of this lane's candidate among the c1 (broadcast LDS reads, no cross-lane dependency chain). The loops
     // below run a fixed 64 steps without conditions (entries past c1 / k are 0) so their loads batch up.
-    const uint64_t mine = lane < c1 ? in[lane] : 0ull;
-    in[lane] = mine;
-    int rank = 0;
+    const uint64_t m0 = lane < c1 ? in[lane] : 0ull;
+    const uint64_t m1 = lane + WAVE < c1 ? in[lane + WAVE] : 0ull;
+    in[lane] = m0;
+    in[lane + WAVE] = m1;
+    int r0 = 0, r1 = 0;
+    if (c1 <= WAVE) {
 #pragma unroll 16
-    for (int j = 0; j < WAVE; ++j) rank += in[j] > mine ? 1 : 0;
+        for (int j = 0; j < WAVE; ++j) r0 += in[j] > m0 ? 1 : 0;
+    } else {
+#pragma unroll 16
+        for (int j = 0; j < 2 * WAVE; ++j) {
+            const uint64_t o = in[j];
+            r0 += o > m0 ? 1 : 0;
+            r1 += o > m1 ? 1 : 0;
+        }
+    }
     uint64_t* sorted = reinterpret_cast<uint64_t*>(wbuf) + WAVE;     // [WAVE] after the [WAVE] doubles
-    if (lane < c1 && rank < k) sorted[rank] = mine;
+    if (m0 != 0ull && r0 < k) sorted[r0] = m0;
+    if (m1 != 0ull && r1 < k) sorted[r1] = m1;
     const uint64_t v = lane < k ? sorted[lane] : 0ull;               // candidate `lane` in ferro's order
-    // softmax at temperature, min-p, top-p, draw (sampler.cpp:37-49). Every sum runs in candidate order, as
-    // ferro's loops: each lane reads the values of the lanes before it.
+    // softmax at temperature, min-p, top-p, draw (sampler.cpp:37-49)
     const fs_row_params& p = rc.p;
     const float mx = val_of(comp_key(sorted[0]));
     const double Td = (double)p.temperature;
@@ -1007,21 +1044,12 @@ __device__ __forceinline__ void wave_finish(const Args& a, const RowCtx& rc, uin
         const float d = val_of(comp_key(v)) - mx;        // fp32 subtraction, as ferro
         e = exp((double)d / Td);
     }
-    wbuf[lane] = e;                                       // lanes >= k hold 0
-    double sum = 0.0;
-#pragma unroll 16
-    for (int j = 0; j < WAVE; ++j) sum += wbuf[j];        // + 0.0 past k: the sum is unchanged
+    const double sum = lane_f64(wave_scan_f64(e), WAVE - 1);   // lanes >= k hold 0
     const double pr = e / sum;
-    wbuf[lane] = pr;
-    double cum = 0.0, run = 0.0;                          // ferro's running c (sampler.cpp:44,47): every lane
-#pragma unroll 16                                         // walks it and keeps the value at its own index
-    for (int j = 0; j < WAVE; ++j) {
-        run += wbuf[j];
-        cum = j == lane ? run : cum;
-    }
+    const double cum = wave_scan_f64(pr);                 // ferro's running c (sampler.cpp:44,47)
     int keep_m = k;
     if (p.min_p > 0.0f) {                                 // keep = 1 + the last index with pr >= pr[0]*min_p
-        const double thr = __shfl(pr, 0) * (double)p.min_p;
+        const double thr = lane_f64(pr, 0) * (double)p.min_p;
         const uint64_t mm = __ballot(lane < k && pr >= thr);
         keep_m = mm ? 64 - __clzll((long long)mm) : 1;
     }
@@ -1033,7 +1061,7 @@ __device__ __forceinline__ void wave_finish(const Args& a, const RowCtx& rc, uin
             keep = first + 1 < keep_m ? first + 1 : keep_m;
         }
     }
-    const double tot = __shfl(cum, keep - 1);
+    const double tot = lane_f64(cum, keep - 1);
     const double u = a.u ? a.u[row] : 0.0;
     const double rr = u * tot + 0.0;
     const uint64_t hm = __ballot(lane < keep && rr <= cum);
@@ -1049,14 +1077,42 @@ __device__ __forceinline__ void wave_finish(const Args& a, const RowCtx& rc, uin
     }
 }
 
-__device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Shared& s) {
+// The segment lists of a row, loaded at the merge kernel's entry (before the row's parameters, whose latency they
+// overlap): tps threads per list, each holding the list's meta and SPEC entries r_me, r_me + tps, ... (entries past
+// the list's count are stale and masked once the counts are known).
+struct Pre {
+    int tps, c_me, r_me;
+    bool act;
+    uint32_t t0m, cnm;
+    uint64_t v[SPEC];
+};
+
+__device__ __forceinline__ void prefetch_lists(const Args& a, int row, Pre& pre) {
+    const int nseg = a.nseg;
+    const int tid = threadIdx.x;
+    pre.tps = nseg > 0 ? BLOCK / nseg : 0;    // >= 1: the host keeps nseg < BLOCK
+    pre.c_me = nseg > 0 ? tid % nseg : 0;
+    pre.r_me = nseg > 0 ? tid / nseg : 0;
+    pre.act = nseg > 0 && pre.r_me < pre.tps;
+    const int64_t slot = (int64_t)row * nseg + pre.c_me;
+    const uint64_t* lst = a.cand + slot * CAP;
+    pre.t0m = 0u;
+    pre.cnm = 0u;
+    if (nseg > 0) {
+        pre.t0m = ld_agent(&a.meta[2 * slot]);
+        pre.cnm = ld_agent(&a.meta[2 * slot + 1]);
+    }
+#pragma unroll
+    for (int q = 0; q < SPEC; ++q) pre.v[q] = nseg > 0 ? ld_agent(lst + (pre.act ? pre.r_me + q * pre.tps : 0)) : 0ull;
+}
+
+__device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Shared& s, const Pre& pre) {
     const int tid = threadIdx.x;
     const int row = rc.row;
     const int V = a.V;
     const int nseg = a.nseg;
     const int tail_lo = (V / TILE) * TILE;            // the segment kernel streamed [0, tail_lo)
     const int ntail = V - tail_lo;                    // < TILE logits left for this kernel
-    const int tslot = a.B * nseg + row;               // workspace slot of this row's tail list
     int k = rc.k;
     int tok = 0, keep = 1;
 
@@ -1103,11 +1159,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
     }
 
     if (rc.greedy) {
-        uint64_t best = 0;
-        for (int c = tid; c < nseg; c += BLOCK) {
-            const uint64_t v = *(a.cand + (int64_t)(row * nseg + c) * CAP);
-            best = v > best ? v : best;
-        }
+        uint64_t best = (pre.act && pre.r_me == 0) ? pre.v[0] : 0ull;    // each segment's best (entry 0)
 #pragma unroll
         for (int r = 0; r < TT; ++r) {                // > -inf, as the segment kernel's IEEE compare from -inf:
             const int e = tail_lo + r * BLOCK + tid;  // NaN and -inf are never taken
@@ -1125,7 +1177,13 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             if (a.cand_probs && a.kcap > 0) a.cand_probs[(int64_t)row * a.kcap] = 1.0;
         }
     } else {
-        // ---- the tail's own top k becomes one more list (agent-scope stores, drained, then read back below)
+        // ---- the tail's own top k becomes one more list, kept in LDS at the top of the candidate buffer
+        // (tl[0, nt); ttkey bounds the k-th key if the tail holds at least k candidates); the gather below then
+        // fills at most gcap entries
+        uint64_t* tl = s.cand + (CAP - KMAX);
+        const uint32_t gcap = ntail > 0 ? (uint32_t)(CAP - KMAX) : (uint32_t)CAP;
+        int nt = 0;
+        uint32_t ttkey = 0u;
         if (ntail > 0) {
             if (tid == 0) s.count = 0u;
             __syncthreads();
@@ -1136,70 +1194,87 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 wave_append(in, in ? comp_of(key_of(tx[r]), (uint32_t)e) : 0ull, s.cand, &s.count, CAP);
             }
             __syncthreads();
-            int nt = (int)s.count;
-            uint32_t tkey = 0u;                       // fewer than k: 0 bounds nothing
+            nt = (int)s.count;
             if (nt > k) {
-                tkey = comp_key(compact_exact(nt, k, s));
+                ttkey = comp_key(compact_exact(nt, k, s));
                 nt = k;
             }
-            uint64_t* tout = a.cand + (int64_t)tslot * CAP;
-            for (int i = tid; i < nt; i += BLOCK) st_agent(tout + i, s.cand[i]);
-            if (tid == 0) {
-                st_agent(&a.meta[2 * tslot], tkey);
-                st_agent(&a.meta[2 * tslot + 1], (uint32_t)nt);
-            }
-            vm_drain();
+            for (int i = tid; i < nt; i += BLOCK) tl[i] = s.cand[i];   // nt <= KMAX: no overlap
             __syncthreads();
         }
-        // One memory round trip: every list's meta and the first SPEC*tps entries of it, tps threads per list
-        // (entries past a list's count are stale and masked once the counts are in). Lists 0..nseg-1 are the
-        // segments', list nseg (if any) the tail's.
-        const int nch = nseg + (ntail > 0 ? 1 : 0);  // >= 1
-        auto slot_of = [&](int c) -> int64_t { return c < nseg ? (int64_t)row * nseg + c : (int64_t)tslot; };
-        const int tps = BLOCK / nch;                 // >= 1: the host keeps nseg < BLOCK
-        const int c_me = tid % nch;
-        const int r_me = tid / nch;
-        const bool act = r_me < tps;
-        const uint64_t* lst = a.cand + slot_of(c_me) * CAP;
-        const uint32_t t0m = ld_agent(&a.meta[2 * slot_of(c_me)]);
-        const uint32_t cnm = ld_agent(&a.meta[2 * slot_of(c_me) + 1]);
-        uint64_t v[SPEC];
-#pragma unroll
-        for (int q = 0; q < SPEC; ++q) v[q] = ld_agent(lst + (act ? r_me + q * tps : 0));
+        // The segment lists (prefetched at kernel entry) and the tail list: L = the largest of their k-th key
+        // bounds bounds the row's k-th key from below.
+        const int tps = pre.tps, c_me = pre.c_me, r_me = pre.r_me;
+        const bool act = pre.act;
+        const uint32_t cnm = pre.cnm;
+        const uint64_t* lst = a.cand + ((int64_t)row * nseg + c_me) * CAP;
         if (act && r_me == 0) s.off[c_me] = cnm;
-        const uint32_t L = (uint32_t)block_max_u64(act ? t0m : 0u, s.red);   // a lower bound of the k-th key
-        // flat offsets of the lists (used when the candidates >= L overflow LDS)
-        uint32_t total;
-        {
-            const uint32_t mine = tid < nch ? s.off[tid] : 0u;
+        if (tid == 0) s.count = 0u;
+        // one reduction: L (bit 63 set when a list is longer than its prefetched window, or the lists' total may
+        // overflow LDS: then the flat offsets below are needed)
+        const bool longl = act && r_me == 0 && cnm > (uint32_t)(SPEC * tps);
+        const uint64_t red = block_max_u64(((uint64_t)(longl ? 1u : 0u) << 63) | (act ? pre.t0m : 0u), s.red);
+        uint32_t L = (uint32_t)red;
+        L = ttkey > L ? ttkey : L;
+        const bool need_off = (red >> 63) != 0ull || (uint32_t)nseg * (uint32_t)(SPEC * tps) + (uint32_t)nt > (uint32_t)CAP;
+        // flat offsets of the segment lists (used when the candidates >= L overflow LDS)
+        uint32_t total = 0u;
+        if (need_off) {
+            const uint32_t mine = tid < nseg ? s.off[tid] : 0u;
             const uint32_t o = block_excl_scan<uint32_t>(mine, s.wsum, &total);
-            if (tid < nch) s.off[tid] = o;
-            if (tid == 0) { s.off[nch] = total; s.count = 0u; }
+            if (tid < nseg) s.off[tid] = o;
+            if (tid == 0) s.off[nseg] = total;
             __syncthreads();
         }
         auto fetch = [&](uint32_t f) -> uint64_t {          // flat index -> candidate (0 past the end)
             const uint32_t g = f < total ? f : total - 1u;  // branch-free: the load is always issued in bounds
-            int c0 = 0, c1 = nch;                            // largest c with off[c] <= g
+            int c0 = 0, c1 = nseg;                           // largest c with off[c] <= g
             while (c1 - c0 > 1) {
                 const int m = (c0 + c1) >> 1;
                 if (s.off[m] <= g) c0 = m; else c1 = m;
             }
-            const uint64_t w = ld_agent(a.cand + slot_of(c0) * CAP + (g - s.off[c0]));
+            const uint64_t w = ld_agent(a.cand + ((int64_t)row * nseg + c0) * CAP + (g - s.off[c0]));
             return f < total ? w : 0ull;
         };
         // gather the candidates >= L into LDS (counted past CAP), tracking their max key
         uint32_t kmax = L;
+        for (int i0 = 0; i0 < nt; i0 += BLOCK) {
+            const int i = i0 + tid;
+            const uint64_t w = i < nt ? tl[i] : 0ull;
+            const bool in = w != 0 && comp_key(w) >= L;
+            if (in) kmax = comp_key(w) > kmax ? comp_key(w) : kmax;
+            wave_append(in, w, s.cand, &s.count, gcap);
+        }
+        {                                           // the prefetched entries: one LDS atomic per wave
+            uint64_t bal[SPEC];
+            uint32_t tot = 0u;
 #pragma unroll
-        for (int q = 0; q < SPEC; ++q) {
-            const bool in = act && (uint32_t)(r_me + q * tps) < cnm && v[q] != 0 && comp_key(v[q]) >= L;
-            if (in) kmax = comp_key(v[q]) > kmax ? comp_key(v[q]) : kmax;
-            wave_append(in, v[q], s.cand, &s.count, CAP);
+            for (int q = 0; q < SPEC; ++q) {
+                const uint64_t w = pre.v[q];
+                const bool in = act && (uint32_t)(r_me + q * tps) < cnm && w != 0 && comp_key(w) >= L;
+                if (in) kmax = comp_key(w) > kmax ? comp_key(w) : kmax;
+                bal[q] = __ballot(in);
+                tot += (uint32_t)__popcll(bal[q]);
+            }
+            if (tot != 0u) {
+                uint32_t base = 0u;
+                if (lane_id() == 0) base = atomicAdd(&s.count, tot);
+                base = __shfl(base, 0);
+#pragma unroll
+                for (int q = 0; q < SPEC; ++q) {
+                    if ((bal[q] >> lane_id()) & 1ull) {
+                        const uint32_t pos = base + mbcnt(bal[q]);
+                        if (pos < gcap) s.cand[pos] = pre.v[q];
+                    }
+                    base += (uint32_t)__popcll(bal[q]);
+                }
+            }
         }
         for (uint32_t i = (uint32_t)(r_me + SPEC * tps); act && i < cnm; i += (uint32_t)tps) {   // long lists
             const uint64_t w = ld_agent(lst + i);
             const bool in = w != 0 && comp_key(w) >= L;
             if (in) kmax = comp_key(w) > kmax ? comp_key(w) : kmax;
-            wave_append(in, w, s.cand, &s.count, CAP);
+            wave_append(in, w, s.cand, &s.count, gcap);
         }
         {                                           // the segments' row histogram is spent: leave it at 0
             uint4* rz = reinterpret_cast<uint4*>(a.rhist + (int64_t)row * RBINS);
@@ -1209,7 +1284,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
         uint32_t kmin = L;
         block_minmax_u32(kmin, kmax, s.red);
         const uint32_t n = s.count;
-        const bool in_lds = n <= (uint32_t)CAP;
+        const bool in_lds = n <= gcap;
         // T1: tight threshold from a histogram of the candidates' keys over [L, kmax]
         const int sh = range_shift(L, kmax);
         if (in_lds) {
@@ -1219,13 +1294,17 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 const uint64_t c = fetch(f);
                 if (c != 0 && comp_key(c) >= L) atomicAdd(&s.bins()[(comp_key(c) - L) >> sh], 1u);
             }
+            for (int i = tid; i < nt; i += BLOCK) {
+                const uint64_t c = tl[i];
+                if (comp_key(c) >= L) atomicAdd(&s.bins()[(comp_key(c) - L) >> sh], 1u);
+            }
         }
         __syncthreads();
         uint32_t c1;
         const uint32_t T1 = hist_threshold(s.bins(), L, sh, k, &c1, s.wsum, s.red);
         // the c1 >= k candidates with key >= T1 contain the top k: sort them
         uint64_t* top;
-        bool wave_done = false;                   // wave 0 finished the row (c1 <= 64)
+        bool wave_done = false;                   // wave 0 finished the row (k <= 64, c1 <= 128)
         uint64_t* small_in = reinterpret_cast<uint64_t*>(s.bins());
         uint64_t* small_out = small_in + SMALL;
         if (tid == 0) s.count = 0u;
@@ -1242,9 +1321,13 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                     const uint64_t c = fetch(f0 + tid);
                     wave_append(c != 0 && comp_key(c) >= T1, c, small_in, &s.count, SMALL);
                 }
+                for (int i0 = 0; i0 < nt; i0 += BLOCK) {
+                    const uint64_t c = i0 + tid < nt ? tl[i0 + tid] : 0ull;
+                    wave_append(c != 0 && comp_key(c) >= T1, c, small_in, &s.count, SMALL);
+                }
             }
             __syncthreads();
-            if (c1 <= (uint32_t)WAVE) {
+            if (c1 <= (uint32_t)(2 * WAVE) && k <= WAVE) {
                 if (tid < WAVE) wave_finish(a, rc, small_in, (int)c1, k, reinterpret_cast<double*>(small_out), tok, keep);
                 wave_done = true;
             } else {
@@ -1256,13 +1339,14 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             int m = (int)n;
             if (!in_lds) {
                 uint64_t X = 0;                         // threshold for a gather of <= CAP entries
-                if (c1 > (uint32_t)CAP) {
+                if (c1 > gcap) {
                     X = radix_kth(
                         [&](auto&& f) {
                             for (uint32_t f0 = tid; f0 < total; f0 += BLOCK) {
                                 const uint64_t c = fetch(f0);
                                 f(c != 0 && comp_key(c) >= L ? c : 0ull);
                             }
+                            for (int i = tid; i < nt; i += BLOCK) f(comp_key(tl[i]) >= L ? tl[i] : 0ull);
                         },
                         k, s.bins(), s.wsum, s.red);
                 }
@@ -1270,7 +1354,11 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 __syncthreads();
                 for (uint32_t f0 = 0; f0 < total; f0 += BLOCK) {
                     const uint64_t c = fetch(f0 + tid);
-                    wave_append(c != 0 && comp_key(c) >= T1 && c >= X, c, s.cand, &s.count, CAP);
+                    wave_append(c != 0 && comp_key(c) >= T1 && c >= X, c, s.cand, &s.count, gcap);
+                }
+                for (int i0 = 0; i0 < nt; i0 += BLOCK) {
+                    const uint64_t c = i0 + tid < nt ? tl[i0 + tid] : 0ull;
+                    wave_append(c != 0 && comp_key(c) >= T1 && c >= X, c, s.cand, &s.count, gcap);
                 }
                 __syncthreads();
                 m = (int)s.count;
@@ -1677,7 +1765,8 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     __syncthreads();                               // LDS is reused by the next item
 }
 
-// Segment kernel (persistent): workgroup g handles items g, g+G, ... (item = row*nseg + segment, row-major).
+// Segment kernel (persistent): workgroup g handles items g, g+G, ... (item = row*nseg + segment, row-major; rows
+// sampled with k > KMAX are left to the merge kernel).
 __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(Args a) {
     static_assert(KMAX + TILE <= CAP, "a compacted buffer plus one tile must fit the candidate buffer");
     __shared__ __align__(16) Shared s;
@@ -1690,11 +1779,15 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(Args a) {
     }
 }
 
-// Merge kernel: one workgroup per row, after the segment kernel has published every segment's candidates.
+// Merge kernel: one workgroup per row, after the segment kernel. The segment lists are requested first, so their
+// latency overlaps the row's parameter loads.
 __global__ __launch_bounds__(BLOCK) void merge_kernel(Args a) {
     static_assert(2 * SMALL * 8 <= NBINS * 4, "rank-sort buffers alias the histogram");
     __shared__ __align__(16) Shared s;
-    merge_row(a, row_ctx(a, (int)blockIdx.x), s);
+    const int row = (int)blockIdx.x;
+    Pre pre;
+    prefetch_lists(a, row, pre);
+    merge_row(a, row_ctx(a, row), s, pre);
 }
 
 // In-place penalty pass (fs_penalize_batch): ferro's sample() leaves its host row penalised (sampler.cpp:11-18),
@@ -1826,13 +1919,14 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
     if (a.nseg > fs::MAX_SEGS) return FS_E_INVALID;
     const int64_t items = rows * a.nseg;
     if (items > 0x7fffffff) return FS_E_INVALID;
-    const int64_t grid = items < 2 * (int64_t)ctx->cus ? items : 2 * (int64_t)ctx->cus;
+    const int64_t seg_grid = items < 2 * (int64_t)ctx->cus ? items : 2 * (int64_t)ctx->cus;
+    a.seg_grid = (int)seg_grid;
     int rc = grow(ctx, (size_t)(items + rows), (size_t)rows, (size_t)(streams > 0 ? streams : 1));
     if (rc != FS_OK) return rc;
     a.cand = ctx->cand; a.meta = ctx->meta; a.row_cnt = ctx->row_cnt; a.rhist = ctx->rhist;
     a.stream_cnt = ctx->stream_cnt; a.err = ctx->err;
-    if (grid > 0) {
-        hipLaunchKernelGGL(fs::segment_kernel, dim3((unsigned)grid), dim3(fs::BLOCK), 0, st, a);
+    if (seg_grid > 0) {
+        hipLaunchKernelGGL(fs::segment_kernel, dim3((unsigned)seg_grid), dim3(fs::BLOCK), 0, st, a);
         if (hipGetLastError() != hipSuccess) return FS_E_HIP;
     }
     hipLaunchKernelGGL(fs::merge_kernel, dim3((unsigned)rows), dim3(fs::BLOCK), 0, st, a);
