@@ -1508,13 +1508,54 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     const int ntiles = left < a.seg_tiles ? left : a.seg_tiles;    // >= 1
     const float* rowp = a.logits + (int64_t)rc.row * a.ld;
 
+    // the first window ids are requested before the tiles (memory returns in order: the bitmap below is then built
+    // while the tiles are still in flight)
+    constexpr int WPF = 2;
+    int wid[WPF];
+#pragma unroll
+    for (int q = 0; q < WPF; ++q) {
+        const int64_t i = rc.b + q * BLOCK + tid;
+        wid[q] = (rc.pen && i < rc.len) ? hist_at(a, rc, i) : -1;
+    }
     float buf[PF][TPT];
 #pragma unroll
     for (int p = 0; p < PF; ++p) load_tile(buf[p], rowp, seg_lo + (p < ntiles ? p : 0) * TILE);
-    if (rc.pen) {
-        const int seg_hi = seg_lo + ntiles * TILE;
-        gather_window(a, rc, seg_lo, seg_hi, s);
+    // Penalties. With a repetition penalty alone (sampler.cpp:11-18) only membership in the window matters: an
+    // exact bitmap of the segment's window ids (bmp, in the merge's offset array, unused by this kernel) is built
+    // once, and a thread's four consecutive logits share one bitmap word, so each tile costs two LDS reads and no
+    // barrier. Frequency / presence penalties need counts: a per-tile count table (apply_penalties).
+    const int seg_hi = seg_lo + ntiles * TILE;
+    const bool fastpen = rc.pen && rc.rep_on && !rc.fp_on && seg_hi - seg_lo <= 32 * (MAX_SEGS + 1);
+    const bool slowpen = rc.pen && !fastpen;
+    uint32_t* bmp = s.off;
+    const float rp = rc.p.repetition_penalty;
+    if (slowpen) gather_window(a, rc, seg_lo, seg_hi, s);
+    if (fastpen) {
+        for (int i = tid; i <= MAX_SEGS; i += BLOCK) bmp[i] = 0u;
+        __syncthreads();
+        auto mark = [&](int id) {
+            const uint32_t rel = (uint32_t)(id - seg_lo);
+            if (id >= seg_lo && id < seg_hi) atomicOr(&bmp[rel >> 5], 1u << (rel & 31u));
+        };
+#pragma unroll
+        for (int q = 0; q < WPF; ++q) mark(wid[q]);
+        for (int64_t i = rc.b + WPF * BLOCK + tid; i < rc.len; i += BLOCK) mark(hist_at(a, rc, i));
+        __syncthreads();
     }
+    auto bitmap_pen = [&](float (&x)[TPT], int lo) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const uint32_t rel = (uint32_t)(lo - seg_lo) + (uint32_t)(j * BLOCK + tid) * 4u;
+            const uint32_t nib = (bmp[rel >> 5] >> (rel & 31u)) & 0xFu;
+            if (nib != 0u) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float l = x[4 * j + q];
+                    if ((nib >> q) & 1u) x[4 * j + q] = l > 0.0f ? __fdiv_rn(l, rp) : __fmul_rn(l, rp);
+                }
+            }
+        }
+    };
 
     const int k = rc.k;
     const bool topk = !rc.greedy;      // large rows never reach this function
@@ -1629,7 +1670,8 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         {
             float (&x)[TPT] = buf[0];
             const int lo = seg_lo;
-            if (rc.pen) apply_penalties(x, a, rc, lo, s);
+            if (slowpen) apply_penalties(x, a, rc, lo, s);
+            if (fastpen) bitmap_pen(x, lo);
             if (rc.greedy) {
                 greedy_update(x, 0);
             } else {
@@ -1678,7 +1720,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 if (R < 1) R = 1;
                 if (!safe && !overflow) row_count(n);
                 if (!safe && ntiles < 3) row_issue();    // short segments: read once, taken at the end
-            } else if (rc.pen) {
+            } else if (slowpen) {
                 __syncthreads();                         // penalty-table reads of this tile are done
             }
         }
@@ -1691,12 +1733,13 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 if (tt >= 1 && tt < ntiles && !overflow) {
                     const int lo = seg_lo + tt * TILE;
                     float (&x)[TPT] = buf[p];
-                    if (rc.pen) apply_penalties(x, a, rc, lo, s);
+                    if (slowpen) apply_penalties(x, a, rc, lo, s);
+                    if (fastpen) bitmap_pen(x, lo);
                     if (rc.greedy) greedy_update(x, tt);
                     else topk_append(x, lo);
                     if (tt + PF < ntiles) load_tile(x, rowp, lo + PF * TILE);
                     if (topk) {
-                        if (++since >= R || rc.pen) {
+                        if (++since >= R || slowpen) {
                             since = 0;
                             overflow = check() > CAP;   // uniform: every thread read the same count
                         }
@@ -1704,7 +1747,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                             if (rpending && tt == 3) row_take();
                             if (tt == 1 && !rpending) row_issue();
                         }
-                    } else if (rc.pen) {
+                    } else if (slowpen) {
                         __syncthreads();                 // penalty-table reads of this tile are done
                     }
                 }
