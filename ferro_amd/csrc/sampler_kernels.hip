@@ -980,9 +980,9 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
 
 // ------------------------------------------------------------------------------------------------ one-wave finish
 // For k <= 64 once the block has narrowed the row to c1 <= 128 candidates (composites, all distinct, containing the
-// top k): wave 0 ranks them (lane i = candidate i in ferro's order) and runs the softmax / min-p / top-p / draw of
-// sampler.cpp:37-49, the sums as DPP wave scans in candidate order. LDS accesses of one wave are ordered, so no
-// block barrier is needed: the other waves go straight to the row's epilogue.
+// top k) and ranked them (block_ranks): wave 0 places them (lane i = candidate i in ferro's order) and runs the
+// softmax / min-p / top-p / draw of sampler.cpp:37-49, the sums as DPP wave scans in candidate order. LDS accesses
+// of one wave are ordered, so no further block barrier is needed: the other waves go straight to the epilogue.
 
 // DPP moves of a double (two 32-bit halves); lanes without a source read 0 (bound_ctrl off, old = 0).
 template <int CTRL, int ROWMASK>
@@ -1009,27 +1009,34 @@ __device__ __forceinline__ double lane_f64(double v, int lane) {   // lane: wave
     return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
-__device__ __forceinline__ void wave_finish(const Args& a, const RowCtx& rc, uint64_t* in, int c1, int k,
-                                            double* wbuf, int& tok_out, int& keep_out) {
+// Ranks of the c1 <= 128 candidates in[0, c1) (whole block, one barrier): thread t compares candidate t % 128
+// with a quarter of the list; rk[q*128 + e] is candidate e's count of larger entries in quarter q. Pads in[c1, 128)
+// with 0 first. Returns after a barrier.
+__device__ __forceinline__ void block_ranks(uint64_t* in, int c1, uint32_t* rk) {
+    const int tid = threadIdx.x;
+    if (tid >= c1 && tid < 2 * WAVE) in[tid] = 0ull;
+    __syncthreads();
+    const int e = tid & (2 * WAVE - 1), q = tid / (2 * WAVE);
+    const uint64_t me = in[e];
+    int r = 0;
+#pragma unroll
+    for (int j = 0; j < 2 * WAVE / 4; ++j) r += in[q * (2 * WAVE / 4) + j] > me ? 1 : 0;
+    rk[q * 2 * WAVE + e] = (uint32_t)r;
+    __syncthreads();
+}
+static_assert(BLOCK == 4 * 2 * WAVE, "block_ranks splits 128 candidates into four quarters");
+
+__device__ __forceinline__ void wave_finish(const Args& a, const RowCtx& rc, const uint64_t* in, const uint32_t* rk,
+                                            int k, double* wbuf, int& tok_out, int& keep_out) {
     const int lane = lane_id();
     const int row = rc.row;
-    // rank of this lane's candidate among the c1 (broadcast LDS reads, no cross-lane dependency chain). The loops
-    // below run a fixed 64 steps without conditions (entries past c1 / k are 0) so their loads batch up.
-    const uint64_t m0 = lane < c1 ? in[lane] : 0ull;
-    const uint64_t m1 = lane + WAVE < c1 ? in[lane + WAVE] : 0ull;
-    in[lane] = m0;
-    in[lane + WAVE] = m1;
+    // lane holds candidates lane and lane + 64 (0 = none) with their ranks from block_ranks
+    const uint64_t m0 = in[lane], m1 = in[lane + WAVE];
     int r0 = 0, r1 = 0;
-    if (c1 <= WAVE) {
-#pragma unroll 16
-        for (int j = 0; j < WAVE; ++j) r0 += in[j] > m0 ? 1 : 0;
-    } else {
-#pragma unroll 16
-        for (int j = 0; j < 2 * WAVE; ++j) {
-            const uint64_t o = in[j];
-            r0 += o > m0 ? 1 : 0;
-            r1 += o > m1 ? 1 : 0;
-        }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        r0 += (int)rk[q * 2 * WAVE + lane];
+        r1 += (int)rk[q * 2 * WAVE + lane + WAVE];
     }
     uint64_t* sorted = reinterpret_cast<uint64_t*>(wbuf) + WAVE;     // [WAVE] after the [WAVE] doubles
     if (m0 != 0ull && r0 < k) sorted[r0] = m0;
@@ -1328,7 +1335,9 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             }
             __syncthreads();
             if (c1 <= (uint32_t)(2 * WAVE) && k <= WAVE) {
-                if (tid < WAVE) wave_finish(a, rc, small_in, (int)c1, k, reinterpret_cast<double*>(small_out), tok, keep);
+                uint32_t* rk = reinterpret_cast<uint32_t*>(small_out + 2 * WAVE);   // past wave_finish's buffers
+                block_ranks(small_in, (int)c1, rk);
+                if (tid < WAVE) wave_finish(a, rc, small_in, rk, k, reinterpret_cast<double*>(small_out), tok, keep);
                 wave_done = true;
             } else {
                 rank_sort(small_in, (int)c1, small_out, k);
