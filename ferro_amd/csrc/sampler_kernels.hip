@@ -30,6 +30,7 @@
 #include <mutex>
 #include <new>
 #include <random>
+#include <vector>
 
 #include "../../include/ferro_sampler.h"
 
@@ -1895,6 +1896,84 @@ __global__ __launch_bounds__(PEN_BLOCK) void penalize_kernel(float* logits, int6
     }
 }
 
+// ------------------------------------------------------------------------------------------------ draw streams
+// std::mt19937_64 (the standard's parameters: n = 312, m = 156, r = 31, a = 0xB5026F5AA96619E9, tempering
+// u = 29 / d = 0x5555555555555555, s = 17 / b = 0x71D67FFFEDA60000, t = 37 / c = 0xFFF7EEE000000000, l = 43) per
+// stream, and libstdc++'s generate_canonical<double, 53> of one 64-bit output: (double)x / 2^64, kept below 1.
+// This is ferro::Sampler's draw (sampler.h:25,32; sampler.cpp:45-46) moved next to the sampler.
+constexpr int MT_N = 312, MT_M = 156;
+constexpr uint64_t MT_A = 0xB5026F5AA96619E9ull, MT_UPPER = 0xFFFFFFFF80000000ull, MT_LOWER = 0x7FFFFFFFull;
+
+__device__ __forceinline__ uint64_t mt_temper(uint64_t y) {
+    y ^= (y >> 29) & 0x5555555555555555ull;
+    y ^= (y << 17) & 0x71D67FFFEDA60000ull;
+    y ^= (y << 37) & 0xFFF7EEE000000000ull;
+    y ^= y >> 43;
+    return y;
+}
+__device__ __forceinline__ uint64_t mt_twist_one(uint64_t cur, uint64_t next, uint64_t far) {
+    const uint64_t x = (cur & MT_UPPER) | (next & MT_LOWER);
+    return far ^ (x >> 1) ^ ((x & 1ull) ? MT_A : 0ull);
+}
+__device__ void mt_twist(uint64_t* mt) {
+    for (int k = 0; k < MT_N; ++k) mt[k] = mt_twist_one(mt[k], mt[(k + 1) % MT_N], mt[(k + MT_M) % MT_N]);
+}
+__device__ __forceinline__ double mt_canonical(uint64_t x) {
+    const double r = __ull2double_rn(x) * 0x1p-64;
+    return r < 1.0 ? r : 0x1.fffffffffffffp-1;
+}
+__device__ __forceinline__ bool samples(const fs_row_params& p) { return p.temperature > 0.0f && p.top_k != 1; }
+
+// One thread per stream. Stream s owns rows row_off[s] .. row_off[s+1]-1 (row_off NULL: row s alone); each row
+// whose stream samples takes one draw, in row order; greedy streams take none and get u = 0. peek != 0 leaves the
+// state unchanged (the draws are computed from it: at most MT_M draws past a twist).
+__global__ __launch_bounds__(64) void drng_draw_kernel(uint64_t* mts, int32_t* idxs, int n_streams,
+                                                       const int64_t* row_off, const fs_row_params* params,
+                                                       double* u, int peek, int32_t* err) {
+    const int sidx = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (sidx >= n_streams) return;
+    uint64_t* mt = mts + (int64_t)sidx * MT_N;
+    int idx = idxs[sidx];
+    const int64_t r0 = row_off ? row_off[sidx] : sidx;
+    const int64_t r1 = row_off ? row_off[sidx + 1] : sidx + 1;
+    const bool smp = samples(params[sidx]);
+    for (int64_t r = r0; r < r1; ++r) {
+        if (!smp) { u[r] = 0.0; continue; }
+        uint64_t y;
+        if (!peek) {
+            if (idx >= MT_N) { mt_twist(mt); idx = 0; }
+            y = mt[idx++];
+        } else {
+            if (idx < MT_N) {
+                y = mt[idx++];
+            } else {
+                const int k = idx - MT_N;                    // the k-th value of the next twist, from the old state
+                if (k >= MT_M) { atomicOr(err, FS_DEVERR_INTERNAL); u[r] = 0.0; continue; }
+                y = mt_twist_one(mt[k], mt[k + 1], mt[k + MT_M]);
+                ++idx;
+            }
+        }
+        u[r] = mt_canonical(mt_temper(y));
+    }
+    if (!peek) idxs[sidx] = idx;
+}
+
+// Advance stream s by counts[s] draws, or, for a stream that does not sample, by none.
+__global__ __launch_bounds__(64) void drng_skip_kernel(uint64_t* mts, int32_t* idxs, int n_streams,
+                                                       const int32_t* counts, const fs_row_params* params) {
+    const int sidx = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (sidx >= n_streams || !samples(params[sidx])) return;
+    uint64_t* mt = mts + (int64_t)sidx * MT_N;
+    int idx = idxs[sidx];
+    for (int32_t c = counts[sidx]; c > 0;) {
+        if (idx >= MT_N) { mt_twist(mt); idx = 0; }
+        const int take = MT_N - idx < c ? MT_N - idx : c;
+        idx += take;
+        c -= take;
+    }
+    idxs[sidx] = idx;
+}
+
 }  // namespace fs
 
 // ================================================================================================ host side
@@ -2114,6 +2193,80 @@ int fs_rng_next_u(fs_rng* r, double* u, int32_t n) {
 int fs_rng_copy(const fs_rng* src, fs_rng* dst) {
     if (!src || !dst) return FS_E_INVALID;
     dst->eng = src->eng;
+    return FS_OK;
+}
+
+// Device draw streams (see fs::drng_draw_kernel): the engines' states live in device memory; seeding follows the
+// standard's seed sequence for mt19937_64 (x0 = seed, x_i = 6364136223846793005 * (x_{i-1} ^ (x_{i-1} >> 62)) + i),
+// so stream s reproduces std::mt19937_64(seed_s) and ferro::Sampler's draws.
+struct fs_drng {
+    int device = -1;
+    int n = 0;
+    uint64_t* mt = nullptr;     // [n][312]
+    int32_t* idx = nullptr;     // [n]
+    int32_t* err = nullptr;
+};
+
+int fs_drng_create(int32_t n_streams, const uint64_t* seeds, void* stream, fs_drng** out) {
+    if (!out || n_streams < 1 || !seeds) return FS_E_INVALID;
+    *out = nullptr;
+    fs_drng* r = new (std::nothrow) fs_drng();
+    if (!r) return FS_E_NOMEM;
+    std::vector<uint64_t> mt((size_t)n_streams * fs::MT_N);
+    std::vector<int32_t> idx((size_t)n_streams, fs::MT_N);
+    std::random_device rd;
+    for (int32_t s = 0; s < n_streams; ++s) {
+        uint64_t* x = mt.data() + (size_t)s * fs::MT_N;
+        x[0] = seeds[s] ? seeds[s] : (uint64_t)rd();                     // seed 0 = random, as ferro
+        for (int i = 1; i < fs::MT_N; ++i) x[i] = 6364136223846793005ull * (x[i - 1] ^ (x[i - 1] >> 62)) + (uint64_t)i;
+    }
+    r->n = n_streams;
+    int rc = FS_OK;
+    if (hipGetDevice(&r->device) != hipSuccess) rc = FS_E_HIP;
+    if (rc == FS_OK && (hipMalloc(&r->mt, mt.size() * sizeof(uint64_t)) != hipSuccess ||
+                        hipMalloc(&r->idx, idx.size() * sizeof(int32_t)) != hipSuccess ||
+                        hipMalloc(&r->err, sizeof(int32_t)) != hipSuccess))
+        rc = FS_E_NOMEM;
+    hipStream_t st = (hipStream_t)stream;
+    if (rc == FS_OK && (hipMemcpyAsync(r->mt, mt.data(), mt.size() * sizeof(uint64_t), hipMemcpyHostToDevice, st) != hipSuccess ||
+                        hipMemcpyAsync(r->idx, idx.data(), idx.size() * sizeof(int32_t), hipMemcpyHostToDevice, st) != hipSuccess ||
+                        hipMemsetAsync(r->err, 0, sizeof(int32_t), st) != hipSuccess ||
+                        hipStreamSynchronize(st) != hipSuccess))
+        rc = FS_E_HIP;
+    if (rc != FS_OK) { fs_drng_destroy(r); return rc; }
+    *out = r;
+    return FS_OK;
+}
+
+int fs_drng_destroy(fs_drng* r) {
+    if (!r) return FS_E_INVALID;
+    (void)hipFree(r->mt);
+    (void)hipFree(r->idx);
+    (void)hipFree(r->err);
+    delete r;
+    return FS_OK;
+}
+
+int fs_drng_draw(fs_drng* r, const int64_t* d_row_off, const fs_row_params* d_params, double* d_u, int32_t peek,
+                 void* stream) {
+    if (!r || !d_params || !d_u) return FS_E_INVALID;
+    hipLaunchKernelGGL(fs::drng_draw_kernel, dim3((unsigned)((r->n + 63) / 64)), dim3(64), 0, (hipStream_t)stream,
+                       r->mt, r->idx, r->n, d_row_off, d_params, d_u, peek ? 1 : 0, r->err);
+    return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
+}
+
+int fs_drng_skip(fs_drng* r, const int32_t* d_counts, const fs_row_params* d_params, void* stream) {
+    if (!r || !d_counts || !d_params) return FS_E_INVALID;
+    hipLaunchKernelGGL(fs::drng_skip_kernel, dim3((unsigned)((r->n + 63) / 64)), dim3(64), 0, (hipStream_t)stream,
+                       r->mt, r->idx, r->n, d_counts, d_params);
+    return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
+}
+
+int fs_drng_error(fs_drng* r, void* stream, int32_t* bits) {
+    if (!r || !bits) return FS_E_INVALID;
+    if (hipStreamSynchronize((hipStream_t)stream) != hipSuccess) return FS_E_HIP;
+    if (hipMemcpy(bits, r->err, sizeof(int32_t), hipMemcpyDeviceToHost) != hipSuccess) return FS_E_HIP;
+    if (hipMemset(r->err, 0, sizeof(int32_t)) != hipSuccess) return FS_E_HIP;
     return FS_OK;
 }
 

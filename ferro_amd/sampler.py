@@ -135,6 +135,59 @@ class Rng:
         return r
 
 
+class DeviceRng:
+    """fs_drng: one std::mt19937_64 draw stream per sampling stream, held on the device (ferro::Sampler's rng_,
+    sampler.h:25,32). draw() gives each row of a sampling stream one generate_canonical draw, in row order; rows of
+    greedy streams get 0 and consume nothing."""
+
+    def __init__(self, seeds, device=None, stream=None):
+        seeds = np.ascontiguousarray(np.asarray(seeds, dtype=np.uint64).reshape(-1))
+        self.n = int(seeds.size)
+        self._dev = torch.device("cuda" if device is None else device)
+        h = ctypes.c_void_p()
+        check(lib().fs_drng_create(self.n, seeds.ctypes.data_as(ctypes.c_void_p), _stream(stream),
+                                   ctypes.byref(h)), "fs_drng_create")
+        self.h = h
+
+    def __del__(self):
+        h = getattr(self, "h", None)
+        if h is not None and h.value:
+            try:
+                lib().fs_drng_destroy(h)
+            except Exception:
+                pass
+
+    def draw(self, params, row_off=None, peek=False, stream=None) -> torch.Tensor:
+        p = _dev_params(params, self._dev)
+        if p.numel() != self.n * PARAMS_DTYPE.itemsize:
+            raise SamplerError("one params record per stream")
+        ro = None
+        rows = self.n
+        if row_off is not None:
+            ro = torch.as_tensor(row_off, dtype=torch.int64, device=self._dev)
+            if ro.numel() != self.n + 1:
+                raise SamplerError("row_off must have n_streams+1 entries")
+            rows = int(ro[-1].item())
+        u = torch.empty(rows, dtype=torch.float64, device=self._dev)
+        check(lib().fs_drng_draw(self.h, _ptr(ro), _ptr(p), _ptr(u), 1 if peek else 0, _stream(stream)),
+              "fs_drng_draw")
+        self._keep = (p, ro)
+        return u
+
+    def skip(self, counts, params, stream=None) -> None:
+        p = _dev_params(params, self._dev)
+        c = torch.as_tensor(counts, dtype=torch.int32, device=self._dev)
+        if c.numel() != self.n:
+            raise SamplerError("one count per stream")
+        check(lib().fs_drng_skip(self.h, _ptr(c), _ptr(p), _stream(stream)), "fs_drng_skip")
+        self._keep = (p, c)
+
+    def error(self, stream=None) -> int:
+        bits = ctypes.c_int32(0)
+        check(lib().fs_drng_error(self.h, _stream(stream), ctypes.byref(bits)), "fs_drng_error")
+        return bits.value
+
+
 def _check_logits(logits: torch.Tensor, V: int | None):
     if not (isinstance(logits, torch.Tensor) and logits.is_cuda and logits.dtype == torch.float32):
         raise SamplerError("logits must be a float32 CUDA tensor")

@@ -102,6 +102,25 @@ int fs_rng_destroy(fs_rng* r);
 int fs_rng_next_u(fs_rng* r, double* u, int32_t n);
 int fs_rng_copy(const fs_rng* src, fs_rng* dst);
 
+/* Device draw streams: n_streams std::mt19937_64 engines held in device memory (seeds[s] from the host; 0 =
+ * random, as ferro), drawing libstdc++ generate_canonical<double,53> values - ferro::Sampler's draw stream
+ * (sampler.h:25,32; sampler.cpp:45-46) without a host round trip. Stream s owns rows d_row_off[s] ..
+ * d_row_off[s+1]-1 (d_row_off NULL: one row per stream, row s); d_params[s] are its sampling parameters.
+ * fs_drng_draw writes d_u[row]: one draw per row of a sampling stream (temperature > 0 and top_k != 1), in row
+ * order, as ferro's sequential sample() calls; rows of greedy streams get 0 and consume nothing. peek != 0 computes
+ * the draws without consuming them (at most 156 draws past the engine's next twist; more sets FS_DEVERR_INTERNAL):
+ * a verify window peeks its rows' draws, then fs_drng_skip consumes d_counts[s] draws per sampling stream (e.g.
+ * fs_verify's d_accepted). The draws equal fs_rng_next_u on the same seeds. Calls on one fs_drng must be ordered
+ * (one stream). */
+typedef struct fs_drng fs_drng;
+int fs_drng_create(int32_t n_streams, const uint64_t* seeds, void* stream, fs_drng** out);
+int fs_drng_destroy(fs_drng* r);
+int fs_drng_draw(fs_drng* r, const int64_t* d_row_off, const fs_row_params* d_params, double* d_u, int32_t peek,
+                 void* stream);
+int fs_drng_skip(fs_drng* r, const int32_t* d_counts, const fs_row_params* d_params, void* stream);
+/* Waits for `stream`, then returns and clears the stream set's error bits. */
+int fs_drng_error(fs_drng* r, void* stream, int32_t* bits);
+
 /* The penalty stage alone, in place: row b of d_logits is left exactly as ferro's sample() leaves its host row
  * (sampler.cpp:11-18: each distinct window id in [0, V) once, l > 0 ? l/rep : l*rep, then the frequency/presence
  * extension). For callers that read the penalised row back (lm_cli.cpp:353); fs_sample_batch does not need it (it

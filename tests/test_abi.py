@@ -48,6 +48,9 @@ def test_invalid_arguments_rejected_without_device():
     assert L.fs_argmax_batch(None, None, 0, 0, 0, None, None, None, None, None) == _lib.FS_E_INVALID
     assert L.fs_penalize_batch(None, None, 0, 0, 0, None, None, None, None) == _lib.FS_E_INVALID
     assert L.fs_rng_create(1, None) == _lib.FS_E_INVALID
+    assert L.fs_drng_create(0, None, None, None) == _lib.FS_E_INVALID
+    assert L.fs_drng_draw(None, None, None, None, 0, None) == _lib.FS_E_INVALID
+    assert L.fs_drng_skip(None, None, None, None) == _lib.FS_E_INVALID
     h = P()
     assert L.fs_create(ctypes.byref(h)) == _lib.FS_OK
     fake = P(16)   # never dereferenced: argument checks fail first

@@ -403,3 +403,73 @@ def test_cpp_dropin_shim_replays_reference_streams(tmp_path):
             np.testing.assert_array_equal(rows[i], want, err_msg=f"stream {s} step {i}")
             hist.append(int(tok[i]))
     assert pos == buf.size
+
+
+def _host_draws(seed, n):
+    r = F.Rng(int(seed))
+    return r.next_u(n)
+
+
+def test_device_draw_streams_match_libstdcxx():
+    """fs_drng: per-stream std::mt19937_64 + generate_canonical on the device equals the host engine (libstdc++)
+    bit for bit, across twists; greedy streams consume nothing."""
+    seeds = np.array([1, 5489, 2**63 + 7, 123456789, 42, 7], dtype=np.uint64)
+    S = len(seeds)
+    p = W.make_params(S, temperature=0.8, top_k=40)
+    p["temperature"][3] = 0.0                                  # greedy stream
+    p["top_k"][5] = 1                                          # greedy through top_k == 1
+    d = F.DeviceRng(seeds)
+    got = np.stack([d.draw(p).cpu().numpy() for _ in range(700)])   # 700 calls: crosses two twists
+    for s_ in range(S):
+        if s_ in (3, 5):
+            assert (got[:, s_] == 0).all()
+        else:
+            np.testing.assert_array_equal(got[:, s_], _host_draws(seeds[s_], 700))
+    # the greedy streams start drawing exactly where they were once they sample
+    p2 = p.copy()
+    p2["temperature"][3] = 0.9
+    np.testing.assert_array_equal(d.draw(p2).cpu().numpy()[3], _host_draws(seeds[3], 1)[0])
+    assert d.error() == 0
+
+
+def test_device_draw_rows_peek_and_skip():
+    """A verify window: rows of a stream draw in row order; peek leaves the engine; skip consumes the accepted count
+    (also across a twist)."""
+    seeds = np.array([11, 22, 33], dtype=np.uint64)
+    p = W.make_params(3, temperature=1.0, top_k=0)
+    d = F.DeviceRng(seeds)
+    one = np.array([0, 1, 2, 3], dtype=np.int64)
+    for _ in range(300):                                       # bring the engines near the end of the state
+        d.draw(p, row_off=one)
+    m = 17
+    row_off = np.arange(0, 3 * m + 1, m, dtype=np.int64)
+    peek = d.draw(p, row_off=row_off, peek=True).cpu().numpy().reshape(3, m)
+    for s_ in range(3):
+        np.testing.assert_array_equal(peek[s_], _host_draws(seeds[s_], 300 + m)[300:])
+    again = d.draw(p, row_off=row_off, peek=True).cpu().numpy().reshape(3, m)
+    np.testing.assert_array_equal(again, peek)                 # peek consumed nothing
+    acc = np.array([5, 17, 0], dtype=np.int32)
+    d.skip(acc, p)
+    nxt = d.draw(p).cpu().numpy()
+    for s_ in range(3):
+        assert nxt[s_] == _host_draws(seeds[s_], 300 + int(acc[s_]) + 1)[-1]
+    assert d.error() == 0
+
+
+def test_device_draws_replay_reference_streams():
+    """ferro's own seeded 40-call streams (tests/golden): device draws + fs_sample_batch give the reference tokens."""
+    gold = np.load(os.path.join(os.path.dirname(__file__), "golden", "sampler_golden.npz"), allow_pickle=False)
+    params = gold["stream_params"].view(F.PARAMS_DTYPE)
+    X = gold["stream_x"]
+    S, steps, V = X.shape
+    d = F.DeviceRng(gold["stream_seed"])
+    hists = [list(gold["stream_h0"][s_]) for s_ in range(S)]
+    for i in range(steps):
+        u = d.draw(params)
+        hist = np.concatenate([np.asarray(h, np.int32) for h in hists])
+        off = np.concatenate([[0], np.cumsum([len(h) for h in hists])]).astype(np.int64)
+        tok = F.sample_batch(torch.from_numpy(np.ascontiguousarray(X[:, i])).cuda(), params, u, hist=hist,
+                             hist_off=off)["tok"].cpu().numpy()
+        np.testing.assert_array_equal(tok, gold["stream_tok"][:, i], err_msg=f"step {i}")
+        for s_ in range(S):
+            hists[s_].append(int(tok[s_]))
