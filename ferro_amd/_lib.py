@@ -24,7 +24,7 @@ FS_DEVERR_COUNT_OVERFLOW = 1
 PARAMS_DTYPE = np.dtype([
     ("temperature", np.float32), ("top_k", np.int32), ("top_p", np.float32), ("min_p", np.float32),
     ("repetition_penalty", np.float32), ("frequency_penalty", np.float32), ("presence_penalty", np.float32),
-    ("repeat_last_n", np.int32), ("penalty_from", np.int32), ("reserved", np.int32),
+    ("repeat_last_n", np.int32), ("penalty_from", np.int32), ("softcap", np.float32),
 ])
 assert PARAMS_DTYPE.itemsize == 40
 

@@ -442,7 +442,7 @@ static_assert((TILE / 2 + NBINS) / 2 >= KMAX, "the stage holds a compacted top k
 struct RowCtx {
     int row, pidx;
     fs_row_params p;
-    bool greedy, large, pen, rep_on, fp_on;
+    bool greedy, large, pen, rep_on, fp_on, capped;
     int k;
     int64_t hA0, lenA, lenB, b, len;     // window [b, len) over the concatenated history
     const int32_t* segB;
@@ -484,12 +484,13 @@ __device__ __forceinline__ RowCtx row_ctx(const Args& a, int row) {
     else {
         rc.p.temperature = 0.f; rc.p.top_k = 1; rc.p.top_p = 1.f; rc.p.min_p = 0.f; rc.p.repetition_penalty = 1.f;
         rc.p.frequency_penalty = 0.f; rc.p.presence_penalty = 0.f; rc.p.repeat_last_n = 0; rc.p.penalty_from = 0;
-        rc.p.reserved = 0;
+        rc.p.softcap = 0.f;
     }
     const int V = a.V;
     rc.greedy = a.mode == MODE_ARGMAX || rc.p.temperature <= 0.0f || rc.p.top_k == 1;
     rc.k = rc.greedy ? 1 : ((rc.p.top_k > 0 && rc.p.top_k < V) ? rc.p.top_k : V);
     rc.large = rc.k > KMAX;                 // not on the segment path: sampled by large_row in the merge kernel
+    rc.capped = rc.p.softcap > 0.0f;
     rc.rep_on = rc.p.repetition_penalty != 1.0f;
     rc.fp_on = rc.p.frequency_penalty != 0.0f || rc.p.presence_penalty != 0.0f;
     rc.len = rc.lenA + rc.lenB;
@@ -514,6 +515,13 @@ __device__ __forceinline__ void load_tile(float (&x)[TPT], const float* rowp, in
         const float4 t = p[j * BLOCK];
         x[4 * j + 0] = t.x; x[4 * j + 1] = t.y; x[4 * j + 2] = t.z; x[4 * j + 3] = t.w;
     }
+}
+// The model's final-logit softcap, moved into the read: l = cap * tanhf(l / cap) (model_gemma4_gpu.cpp:282-283:
+// fp32 divide, tanhf, fp32 multiply), before the penalties as in ferro, where the model caps the row first.
+template <int N>
+__device__ __forceinline__ void softcap_vals(float (&x)[N], float cap) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] = __fmul_rn(cap, tanhf(__fdiv_rn(x[i], cap)));
 }
 // element id of this thread's i-th logit of the tile starting at lo
 __device__ __forceinline__ int elem_id(int lo, int i) { return lo + ((i >> 2) * BLOCK + (int)threadIdx.x) * 4 + (i & 3); }
@@ -716,6 +724,7 @@ __device__ __forceinline__ void row_tiles(const Args& a, const RowCtx& rc, Share
                 const int nt = t + LPF;
                 if (nt < full) load_tile(buf[p], rowp, nt * TILE);
                 else if (nt < ntile) load_tile_masked(buf[p], rowp, nt * TILE, V);
+                if (rc.capped) softcap_vals(x, rc.p.softcap);
                 if (rc.pen) {
                     __syncthreads();                 // the previous tile's table reads are done
                     apply_penalties(x, a, rc, t * TILE, s);
@@ -1136,6 +1145,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
         const int e = tail_lo + r * BLOCK + tid;
         tx[r] = e < V ? rowp[e] : 0.f;
     }
+    if (ntail > 0 && rc.capped) softcap_vals(tx, rc.p.softcap);
     if (ntail > 0 && rc.pen) {
         for (int i = tid; i < TILE / 8; i += BLOCK) reinterpret_cast<uint4*>(s.cnt())[i] = make_uint4(0u, 0u, 0u, 0u);
         __syncthreads();
@@ -1680,6 +1690,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         {
             float (&x)[TPT] = buf[0];
             const int lo = seg_lo;
+            if (rc.capped) softcap_vals(x, rc.p.softcap);
             if (slowpen) apply_penalties(x, a, rc, lo, s);
             if (fastpen) bitmap_pen(x, lo);
             if (rc.greedy) {
@@ -1743,6 +1754,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 if (tt >= 1 && tt < ntiles && !overflow) {
                     const int lo = seg_lo + tt * TILE;
                     float (&x)[TPT] = buf[p];
+                    if (rc.capped) softcap_vals(x, rc.p.softcap);
                     if (slowpen) apply_penalties(x, a, rc, lo, s);
                     if (fastpen) bitmap_pen(x, lo);
                     if (rc.greedy) greedy_update(x, tt);

@@ -37,6 +37,7 @@ class SamplerParams:
     seed: int = 0
     frequency_penalty: float = 0.0
     presence_penalty: float = 0.0
+    softcap: float = 0.0              # > 0: the model's final-logit softcap, fused into the sampler's read
 
     def validate(self) -> None:
         """The server's range check (src/server.cpp:1071)."""
@@ -57,7 +58,7 @@ def params_array(params) -> np.ndarray:
     out = np.zeros(len(params), PARAMS_DTYPE)
     for i, p in enumerate(params):
         out[i] = (p.temperature, p.top_k, p.top_p, p.min_p, p.repetition_penalty, p.frequency_penalty,
-                  p.presence_penalty, p.repeat_last_n, p.penalty_from, 0)
+                  p.presence_penalty, p.repeat_last_n, p.penalty_from, p.softcap)
     return out
 
 

@@ -41,7 +41,8 @@ extern "C" {
 /* Per-row sampling parameters. Fields 1-5 and 8-9 are ferro's SamplerParams (src/sampler.h:12-21) with the
  * same meaning and defaults; the seed is replaced by the per-row draw u. frequency_penalty / presence_penalty
  * extend ferro (llama.cpp convention: l -= cnt*freq + (cnt>0)*pres over the penalty window, after the
- * repetition step); 0 leaves a row bit-identical to ferro. */
+ * repetition step); 0 leaves a row bit-identical to ferro. softcap moves the model's final-logit transform into
+ * the sampler's read (the logits stay as produced); fs_penalize_batch ignores it. */
 typedef struct fs_row_params {
     float temperature;        /* <= 0: greedy (argmax after penalties)        sampler.h:13 */
     int32_t top_k;            /* 0 = all tokens; 1 = greedy                   sampler.h:14 */
@@ -52,7 +53,8 @@ typedef struct fs_row_params {
     float presence_penalty;   /* 0 = off (extension) */
     int32_t repeat_last_n;    /* -1 whole history, 0 off, N last tokens       sampler.h:18 */
     int32_t penalty_from;     /* history positions before this never count    sampler.h:19 */
-    int32_t reserved;         /* must be 0 */
+    float softcap;            /* > 0: logits become softcap * tanhf(l / softcap) before the penalties (Gemma 4's
+                                 final-logit softcap, model_gemma4_gpu.cpp:282-283, fused into the read); 0 = off */
 } fs_row_params;
 
 typedef struct fs_context fs_context;

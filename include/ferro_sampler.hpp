@@ -35,6 +35,9 @@ struct SamplerParams {
     uint64_t seed = 0;
     float frequency_penalty = 0.0f;
     float presence_penalty = 0.0f;
+    float softcap = 0.0f;             // > 0: Gemma 4's final-logit softcap fused into the read (0 = off). For
+                                      // sample_device on the model's raw output; a host row from ferro's model
+                                      // code is already capped (model_gemma4_gpu.cpp:282-283): leave it 0 there.
 };
 
 class Sampler {
@@ -54,7 +57,7 @@ public:
         rec_.presence_penalty = p.presence_penalty;
         rec_.repeat_last_n = p.repeat_last_n;
         rec_.penalty_from = p.penalty_from;
-        rec_.reserved = 0;
+        rec_.softcap = p.softcap;
         hip(hipMalloc(&d_small_, sizeof(Small)), "hipMalloc");
         hip(hipMemcpy(&d_small_->rec, &rec_, sizeof(rec_), hipMemcpyHostToDevice), "hipMemcpy");
     }

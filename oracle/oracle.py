@@ -22,13 +22,13 @@ REF_PATH = os.path.join(HERE, "_ref", "libferro_ref.so")
 PARAMS_DTYPE = np.dtype([
     ("temperature", np.float32), ("top_k", np.int32), ("top_p", np.float32), ("min_p", np.float32),
     ("repetition_penalty", np.float32), ("frequency_penalty", np.float32), ("presence_penalty", np.float32),
-    ("repeat_last_n", np.int32), ("penalty_from", np.int32), ("reserved", np.int32),
+    ("repeat_last_n", np.int32), ("penalty_from", np.int32), ("softcap", np.float32),
 ])
 assert PARAMS_DTYPE.itemsize == 40
 
 
 def make_params(n=1, temperature=0.05, top_k=50, top_p=1.0, min_p=0.0, repetition_penalty=1.05,
-                frequency_penalty=0.0, presence_penalty=0.0, repeat_last_n=-1, penalty_from=0):
+                frequency_penalty=0.0, presence_penalty=0.0, repeat_last_n=-1, penalty_from=0, softcap=0.0):
     """Params array with ferro's SamplerParams defaults (sampler.h:12-20)."""
     p = np.zeros(n, PARAMS_DTYPE)
     p["temperature"] = temperature
@@ -40,6 +40,7 @@ def make_params(n=1, temperature=0.05, top_k=50, top_p=1.0, min_p=0.0, repetitio
     p["presence_penalty"] = presence_penalty
     p["repeat_last_n"] = repeat_last_n
     p["penalty_from"] = penalty_from
+    p["softcap"] = softcap
     return p
 
 

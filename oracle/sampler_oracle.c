@@ -105,6 +105,9 @@ static cand_t* top_k_sorted(const float* row, int n, int k) {
 /* ------------------------------------------------------------------ sample: sampler.cpp:10-50 */
 int fso_sample(float* row, int n, const int32_t* hist, int64_t hlen, const fso_params* p, double u,
                int32_t* cand_ids, double* cand_probs, int kcap, int32_t* keep_out, int32_t* ncand_out) {
+    if (p->softcap > 0.0f)                                     /* the model's final-logit softcap, applied to the */
+        for (int i = 0; i < n; ++i)                            /* row before sample() (model_gemma4_gpu.cpp:282-283) */
+            row[i] = p->softcap * tanhf(row[i] / p->softcap);
     fso_penalize(row, n, hist, hlen, p);
     if (p->temperature <= 0.0f || p->top_k == 1) {            /* greedy: sampler.cpp:19-23 */
         int best = 0;

@@ -29,7 +29,7 @@ typedef struct fso_params {
     float presence_penalty;   /* 0 = off (extension) */
     int32_t repeat_last_n;    /* -1 whole history, 0 off, N last tokens */
     int32_t penalty_from;     /* history positions before this are never penalised */
-    int32_t reserved;
+    float softcap;            /* > 0: l = softcap * tanhf(l / softcap) first (model_gemma4_gpu.cpp:282-283) */
 } fso_params;
 
 /* Penalty stage in place (sampler.cpp:11-18 + extension). Returns the number of distinct ids changed. */

@@ -473,3 +473,26 @@ def test_device_draws_replay_reference_streams():
         np.testing.assert_array_equal(tok, gold["stream_tok"][:, i], err_msg=f"step {i}")
         for s_ in range(S):
             hists[s_].append(int(tok[s_]))
+
+
+def test_softcap_fused_read():
+    """Gemma 4's final-logit softcap (cap 30) fused into the read, on every path: top-k, greedy, large k, penalties,
+    and a row tail; probabilities to 1e-5 against the oracle (glibc tanhf, as ferro's model code)."""
+    rng = np.random.default_rng(30)
+    V = 262144 + 77
+    B = 8
+    # |x| <= 150: no logit saturates tanhf (where two libm implementations may round differently)
+    x = np.clip(W.mixture_logits(rng, B, V) * np.float32(3.0), -150.0, 150.0).astype(np.float32)
+    p = W.make_params(B, temperature=0.8, top_k=64, top_p=0.95, repetition_penalty=1.05)
+    p["softcap"] = 30.0
+    p["temperature"][1] = 0.0
+    p["top_k"][2] = 0
+    p["frequency_penalty"][3], p["presence_penalty"][3] = 0.4, 0.2
+    hists = [rng.integers(0, V, 300) for _ in range(B)]
+    g, o, nb = check(_case(list(x), p, hists, rng.random(B), "softcap"), kcap=64)
+    assert nb == 0
+    t2 = F.argmax_batch(torch.from_numpy(x).cuda(), params=p, hist=np.concatenate(hists).astype(np.int32),
+                        hist_off=np.concatenate([[0], np.cumsum([len(h) for h in hists])]).astype(np.int64))
+    np.testing.assert_array_equal(t2.cpu().numpy(), [O.sample(x[b], hists[b], O.make_params(
+        temperature=0.0, repetition_penalty=1.05, softcap=30.0, frequency_penalty=float(p["frequency_penalty"][b]),
+        presence_penalty=float(p["presence_penalty"][b])))[0] for b in range(B)])

@@ -200,3 +200,22 @@ def test_live_reference_random():
                           repetition_penalty=float(rng.uniform(0.8, 1.6)),
                           repeat_last_n=int(rng.choice([-1, 0, 5, 64])), penalty_from=int(rng.choice([0, 3])))
         assert O.sample(x, h, p, W.first_u(s))[0] == O.ref_sample_stream(p, s, [x], [h])[0], s
+
+
+def test_softcap_closed_form():
+    """softcap (the model's final-logit transform, model_gemma4_gpu.cpp:282-283): sampling raw logits with softcap
+    set equals sampling the capped row (numpy's float32 tanh, an independent implementation) with softcap off."""
+    rng = np.random.default_rng(17)
+    row = (rng.standard_normal(5000) * 12).astype(np.float32)
+    cap = np.float32(30.0)
+    capped = (cap * np.tanh(row / cap)).astype(np.float32)
+    for kw in [dict(temperature=0.8, top_k=50, top_p=0.9), dict(temperature=0.0), dict(temperature=1.2, top_k=0)]:
+        p0 = O.make_params(repetition_penalty=1.2, **kw)
+        p1 = O.make_params(repetition_penalty=1.2, softcap=30.0, **kw)
+        h = rng.integers(0, 5000, 40).astype(np.int32)
+        t0, ids0, pr0, k0, n0 = O.sample(capped, h, p0, 0.37, kcap=64)
+        t1, ids1, pr1, k1, n1 = O.sample(row, h, p1, 0.37, kcap=64)
+        assert t0 == t1 and k0 == k1 and n0 == n1
+        np.testing.assert_array_equal(ids0, ids1)
+        np.testing.assert_allclose(pr0, pr1, rtol=1e-5)          # tanh implementations differ by ulps
+    assert (O.penalize(row, h, p1) == O.penalize(row, h, p0)).all()   # the penalty pass alone ignores softcap
