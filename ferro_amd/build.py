@@ -23,6 +23,9 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # the persistent kernel's loop would otherwise hoist exp()'s constants and lane masks out of it and spill them
     "-mllvm", "-disable-machine-licm",
+    # the kernels' leading scalar parameters arrive in SGPRs at wave launch (no argument loads before the first
+    # memory requests)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-I" + os.path.join(ROOT, "include"),
 ]
 

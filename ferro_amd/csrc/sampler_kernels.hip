@@ -1520,16 +1520,30 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
 //     whole row's evidence instead of one segment's.
 // The segment publishes its candidates with key >= the final tkey (plain stores; the merge kernel runs after this
 // kernel). They include every logit of the row's top k that lies in this segment.
-__device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc, int seg, Shared& s) {
-    const int tid = threadIdx.x;
-    const int V = a.V;
-    const int seg_lo = seg * a.seg_tiles * TILE;
-    const int left = V / TILE - seg * a.seg_tiles;                 // full tiles left in the row
-    const int ntiles = left < a.seg_tiles ? left : a.seg_tiles;    // >= 1
-    const float* rowp = a.logits + (int64_t)rc.row * a.ld;
+// The first PF tiles of a segment, requested from the kernel arguments alone (before the row's parameters arrive).
+struct SegStart {
+    int seg_lo, ntiles;
+    const float* rowp;
+};
+__device__ __forceinline__ SegStart seg_start(const Args& a, int row, int seg, float (&buf)[PF][TPT]) {
+    SegStart g;
+    g.seg_lo = seg * a.seg_tiles * TILE;
+    const int left = a.V / TILE - seg * a.seg_tiles;                // full tiles left in the row
+    g.ntiles = left < a.seg_tiles ? left : a.seg_tiles;             // >= 1
+    g.rowp = a.logits + (int64_t)row * a.ld;
+#pragma unroll
+    for (int p = 0; p < PF; ++p) load_tile(buf[p], g.rowp, g.seg_lo + (p < g.ntiles ? p : 0) * TILE);
+    return g;
+}
 
-    // the first window ids are requested before the tiles (memory returns in order: the bitmap below is then built
-    // while the tiles are still in flight)
+__device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc, int seg, Shared& s,
+                                                float (&buf)[PF][TPT], const SegStart& g) {
+    const int tid = threadIdx.x;
+    const int seg_lo = g.seg_lo;
+    const int ntiles = g.ntiles;
+    const float* rowp = g.rowp;
+
+    // the window ids (their loads return after the first tiles': the bitmap below waits for those anyway)
     constexpr int WPF = 2;
     int wid[WPF];
 #pragma unroll
@@ -1537,9 +1551,6 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         const int64_t i = rc.b + q * BLOCK + tid;
         wid[q] = (rc.pen && i < rc.len) ? hist_at(a, rc, i) : -1;
     }
-    float buf[PF][TPT];
-#pragma unroll
-    for (int p = 0; p < PF; ++p) load_tile(buf[p], rowp, seg_lo + (p < ntiles ? p : 0) * TILE);
     // Penalties. With a repetition penalty alone (sampler.cpp:11-18) only membership in the window matters: an
     // exact bitmap of the segment's window ids (bmp, in the merge's offset array, unused by this kernel) is built
     // once, and a thread's four consecutive logits share one bitmap word, so each tile costs two LDS reads and no
@@ -1832,24 +1843,36 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
 
 // Segment kernel (persistent): workgroup g handles items g, g+G, ... (item = row*nseg + segment, row-major; rows
 // sampled with k > KMAX are left to the merge kernel).
-__global__ __launch_bounds__(BLOCK, 4) void segment_kernel(Args a) {
+// The fields a workgroup needs first come as separate leading parameters: gfx950 preloads those into SGPRs at
+// wave launch (build flag -amdgpu-kernarg-preload-count), so the first tile loads wait for no argument load.
+__global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, int64_t ld, int B, int V, int nseg,
+                                                           int seg_tiles, const fs_row_params* params,
+                                                           const int64_t* hist_off, Args a) {
     static_assert(KMAX + TILE <= CAP, "a compacted buffer plus one tile must fit the candidate buffer");
     __shared__ __align__(16) Shared s;
+    a.logits = logits; a.ld = ld; a.B = B; a.V = V; a.nseg = nseg; a.seg_tiles = seg_tiles; a.params = params;
+    a.hist_off = hist_off;
     const int total = a.B * a.nseg;
     for (int item = (int)blockIdx.x; item < total; item += (int)gridDim.x) {
-        const int row = item / a.nseg;
+        // uniform by construction; readfirstlane lets the compiler use scalar loads for the row's parameters
+        const int row = __builtin_amdgcn_readfirstlane(item / a.nseg);
+        const int seg = item - row * a.nseg;
+        float buf[PF][TPT];
+        const SegStart g = seg_start(a, row, seg, buf);   // the tiles are on their way before the parameters
         const RowCtx rc = row_ctx(a, row);
         if (rc.large) continue;                    // the merge kernel samples the whole row
-        process_segment(a, rc, item - row * a.nseg, s);
+        process_segment(a, rc, seg, s, buf, g);
     }
 }
 
 // Merge kernel: one workgroup per row, after the segment kernel. The segment lists are requested first, so their
 // latency overlaps the row's parameter loads.
-__global__ __launch_bounds__(BLOCK) void merge_kernel(Args a) {
+__global__ __launch_bounds__(BLOCK) void merge_kernel(int nseg, uint64_t* cand, uint32_t* meta, uint32_t* rhist,
+                                                      const fs_row_params* params, Args a) {
     static_assert(2 * SMALL * 8 <= NBINS * 4, "rank-sort buffers alias the histogram");
     __shared__ __align__(16) Shared s;
-    const int row = (int)blockIdx.x;
+    a.nseg = nseg; a.cand = cand; a.meta = meta; a.rhist = rhist; a.params = params;
+    const int row = __builtin_amdgcn_readfirstlane((int)blockIdx.x);
     Pre pre;
     prefetch_lists(a, row, pre);
     merge_row(a, row_ctx(a, row), s, pre);
@@ -2069,10 +2092,12 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
     a.cand = ctx->cand; a.meta = ctx->meta; a.row_cnt = ctx->row_cnt; a.rhist = ctx->rhist;
     a.stream_cnt = ctx->stream_cnt; a.err = ctx->err;
     if (seg_grid > 0) {
-        hipLaunchKernelGGL(fs::segment_kernel, dim3((unsigned)seg_grid), dim3(fs::BLOCK), 0, st, a);
+        hipLaunchKernelGGL(fs::segment_kernel, dim3((unsigned)seg_grid), dim3(fs::BLOCK), 0, st, a.logits, a.ld, a.B, a.V,
+                           a.nseg, a.seg_tiles, a.params, a.hist_off, a);
         if (hipGetLastError() != hipSuccess) return FS_E_HIP;
     }
-    hipLaunchKernelGGL(fs::merge_kernel, dim3((unsigned)rows), dim3(fs::BLOCK), 0, st, a);
+    hipLaunchKernelGGL(fs::merge_kernel, dim3((unsigned)rows), dim3(fs::BLOCK), 0, st, a.nseg, a.cand, a.meta, a.rhist,
+                       a.params, a);
     return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
 }
 
