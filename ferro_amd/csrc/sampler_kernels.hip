@@ -1931,6 +1931,56 @@ __global__ __launch_bounds__(PEN_BLOCK) void penalize_kernel(float* logits, int6
     }
 }
 
+// ------------------------------------------------------------------------------------------------ prompt lookup
+// Prompt-lookup drafting (server.cpp:552-564), one workgroup per stream: for n = min(4, L-1) down to min_n, every
+// thread tests its positions p for h[p, p+n) == the history's last n tokens with a non-eos token after the match
+// (the reference skips a match whose continuation is empty); the largest such p (the most recent occurrence) wins,
+// and the tokens after it, up to kmax and stopping before eos, are the draft.
+constexpr int LD_BLOCK = 256;
+
+__global__ __launch_bounds__(LD_BLOCK) void lookup_draft_kernel(const int32_t* hist, const int64_t* hist_off,
+                                                                const int32_t* kmax_arr, const int32_t* min_n_arr,
+                                                                int eos, int32_t* draft, int draft_ld,
+                                                                int32_t* ndraft) {
+    __shared__ int64_t wbest[LD_BLOCK / WAVE];
+    const int st = (int)blockIdx.x;
+    const int tid = threadIdx.x;
+    const int64_t h0 = hist_off[st];
+    const int64_t L = hist_off[st + 1] - h0;
+    const int32_t* h = hist + h0;
+    int kmax = kmax_arr ? kmax_arr[st] : draft_ld;
+    kmax = kmax < draft_ld ? kmax : draft_ld;
+    const int min_n = min_n_arr ? min_n_arr[st] : 2;
+    int d = 0;
+    for (int64_t n = (L - 1 < 4 ? L - 1 : 4); n >= min_n && kmax > 0; --n) {
+        int32_t t[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) t[q] = q < n ? h[L - n + q] : 0;
+        int64_t best = -1;
+        for (int64_t p = tid; p <= L - n - 1; p += LD_BLOCK) {
+            bool eq = true;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) eq = eq && (q >= n || h[p + q] == t[q]);
+            if (eq && h[p + n] != eos) best = p;               // p grows: the last hit is this thread's largest
+        }
+        best = wave_max(best);
+        if (lane_id() == 0) wbest[tid / WAVE] = best;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < LD_BLOCK / WAVE; ++w) best = wbest[w] > best ? wbest[w] : best;
+        __syncthreads();
+        if (best >= 0) {
+            if (tid == 0)
+                for (int64_t k = best + n; k < L && d < kmax; ++k) {
+                    if (h[k] == eos) break;
+                    draft[(int64_t)st * draft_ld + d++] = h[k];
+                }
+            break;
+        }
+    }
+    if (tid == 0) ndraft[st] = d;
+}
+
 // ------------------------------------------------------------------------------------------------ draw streams
 // std::mt19937_64 (the standard's parameters: n = 312, m = 156, r = 31, a = 0xB5026F5AA96619E9, tempering
 // u = 29 / d = 0x5555555555555555, s = 17 / b = 0x71D67FFFEDA60000, t = 37 / c = 0xFFF7EEE000000000, l = 43) per
@@ -2188,6 +2238,16 @@ int fs_penalize_batch(fs_context* ctx, float* d_logits, int64_t ld, int32_t B, i
     }
     hipLaunchKernelGGL(fs::penalize_kernel, dim3((unsigned)(B * nchunk)), dim3(fs::PEN_BLOCK), 0, (hipStream_t)stream,
                        d_logits, ld, V, d_hist, d_hist_off, d_params, (int)nchunk, ctx->err);
+    return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
+}
+
+int fs_lookup_draft(fs_context* ctx, int32_t n_streams, const int32_t* d_hist, const int64_t* d_hist_off,
+                    const int32_t* d_kmax, const int32_t* d_min_n, int32_t eos_id, int32_t* d_draft, int32_t draft_ld,
+                    int32_t* d_ndraft, void* stream) {
+    if (!ctx || n_streams < 0 || !d_hist_off || !d_draft || !d_ndraft || draft_ld < 1) return FS_E_INVALID;
+    if (n_streams == 0) return FS_OK;
+    hipLaunchKernelGGL(fs::lookup_draft_kernel, dim3((unsigned)n_streams), dim3(fs::LD_BLOCK), 0, (hipStream_t)stream,
+                       d_hist, d_hist_off, d_kmax, d_min_n, eos_id, d_draft, draft_ld, d_ndraft);
     return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
 }
 

@@ -301,6 +301,25 @@ def penalize_batch(logits, params, hist=None, hist_off=None, V=None, ctx=None, s
     return target
 
 
+def lookup_draft(hist, hist_off, kmax, min_n=None, eos_id=-1, draft_ld=None, ctx=None, stream=None):
+    """fs_lookup_draft: prompt-lookup drafts per stream (server.cpp:552-564). Returns (draft [S, draft_ld], n [S])."""
+    hist_off = torch.as_tensor(hist_off, dtype=torch.int64, device="cuda")
+    S = hist_off.numel() - 1
+    dev = hist_off.device
+    hist = torch.as_tensor(hist, dtype=torch.int32, device=dev)
+    km = torch.as_tensor(np.broadcast_to(np.asarray(kmax, np.int32), (S,)).copy(), device=dev)
+    mn = None if min_n is None else torch.as_tensor(np.broadcast_to(np.asarray(min_n, np.int32), (S,)).copy(),
+                                                     device=dev)
+    ld = int(draft_ld if draft_ld is not None else max(int(km.max().item()) if S else 1, 1))
+    draft = torch.zeros((S, ld), dtype=torch.int32, device=dev)
+    nd = torch.zeros(S, dtype=torch.int32, device=dev)
+    ctx = ctx or Context.default(dev)
+    with ctx.lock:
+        check(lib().fs_lookup_draft(ctx.h, S, _ptr(hist), _ptr(hist_off), _ptr(km), _ptr(mn), int(eos_id),
+                                    _ptr(draft), ld, _ptr(nd), _stream(stream)), "fs_lookup_draft")
+    return draft, nd
+
+
 def device_error(ctx=None, stream=None) -> int:
     ctx = ctx or Context.default()
     bits = ctypes.c_int32(0)

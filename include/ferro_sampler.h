@@ -104,6 +104,15 @@ int fs_rng_destroy(fs_rng* r);
 int fs_rng_next_u(fs_rng* r, double* u, int32_t n);
 int fs_rng_copy(const fs_rng* src, fs_rng* dst);
 
+/* Prompt-lookup drafting (src/server.cpp:552-564, src/lm_cli.cpp:145): for stream s with history
+ * d_hist[d_hist_off[s] .. d_hist_off[s+1]) (L tokens), the tokens that followed the most recent earlier
+ * occurrence of its last n tokens, trying n = min(4, L-1) down to d_min_n[s] (NULL: 2), at most d_kmax[s] (NULL:
+ * draft_ld; clamped to draft_ld), stopping before eos_id (-1: none); a match followed directly by eos is passed
+ * over. Writes d_draft[s*draft_ld + i] and d_ndraft[s] (0: no draft): the drafts that fs_verify then checks. */
+int fs_lookup_draft(fs_context* ctx, int32_t n_streams, const int32_t* d_hist, const int64_t* d_hist_off,
+                    const int32_t* d_kmax, const int32_t* d_min_n, int32_t eos_id, int32_t* d_draft, int32_t draft_ld,
+                    int32_t* d_ndraft, void* stream);
+
 /* Device draw streams: n_streams std::mt19937_64 engines held in device memory (seeds[s] from the host; 0 =
  * random, as ferro), drawing libstdc++ generate_canonical<double,53> values - ferro::Sampler's draw stream
  * (sampler.h:25,32; sampler.cpp:45-46) without a host round trip. Stream s owns rows d_row_off[s] ..

@@ -71,6 +71,8 @@ def lib():
         L.fso_sample_batch.restype = None
         L.fso_sample_batch.argtypes = [_P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, _P, _P, _P, _P, _P, _P, _P,
                                        ctypes.c_int, _P, _P, ctypes.c_int]
+        L.fso_lookup_draft.restype = ctypes.c_int
+        L.fso_lookup_draft.argtypes = [_P, ctypes.c_int64, ctypes.c_int, ctypes.c_int32, ctypes.c_int, _P]
         L.fso_verify.restype = None
         L.fso_verify.argtypes = [_P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, _P, _P, _P, _P, _P, _P,
                                  ctypes.c_int32, _P, _P]
@@ -170,6 +172,14 @@ class MT64:
 
     def next(self):
         return int(lib().fso_mt64_next(self._state))
+
+
+def lookup_draft(hist, kmax, eos=-1, min_n=2):
+    """server.cpp:552-564 restated in C (fso_lookup_draft)."""
+    h = np.ascontiguousarray(hist, np.int32)
+    out = np.zeros(max(kmax, 1), np.int32)
+    d = lib().fso_lookup_draft(_ptr(h), h.size, kmax, eos, min_n, _ptr(out))
+    return out[:d].copy()
 
 
 def canonical(x):

@@ -258,3 +258,27 @@ double fso_canonical(uint64_t x) {
     if (r >= 1.0) r = nextafter(1.0, 0.0);
     return r;
 }
+
+/* ------------------------------------------------------------------ prompt-lookup drafting: server.cpp:552-564 */
+/* The tokens that followed the most recent earlier occurrence of the history's last n tokens, for n = min(4, L-1)
+ * down to min_n; at most kmax of them, stopping before an eos token; a match whose continuation is empty (its next
+ * token is eos) is passed over. Writes the draft to out and returns its length (0: none). */
+int fso_lookup_draft(const int32_t* h, int64_t L, int kmax, int32_t eos, int min_n, int32_t* out) {
+    int64_t n;
+    for (n = (L - 1 < 4 ? L - 1 : 4); n >= min_n; --n) {
+        int64_t p;
+        for (p = L - n - 1; p >= 0; --p) {
+            int eq = 1;
+            for (int64_t k = 0; k < n; ++k)
+                if (h[p + k] != h[L - n + k]) { eq = 0; break; }
+            if (!eq) continue;
+            int d = 0;
+            for (int64_t k = p + n; k < L && d < kmax; ++k) {
+                if (h[k] == eos) break;
+                out[d++] = h[k];
+            }
+            if (d > 0) return d;
+        }
+    }
+    return 0;
+}

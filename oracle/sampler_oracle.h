@@ -57,6 +57,10 @@ void fso_verify(float* logits, int64_t ld, int n_streams, int n, const int32_t* 
                 const int32_t* hist, const int64_t* hist_off, const fso_params* params, const double* u,
                 int32_t eos_id, int32_t* tok, int32_t* accepted);
 
+/* Prompt-lookup drafting (server.cpp:552-564): the tokens that followed the most recent earlier occurrence of the
+ * last n tokens of h[0, L), n = min(4, L-1) down to min_n; at most kmax, stopping before eos. Returns the length. */
+int fso_lookup_draft(const int32_t* h, int64_t L, int kmax, int32_t eos, int min_n, int32_t* out);
+
 /* mt19937_64 (Matsumoto & Nishimura 2004 parameters, as std::mt19937_64) and the libstdc++ canonical mapping. */
 typedef struct fso_mt64 { uint64_t mt[312]; int mti; } fso_mt64;
 void fso_mt64_seed(fso_mt64* s, uint64_t seed);

@@ -496,3 +496,32 @@ def test_softcap_fused_read():
     np.testing.assert_array_equal(t2.cpu().numpy(), [O.sample(x[b], hists[b], O.make_params(
         temperature=0.0, repetition_penalty=1.05, softcap=30.0, frequency_penalty=float(p["frequency_penalty"][b]),
         presence_penalty=float(p["presence_penalty"][b])))[0] for b in range(B)])
+
+
+def test_lookup_draft_matches_oracle():
+    """fs_lookup_draft (server.cpp:552-564) on histories with copied runs, eos tokens and per-stream kmax / min_n,
+    including long histories."""
+    rng = np.random.default_rng(52)
+    E = 7
+    hists = []
+    for s_ in range(40):
+        L = int(rng.integers(0, 60)) if s_ < 30 else int(rng.integers(2000, 6000))
+        base = list(rng.integers(0, 12 if s_ % 3 == 0 else 400, L))
+        for _ in range(int(rng.integers(0, 4))):          # copy runs so that tails recur
+            if len(base) > 8:
+                a_ = int(rng.integers(0, len(base) - 6))
+                base += base[a_:a_ + int(rng.integers(2, 7))]
+        hists.append(np.asarray(base, np.int32))
+    off = np.concatenate([[0], np.cumsum([len(h) for h in hists])]).astype(np.int64)
+    hist = np.concatenate(hists).astype(np.int32)
+    kmax = rng.integers(0, 17, len(hists)).astype(np.int32)
+    min_n = rng.integers(2, 4, len(hists)).astype(np.int32)
+    draft, nd = F.lookup_draft(hist, off, kmax, min_n=min_n, eos_id=E, draft_ld=16)
+    draft, nd = draft.cpu().numpy(), nd.cpu().numpy()
+    hits = 0
+    for s_, h in enumerate(hists):
+        want = O.lookup_draft(h, int(kmax[s_]), eos=E, min_n=int(min_n[s_]))
+        assert nd[s_] == len(want), s_
+        np.testing.assert_array_equal(draft[s_, :nd[s_]], want)
+        hits += len(want) > 0
+    assert hits >= 10

@@ -219,3 +219,22 @@ def test_softcap_closed_form():
         np.testing.assert_array_equal(ids0, ids1)
         np.testing.assert_allclose(pr0, pr1, rtol=1e-5)          # tanh implementations differ by ulps
     assert (O.penalize(row, h, p1) == O.penalize(row, h, p0)).all()   # the penalty pass alone ignores softcap
+
+
+def test_lookup_draft_known_answers():
+    """server.cpp:552-564 on hand-built histories: the most recent match of the last n tokens (n = 4, 3, 2) wins;
+    a match followed by eos is passed over; the draft stops before eos and at kmax."""
+    h = [1, 2, 3, 4, 5, 1, 2, 3]                      # no 4-token repeat; the 3-token tail [1,2,3] occurs at 0
+    assert list(O.lookup_draft(h, 3)) == [4, 5, 1]
+    assert list(O.lookup_draft(h, 10)) == [4, 5, 1, 2, 3]
+    E = 99
+    h = [7, 8, 9, 2, 5, 7, 8, 9, E, 6, 7, 8, 9]       # most recent [7,8,9] is followed by eos: skipped
+    assert list(O.lookup_draft(h, 8, eos=E)) == [2, 5, 7, 8, 9]
+    assert list(O.lookup_draft(h, 8)) == [E, 6, 7, 8, 9]  # no eos: the most recent match wins
+    h = [4, 4, 4, 4, 4]                               # self-overlapping repeat: n = 4 matches at p = 0
+    assert list(O.lookup_draft(h, 5)) == [4]
+    assert list(O.lookup_draft([1, 2, 3, 1, 2], 4, min_n=3)) == []      # only a 2-token repeat
+    assert list(O.lookup_draft([1, 2, 3, 1, 2], 4, min_n=2)) == [3, 1, 2]
+    assert list(O.lookup_draft([5], 4)) == [] and list(O.lookup_draft([], 4)) == []
+    assert list(O.lookup_draft([5, 5], 4)) == []      # n = min(4, L-1) = 1 < min_n
+    assert list(O.lookup_draft([1, 2, 1, 2], 0)) == []  # kmax = 0: nothing to draft
