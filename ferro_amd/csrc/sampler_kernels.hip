@@ -480,8 +480,14 @@ __device__ __forceinline__ RowCtx row_ctx(const Args& a, int row) {
         rc.hA0 = ld_const(a.hist_off + rc.pidx);
         rc.lenA = ld_const(a.hist_off + rc.pidx + 1) - rc.hA0;
     }
-    if (a.params) rc.p = ld_const(a.params + rc.pidx);
-    else {
+    if (a.params) {                           // dword by dword: scalar loads (a struct copy becomes vector loads)
+        static_assert(sizeof(fs_row_params) % 4 == 0, "fs_row_params is a sequence of dwords");
+        uint32_t w[sizeof(fs_row_params) / 4];
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(a.params + rc.pidx);
+#pragma unroll
+        for (int i = 0; i < (int)(sizeof(fs_row_params) / 4); ++i) w[i] = ld_const(src + i);
+        __builtin_memcpy(&rc.p, w, sizeof(fs_row_params));
+    } else {
         rc.p.temperature = 0.f; rc.p.top_k = 1; rc.p.top_p = 1.f; rc.p.min_p = 0.f; rc.p.repetition_penalty = 1.f;
         rc.p.frequency_penalty = 0.f; rc.p.presence_penalty = 0.f; rc.p.repeat_last_n = 0; rc.p.penalty_from = 0;
         rc.p.softcap = 0.f;
@@ -1524,15 +1530,31 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
 struct SegStart {
     int seg_lo, ntiles;
     const float* rowp;
+    __amdgpu_buffer_rsrc_t rs;   // [seg_lo, seg_lo + ntiles * TILE) of the row
 };
+// Tile t of a segment through its buffer resource: a tile past the segment's end reads zeros without a memory
+// access, so the tile loop requests its next tiles unconditionally (straight-line loads keep the compiler's
+// memory-counter waits exact: consuming a tile waits for that tile only).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ f32x4 raw_buffer_load_f32x4(__amdgpu_buffer_rsrc_t rs, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.load.v4f32");
+__device__ __forceinline__ void load_seg_tile(float (&x)[TPT], __amdgpu_buffer_rsrc_t rs, int t) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const f32x4 v = raw_buffer_load_f32x4(rs, (j * BLOCK + (int)threadIdx.x) * 16, t * TILE * 4, 0);
+        x[4 * j + 0] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
+    }
+}
 __device__ __forceinline__ SegStart seg_start(const Args& a, int row, int seg, float (&buf)[PF][TPT]) {
     SegStart g;
     g.seg_lo = seg * a.seg_tiles * TILE;
     const int left = a.V / TILE - seg * a.seg_tiles;                // full tiles left in the row
     g.ntiles = left < a.seg_tiles ? left : a.seg_tiles;             // >= 1
     g.rowp = a.logits + (int64_t)row * a.ld;
+    g.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(g.rowp + g.seg_lo), (short)0, g.ntiles * TILE * 4,
+                                             0x00020000);
 #pragma unroll
-    for (int p = 0; p < PF; ++p) load_tile(buf[p], g.rowp, g.seg_lo + (p < g.ntiles ? p : 0) * TILE);
+    for (int p = 0; p < PF; ++p) load_seg_tile(buf[p], g.rs, p);
     return g;
 }
 
@@ -1541,7 +1563,6 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     const int tid = threadIdx.x;
     const int seg_lo = g.seg_lo;
     const int ntiles = g.ntiles;
-    const float* rowp = g.rowp;
 
     // the window ids (their loads return after the first tiles': the bitmap below waits for those anyway)
     constexpr int WPF = 2;
@@ -1595,9 +1616,11 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     uint32_t tkey = 0u;                // top-k: candidates are the logits with key >= tkey
     float tf = -__builtin_huge_valf(); //         in fp32: x >= tf (NaN never passes)
     uint32_t* rh = a.rhist + (int64_t)rc.row * RBINS;
-    uint32_t rcnt = 0u;                // row histogram read in flight: thread t holds bin rb0 + BLOCK-1-t
-    uint32_t rb0 = 0u;
-    bool rpending = false;
+    // row histogram reads: thread t holds bin b0 + BLOCK-1-t. Segments of >= 3 tiles read at tile 1 and use the
+    // read at tile 2, within one iteration of the tile loop (no load outstanding across its back edge); shorter
+    // segments read at tile 0 and use it after the loop.
+    uint32_t scnt = 0u, sb0 = 0u;
+    bool spending = false;
     if (tid == 0) s.count = 0u;
     __syncthreads();
 
@@ -1607,21 +1630,18 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
             tf = kq > 0x007FFFFFu ? val_of(kq) : -__builtin_huge_valf();   // keys below -inf's are NaN patterns
         }
     };
-    auto row_issue = [&]() {
-        rb0 = tkey >> RSHIFT;
-        const uint32_t b = rb0 + (uint32_t)(BLOCK - 1 - tid);
-        rcnt = ld_agent(rh + (b < (uint32_t)RBINS ? b : (uint32_t)RBINS - 1u));   // consumed a tile later
-        rpending = true;
+    auto row_read = [&](uint32_t b0) -> uint32_t {
+        const uint32_t b = b0 + (uint32_t)(BLOCK - 1 - tid);
+        return ld_agent(rh + (b < (uint32_t)RBINS ? b : (uint32_t)RBINS - 1u));
     };
     // the highest bin b (>= rb0) with at least k counted logits in bins [b, rb0 + BLOCK - 1]: a row-wide bound
-    auto row_take = [&]() {
+    auto row_take = [&](uint32_t rb0, uint32_t rcnt) {
         const uint32_t c = rb0 + (uint32_t)(BLOCK - 1 - tid) < (uint32_t)RBINS ? rcnt : 0u;
         uint32_t tot;
         const uint32_t above = block_excl_scan<uint32_t>(c, s.wsum, &tot);   // thread order = descending bins
         const int hit = (c != 0u && above + c >= (uint32_t)k) ? tid : BLOCK;
         const int first = block_min_i32(hit, s.red);
         if (first < BLOCK) raise_key((rb0 + (uint32_t)(BLOCK - 1 - first)) << RSHIFT);
-        rpending = false;
     };
     // count the n buffered candidates (all >= tkey) into the row histogram: LDS bins relative to tkey's bin, then
     // one global atomic per non-empty bin. A candidate beyond the LDS range is counted in a lower bin (still a
@@ -1693,6 +1713,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         }
         return n;
     };
+    static_assert(PF == 2, "the row read is issued and taken within one iteration of the tile loop");
     for (int pass = 0; pass < 2; ++pass) {
         const bool safe = pass == 1;
         bool overflow = false;
@@ -1743,7 +1764,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 }
                 topk_append(x, lo);
             }
-            if (PF < ntiles) load_tile(x, rowp, lo + PF * TILE);
+            load_seg_tile(x, g.rs, PF);
             if (topk) {
                 const int n = check();
                 overflow = n > CAP;
@@ -1751,34 +1772,48 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 R = safe ? 1 : (CAP - n) / (2 * per_tile);
                 if (R < 1) R = 1;
                 if (!safe && !overflow) row_count(n);
-                if (!safe && ntiles < 3) row_issue();    // short segments: read once, taken at the end
+                if (!safe && ntiles < 3) {               // short segments: read once, taken at the end
+                    sb0 = tkey >> RSHIFT;
+                    scnt = row_read(sb0);
+                    spending = true;
+                }
             } else if (slowpen) {
                 __syncthreads();                         // penalty-table reads of this tile are done
             }
         }
-        // ---- tiles 1.. (PF in flight; buffer p holds tiles p, p+PF, ...)
+        // ---- tiles 1.. (PF in flight; tile t is in buf[t % 2]). Iterations start at odd tiles, so the order in
+        // which the two buffers were requested is the same on entry and around the back edge.
         int since = 0;
-        for (int t0 = 0; t0 < ntiles && !overflow; t0 += PF) {
+        for (int t0 = 1; t0 < ntiles && !overflow; t0 += PF) {
+            const bool exch = topk && !safe && t0 == 1 && ntiles >= 3;   // tile 1 reads, tile 2 takes
+            uint32_t rcnt, rb0;                          // set at p == 0 wherever p == 1 takes them
 #pragma unroll
             for (int p = 0; p < PF; ++p) {
                 const int tt = t0 + p;
-                if (tt >= 1 && tt < ntiles && !overflow) {
+                float (&x)[TPT] = buf[(p + 1) & 1];
+                const bool live = tt < ntiles && !overflow;
+                if (live) {
                     const int lo = seg_lo + tt * TILE;
-                    float (&x)[TPT] = buf[p];
                     if (rc.capped) softcap_vals(x, rc.p.softcap);
                     if (slowpen) apply_penalties(x, a, rc, lo, s);
                     if (fastpen) bitmap_pen(x, lo);
                     if (rc.greedy) greedy_update(x, tt);
                     else topk_append(x, lo);
-                    if (tt + PF < ntiles) load_tile(x, rowp, lo + PF * TILE);
+                }
+                load_seg_tile(x, g.rs, tt + PF);         // past the end: zeros, no memory access
+                if (live) {
                     if (topk) {
                         if (++since >= R || slowpen) {
                             since = 0;
                             overflow = check() > CAP;   // uniform: every thread read the same count
                         }
-                        if (!safe && !overflow) {       // read the row bound at tile 1, use it at tile 3
-                            if (rpending && tt == 3) row_take();
-                            if (tt == 1 && !rpending) row_issue();
+                        if (exch && !overflow) {
+                            if (p == 0) {
+                                rb0 = tkey >> RSHIFT;
+                                rcnt = row_read(rb0);
+                            } else {
+                                row_take(rb0, rcnt);
+                            }
                         }
                     } else if (slowpen) {
                         __syncthreads();                 // penalty-table reads of this tile are done
@@ -1793,12 +1828,12 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         // (its logits are already counted in the row histogram).
         __syncthreads();
         if (tid == 0) s.count = 0u;
-        rpending = false;
+        spending = false;
 #pragma unroll
-        for (int p = 0; p < PF; ++p) load_tile(buf[p], rowp, seg_lo + (p < ntiles ? p : 0) * TILE);
+        for (int p = 0; p < PF; ++p) load_seg_tile(buf[p], g.rs, p);
         __syncthreads();
     }
-    if (topk && rpending) row_take();
+    if (topk && spending) row_take(sb0, scnt);
 
     // ---- publish this segment's candidates (read by the merge kernel after this kernel completes)
     const int nseg = a.nseg;
