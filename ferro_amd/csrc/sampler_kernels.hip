@@ -142,17 +142,61 @@ __device__ __forceinline__ uint32_t mbcnt(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+// Cross-lane moves for whole waves (every call site runs with all 64 lanes active). DPP moves and lane reads stay
+// in the VALU; the LDS permute path (__shfl*) costs an LDS round trip per step.
+template <int CTRL, int ROWMASK = 0xF>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {        // lanes without a source read 0
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWMASK, 0xF, false);
+}
+template <int CTRL, class T>
+__device__ __forceinline__ T dpp_move(T v) {
+    static_assert(sizeof(T) == 4 || sizeof(T) == 8, "32- or 64-bit lanes");
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, dpp32<CTRL>(__builtin_bit_cast(uint32_t, v)));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint64_t lo = dpp32<CTRL>((uint32_t)u), hi = dpp32<CTRL>((uint32_t)(u >> 32));
+        return __builtin_bit_cast(T, (hi << 32) | lo);
+    }
+}
+template <class T>
+__device__ __forceinline__ T read_lane(T v, int lane) {
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint64_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
+        const uint64_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), lane);
+        return __builtin_bit_cast(T, (hi << 32) | lo);
+    }
+}
+// op over the wave, result uniform: butterflies within each row of 16 lanes (quad swaps, half-row and row
+// mirrors), then the four rows' lane 0
+template <class T, class Op>
+__device__ __forceinline__ T wave_allreduce(T v, Op op) {
+    v = op(v, dpp_move<0xB1>(v));     // quad_perm [1,0,3,2]
+    v = op(v, dpp_move<0x4E>(v));     // quad_perm [2,3,0,1]
+    v = op(v, dpp_move<0x141>(v));    // row_half_mirror
+    v = op(v, dpp_move<0x140>(v));    // row_mirror
+    return op(op(read_lane(v, 0), read_lane(v, 16)), op(read_lane(v, 32), read_lane(v, 48)));
+}
 template <class T>
 __device__ __forceinline__ T wave_max(T v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) { const T w = __shfl_xor(v, o); v = w > v ? w : v; }
-    return v;
+    return wave_allreduce(v, [](T x, T y) { return y > x ? y : x; });
 }
 template <class T>
 __device__ __forceinline__ T wave_min(T v) {
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) { const T w = __shfl_xor(v, o); v = w < v ? w : v; }
-    return v;
+    return wave_allreduce(v, [](T x, T y) { return y < x ? y : x; });
+}
+// inclusive sum over lanes 0..lane (32-bit integers): row shifts 1, 2, 4, 8, then row broadcasts 15 and 31
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t x) {
+    x += dpp32<0x111>(x);
+    x += dpp32<0x112>(x);
+    x += dpp32<0x114>(x);
+    x += dpp32<0x118>(x);
+    x += dpp32<0x142, 0xA>(x);
+    x += dpp32<0x143, 0xC>(x);
+    return x;
 }
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
@@ -242,14 +286,20 @@ __device__ __forceinline__ double block_sum_f64(double v, Red& r) {
 template <class T>
 __device__ __forceinline__ T block_excl_scan(T v, T* wsum /*NWAVES*/, T* total) {
     const int lane = lane_id(), w = threadIdx.x / WAVE;
-    T x = v;
+    T x, ex;
+    if constexpr (sizeof(T) == 4 && T(-1) > T(0)) {            // 32-bit unsigned: DPP scan (exact in any order)
+        x = wave_incl_scan_u32(v);
+        ex = x - v;
+    } else {                                                   // the fixed shuffle order of the double sums
+        x = v;
 #pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-        const T y = __shfl_up(x, o);
-        if (lane >= o) x += y;
+        for (int o = 1; o < WAVE; o <<= 1) {
+            const T y = __shfl_up(x, o);
+            if (lane >= o) x += y;
+        }
+        ex = __shfl_up(x, 1);
+        if (lane == 0) ex = T(0);
     }
-    T ex = __shfl_up(x, 1);
-    if (lane == 0) ex = T(0);
     if (lane == WAVE - 1) wsum[w] = x;
     __syncthreads();
     T off = T(0), tot = T(0);
