@@ -478,7 +478,8 @@ struct Shared {
     int32_t ids[WIDS];                 // the penalty window's ids that fall in the current segment
     uint32_t wsum[NWAVES];
     uint32_t count;
-    uint32_t flag;
+    uint32_t tmin;                     // segment kernel: the smallest of the waves' tile-0 bounds
+    uint32_t rc64[WAVE];               // segment kernel: tile-0 row counts, coarse bins above T0's
     uint32_t nids;
     Red red;
     __device__ __forceinline__ uint32_t* cnt() { return scr; }
@@ -1670,8 +1671,9 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     // read at tile 2, within one iteration of the tile loop (no load outstanding across its back edge); shorter
     // segments read at tile 0 and use it after the loop.
     uint32_t scnt = 0u, sb0 = 0u;
+    uint32_t rc0 = 0u;                 // coarse bin of T0: base of the tile-0 row counts
     bool spending = false;
-    if (tid == 0) s.count = 0u;
+    if (tid == 0) { s.count = 0u; s.tmin = 0xFFFFFFFFu; }
     __syncthreads();
 
     auto raise_key = [&](uint32_t kq) {
@@ -1693,27 +1695,6 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         const int first = block_min_i32(hit, s.red);
         if (first < BLOCK) raise_key((rb0 + (uint32_t)(BLOCK - 1 - first)) << RSHIFT);
     };
-    // count the n buffered candidates (all >= tkey) into the row histogram: LDS bins relative to tkey's bin, then
-    // one global atomic per non-empty bin. A candidate beyond the LDS range is counted in a lower bin (still a
-    // valid count for every threshold at or below that bin).
-    auto row_count = [&](int n) {
-        const uint32_t rb = tkey >> RSHIFT;
-        for (int i = tid; i < NBINS; i += BLOCK) s.bins()[i] = 0u;
-        __syncthreads();
-        for (int i = tid; i < n; i += BLOCK) {
-            const uint32_t b = (comp_key(s.cand[i]) >> RSHIFT) - rb;
-            atomicAdd(&s.bins()[b < (uint32_t)NBINS ? b : (uint32_t)NBINS - 1u], 1u);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < NBINS / BLOCK; ++q) {
-            const uint32_t bi = (uint32_t)(q * BLOCK + tid);
-            const uint32_t c = s.bins()[bi];
-            const uint32_t g = rb + bi < (uint32_t)RBINS ? rb + bi : (uint32_t)RBINS - 1u;
-            if (c != 0u) __hip_atomic_fetch_add(rh + g, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    };
-
     // Top-k buffer discipline: after tile 0 the buffer is checked (barrier) only every R tiles, R sized so the
     // expected appends fill at most half the headroom; an overflow (appends past CAP are dropped) is detected at
     // the next check and the segment is streamed again in safe mode (a check after every tile).
@@ -1778,50 +1759,63 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
             if (rc.greedy) {
                 greedy_update(x, 0);
             } else {
-                if (!safe) {                             // k <= KMAX < TILE
-                    // maxima of >= 2k groups of tile 0 (G per thread), histogrammed over their [min, max]:
-                    // at least k of the tile's logits reach T0
-                    int G = 1;
-                    while (G * BLOCK < 2 * k && G < TPT) G <<= 1;
-                    const int per = TPT / G;
-                    uint32_t gmin = 0xFFFFFFFFu, gmax = 0u;
-                    uint32_t gm = 0u;
+                if (!safe) {
+                    // T0: in each wave, the kw-th largest (kw = ceil(k / NWAVES)) of the lanes' two largest keys
+                    // (128 logits), to its top 16 key bits, by bisection on wave ballots; the smallest over the
+                    // waves. kw logits of every wave reach it: k logits of the tile reach T0. (kw > 128: no bound;
+                    // the check after this tile compacts the buffer to the exact k-th.)
+                    uint32_t m1 = 0u, m2 = 0u;
 #pragma unroll
                     for (int i = 0; i < TPT; ++i) {
                         const uint32_t kq = key_of(x[i]);
-                        gm = kq > gm ? kq : gm;
-                        if ((i + 1) % per == 0) {
-                            gmin = gm < gmin ? gm : gmin;
-                            gmax = gm > gmax ? gm : gmax;
-                            gm = 0u;
-                        }
+                        const uint32_t lo2 = kq < m1 ? kq : m1;
+                        m2 = lo2 > m2 ? lo2 : m2;
+                        m1 = kq > m1 ? kq : m1;
                     }
-                    for (int i = tid; i < NBINS; i += BLOCK) s.bins()[i] = 0u;
-                    block_minmax_u32(gmin, gmax, s.red);
-                    const int sh = range_shift(gmin, gmax);
+                    const int kw = (k + NWAVES - 1) / NWAVES;
+                    uint32_t T = 0u;
+                    if (kw <= 2 * WAVE) {
 #pragma unroll
-                    for (int i = 0; i < TPT; ++i) {
-                        const uint32_t kq = key_of(x[i]);
-                        gm = kq > gm ? kq : gm;
-                        if ((i + 1) % per == 0) {
-                            atomicAdd(&s.bins()[(gm - gmin) >> sh], 1u);
-                            gm = 0u;
+                        for (int b = 31; b >= 16; --b) {
+                            const uint32_t c = T | (1u << b);
+                            if (__popcll(__ballot(m1 >= c)) + __popcll(__ballot(m2 >= c)) >= kw) T = c;
                         }
                     }
+                    if (lane_id() == 0) atomicMin(&s.tmin, T);
+                    if (tid < WAVE) s.rc64[tid] = 0u;
                     __syncthreads();
-                    uint32_t c0;
-                    raise_key(hist_threshold(s.bins(), gmin, sh, k, &c0, s.wsum, s.red));
+                    raise_key(s.tmin);
                 }
                 topk_append(x, lo);
+                if (!safe) {
+                    // row counts: this lane's tile-0 logits >= T0, all counted at the coarse bin of the lowest of
+                    // them (at or below each one's own bin: every row-wide bound read back stays valid), gathered
+                    // in LDS over the 64 coarse bins from T0's (higher ones at the 64th) and added to the row
+                    // histogram after the check below
+                    uint32_t c = 0u, lowk = 0xFFFFFFFFu;
+#pragma unroll
+                    for (int i = 0; i < TPT; ++i) {             // branch-free
+                        const uint32_t kq = key_of(x[i]);
+                        const bool in = x[i] >= tf;
+                        c += in ? 1u : 0u;
+                        lowk = (in && kq < lowk) ? kq : lowk;
+                    }
+                    rc0 = tkey >> RSHIFT;
+                    const uint32_t d = (lowk >> RSHIFT) - rc0;
+                    if (c != 0u) atomicAdd(&s.rc64[d < (uint32_t)WAVE ? d : (uint32_t)WAVE - 1u], c);
+                }
             }
             load_seg_tile(x, g.rs, PF);
             if (topk) {
                 const int n = check();
                 overflow = n > CAP;
+                if (!safe && tid < WAVE) {
+                    const uint32_t c = s.rc64[tid];
+                    if (c != 0u) __hip_atomic_fetch_add(rh + rc0 + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
                 const int per_tile = n > 32 ? n : 32;
                 R = safe ? 1 : (CAP - n) / (2 * per_tile);
                 if (R < 1) R = 1;
-                if (!safe && !overflow) row_count(n);
                 if (!safe && ntiles < 3) {               // short segments: read once, taken at the end
                     sb0 = tkey >> RSHIFT;
                     scnt = row_read(sb0);
