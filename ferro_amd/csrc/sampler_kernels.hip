@@ -55,6 +55,7 @@ constexpr int NBINS = 1 << HBITS;         // threshold histograms
 constexpr int SMALL = 512;                // rank-sort capacity of the merge
 constexpr int MAX_SEGS = 1024;            // segments per row
 constexpr int SPEC = 8;                   // merge gather: loads in flight per thread per round
+constexpr int FAST_SEGS = 64;             // merge fast path: a wave reads every list's bound and count
 constexpr int RBITS = 12;                 // row histogram: bins of the top key bits, shared by a row's segments
 constexpr int RBINS = 1 << RBITS;
 constexpr int RSHIFT = 32 - RBITS;
@@ -84,7 +85,6 @@ struct Args {
     int mode;
     int nseg;                      // segments per row
     int seg_tiles;                 // tiles per segment
-    int seg_grid;                  // segment workgroups (the merge workgroups follow, one per row)
     uint64_t* cand;                // [B*nseg][CAP]
     uint32_t* meta;                // [B*nseg][2]: lower bound of the k-th key, count
     uint32_t* row_cnt;             // [B] segment completion counters, left at 0
@@ -232,6 +232,16 @@ __device__ __forceinline__ uint64_t block_min_u64(uint64_t v, Red& r) {
     uint64_t m = r.u64[0];
 #pragma unroll
     for (int w = 1; w < NWAVES; ++w) m = r.u64[w] < m ? r.u64[w] : m;
+    __syncthreads();
+    return m;
+}
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, Red& r) {
+    v = wave_max(v);
+    if (lane_id() == 0) r.u32[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    uint32_t m = r.u32[0];
+#pragma unroll
+    for (int w = 1; w < NWAVES; ++w) m = r.u32[w] > m ? r.u32[w] : m;
     __syncthreads();
     return m;
 }
@@ -1252,6 +1262,60 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             if (a.cand_probs && a.kcap > 0) a.cand_probs[(int64_t)row * a.kcap] = 1.0;
         }
     } else {
+        // ---- fast path: no tail, every list inside its prefetched window, k <= 64. L (the largest list bound)
+        // comes from a wave reduction over the lists' bounds; T1 from a histogram of the prefetched registers over
+        // [L, max]; the <= 128 candidates reaching T1 are ranked and finished by wave 0. Any other shape (or more
+        // than 128 candidates at T1) takes the general path below.
+        bool fast_done = false;
+        if (ntail == 0 && k <= WAVE && nseg <= FAST_SEGS) {
+            uint32_t L = 0u, cmax = 0u;               // every wave reads all the (bound, count) pairs: no barrier
+            const int j = lane_id();
+            if (j < nseg) {
+                const uint32_t* mrow = a.meta + 2 * ((int64_t)row * nseg + j);
+                L = ld_agent(mrow);
+                cmax = ld_agent(mrow + 1);
+            }
+            L = wave_max(L);
+            cmax = wave_max(cmax);
+            if (cmax <= (uint32_t)(SPEC * pre.tps)) {
+                for (int i = tid; i < NBINS; i += BLOCK) s.bins()[i] = 0u;
+                {                                     // the segments' row histogram is spent: leave it at 0
+                    uint4* rz = reinterpret_cast<uint4*>(a.rhist + (int64_t)row * RBINS);
+                    for (int i = tid; i < RBINS / 4; i += BLOCK) rz[i] = make_uint4(0u, 0u, 0u, 0u);
+                }
+                bool in[SPEC];
+                uint32_t kmax = L;
+#pragma unroll
+                for (int q = 0; q < SPEC; ++q) {
+                    const uint64_t w = pre.v[q];
+                    in[q] = pre.act && (uint32_t)(pre.r_me + q * pre.tps) < pre.cnm && w != 0 && comp_key(w) >= L;
+                    if (in[q]) kmax = comp_key(w) > kmax ? comp_key(w) : kmax;
+                }
+                kmax = block_max_u32(kmax, s.red);            // its barrier also orders the zeroed bins
+                const int sh = range_shift(L, kmax);
+#pragma unroll
+                for (int q = 0; q < SPEC; ++q)
+                    if (in[q]) atomicAdd(&s.bins()[(comp_key(pre.v[q]) - L) >> sh], 1u);
+                __syncthreads();
+                uint32_t c1;
+                const uint32_t T1 = hist_threshold(s.bins(), L, sh, k, &c1, s.wsum, s.red);
+                if (c1 >= (uint32_t)k && c1 <= (uint32_t)(2 * WAVE)) {
+                    uint64_t* small_in = reinterpret_cast<uint64_t*>(s.bins());
+                    uint64_t* small_out = small_in + SMALL;
+                    if (tid == 0) s.count = 0u;
+                    __syncthreads();
+#pragma unroll
+                    for (int q = 0; q < SPEC; ++q)
+                        wave_append(in[q] && comp_key(pre.v[q]) >= T1, pre.v[q], small_in, &s.count, SMALL);
+                    __syncthreads();
+                    uint32_t* rk = reinterpret_cast<uint32_t*>(small_out + 2 * WAVE);   // past wave_finish's buffers
+                    block_ranks(small_in, (int)c1, rk);
+                    if (tid < WAVE) wave_finish(a, rc, small_in, rk, k, reinterpret_cast<double*>(small_out), tok, keep);
+                    fast_done = true;
+                }
+            }
+        }
+        if (!fast_done) {
         // ---- the tail's own top k becomes one more list, kept in LDS at the top of the candidate buffer
         // (tl[0, nt); ttkey bounds the k-th key if the tail holds at least k candidates); the gather below then
         // fills at most gcap entries
@@ -1535,6 +1599,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 }
             }
         }
+        }                                             // general path
     }
     }
     if (a.mode != MODE_VERIFY) {
@@ -1931,17 +1996,15 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, 
     __shared__ __align__(16) Shared s;
     a.logits = logits; a.ld = ld; a.B = B; a.V = V; a.nseg = nseg; a.seg_tiles = seg_tiles; a.params = params;
     a.hist_off = hist_off;
-    const int total = a.B * a.nseg;
-    for (int item = (int)blockIdx.x; item < total; item += (int)gridDim.x) {
-        // uniform by construction; readfirstlane lets the compiler use scalar loads for the row's parameters
-        const int row = __builtin_amdgcn_readfirstlane(item / a.nseg);
-        const int seg = item - row * a.nseg;
-        float buf[PF][TPT];
-        const SegStart g = seg_start(a, row, seg, buf);   // the tiles are on their way before the parameters
-        const RowCtx rc = row_ctx(a, row);
-        if (rc.large) continue;                    // the merge kernel samples the whole row
-        process_segment(a, rc, seg, s, buf, g);
-    }
+    const int item = (int)blockIdx.x;                // one (row, segment) item per workgroup
+    // uniform by construction; readfirstlane lets the compiler use scalar loads for the row's parameters
+    const int row = __builtin_amdgcn_readfirstlane(item / a.nseg);
+    const int seg = item - row * a.nseg;
+    float buf[PF][TPT];
+    const SegStart g = seg_start(a, row, seg, buf);   // the tiles are on their way before the parameters
+    const RowCtx rc = row_ctx(a, row);
+    if (rc.large) return;                            // the merge kernel samples the whole row
+    process_segment(a, rc, seg, s, buf, g);
 }
 
 // Merge kernel: one workgroup per row, after the segment kernel. The segment lists are requested first, so their
@@ -2214,8 +2277,7 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
     if (a.nseg > fs::MAX_SEGS) return FS_E_INVALID;
     const int64_t items = rows * a.nseg;
     if (items > 0x7fffffff) return FS_E_INVALID;
-    const int64_t seg_grid = items < 2 * (int64_t)ctx->cus ? items : 2 * (int64_t)ctx->cus;
-    a.seg_grid = (int)seg_grid;
+    const int64_t seg_grid = items;                // one workgroup per (row, segment)
     int rc = grow(ctx, (size_t)(items + rows), (size_t)rows, (size_t)(streams > 0 ? streams : 1));
     if (rc != FS_OK) return rc;
     a.cand = ctx->cand; a.meta = ctx->meta; a.row_cnt = ctx->row_cnt; a.rhist = ctx->rhist;
