@@ -1810,6 +1810,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         return n;
     };
     static_assert(PF == 2, "the row read is issued and taken within one iteration of the tile loop");
+    float x0[TPT];                     // tile 0 of a segment of >= 3 tiles, appended once the row bound is taken
     for (int pass = 0; pass < 2; ++pass) {
         const bool safe = pass == 1;
         bool overflow = false;
@@ -1851,7 +1852,12 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     __syncthreads();
                     raise_key(s.tmin);
                 }
-                topk_append(x, lo);
+                if (!safe && ntiles >= 3) {              // tile 0 joins the buffer at tile 2, after the row bound
+#pragma unroll
+                    for (int i = 0; i < TPT; ++i) x0[i] = x[i];
+                } else {
+                    topk_append(x, lo);
+                }
                 if (!safe) {
                     // row counts: this lane's tile-0 logits >= T0, all counted at the coarse bin of the lowest of
                     // them (at or below each one's own bin: every row-wide bound read back stays valid), gathered
@@ -1922,6 +1928,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                                 rcnt = row_read(rb0);
                             } else {
                                 row_take(rb0, rcnt);
+                                topk_append(x0, seg_lo); // tile 0, held since its bound was taken
                             }
                         }
                     } else if (slowpen) {
