@@ -1642,6 +1642,44 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
 //     whole row's evidence instead of one segment's.
 // The segment publishes its candidates with key >= the final tkey (plain stores; the merge kernel runs after this
 // kernel). They include every logit of the row's top k that lies in this segment.
+// A wave's snapshot of its row's histogram: lane l holds the counts of bins b0 + 4 (63 - l) + j, j = 0..3, where
+// b0 is the wave's current bound's bin rounded down to a multiple of 4: the 256 bins (32 binades) from the bound
+// up, in lane order = descending bins; counts above the window are left out (fewer counts: the bound stays
+// valid). Agent-scope loads: the counts come from every segment of the row, on any XCD.
+struct RowSnap {
+    uint64_t w[2];
+    uint32_t b0;
+};
+__device__ __forceinline__ RowSnap row_snap(const uint32_t* rh, uint32_t tkey) {
+    RowSnap r;
+    r.b0 = (tkey >> RSHIFT) & ~3u;
+    const uint32_t first = r.b0 + 4u * (uint32_t)(WAVE - 1 - lane_id());
+    const uint32_t f = first <= (uint32_t)RBINS - 4u ? first : (uint32_t)RBINS - 4u;   // past the top: ignored
+    const uint64_t* p = reinterpret_cast<const uint64_t*>(rh + f);
+    r.w[0] = ld_agent(p);
+    r.w[1] = ld_agent(p + 1);
+    return r;
+}
+// From a snapshot: the lower edge of the highest bin with at least k counted logits in it and the bins above. At
+// least k logits of the row reach it, so it bounds the row's k-th key from below (0: the snapshot holds fewer than
+// k). No barrier: each wave takes its own snapshot, and any snapshot gives a valid bound.
+__device__ __forceinline__ uint32_t row_bound(const RowSnap& r, int k) {
+    const int lane = lane_id();
+    const uint32_t first = r.b0 + 4u * (uint32_t)(WAVE - 1 - lane);
+    const bool valid = first <= (uint32_t)RBINS - 4u;
+    const uint32_t c0 = valid ? (uint32_t)r.w[0] : 0u, c1 = valid ? (uint32_t)(r.w[0] >> 32) : 0u;
+    const uint32_t c2 = valid ? (uint32_t)r.w[1] : 0u, c3 = valid ? (uint32_t)(r.w[1] >> 32) : 0u;
+    const uint32_t mine = c0 + c1 + c2 + c3;
+    const uint32_t cum = wave_incl_scan_u32(mine);
+    const uint32_t ex = cum - mine;
+    const bool hit = ex < (uint32_t)k && cum >= (uint32_t)k;
+    const uint32_t a3 = ex + c3, a2 = a3 + c2, a1 = a2 + c1;
+    const uint32_t bin = first + (a3 >= (uint32_t)k ? 3u : a2 >= (uint32_t)k ? 2u : a1 >= (uint32_t)k ? 1u : 0u);
+    const uint64_t hb = __ballot(hit);
+    if (hb == 0ull) return 0u;
+    return (uint32_t)__builtin_amdgcn_readlane((int)bin, __ffsll((unsigned long long)hb) - 1) << RSHIFT;
+}
+
 // The first PF tiles of a segment, requested from the kernel arguments alone (before the row's parameters arrive).
 struct SegStart {
     int seg_lo, ntiles;
@@ -1732,9 +1770,10 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     uint32_t tkey = 0u;                // top-k: candidates are the logits with key >= tkey
     float tf = -__builtin_huge_valf(); //         in fp32: x >= tf (NaN never passes)
     uint32_t* rh = a.rhist + (int64_t)rc.row * RBINS;
-    // row histogram reads: thread t holds bin b0 + BLOCK-1-t. Segments of >= 3 tiles read at tile 1 and use the
-    // read at tile 2, within one iteration of the tile loop (no load outstanding across its back edge); shorter
-    // segments read at tile 0 and use it after the loop.
+    // Row bounds from the row histogram. Segments of >= 3 tiles: each wave snapshots it after tile 0 and takes the
+    // bound before appending tile 1; segments of >= 5 tiles snapshot again at tile 3 and take at tile 4, within one
+    // iteration of the tile loop (no load outstanding across its back edge).
+    // Shorter segments: one block-wide read at tile 0 (thread t holds bin b0 + BLOCK-1-t), taken after the loop.
     uint32_t scnt = 0u, sb0 = 0u;
     uint32_t rc0 = 0u;                 // coarse bin of T0: base of the tile-0 row counts
     bool spending = false;
@@ -1810,7 +1849,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         return n;
     };
     static_assert(PF == 2, "the row read is issued and taken within one iteration of the tile loop");
-    float x0[TPT];                     // tile 0 of a segment of >= 3 tiles, appended once the row bound is taken
+    RowSnap snap1;                     // the row histogram after tile 0 (segments of >= 3 tiles)
     for (int pass = 0; pass < 2; ++pass) {
         const bool safe = pass == 1;
         bool overflow = false;
@@ -1852,12 +1891,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     __syncthreads();
                     raise_key(s.tmin);
                 }
-                if (!safe && ntiles >= 3) {              // tile 0 joins the buffer at tile 2, after the row bound
-#pragma unroll
-                    for (int i = 0; i < TPT; ++i) x0[i] = x[i];
-                } else {
-                    topk_append(x, lo);
-                }
+                topk_append(x, lo);
                 if (!safe) {
                     // row counts: this lane's tile-0 logits >= T0, all counted at the coarse bin of the lowest of
                     // them (at or below each one's own bin: every row-wide bound read back stays valid), gathered
@@ -1884,6 +1918,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     const uint32_t c = s.rc64[tid];
                     if (c != 0u) __hip_atomic_fetch_add(rh + rc0 + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
+                if (!safe && ntiles >= 3) snap1 = row_snap(rh, tkey);
                 const int per_tile = n > 32 ? n : 32;
                 R = safe ? 1 : (CAP - n) / (2 * per_tile);
                 if (R < 1) R = 1;
@@ -1900,8 +1935,9 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         // which the two buffers were requested is the same on entry and around the back edge.
         int since = 0;
         for (int t0 = 1; t0 < ntiles && !overflow; t0 += PF) {
-            const bool exch = topk && !safe && t0 == 1 && ntiles >= 3;   // tile 1 reads, tile 2 takes
-            uint32_t rcnt, rb0;                          // set at p == 0 wherever p == 1 takes them
+            const bool take1 = topk && !safe && t0 == 1 && ntiles >= 3;   // bound before tile 1
+            const bool snap = topk && !safe && t0 == 3 && ntiles >= 5;    // snapshot at tile 3, bound before tile 4
+            RowSnap snap2;
 #pragma unroll
             for (int p = 0; p < PF; ++p) {
                 const int tt = t0 + p;
@@ -1912,6 +1948,8 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     if (rc.capped) softcap_vals(x, rc.p.softcap);
                     if (slowpen) apply_penalties(x, a, rc, lo, s);
                     if (fastpen) bitmap_pen(x, lo);
+                    if (p == 0 && take1) raise_key(row_bound(snap1, k));
+                    if (p == 1 && snap) raise_key(row_bound(snap2, k));
                     if (rc.greedy) greedy_update(x, tt);
                     else topk_append(x, lo);
                 }
@@ -1922,15 +1960,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                             since = 0;
                             overflow = check() > CAP;   // uniform: every thread read the same count
                         }
-                        if (exch && !overflow) {
-                            if (p == 0) {
-                                rb0 = tkey >> RSHIFT;
-                                rcnt = row_read(rb0);
-                            } else {
-                                row_take(rb0, rcnt);
-                                topk_append(x0, seg_lo); // tile 0, held since its bound was taken
-                            }
-                        }
+                        if (p == 0 && snap) snap2 = row_snap(rh, tkey);
                     } else if (slowpen) {
                         __syncthreads();                 // penalty-table reads of this tile are done
                     }
