@@ -1291,6 +1291,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                     in[q] = pre.act && (uint32_t)(pre.r_me + q * pre.tps) < pre.cnm && w != 0 && comp_key(w) >= L;
                     if (in[q]) kmax = comp_key(w) > kmax ? comp_key(w) : kmax;
                 }
+                if (tid == 0) s.count = 0u;
                 kmax = block_max_u32(kmax, s.red);            // its barrier also orders the zeroed bins
                 const int sh = range_shift(L, kmax);
 #pragma unroll
@@ -1300,10 +1301,8 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 uint32_t c1;
                 const uint32_t T1 = hist_threshold(s.bins(), L, sh, k, &c1, s.wsum, s.red);
                 if (c1 >= (uint32_t)k && c1 <= (uint32_t)(2 * WAVE)) {
-                    uint64_t* small_in = reinterpret_cast<uint64_t*>(s.bins());
+                    uint64_t* small_in = s.cand;              // the candidate buffer is unused on this path
                     uint64_t* small_out = small_in + SMALL;
-                    if (tid == 0) s.count = 0u;
-                    __syncthreads();
 #pragma unroll
                     for (int q = 0; q < SPEC; ++q)
                         wave_append(in[q] && comp_key(pre.v[q]) >= T1, pre.v[q], small_in, &s.count, SMALL);
