@@ -488,8 +488,8 @@ struct Shared {
     int32_t ids[WIDS];                 // the penalty window's ids that fall in the current segment
     uint32_t wsum[NWAVES];
     uint32_t count;
-    uint32_t tmin;                     // segment kernel: the smallest of the waves' tile-0 bounds
-    uint32_t rc64[WAVE];               // segment kernel: tile-0 row counts, coarse bins above T0's
+    uint32_t tmax;                     // segment kernel: the largest key of tile 0
+    uint32_t rc64[WAVE];               // segment kernel: tile-0 counts in the 64 coarse bins up to tmax's
     uint32_t nids;
     Red red;
     __device__ __forceinline__ uint32_t* cnt() { return scr; }
@@ -1774,9 +1774,10 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     // iteration of the tile loop (no load outstanding across its back edge).
     // Shorter segments: one block-wide read at tile 0 (thread t holds bin b0 + BLOCK-1-t), taken after the loop.
     uint32_t scnt = 0u, sb0 = 0u;
-    uint32_t rc0 = 0u;                 // coarse bin of T0: base of the tile-0 row counts
+    uint32_t rc0 = 0u;                 // lowest coarse bin of the tile-0 counts
     bool spending = false;
-    if (tid == 0) { s.count = 0u; s.tmin = 0xFFFFFFFFu; }
+    if (tid == 0) { s.count = 0u; s.tmax = 0u; }
+    if (tid < WAVE) s.rc64[tid] = 0u;
     __syncthreads();
 
     auto raise_key = [&](uint32_t kq) {
@@ -1864,59 +1865,49 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 greedy_update(x, 0);
             } else {
                 if (!safe) {
-                    // T0: in each wave, the kw-th largest (kw = ceil(k / NWAVES)) of the lanes' two largest keys
-                    // (128 logits), to its top 16 key bits, by bisection on wave ballots; the smallest over the
-                    // waves. kw logits of every wave reach it: k logits of the tile reach T0. (kw > 128: no bound;
-                    // the check after this tile compacts the buffer to the exact k-th.)
-                    uint32_t m1 = 0u, m2 = 0u;
+                    // T0 and the row counts from the tile's lane maxima (all 8 logits of a lane when k > 64): a
+                    // histogram over the 64 coarse bins up to the tile's largest key (rc0 = its lowest), in LDS.
+                    // Its bins go to the row histogram at once, and T0 = the lower edge of the highest bin with at
+                    // least k counted logits at or above it. Logits below the 64 bins are not counted (fewer
+                    // counts: every bound read from them stays valid).
+                    uint32_t kq[TPT];
+                    uint32_t m1 = 0u;
 #pragma unroll
                     for (int i = 0; i < TPT; ++i) {
-                        const uint32_t kq = key_of(x[i]);
-                        const uint32_t lo2 = kq < m1 ? kq : m1;
-                        m2 = lo2 > m2 ? lo2 : m2;
-                        m1 = kq > m1 ? kq : m1;
+                        kq[i] = key_of(x[i]);
+                        m1 = kq[i] > m1 ? kq[i] : m1;
                     }
-                    const int kw = (k + NWAVES - 1) / NWAVES;
-                    uint32_t T = 0u;
-                    if (kw <= 2 * WAVE) {
-#pragma unroll
-                        for (int b = 31; b >= 16; --b) {
-                            const uint32_t c = T | (1u << b);
-                            if (__popcll(__ballot(m1 >= c)) + __popcll(__ballot(m2 >= c)) >= kw) T = c;
-                        }
-                    }
-                    if (lane_id() == 0) atomicMin(&s.tmin, T);
-                    if (tid < WAVE) s.rc64[tid] = 0u;
+                    const uint32_t wm = wave_max(m1);
+                    if (lane_id() == 0) atomicMax(&s.tmax, wm);
                     __syncthreads();
-                    raise_key(s.tmin);
+                    const uint32_t topb = s.tmax >> RSHIFT;
+                    rc0 = topb >= (uint32_t)(WAVE - 1) ? topb - (uint32_t)(WAVE - 1) : 0u;
+                    if (k > WAVE) {
+#pragma unroll
+                        for (int i = 0; i < TPT; ++i) {
+                            const uint32_t d = (kq[i] >> RSHIFT) - rc0;
+                            if (d < (uint32_t)WAVE) atomicAdd(&s.rc64[d], 1u);
+                        }
+                    } else {
+                        const uint32_t d = (m1 >> RSHIFT) - rc0;
+                        if (d < (uint32_t)WAVE) atomicAdd(&s.rc64[d], 1u);
+                    }
+                    __syncthreads();
+                    const uint32_t cb = s.rc64[WAVE - 1 - lane_id()];   // lane order = descending bins
+                    const uint64_t hb = __ballot(wave_incl_scan_u32(cb) >= (uint32_t)k);
+                    if (hb != 0ull)
+                        raise_key((rc0 + (uint32_t)(WAVE - 1) - (uint32_t)(__ffsll((unsigned long long)hb) - 1)) << RSHIFT);
+                    if (tid < WAVE) {
+                        const uint32_t c = s.rc64[tid];
+                        if (c != 0u) __hip_atomic_fetch_add(rh + rc0 + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
                 }
                 topk_append(x, lo);
-                if (!safe) {
-                    // row counts: this lane's tile-0 logits >= T0, all counted at the coarse bin of the lowest of
-                    // them (at or below each one's own bin: every row-wide bound read back stays valid), gathered
-                    // in LDS over the 64 coarse bins from T0's (higher ones at the 64th) and added to the row
-                    // histogram after the check below
-                    uint32_t c = 0u, lowk = 0xFFFFFFFFu;
-#pragma unroll
-                    for (int i = 0; i < TPT; ++i) {             // branch-free
-                        const uint32_t kq = key_of(x[i]);
-                        const bool in = x[i] >= tf;
-                        c += in ? 1u : 0u;
-                        lowk = (in && kq < lowk) ? kq : lowk;
-                    }
-                    rc0 = tkey >> RSHIFT;
-                    const uint32_t d = (lowk >> RSHIFT) - rc0;
-                    if (c != 0u) atomicAdd(&s.rc64[d < (uint32_t)WAVE ? d : (uint32_t)WAVE - 1u], c);
-                }
             }
             load_seg_tile(x, g.rs, PF);
             if (topk) {
                 const int n = check();
                 overflow = n > CAP;
-                if (!safe && tid < WAVE) {
-                    const uint32_t c = s.rc64[tid];
-                    if (c != 0u) __hip_atomic_fetch_add(rh + rc0 + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
                 if (!safe && ntiles >= 3) snap1 = row_snap(rh, tkey);
                 const int per_tile = n > 32 ? n : 32;
                 R = safe ? 1 : (CAP - n) / (2 * per_tile);
