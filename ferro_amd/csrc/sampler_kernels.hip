@@ -56,6 +56,7 @@ constexpr int SMALL = 512;                // rank-sort capacity of the merge
 constexpr int MAX_SEGS = 1024;            // segments per row
 constexpr int SPEC = 8;                   // merge gather: loads in flight per thread per round
 constexpr int FAST_SEGS = 64;             // merge fast path: a wave reads every list's bound and count
+static_assert(SPEC * BLOCK + SMALL + 2 * WAVE + 4 * 2 * WAVE / 2 <= CAP, "merge fast path: list, ranks and finish buffers fit");
 constexpr int RBITS = 12;                 // row histogram: bins of the top key bits, shared by a row's segments
 constexpr int RBINS = 1 << RBITS;
 constexpr int RSHIFT = 32 - RBITS;
@@ -490,6 +491,7 @@ struct Shared {
     uint32_t count;
     uint32_t tmax;                     // segment kernel: the largest key of tile 0
     uint32_t rc64[WAVE];               // segment kernel: tile-0 counts in the 64 coarse bins up to tmax's
+    uint32_t rc64b[WAVE];              // segment kernel: tiles 1-4 counts in the 64 coarse bins from tkey's
     uint32_t nids;
     Red red;
     __device__ __forceinline__ uint32_t* cnt() { return scr; }
@@ -1278,38 +1280,47 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             L = wave_max(L);
             cmax = wave_max(cmax);
             if (cmax <= (uint32_t)(SPEC * pre.tps)) {
-                for (int i = tid; i < NBINS; i += BLOCK) s.bins()[i] = 0u;
                 {                                     // the segments' row histogram is spent: leave it at 0
                     uint4* rz = reinterpret_cast<uint4*>(a.rhist + (int64_t)row * RBINS);
                     for (int i = tid; i < RBINS / 4; i += BLOCK) rz[i] = make_uint4(0u, 0u, 0u, 0u);
                 }
-                bool in[SPEC];
+                for (int i = tid; i < NBINS; i += BLOCK) s.bins()[i] = 0u;
+                if (tid == 0) { s.count = 0u; s.nids = 0u; }
+                __syncthreads();
+                // every candidate >= L into the candidate buffer (<= SPEC * BLOCK of them), tracking the max key
                 uint32_t kmax = L;
 #pragma unroll
                 for (int q = 0; q < SPEC; ++q) {
                     const uint64_t w = pre.v[q];
-                    in[q] = pre.act && (uint32_t)(pre.r_me + q * pre.tps) < pre.cnm && w != 0 && comp_key(w) >= L;
-                    if (in[q]) kmax = comp_key(w) > kmax ? comp_key(w) : kmax;
+                    const bool in = pre.act && (uint32_t)(pre.r_me + q * pre.tps) < pre.cnm && w != 0 && comp_key(w) >= L;
+                    if (in) kmax = comp_key(w) > kmax ? comp_key(w) : kmax;
+                    wave_append(in, w, s.cand, &s.count, CAP);
                 }
-                if (tid == 0) s.count = 0u;
-                kmax = block_max_u32(kmax, s.red);            // its barrier also orders the zeroed bins
-                const int sh = range_shift(L, kmax);
-#pragma unroll
-                for (int q = 0; q < SPEC; ++q)
-                    if (in[q]) atomicAdd(&s.bins()[(comp_key(pre.v[q]) - L) >> sh], 1u);
-                __syncthreads();
-                uint32_t c1;
-                const uint32_t T1 = hist_threshold(s.bins(), L, sh, k, &c1, s.wsum, s.red);
-                if (c1 >= (uint32_t)k && c1 <= (uint32_t)(2 * WAVE)) {
-                    uint64_t* small_in = s.cand;              // the candidate buffer is unused on this path
-                    uint64_t* small_out = small_in + SMALL;
-#pragma unroll
-                    for (int q = 0; q < SPEC; ++q)
-                        wave_append(in[q] && comp_key(pre.v[q]) >= T1, pre.v[q], small_in, &s.count, SMALL);
+                kmax = block_max_u32(kmax, s.red);            // its barrier also completes the appends
+                const uint32_t n = s.count;
+                uint64_t* list = s.cand;
+                uint32_t c1 = n;
+                if (n > (uint32_t)(2 * WAVE)) {
+                    // more than 128: T1 from a histogram of the list over [L, kmax], then the <= 128 >= T1
+                    const int sh = range_shift(L, kmax);
+                    for (uint32_t i = tid; i < n; i += BLOCK) atomicAdd(&s.bins()[(comp_key(s.cand[i]) - L) >> sh], 1u);
                     __syncthreads();
+                    const uint32_t T1 = hist_threshold(s.bins(), L, sh, k, &c1, s.wsum, s.red);
+                    if (c1 >= (uint32_t)k && c1 <= (uint32_t)(2 * WAVE)) {
+                        list = s.cand + SPEC * BLOCK;         // past the full list
+                        for (uint32_t i0 = 0; i0 < n; i0 += BLOCK) {
+                            const uint32_t i = i0 + tid;
+                            const uint64_t c = i < n ? s.cand[i] : 0ull;
+                            wave_append(c != 0 && comp_key(c) >= T1, c, list, &s.nids, 2 * WAVE);
+                        }
+                        __syncthreads();
+                    }
+                }
+                if (c1 >= (uint32_t)k && c1 <= (uint32_t)(2 * WAVE)) {
+                    uint64_t* small_out = list + SMALL;
                     uint32_t* rk = reinterpret_cast<uint32_t*>(small_out + 2 * WAVE);   // past wave_finish's buffers
-                    block_ranks(small_in, (int)c1, rk);
-                    if (tid < WAVE) wave_finish(a, rc, small_in, rk, k, reinterpret_cast<double*>(small_out), tok, keep);
+                    block_ranks(list, (int)c1, rk);
+                    if (tid < WAVE) wave_finish(a, rc, list, rk, k, reinterpret_cast<double*>(small_out), tok, keep);
                     fast_done = true;
                 }
             }
@@ -1777,7 +1788,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     uint32_t rc0 = 0u;                 // lowest coarse bin of the tile-0 counts
     bool spending = false;
     if (tid == 0) { s.count = 0u; s.tmax = 0u; }
-    if (tid < WAVE) s.rc64[tid] = 0u;
+    if (tid < WAVE) { s.rc64[tid] = 0u; s.rc64b[tid] = 0u; }
     __syncthreads();
 
     auto raise_key = [&](uint32_t kq) {
@@ -1926,7 +1937,8 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         int since = 0;
         for (int t0 = 1; t0 < ntiles && !overflow; t0 += PF) {
             const bool take1 = topk && !safe && t0 == 1 && ntiles >= 3;   // bound before tile 1
-            const bool snap = topk && !safe && t0 == 3 && ntiles >= 5;    // snapshot at tile 3, bound before tile 4
+            const bool snap = topk && !safe && (t0 == 3 || t0 == 5) && t0 + 1 < ntiles;   // snapshot at 3/5, bound at 4/6
+            const bool count2 = topk && !safe && t0 == 3 && ntiles >= 7;  // tiles 1-4 counted at tile 4
             RowSnap snap2;
 #pragma unroll
             for (int p = 0; p < PF; ++p) {
@@ -1951,6 +1963,28 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                             overflow = check() > CAP;   // uniform: every thread read the same count
                         }
                         if (p == 0 && snap) snap2 = row_snap(rh, tkey);
+                        if (p == 1 && count2 && !overflow) {
+                            // second count: the buffered logits of tiles 1-4 (tile 0's are counted already), at
+                            // their coarse bins from tkey's (higher ones at the 64th: fewer counts, still valid)
+                            __syncthreads();
+                            const uint32_t nb = s.count;
+                            const uint32_t rb = tkey >> RSHIFT;
+                            if (nb <= (uint32_t)CAP) {
+                                for (uint32_t i = tid; i < nb; i += BLOCK) {
+                                    const uint64_t c = s.cand[i];
+                                    if (comp_id(c) >= (uint32_t)(seg_lo + TILE) && comp_key(c) >= tkey) {
+                                        const uint32_t d = (comp_key(c) >> RSHIFT) - rb;
+                                        atomicAdd(&s.rc64b[d < (uint32_t)WAVE ? d : (uint32_t)WAVE - 1u], 1u);
+                                    }
+                                }
+                            }
+                            __syncthreads();
+                            if (tid < WAVE) {
+                                const uint32_t c = s.rc64b[tid];
+                                if (c != 0u)
+                                    __hip_atomic_fetch_add(rh + rb + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            }
+                        }
                     } else if (slowpen) {
                         __syncthreads();                 // penalty-table reads of this tile are done
                     }
