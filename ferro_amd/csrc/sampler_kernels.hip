@@ -1641,17 +1641,6 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
     __syncthreads();                                   // LDS is reused by the caller's next chunk
 }
 
-// One (row, segment) item: stream the segment's full tiles with PF tiles in flight, apply the penalties, and keep
-// the running candidates.
-//   - greedy rows: each lane's first maximum;
-//   - top-k rows: every logit with key >= tkey, a lower bound of the row's k-th key (at least k logits of the row
-//     reach it). tkey starts from tile 0 (the maxima of >= 2k groups: at least k of the tile's logits reach it) and
-//     is raised from the row histogram (a_rhist): every appended logit counts itself in its row's bin of the top
-//     key bits, every segment reads the counts back asynchronously and takes the highest bin with >= k counted
-//     logits at or above it. Counts only grow, so any snapshot gives a valid bound, and the bound combines the
-//     whole row's evidence instead of one segment's.
-// The segment publishes its candidates with key >= the final tkey (plain stores; the merge kernel runs after this
-// kernel). They include every logit of the row's top k that lies in this segment.
 // A wave's snapshot of its row's histogram: lane l holds the counts of bins b0 + 4 (63 - l) + j, j = 0..3, where
 // b0 is the wave's current bound's bin rounded down to a multiple of 4: the 256 bins (32 binades) from the bound
 // up, in lane order = descending bins; counts above the window are left out (fewer counts: the bound stays
@@ -1722,6 +1711,17 @@ __device__ __forceinline__ SegStart seg_start(const Args& a, int row, int seg, f
     return g;
 }
 
+// One (row, segment) item: stream the segment's full tiles with PF tiles in flight, apply the penalties, and keep
+// the running candidates.
+//   - greedy rows: each lane's first maximum;
+//   - top-k rows: every logit with key >= tkey, a lower bound of the row's k-th key (at least k logits of the row
+//     reach it). tkey starts from tile 0 (the highest coarse bin with >= k of the tile's lane maxima at or above
+//     it) and is raised from the row histogram (a.rhist): the segments add counts of real logits to their row's
+//     coarse bins (tile 0's lane maxima, then the buffered logits of tiles 1-4), and every wave snapshots the
+//     counts and takes the highest bin with >= k counted logits at or above it. Counts only grow, so any snapshot
+//     gives a valid bound, and the bound combines the whole row's evidence instead of one segment's.
+// The segment publishes its candidates with key >= the final tkey (plain stores; the merge kernel runs after this
+// kernel). They include every logit of the row's top k that lies in this segment.
 __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc, int seg, Shared& s,
                                                 float (&buf)[PF][TPT], const SegStart& g) {
     const int tid = threadIdx.x;
