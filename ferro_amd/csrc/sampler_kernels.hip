@@ -1106,7 +1106,7 @@ __device__ __forceinline__ void block_ranks(uint64_t* in, int c1, uint32_t* rk) 
 static_assert(BLOCK == 4 * 2 * WAVE, "block_ranks splits 128 candidates into four quarters");
 
 __device__ __forceinline__ void wave_finish(const Args& a, const RowCtx& rc, const uint64_t* in, const uint32_t* rk,
-                                            int k, double* wbuf, int& tok_out, int& keep_out) {
+                                            int k, double u, double* wbuf, int& tok_out, int& keep_out) {
     const int lane = lane_id();
     const int row = rc.row;
     // lane holds candidates lane and lane + 64 (0 = none) with their ranks from block_ranks
@@ -1148,7 +1148,6 @@ __device__ __forceinline__ void wave_finish(const Args& a, const RowCtx& rc, con
         }
     }
     const double tot = lane_f64(cum, keep - 1);
-    const double u = a.u ? a.u[row] : 0.0;
     const double rr = u * tot + 0.0;
     const uint64_t hm = __ballot(lane < keep && rr <= cum);
     const int at = hm ? __ffsll((unsigned long long)hm) - 1 : keep - 1;
@@ -1171,6 +1170,7 @@ struct Pre {
     bool act;
     uint32_t t0m, cnm;
     uint64_t v[SPEC];
+    double u;                              // the row's draw (requested with the lists)
 };
 
 __device__ __forceinline__ void prefetch_lists(const Args& a, int row, Pre& pre) {
@@ -1182,6 +1182,7 @@ __device__ __forceinline__ void prefetch_lists(const Args& a, int row, Pre& pre)
     pre.act = nseg > 0 && pre.r_me < pre.tps;
     const int64_t slot = (int64_t)row * nseg + pre.c_me;
     const uint64_t* lst = a.cand + slot * CAP;
+    pre.u = a.u ? ld_const(a.u + row) : 0.0;
     pre.t0m = 0u;
     pre.cnm = 0u;
     if (nseg > 0) {
@@ -1270,15 +1271,9 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
         // than 128 candidates at T1) takes the general path below.
         bool fast_done = false;
         if (ntail == 0 && k <= WAVE && nseg <= FAST_SEGS) {
-            uint32_t L = 0u, cmax = 0u;               // every wave reads all the (bound, count) pairs: no barrier
-            const int j = lane_id();
-            if (j < nseg) {
-                const uint32_t* mrow = a.meta + 2 * ((int64_t)row * nseg + j);
-                L = ld_agent(mrow);
-                cmax = ld_agent(mrow + 1);
-            }
-            L = wave_max(L);
-            cmax = wave_max(cmax);
+            // every wave holds every list's (bound, count) pair (lane l: list l % nseg): no barrier
+            const uint32_t L = wave_max(pre.t0m);
+            const uint32_t cmax = wave_max(pre.cnm);
             if (cmax <= (uint32_t)(SPEC * pre.tps)) {
                 {                                     // the segments' row histogram is spent: leave it at 0
                     uint4* rz = reinterpret_cast<uint4*>(a.rhist + (int64_t)row * RBINS);
@@ -1320,7 +1315,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                     uint64_t* small_out = list + SMALL;
                     uint32_t* rk = reinterpret_cast<uint32_t*>(small_out + 2 * WAVE);   // past wave_finish's buffers
                     block_ranks(list, (int)c1, rk);
-                    if (tid < WAVE) wave_finish(a, rc, list, rk, k, reinterpret_cast<double*>(small_out), tok, keep);
+                    if (tid < WAVE) wave_finish(a, rc, list, rk, k, pre.u, reinterpret_cast<double*>(small_out), tok, keep);
                     fast_done = true;
                 }
             }
@@ -1479,7 +1474,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             if (c1 <= (uint32_t)(2 * WAVE) && k <= WAVE) {
                 uint32_t* rk = reinterpret_cast<uint32_t*>(small_out + 2 * WAVE);   // past wave_finish's buffers
                 block_ranks(small_in, (int)c1, rk);
-                if (tid < WAVE) wave_finish(a, rc, small_in, rk, k, reinterpret_cast<double*>(small_out), tok, keep);
+                if (tid < WAVE) wave_finish(a, rc, small_in, rk, k, pre.u, reinterpret_cast<double*>(small_out), tok, keep);
                 wave_done = true;
             } else {
                 rank_sort(small_in, (int)c1, small_out, k);
@@ -1589,7 +1584,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 if (i0 + q == keep - 1) s.red.dmisc[0] = c[q];
             __syncthreads();
             const double tot = s.red.dmisc[0];
-            const double u = a.u ? a.u[row] : 0.0;
+            const double u = pre.u;
             const double rr = u * tot + 0.0;
             int hit = 0x7fffffff;
     #pragma unroll
