@@ -2014,24 +2014,16 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
             a.meta[2 * slot + 1] = 1u;
         }
     } else {
-        // the buffered candidates with key >= tkey, in buffer order
-        constexpr int RPT = (CAP + BLOCK - 1) / BLOCK;
+        // the buffered candidates with key >= tkey, in buffer order (thread t: entries t, t + BLOCK, ...)
         const int n = (int)s.count;              // <= CAP: no overflow past the checks above
         uint32_t mine = 0u;
-#pragma unroll
-        for (int r = 0; r < RPT; ++r) {
-            const int i = r * BLOCK + tid;
-            if (i < n && comp_key(s.cand[i]) >= tkey) ++mine;
-        }
+        for (int i = tid; i < n; i += BLOCK)
+            if (comp_key(s.cand[i]) >= tkey) ++mine;
         uint32_t tot;
         uint32_t pos = block_excl_scan<uint32_t>(mine, s.wsum, &tot);
-#pragma unroll
-        for (int r = 0; r < RPT; ++r) {
-            const int i = r * BLOCK + tid;
-            if (i < n) {
-                const uint64_t c = s.cand[i];
-                if (comp_key(c) >= tkey) gout[pos++] = c;
-            }
+        for (int i = tid; i < n; i += BLOCK) {
+            const uint64_t c = s.cand[i];
+            if (comp_key(c) >= tkey) gout[pos++] = c;
         }
         if (tid == 0) {
             a.meta[2 * slot] = tkey;              // at least k of the row's logits reach it
