@@ -1845,14 +1845,48 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         }
     };
     // barrier + count; compacts when another tile could overflow; returns the count (> CAP: overflowed)
-    auto check = [&]() -> int {
+    int counted = 0;                   // buffer entries [0, counted) are in the row histogram or never will be
+    // barrier + count; returns it (> CAP: overflowed). Compacts to the exact k-th when the headroom gets short:
+    // for k <= 256, in safe mode and at the end (the published list then holds at most max(k, CAP - TILE)), when
+    // another whole tile could overflow (a compaction then also raises the bound a lot); otherwise when less
+    // than 3 tiles' worth at the observed append rate (at least 1024) is left - an overflow past that is caught
+    // at the next check and the segment streamed again in safe mode.
+    int lastn = 0;
+    auto check = [&](int tiles, bool strict) -> int {
         __syncthreads();
         int n = (int)s.count;
-        if (n <= CAP && n > CAP - TILE && n > k) {
+        int rate = (n - lastn) / (tiles > 0 ? tiles : 1);
+        rate = rate > 341 ? rate : 341;
+        if (n <= CAP && n > k && (strict || k <= 4 * WAVE ? n > CAP - TILE : CAP - n < 3 * rate)) {
             raise_key(comp_key(compact_exact(n, k, s)));
             n = k;
+            counted = n;                   // the survivors are left uncounted (fewer counts: bounds stay valid)
         }
+        lastn = n;
         return n;
+    };
+    // Adds the buffered logits [from, count) of tiles >= 1 with key >= tkey to the row histogram, at their coarse
+    // bins from tkey's (higher ones at the 64th: fewer counts, bounds stay valid). Tile 0 is counted already.
+    // Entry: a barrier since the last append (a check).
+    auto count_row = [&](int from) {
+        const int nb = (int)s.count;
+        const uint32_t rb = tkey >> RSHIFT;
+        if (nb <= CAP) {
+            for (int i = from + tid; i < nb; i += BLOCK) {
+                const uint64_t c = s.cand[i];
+                if (comp_id(c) >= (uint32_t)(seg_lo + TILE) && comp_key(c) >= tkey) {
+                    const uint32_t d = (comp_key(c) >> RSHIFT) - rb;
+                    atomicAdd(&s.rc64b[d < (uint32_t)WAVE ? d : (uint32_t)WAVE - 1u], 1u);
+                }
+            }
+        }
+        __syncthreads();
+        if (tid < WAVE) {
+            const uint32_t c = s.rc64b[tid];
+            s.rc64b[tid] = 0u;
+            if (c != 0u) __hip_atomic_fetch_add(rh + rb + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        counted = nb;
     };
     static_assert(PF == 2, "the row read is issued and taken within one iteration of the tile loop");
     RowSnap snap1;                     // the row histogram after tile 0 (segments of >= 3 tiles)
@@ -1912,7 +1946,8 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
             }
             load_seg_tile(x, g.rs, PF);
             if (topk) {
-                const int n = check();
+                lastn = 0;
+                const int n = check(1, safe);
                 overflow = n > CAP;
                 if (!safe && ntiles >= 3) snap1 = row_snap(rh, tkey);
                 const int per_tile = n > 32 ? n : 32;
@@ -1933,7 +1968,8 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         for (int t0 = 1; t0 < ntiles && !overflow; t0 += PF) {
             const bool take1 = topk && !safe && t0 == 1 && ntiles >= 3;   // bound before tile 1
             const bool snap = topk && !safe && (t0 == 3 || t0 == 5) && t0 + 1 < ntiles;   // snapshot at 3/5, bound at 4/6
-            const bool count2 = topk && !safe && t0 == 3 && ntiles >= 7;  // tiles 1-4 counted at tile 4
+            const bool count2 = topk && !safe && t0 == 3 && ntiles >= 7 && k <= WAVE;   // tiles 1-4 at tile 4
+            bool dyn = false;              // k > 64: counted at this iteration's first check, bound taken at p == 1
             RowSnap snap2;
 #pragma unroll
             for (int p = 0; p < PF; ++p) {
@@ -1946,39 +1982,29 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     if (slowpen) apply_penalties(x, a, rc, lo, s);
                     if (fastpen) bitmap_pen(x, lo);
                     if (p == 0 && take1) raise_key(row_bound(snap1, k));
-                    if (p == 1 && snap) raise_key(row_bound(snap2, k));
+                    if (p == 1 && (snap || dyn)) raise_key(row_bound(snap2, k));
                     if (rc.greedy) greedy_update(x, tt);
                     else topk_append(x, lo);
                 }
                 load_seg_tile(x, g.rs, tt + PF);         // past the end: zeros, no memory access
                 if (live) {
                     if (topk) {
+                        bool checked = false;
                         if (++since >= R || slowpen) {
+                            overflow = check(since, safe) > CAP;   // uniform: every thread read the same count
                             since = 0;
-                            overflow = check() > CAP;   // uniform: every thread read the same count
+                            checked = true;
                         }
-                        if (p == 0 && snap) snap2 = row_snap(rh, tkey);
+                        if (p == 0 && checked && !safe && !overflow && k > WAVE && t0 + 1 < ntiles) {
+                            // large k: every check also counts the new entries, and the next tile takes the bound
+                            count_row(counted);
+                            dyn = true;
+                        }
+                        if (p == 0 && (snap || dyn)) snap2 = row_snap(rh, tkey);
                         if (p == 1 && count2 && !overflow) {
-                            // second count: the buffered logits of tiles 1-4 (tile 0's are counted already), at
-                            // their coarse bins from tkey's (higher ones at the 64th: fewer counts, still valid)
+                            // second count: the buffered logits of tiles 1-4
                             __syncthreads();
-                            const uint32_t nb = s.count;
-                            const uint32_t rb = tkey >> RSHIFT;
-                            if (nb <= (uint32_t)CAP) {
-                                for (uint32_t i = tid; i < nb; i += BLOCK) {
-                                    const uint64_t c = s.cand[i];
-                                    if (comp_id(c) >= (uint32_t)(seg_lo + TILE) && comp_key(c) >= tkey) {
-                                        const uint32_t d = (comp_key(c) >> RSHIFT) - rb;
-                                        atomicAdd(&s.rc64b[d < (uint32_t)WAVE ? d : (uint32_t)WAVE - 1u], 1u);
-                                    }
-                                }
-                            }
-                            __syncthreads();
-                            if (tid < WAVE) {
-                                const uint32_t c = s.rc64b[tid];
-                                if (c != 0u)
-                                    __hip_atomic_fetch_add(rh + rb + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            }
+                            count_row(0);
                         }
                     } else if (slowpen) {
                         __syncthreads();                 // penalty-table reads of this tile are done
@@ -1987,7 +2013,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
             }
         }
         if (!topk) break;
-        if (!overflow) overflow = check() > CAP;
+        if (!overflow) overflow = check(since, true) > CAP;
         if (!overflow) break;
         // overflow: the buffer lost candidates. tkey is still a valid bound; stream the segment again in safe mode
         // (its logits are already counted in the row histogram).
