@@ -261,6 +261,28 @@ def test_large_k_serving_rows_mixed_with_topk():
     assert nb == 0
 
 
+def test_buffer_pressure_multi_tile_segments():
+    """Segments of 8 tiles (B = 256, V = 65536) with k up to 2048: the candidate buffer is compacted under load and
+    the row bound is refreshed from counts at every check. Some rows rise tile after tile (every logit beats the
+    running bound: the buffer overflows and the segment is streamed again in safe mode); some are constant
+    (every logit ties)."""
+    rng = np.random.default_rng(31)
+    B, V = 256, 65536
+    x = (rng.standard_normal((B, V)) * 1.5).astype(np.float32)
+    x[::17] = np.sort(x[::17], axis=1)                                # ascending rows
+    x[5] = 0.25
+    p = W.make_params(B, temperature=0.9, top_k=2048, top_p=0.97, repetition_penalty=1.1)
+    p["top_k"][1::4] = 1500
+    p["top_k"][2::4] = 300
+    p["top_k"][3::8] = 64
+    p["frequency_penalty"][::5], p["presence_penalty"][::5] = 0.4, 0.2
+    hists = [rng.integers(0, V, 300) for _ in range(B)]
+    u = rng.random(B)
+    g, o, nb = check(_case(list(x), p, hists, u, "buffer_pressure"), kcap=2048)
+    say(f"buffer_pressure boundary rows: {nb}")
+    assert nb <= 8                              # 256 rows of up to 2048 fp64 probabilities: draws near a c_i
+
+
 def test_verify_large_k():
     rng = np.random.default_rng(8)
     S, M, V = 3, 4, 3000
