@@ -448,20 +448,75 @@ __device__ __forceinline__ uint64_t radix_kth(Each each, int k, uint32_t* hist25
     return prefix;
 }
 
-// Descending bitonic sort of n (power of two) composites in LDS.
+// Descending bitonic sort of n (a power of two, n <= 4 * BLOCK) composites in LDS, whole block. The stages of the
+// network are taken two at a time: for a pair of strides 2^p1, 2^p2 thread t loads the four entries whose indices
+// are t with zero bits inserted at p1 and p2, plus 0/1 in those bits, applies both stages in registers and stores
+// them back. While both bits are below 8 the four entries lie in the 256-entry block of the thread's wave
+// (index bits 8.. = wave id), and a wave's LDS accesses complete in order, so such rounds need no barrier; a
+// barrier is placed only on each side of a round that crosses blocks.
 __device__ __forceinline__ void bitonic_desc(uint64_t* a, int n) {
-    for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int t = threadIdx.x; t < n / 2; t += BLOCK) {
-                const int i = 2 * t - (t & (stride - 1));
-                const int j = i + stride;
-                const bool desc = (i & size) == 0;
-                const uint64_t x = a[i], y = a[j];
-                if ((x < y) == desc) { a[i] = y; a[j] = x; }
+    static_assert(4 * BLOCK >= KMAX && 4 * WAVE == 256, "four entries per thread; a wave spans 256 entries");
+    const int tid = threadIdx.x;
+    if (n < 4) {
+        if (n == 2 && tid == 0) {
+            const uint64_t x = a[0], y = a[1];
+            if (x < y) { a[0] = y; a[1] = x; }
+        }
+        __syncthreads();
+        return;
+    }
+    int lg = 0;
+    while ((1 << lg) < n) ++lg;
+    const bool act = tid < (n >> 2);
+    int m = 1, p = 0;                               // next stage: merge size 2^m, stride 2^p
+    bool prev_cross = false;
+    while (m <= lg) {
+        // this round: the stage (m, p), the next one, and a third while its stride is one of the two
+        int sm[3], sp[3], ns = 0;
+        int b0 = p, b1 = -1;
+        while (m <= lg && ns < 3) {
+            if (p != b0 && p != b1) {
+                if (b1 >= 0) break;
+                b1 = p;
             }
-            __syncthreads();
+            sm[ns] = m; sp[ns] = p; ++ns;
+            if (p == 0) { ++m; p = m - 1; } else { --p; }
+        }
+        if (b1 < 0) b1 = b0 == 0 ? 1 : 0;           // a lone last stage: any second bit
+        const int hi = b0 > b1 ? b0 : b1, lo = b0 > b1 ? b1 : b0;
+        const bool cross = hi >= 8;
+        if (cross || prev_cross) __syncthreads();
+        prev_cross = cross;
+        if (act) {
+            const int t = tid;
+            const int base = (t & ((1 << lo) - 1)) | (((t >> lo) & ((1 << (hi - lo - 1)) - 1)) << (lo + 1)) |
+                             ((t >> (hi - 1)) << (hi + 1));
+            const int ix[4] = {base, base + (1 << lo), base + (1 << hi), base + (1 << hi) + (1 << lo)};
+            uint64_t e[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) e[j] = a[ix[j]];
+            auto cx = [](uint64_t& x, uint64_t& y, bool desc) {
+                const uint64_t lo_v = x < y ? x : y, hi_v = x < y ? y : x;
+                x = desc ? hi_v : lo_v;
+                y = desc ? lo_v : hi_v;
+            };
+#pragma unroll
+            for (int q = 0; q < 3; ++q) {
+                if (q >= ns) break;
+                const int sh = sm[q];
+                if (sp[q] == hi) {                      // partners two registers apart
+                    cx(e[0], e[2], ((ix[0] >> sh) & 1) == 0);
+                    cx(e[1], e[3], ((ix[1] >> sh) & 1) == 0);
+                } else {
+                    cx(e[0], e[1], ((ix[0] >> sh) & 1) == 0);
+                    cx(e[2], e[3], ((ix[2] >> sh) & 1) == 0);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a[ix[j]] = e[j];
         }
     }
+    __syncthreads();
 }
 
 // Rank sort of n <= SMALL distinct composites: out[rank] = in[i] for ranks < k.
@@ -491,13 +546,99 @@ struct Shared {
     uint32_t count;
     uint32_t tmax;                     // segment kernel: the largest key of tile 0
     uint32_t rc64[WAVE];               // segment kernel: tile-0 counts in the 64 coarse bins up to tmax's
-    uint32_t rc64b[WAVE];              // segment kernel: tiles 1-4 counts in the 64 coarse bins from tkey's
     uint32_t nids;
     Red red;
     __device__ __forceinline__ uint32_t* cnt() { return scr; }
     __device__ __forceinline__ uint32_t* bins() { return scr + TILE / 2; }
     __device__ __forceinline__ uint64_t* stage() { return reinterpret_cast<uint64_t*>(scr); }   // KMAX entries
 };
+
+// Descending sort of m <= KMAX distinct composites a[0, m), in place (whole block; returns after a barrier). A
+// counting sort: NB bins span [min, max] of the composites (bin 0 = the largest); each entry takes a slot in its
+// bin with an LDS atomic (cnt) and is scattered to tmp[bin start + slot]; then each entry counts the larger entries
+// of its own bin and lands at bin start + that count. Bins of a smooth tail hold a few entries each (equal keys
+// spread over the id bits); when one holds more than BIN_SORT_MAX the bitonic network sorts instead (a must then
+// hold the next power of two >= m entries). cnt and start hold NB counters each; tmp holds m entries.
+constexpr int BIN_SORT_MAX = 48;
+template <int NB>
+__device__ __forceinline__ void bin_sort_desc(uint64_t* a, int m, uint64_t* tmp, uint32_t* cnt, uint32_t* start,
+                                              Red& red, uint32_t* wsum) {
+    constexpr int EPT = KMAX / BLOCK;            // entries per thread
+    constexpr int BPT = NB / BLOCK;              // bins per thread
+    static_assert(BPT >= 1 && NB == BPT * BLOCK, "whole bins per thread");
+    const int tid = threadIdx.x;
+    uint64_t v[EPT];
+    uint64_t cmn = ~0ull, cmx = 0ull;
+#pragma unroll
+    for (int q = 0; q < EPT; ++q) {
+        const int i = q * BLOCK + tid;
+        v[q] = i < m ? a[i] : 0ull;
+        if (i < m) {
+            cmn = v[q] < cmn ? v[q] : cmn;
+            cmx = v[q] > cmx ? v[q] : cmx;
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) cnt[q * BLOCK + tid] = 0u;
+    cmn = block_min_u64(cmn, red);               // its barriers also order the zeroed counts
+    cmx = block_max_u64(cmx, red);
+    if (m <= 1) return;
+    int sh = 0;                                  // composites cmn..cmx map to bins NB-1..0
+    while (((cmx - cmn) >> sh) >= (uint64_t)NB) ++sh;
+    uint32_t bin[EPT], slot[EPT];
+#pragma unroll
+    for (int q = 0; q < EPT; ++q) {
+        bin[q] = 0u;
+        slot[q] = 0u;
+        if (q * BLOCK + tid < m) {
+            bin[q] = (uint32_t)(NB - 1) - (uint32_t)((v[q] - cmn) >> sh);
+            slot[q] = atomicAdd(&cnt[bin[q]], 1u);
+        }
+    }
+    __syncthreads();
+    uint32_t c[BPT], sum = 0u, big = 0u;
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+        c[j] = cnt[BPT * tid + j];
+        sum += c[j];
+        big = c[j] > big ? c[j] : big;
+    }
+    uint32_t tot;
+    uint32_t off = block_excl_scan<uint32_t>(sum, wsum, &tot);
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+        start[BPT * tid + j] = off;
+        off += c[j];
+    }
+    big = block_max_u32(big, red);               // its barriers also publish the starts
+    if (big > (uint32_t)BIN_SORT_MAX) {
+        int np = 1;
+        while (np < m) np <<= 1;
+        for (int i = m + tid; i < np; i += BLOCK) a[i] = 0ull;
+        __syncthreads();
+        bitonic_desc(a, np);
+        return;
+    }
+#pragma unroll
+    for (int q = 0; q < EPT; ++q)
+        if (q * BLOCK + tid < m) tmp[start[bin[q]] + slot[q]] = v[q];
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < EPT; ++q) {
+        if (q * BLOCK + tid < m) {
+            const uint32_t b0 = start[bin[q]], n = cnt[bin[q]];
+            uint32_t r = 0u;
+            for (uint32_t j = 0; j < n; ++j) r += tmp[b0 + j] > v[q] ? 1u : 0u;
+            a[b0 + r] = v[q];
+        }
+    }
+    __syncthreads();
+}
+// The candidate buffer's first m <= KMAX entries, with the second KMAX entries as the scatter area.
+__device__ __forceinline__ void bin_sort_desc(int m, Shared& s) {
+    static_assert(TILE / 2 >= NBINS && 2 * KMAX <= CAP, "counts in cnt(), starts in bins(), scatter after the input");
+    bin_sort_desc<NBINS>(s.cand, m, s.cand + KMAX, s.cnt(), s.bins(), s.red, s.wsum);
+}
 static_assert((TILE / 2 + NBINS) / 2 >= KMAX, "the stage holds a compacted top k");
 
 // Per-row view of the arguments: params, greedy/k, and the two history segments (a verify row sees its stream's
@@ -687,6 +828,27 @@ __device__ __forceinline__ void narrow32(Each each, int kk, uint32_t& rlo, uint3
     }
 }
 
+// Keeps the entries >= X of the n in s.cand (at the front, through the stage) and returns their count; when more
+// than KMAX would remain, changes nothing and returns -1. Whole block; returns after a barrier.
+__device__ __forceinline__ int keep_from(int n, uint64_t X, Shared& s) {
+    const int tid = threadIdx.x;
+    uint32_t mine = 0u;
+    for (int i = tid; i < n; i += BLOCK) mine += s.cand[i] >= X ? 1u : 0u;
+    uint32_t tot;
+    uint32_t pos = block_excl_scan<uint32_t>(mine, s.wsum, &tot);
+    if (tot > (uint32_t)KMAX) return -1;
+    uint64_t* st = s.stage();
+    for (int i = tid; i < n; i += BLOCK) {
+        const uint64_t c = s.cand[i];
+        if (c >= X) st[pos++] = c;
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < tot; i += BLOCK) s.cand[i] = st[i];
+    if (tid == 0) s.count = tot;
+    __syncthreads();
+    return (int)tot;
+}
+
 // Exact k-th largest composite X among the n > k candidates in s.cand, then keep exactly the k entries >= X.
 // Returns X. Keys first (histogram levels over [min, max]), then, if the k-th key is tied, the ids among the ties.
 __device__ __forceinline__ uint64_t compact_exact(int n, int k, Shared& s) {
@@ -727,20 +889,7 @@ __device__ __forceinline__ uint64_t compact_exact(int n, int k, Shared& s) {
             (int)need, lmn, lmx, &ab2, &at2, s);
         X |= lmn;
     }
-    // keep the entries >= X (exactly k): compact into the stage, then copy back to the front of the buffer
-    uint32_t mine = 0u;
-    for (int i = tid; i < n; i += BLOCK) mine += s.cand[i] >= X ? 1u : 0u;
-    uint32_t tot;
-    uint32_t pos = block_excl_scan<uint32_t>(mine, s.wsum, &tot);
-    uint64_t* st = s.stage();
-    for (int i = tid; i < n; i += BLOCK) {
-        const uint64_t c = s.cand[i];
-        if (c >= X) st[pos++] = c;
-    }
-    __syncthreads();
-    for (uint32_t i = tid; i < tot; i += BLOCK) s.cand[i] = st[i];
-    if (tid == 0) s.count = tot;
-    __syncthreads();
+    (void)keep_from(n, X, s);                                 // exactly k entries are >= X
     return X;
 }
 
@@ -1039,11 +1188,7 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
                     wave_append(in, in ? comp_of(key_of(x[i]), (uint32_t)e) : 0ull, s.cand, &s.count, CAP);
                 }
             });
-            int np = 1;
-            while (np < m) np <<= 1;
-            for (int i = m + tid; i < np; i += BLOCK) s.cand[i] = 0ull;
-            __syncthreads();
-            bitonic_desc(s.cand, np);
+            bin_sort_desc(m, s);
             for (int i = tid; i < m; i += BLOCK) {
                 const uint64_t c = s.cand[i];
                 const int64_t o = (int64_t)row * a.kcap + done + i;
@@ -1476,10 +1621,14 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 block_ranks(small_in, (int)c1, rk);
                 if (tid < WAVE) wave_finish(a, rc, small_in, rk, k, pre.u, reinterpret_cast<double*>(small_out), tok, keep);
                 wave_done = true;
-            } else {
+            } else if (c1 <= (uint32_t)(4 * WAVE)) {
                 rank_sort(small_in, (int)c1, small_out, k);
+            } else {
+                // the gathered list is spent: its buffer takes the scatter; counts and starts in cnt()
+                static_assert(2 * (NBINS / 2) <= TILE / 2, "two half-size bin arrays in cnt()");
+                bin_sort_desc<NBINS / 2>(small_in, (int)c1, s.cand, s.cnt(), s.cnt() + NBINS / 2, s.red, s.wsum);
             }
-            top = small_out;
+            top = !wave_done && c1 > (uint32_t)(4 * WAVE) ? small_in : small_out;   // binned sort: in place
         } else {
             // more than SMALL candidates reach T1: reduce to exactly the k >= X in LDS, then sort those
             int m = (int)n;
@@ -1513,11 +1662,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 compact_exact(m, k, s);
                 m = k;
             }
-            int np = 1;
-            while (np < m) np <<= 1;                    // <= KMAX
-            for (int i = m + tid; i < np; i += BLOCK) s.cand[i] = 0ull;
-            __syncthreads();
-            bitonic_desc(s.cand, np);
+            bin_sort_desc(m, s);                        // m <= KMAX
             top = s.cand;
             c1 = (uint32_t)m;
         }
@@ -1654,6 +1799,23 @@ __device__ __forceinline__ RowSnap row_snap(const uint32_t* rh, uint32_t tkey) {
     r.w[1] = ld_agent(p + 1);
     return r;
 }
+// The same snapshot through a buffer resource over the row histogram (agent-coherent: sc1). With 0 records the load
+// returns zeros without a memory access, so the tile loop can request it unconditionally (straight-line loads keep
+// the compiler's memory-counter waits exact).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ u32x4 raw_buffer_load_u32x4(__amdgpu_buffer_rsrc_t rs, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.load.v4i32");
+constexpr int AUX_SC1 = 16;              // cache policy: system-coherent level 1 (bypass the XCD's L2)
+__device__ __forceinline__ RowSnap row_snap_buf(__amdgpu_buffer_rsrc_t rs, uint32_t tkey) {
+    RowSnap r;
+    r.b0 = (tkey >> RSHIFT) & ~3u;
+    const uint32_t first = r.b0 + 4u * (uint32_t)(WAVE - 1 - lane_id());
+    const uint32_t f = first <= (uint32_t)RBINS - 4u ? first : (uint32_t)RBINS - 4u;
+    const u32x4 v = raw_buffer_load_u32x4(rs, (int)(f * 4u), 0, AUX_SC1);
+    r.w[0] = (uint64_t)v.x | ((uint64_t)v.y << 32);
+    r.w[1] = (uint64_t)v.z | ((uint64_t)v.w << 32);
+    return r;
+}
 // From a snapshot: the lower edge of the highest bin with at least k counted logits in it and the bins above. At
 // least k logits of the row reach it, so it bounds the row's k-th key from below (0: the snapshot holds fewer than
 // k). No barrier: each wave takes its own snapshot, and any snapshot gives a valid bound.
@@ -1783,7 +1945,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     uint32_t rc0 = 0u;                 // lowest coarse bin of the tile-0 counts
     bool spending = false;
     if (tid == 0) { s.count = 0u; s.tmax = 0u; }
-    if (tid < WAVE) { s.rc64[tid] = 0u; s.rc64b[tid] = 0u; }
+    if (tid < WAVE) s.rc64[tid] = 0u;
     __syncthreads();
 
     auto raise_key = [&](uint32_t kq) {
@@ -1844,49 +2006,64 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
             }
         }
     };
-    // barrier + count; compacts when another tile could overflow; returns the count (> CAP: overflowed)
     int counted = 0;                   // buffer entries [0, counted) are in the row histogram or never will be
-    // barrier + count; returns it (> CAP: overflowed). Compacts to the exact k-th when the headroom gets short:
-    // for k <= 256, in safe mode and at the end (the published list then holds at most max(k, CAP - TILE)), when
-    // another whole tile could overflow (a compaction then also raises the bound a lot); otherwise when less
-    // than 3 tiles' worth at the observed append rate (at least 1024) is left - an overflow past that is caught
-    // at the next check and the segment streamed again in safe mode.
-    int lastn = 0;
-    auto check = [&](int tiles, bool strict) -> int {
-        __syncthreads();
-        int n = (int)s.count;
-        int rate = (n - lastn) / (tiles > 0 ? tiles : 1);
-        rate = rate > 341 ? rate : 341;
-        if (n <= CAP && n > k && (strict || k <= 4 * WAVE ? n > CAP - TILE : CAP - n < 3 * rate)) {
-            raise_key(comp_key(compact_exact(n, k, s)));
-            n = k;
-            counted = n;                   // the survivors are left uncounted (fewer counts: bounds stay valid)
-        }
-        lastn = n;
-        return n;
-    };
     // Adds the buffered logits [from, count) of tiles >= 1 with key >= tkey to the row histogram, at their coarse
-    // bins from tkey's (higher ones at the 64th: fewer counts, bounds stay valid). Tile 0 is counted already.
-    // Entry: a barrier since the last append (a check).
+    // bins from tkey's (higher ones at the 64th: fewer counts, bounds stay valid). Tile 0 is counted already. The
+    // waves' tkeys can differ (each wave takes its own row bounds), so each wave histograms the entries it reads
+    // relative to its own tkey in its own 64 bins (in bins(), free between checks) and adds them to the row at
+    // that base; a wave's LDS accesses complete in order, so no barrier is needed.
+    // Entry: a barrier since the last append (a check); the next check's barrier ends the bins' use.
     auto count_row = [&](int from) {
         const int nb = (int)s.count;
         const uint32_t rb = tkey >> RSHIFT;
+        uint32_t* wb = s.bins() + (tid / WAVE) * WAVE;
+        wb[lane_id()] = 0u;
         if (nb <= CAP) {
             for (int i = from + tid; i < nb; i += BLOCK) {
                 const uint64_t c = s.cand[i];
                 if (comp_id(c) >= (uint32_t)(seg_lo + TILE) && comp_key(c) >= tkey) {
                     const uint32_t d = (comp_key(c) >> RSHIFT) - rb;
-                    atomicAdd(&s.rc64b[d < (uint32_t)WAVE ? d : (uint32_t)WAVE - 1u], 1u);
+                    atomicAdd(&wb[d < (uint32_t)WAVE ? d : (uint32_t)WAVE - 1u], 1u);
                 }
             }
         }
-        __syncthreads();
-        if (tid < WAVE) {
-            const uint32_t c = s.rc64b[tid];
-            s.rc64b[tid] = 0u;
-            if (c != 0u) __hip_atomic_fetch_add(rh + rb + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        const uint32_t c = wb[lane_id()];
+        if (c != 0u && rb + (uint32_t)lane_id() < (uint32_t)RBINS)
+            __hip_atomic_fetch_add(rh + rb + lane_id(), c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         counted = nb;
+    };
+    // barrier + count; returns it (> CAP: overflowed). Compacts when the headroom gets short: for k <= 256, in safe
+    // mode and at the end (the published list then holds at most max(k, CAP - TILE)), when another whole tile could
+    // overflow; otherwise when less than 3 tiles' worth at the observed append rate (at least 341) is left - an
+    // overflow past that is caught at the next check and the segment streamed again in safe mode. A compaction
+    // first drops the entries below the row bound (the largest of the waves' tkeys: one pass); only if that leaves
+    // the headroom short (or more than KMAX entries) it keeps exactly the segment's k largest.
+    int lastn = 0;
+    const bool dyncount = topk && k > WAVE;      // k > 64: the buffered entries are counted at checks
+    auto check = [&](int tiles, bool strict) -> int {
+        __syncthreads();
+        int n = (int)s.count;
+        int rate = (n - lastn) / (tiles > 0 ? tiles : 1);
+        rate = rate > 341 ? rate : 341;
+        auto short_room = [&](int m) {
+            return m > k && (strict || k <= 4 * WAVE ? m > CAP - TILE : CAP - m < 3 * rate);
+        };
+        if (n <= CAP && short_room(n)) {
+            if (dyncount && !strict) count_row(counted);   // before the order changes (not in safe mode)
+            raise_key(block_max_u32(tkey, s.red));          // its barriers also end count_row's use of bins()
+            const int m = keep_from(n, (uint64_t)tkey << 32, s);
+            if (m >= 0) {
+                n = m;
+                counted = m;
+            }
+            if (m < 0 || short_room(n)) {
+                raise_key(comp_key(compact_exact(n, k, s)));
+                n = k;
+                counted = n;               // the survivors are left uncounted (fewer counts: bounds stay valid)
+            }
+        }
+        lastn = n;
+        return n;
     };
     static_assert(PF == 2, "the row read is issued and taken within one iteration of the tile loop");
     RowSnap snap1;                     // the row histogram after tile 0 (segments of >= 3 tiles)
@@ -1965,11 +2142,18 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         // ---- tiles 1.. (PF in flight; tile t is in buf[t % 2]). Iterations start at odd tiles, so the order in
         // which the two buffers were requested is the same on entry and around the back edge.
         int since = 0;
+        // k > 64: a snapshot requested at every iteration's first tile (after its check and row count, before its
+        // successor's loads), read at the next iteration's first tile: waiting for that tile covers it. Other rows
+        // request it from an empty resource (no memory access).
+        const bool dynrow = topk && !safe && k > WAVE;
+        const __amdgpu_buffer_rsrc_t rsh = __builtin_amdgcn_make_buffer_rsrc(rh, (short)0, dynrow ? RBINS * 4 : 0,
+                                                                             0x00020000);
+        RowSnap snapd;
+        bool dpend = false;
         for (int t0 = 1; t0 < ntiles && !overflow; t0 += PF) {
             const bool take1 = topk && !safe && t0 == 1 && ntiles >= 3;   // bound before tile 1
             const bool snap = topk && !safe && (t0 == 3 || t0 == 5) && t0 + 1 < ntiles;   // snapshot at 3/5, bound at 4/6
             const bool count2 = topk && !safe && t0 == 3 && ntiles >= 7 && k <= WAVE;   // tiles 1-4 at tile 4
-            bool dyn = false;              // k > 64: counted at this iteration's first check, bound taken at p == 1
             RowSnap snap2;
 #pragma unroll
             for (int p = 0; p < PF; ++p) {
@@ -1982,11 +2166,15 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     if (slowpen) apply_penalties(x, a, rc, lo, s);
                     if (fastpen) bitmap_pen(x, lo);
                     if (p == 0 && take1) raise_key(row_bound(snap1, k));
-                    if (p == 1 && (snap || dyn)) raise_key(row_bound(snap2, k));
+                    if (p == 0 && dpend) raise_key(row_bound(snapd, k));
+                    if (p == 1 && snap) raise_key(row_bound(snap2, k));
                     if (rc.greedy) greedy_update(x, tt);
                     else topk_append(x, lo);
                 }
-                load_seg_tile(x, g.rs, tt + PF);         // past the end: zeros, no memory access
+                // past the end: zeros, no memory access. The first tile of an iteration requests its successor
+                // after the check and the row snapshot: the snapshot is then taken at the next tile with that
+                // tile's successor still in flight (waits on the memory counter complete in request order).
+                if (p == 1) load_seg_tile(x, g.rs, tt + PF);
                 if (live) {
                     if (topk) {
                         bool checked = false;
@@ -1995,12 +2183,9 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                             since = 0;
                             checked = true;
                         }
-                        if (p == 0 && checked && !safe && !overflow && k > WAVE && t0 + 1 < ntiles) {
-                            // large k: every check also counts the new entries, and the next tile takes the bound
-                            count_row(counted);
-                            dyn = true;
-                        }
-                        if (p == 0 && (snap || dyn)) snap2 = row_snap(rh, tkey);
+                        if (p == 0 && checked && dynrow && !overflow && t0 + PF < ntiles) count_row(counted);
+                        if (p == 0) dpend = dynrow && !overflow && t0 + PF < ntiles;
+                        if (p == 0 && snap) snap2 = row_snap(rh, tkey);
                         if (p == 1 && count2 && !overflow) {
                             // second count: the buffered logits of tiles 1-4
                             __syncthreads();
@@ -2009,6 +2194,10 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     } else if (slowpen) {
                         __syncthreads();                 // penalty-table reads of this tile are done
                     }
+                }
+                if (p == 0) {
+                    snapd = row_snap_buf(rsh, tkey);
+                    load_seg_tile(x, g.rs, tt + PF);
                 }
             }
         }

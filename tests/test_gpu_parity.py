@@ -283,6 +283,42 @@ def test_buffer_pressure_multi_tile_segments():
     assert nb <= 8                              # 256 rows of up to 2048 fp64 probabilities: draws near a c_i
 
 
+def test_candidate_sort_tie_clusters():
+    """The candidate sort bins the composites (key, id) over their span; a cluster of tied logits inside a spread
+    of distinct ones puts more entries in one bin than the binned sort handles, and the sort falls back to the
+    bitonic network. Rows mix both, for k on the small-list path (<= 512 reach the threshold) and on the KMAX
+    path, with the candidate outputs compared in full."""
+    rng = np.random.default_rng(47)
+    B, V = 32, 65536
+    x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    for b in range(0, B, 2):                                        # ties: 60 .. 1900 logits at one value
+        n = int(60 + (b * 61) % 1840)
+        idx = rng.choice(V, n, replace=False)
+        x[b, idx] = np.float32(x[b].max() - 0.5 - 0.1 * (b % 3))
+    x[3, :3000] = np.float32(4.0)                                   # a constant block above a tail
+    x[9, ::2] = np.float32(-1.0)
+    p = W.make_params(B, temperature=0.8, top_k=2048, top_p=0.99, repetition_penalty=1.0)
+    p["top_k"][1::4] = 100
+    p["top_k"][2::4] = 300
+    p["top_k"][3::4] = 700
+    u = rng.random(B)
+    g, o, nb = check(_case(list(x), p, [np.zeros(0, np.int64)] * B, u, "tie_clusters"), kcap=2048)
+    say(f"tie_clusters boundary rows: {nb}")
+    assert nb <= 6                              # tied probabilities: many equal steps of the cumulative sum
+
+
+def test_large_k_candidate_chunks():
+    """k > 2048 (top_k = 0: the whole row): candidates are written in sorted chunks of 2048 past the first."""
+    rng = np.random.default_rng(53)
+    B, V = 4, 9000
+    x = (rng.standard_normal((B, V)) * 1.5).astype(np.float32)
+    x[1, 100:4000] = np.float32(0.5)
+    p = W.make_params(B, temperature=1.0, top_k=0, top_p=0.9, repetition_penalty=1.0)
+    u = rng.random(B)
+    g, o, nb = check(_case(list(x), p, [np.zeros(0, np.int64)] * B, u, "large_chunks"), kcap=5000)
+    assert nb <= 1
+
+
 def test_verify_large_k():
     rng = np.random.default_rng(8)
     S, M, V = 3, 4, 3000
