@@ -331,7 +331,7 @@ __device__ __forceinline__ void wave_append(bool pred, uint64_t v, uint64_t* lis
     uint32_t base = 0;
     const int leader = __ffsll((unsigned long long)m) - 1;
     if (lane_id() == leader) base = atomicAdd(count, (uint32_t)__popcll(m));
-    base = __shfl(base, leader);
+    base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);   // a scalar read, no LDS round trip
     if (pred) {
         const uint32_t pos = base + mbcnt(m);
         if (pos < cap) list[pos] = v;
@@ -346,7 +346,7 @@ __device__ __forceinline__ void wave_append_kv(bool pred, uint32_t key, uint32_t
     uint32_t base = 0;
     const int leader = __ffsll((unsigned long long)m) - 1;
     if (lane_id() == leader) base = atomicAdd(count, (uint32_t)__popcll(m));
-    base = __shfl(base, leader);
+    base = (uint32_t)__builtin_amdgcn_readlane((int)base, leader);   // a scalar read, no LDS round trip
     if (pred) {
         const uint32_t pos = base + mbcnt(m);
         if (pos < cap) list[pos] = comp_of(key, id);
@@ -796,7 +796,7 @@ __device__ __forceinline__ void gather_window(const Args& a, const RowCtx& rc, i
         if (m != 0ull) {
             uint32_t base = 0u;
             if (lane_id() == 0) base = atomicAdd(&s.nids, (uint32_t)__popcll(m));
-            base = __shfl(base, 0);
+            base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
             const uint32_t pos = base + mbcnt(m);
             if (in && pos < (uint32_t)WIDS) s.ids[pos] = id;
         }
@@ -1548,7 +1548,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             if (tot != 0u) {
                 uint32_t base = 0u;
                 if (lane_id() == 0) base = atomicAdd(&s.count, tot);
-                base = __shfl(base, 0);
+                base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
 #pragma unroll
                 for (int q = 0; q < SPEC; ++q) {
                     if ((bal[q] >> lane_id()) & 1ull) {
@@ -1993,7 +1993,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         for (int i = 0; i < TPT; ++i) tot += (uint32_t)__popcll(bal[i]);
         uint32_t base = 0u;
         if (lane == 0) base = atomicAdd(&s.count, tot);
-        base = __shfl(base, 0);
+        base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
 #pragma unroll
         for (int i = 0; i < TPT; ++i) {
             if (bal[i] != 0ull) {
