@@ -60,6 +60,7 @@ static_assert(SPEC * BLOCK + SMALL + 2 * WAVE + 4 * 2 * WAVE / 2 <= CAP, "merge 
 constexpr int RBITS = 12;                 // row histogram: bins of the top key bits, shared by a row's segments
 constexpr int RBINS = 1 << RBITS;
 constexpr int RSHIFT = 32 - RBITS;
+constexpr int XCDS = 8;                   // MI355X: 8 XCDs, workgroups dealt round-robin by index
 constexpr int WIDS = 2048;                // penalty-window ids of one segment kept in LDS (longer: rescanned per tile)
 
 enum Mode : int { MODE_SAMPLE = 0, MODE_ARGMAX = 1, MODE_VERIFY = 2 };
@@ -1784,34 +1785,30 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
 // A wave's snapshot of its row's histogram: lane l holds the counts of bins b0 + 4 (63 - l) + j, j = 0..3, where
 // b0 is the wave's current bound's bin rounded down to a multiple of 4: the 256 bins (32 binades) from the bound
 // up, in lane order = descending bins; counts above the window are left out (fewer counts: the bound stays
-// valid). Agent-scope loads: the counts come from every segment of the row, on any XCD.
+// valid).
+// The row histogram lives in the L2 of the XCD that runs the row's segments (the grid places them there): counts
+// are L2 atomics and snapshots are loads that skip the CU's L1 (sc0) and hit that L2. Every access is an increment
+// of zeroed memory or a read, so a read returns at most the row's true counts wherever the segments run - if one
+// ran on another XCD its counts would only be missing - and every bound stays valid.
 struct RowSnap {
     uint64_t w[2];
     uint32_t b0;
 };
-__device__ __forceinline__ RowSnap row_snap(const uint32_t* rh, uint32_t tkey) {
+// Through a buffer resource over the row histogram. With 0 records the load returns zeros without a memory access,
+// so the tile loop can request it unconditionally (straight-line loads keep the compiler's memory-counter waits
+// exact).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ u32x4 raw_buffer_load_u32x4(__amdgpu_buffer_rsrc_t rs, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.load.v4i32");
+__device__ uint32_t raw_buffer_load_u32(__amdgpu_buffer_rsrc_t rs, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.load.i32");
+constexpr int AUX_SC0 = 1;               // cache policy: group scope (miss in the CU's L1, served by the XCD's L2)
+__device__ __forceinline__ RowSnap row_snap(__amdgpu_buffer_rsrc_t rs, uint32_t tkey) {
     RowSnap r;
     r.b0 = (tkey >> RSHIFT) & ~3u;
     const uint32_t first = r.b0 + 4u * (uint32_t)(WAVE - 1 - lane_id());
     const uint32_t f = first <= (uint32_t)RBINS - 4u ? first : (uint32_t)RBINS - 4u;   // past the top: ignored
-    const uint64_t* p = reinterpret_cast<const uint64_t*>(rh + f);
-    r.w[0] = ld_agent(p);
-    r.w[1] = ld_agent(p + 1);
-    return r;
-}
-// The same snapshot through a buffer resource over the row histogram (agent-coherent: sc1). With 0 records the load
-// returns zeros without a memory access, so the tile loop can request it unconditionally (straight-line loads keep
-// the compiler's memory-counter waits exact).
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-__device__ u32x4 raw_buffer_load_u32x4(__amdgpu_buffer_rsrc_t rs, int voffset, int soffset, int aux)
-    __asm("llvm.amdgcn.raw.ptr.buffer.load.v4i32");
-constexpr int AUX_SC1 = 16;              // cache policy: system-coherent level 1 (bypass the XCD's L2)
-__device__ __forceinline__ RowSnap row_snap_buf(__amdgpu_buffer_rsrc_t rs, uint32_t tkey) {
-    RowSnap r;
-    r.b0 = (tkey >> RSHIFT) & ~3u;
-    const uint32_t first = r.b0 + 4u * (uint32_t)(WAVE - 1 - lane_id());
-    const uint32_t f = first <= (uint32_t)RBINS - 4u ? first : (uint32_t)RBINS - 4u;
-    const u32x4 v = raw_buffer_load_u32x4(rs, (int)(f * 4u), 0, AUX_SC1);
+    const u32x4 v = raw_buffer_load_u32x4(rs, (int)(f * 4u), 0, AUX_SC0);
     r.w[0] = (uint64_t)v.x | ((uint64_t)v.y << 32);
     r.w[1] = (uint64_t)v.z | ((uint64_t)v.w << 32);
     return r;
@@ -1937,6 +1934,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     uint32_t tkey = 0u;                // top-k: candidates are the logits with key >= tkey
     float tf = -__builtin_huge_valf(); //         in fp32: x >= tf (NaN never passes)
     uint32_t* rh = a.rhist + (int64_t)rc.row * RBINS;
+    const __amdgpu_buffer_rsrc_t rsr = __builtin_amdgcn_make_buffer_rsrc(rh, (short)0, RBINS * 4, 0x00020000);
     // Row bounds from the row histogram. Segments of >= 3 tiles: each wave snapshots it after tile 0 and takes the
     // bound before appending tile 1; segments of >= 5 tiles snapshot again at tile 3 and take at tile 4, within one
     // iteration of the tile loop (no load outstanding across its back edge).
@@ -1956,7 +1954,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     };
     auto row_read = [&](uint32_t b0) -> uint32_t {
         const uint32_t b = b0 + (uint32_t)(BLOCK - 1 - tid);
-        return ld_agent(rh + (b < (uint32_t)RBINS ? b : (uint32_t)RBINS - 1u));
+        return raw_buffer_load_u32(rsr, (int)(4u * (b < (uint32_t)RBINS ? b : (uint32_t)RBINS - 1u)), 0, AUX_SC0);
     };
     // the highest bin b (>= rb0) with at least k counted logits in bins [b, rb0 + BLOCK - 1]: a row-wide bound
     auto row_take = [&](uint32_t rb0, uint32_t rcnt) {
@@ -2029,7 +2027,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         }
         const uint32_t c = wb[lane_id()];
         if (c != 0u && rb + (uint32_t)lane_id() < (uint32_t)RBINS)
-            __hip_atomic_fetch_add(rh + rb + lane_id(), c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_fetch_add(rh + rb + lane_id(), c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);   // an L2 atomic
         counted = nb;
     };
     // barrier + count; returns it (> CAP: overflowed). Compacts when the headroom gets short: for k <= 256, in safe
@@ -2116,7 +2114,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                         raise_key((rc0 + (uint32_t)(WAVE - 1) - (uint32_t)(__ffsll((unsigned long long)hb) - 1)) << RSHIFT);
                     if (tid < WAVE) {
                         const uint32_t c = s.rc64[tid];
-                        if (c != 0u) __hip_atomic_fetch_add(rh + rc0 + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if (c != 0u) __hip_atomic_fetch_add(rh + rc0 + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                     }
                 }
                 topk_append(x, lo);
@@ -2126,7 +2124,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 lastn = 0;
                 const int n = check(1, safe);
                 overflow = n > CAP;
-                if (!safe && ntiles >= 3) snap1 = row_snap(rh, tkey);
+                if (!safe && ntiles >= 3) snap1 = row_snap(rsr, tkey);
                 const int per_tile = n > 32 ? n : 32;
                 R = safe ? 1 : (CAP - n) / (2 * per_tile);
                 if (R < 1) R = 1;
@@ -2185,7 +2183,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                         }
                         if (p == 0 && checked && dynrow && !overflow && t0 + PF < ntiles) count_row(counted);
                         if (p == 0) dpend = dynrow && !overflow && t0 + PF < ntiles;
-                        if (p == 0 && snap) snap2 = row_snap(rh, tkey);
+                        if (p == 0 && snap) snap2 = row_snap(rsr, tkey);
                         if (p == 1 && count2 && !overflow) {
                             // second count: the buffered logits of tiles 1-4
                             __syncthreads();
@@ -2196,7 +2194,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     }
                 }
                 if (p == 0) {
-                    snapd = row_snap_buf(rsh, tkey);
+                    snapd = row_snap(rsh, tkey);
                     load_seg_tile(x, g.rs, tt + PF);
                 }
             }
@@ -2259,10 +2257,15 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, 
     __shared__ __align__(16) Shared s;
     a.logits = logits; a.ld = ld; a.B = B; a.V = V; a.nseg = nseg; a.seg_tiles = seg_tiles; a.params = params;
     a.hist_off = hist_off;
-    const int item = (int)blockIdx.x;                // one (row, segment) item per workgroup
-    // uniform by construction; readfirstlane lets the compiler use scalar loads for the row's parameters
-    const int row = __builtin_amdgcn_readfirstlane(item / a.nseg);
-    const int seg = item - row * a.nseg;
+    // One (row, segment) item per workgroup. Workgroup i runs on XCD i % XCDS (round-robin dispatch): slot
+    // x = i % XCDS takes the rows x, x + XCDS, ..., all segments of a row in consecutive rounds, so a row's segments
+    // share one XCD and its L2 (the row histogram). Slots past the last row return at once.
+    const int x = (int)(blockIdx.x % (unsigned)XCDS);
+    const int j = (int)(blockIdx.x / (unsigned)XCDS);
+    const int q = __builtin_amdgcn_readfirstlane(j / a.nseg);    // uniform: lets the compiler use scalar loads
+    const int seg = j - q * a.nseg;
+    const int row = x + XCDS * q;
+    if (row >= a.B) return;
     float buf[PF][TPT];
     const SegStart g = seg_start(a, row, seg, buf);   // the tiles are on their way before the parameters
     const RowCtx rc = row_ctx(a, row);
@@ -2540,7 +2543,9 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
     if (a.nseg > fs::MAX_SEGS) return FS_E_INVALID;
     const int64_t items = rows * a.nseg;
     if (items > 0x7fffffff) return FS_E_INVALID;
-    const int64_t seg_grid = items;                // one workgroup per (row, segment)
+    // one workgroup per (row, segment), the rows dealt to XCDS slots (segment_kernel)
+    const int64_t seg_grid = items > 0 ? (int64_t)fs::XCDS * a.nseg * ((rows + fs::XCDS - 1) / fs::XCDS) : 0;
+    if (seg_grid > 0x7fffffff) return FS_E_INVALID;
     int rc = grow(ctx, (size_t)(items + rows), (size_t)rows, (size_t)(streams > 0 ? streams : 1));
     if (rc != FS_OK) return rc;
     a.cand = ctx->cand; a.meta = ctx->meta; a.row_cnt = ctx->row_cnt; a.rhist = ctx->rhist;
