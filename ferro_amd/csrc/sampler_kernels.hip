@@ -2,28 +2,29 @@
 //
 // Two kernels per call on the caller's stream.
 //
-// segment_kernel (persistent, two 512-thread workgroups per CU): a row of V fp32 logits is split into nseg
-// segments of seg_tiles tiles (TILE = 4096 logits); workgroup g handles items g, g+G, ... (item = row*nseg + seg,
-// row-major). A segment is streamed from HBM with PF tiles in flight (16-byte loads, the only pass over the
-// logits). Per tile:
-//   - penalty pass on the fly (reference src/sampler.cpp:11-18, plus the frequency/presence extension): the row's
-//     history window ids that fall in the tile are counted in a 16-bit LDS table and each thread patches the few
-//     penalised logits it holds;
-//   - greedy rows (temperature <= 0 or top_k == 1, sampler.cpp:19): each lane keeps its first maximum
-//     (order-preserving 32-bit keys, -0 folded onto +0, so ties go to the lowest id);
-//   - top-k rows: every logit is compared with a running fp32 threshold tf; the few that pass are checked against
-//     the exact 64-bit composite threshold X (key << 32 | ~id: integer order = ferro's candidate order, value desc
-//     then id asc, sampler.cpp:30) and appended to an LDS buffer with one LDS atomic per wave per tile.
-// The initial threshold comes from tile 0 (the maxima of >= 2k groups, histogrammed over their [min, max]: at least
-// k logits reach it); the buffer is compacted to the exact k-th composite when another tile could overflow it,
-// and at the end of the segment, so each segment publishes exactly its top k (or everything, if fewer).
+// segment_kernel (one 512-thread workgroup per (row, segment) item, two per CU): a row of V fp32 logits is split
+// into nseg segments of seg_tiles tiles (TILE = 4096 logits); the items are dealt to the 8 XCDs so that a row's
+// segments share one XCD and its L2. A segment is streamed from HBM with PF tiles in flight (16-byte buffer
+// loads, the only pass over the logits). Per tile:
+//   - penalty pass on the fly (reference src/sampler.cpp:11-18, plus the frequency/presence extension):
+//     repetition only - an exact bitmap of the window's ids in the segment; with counts - the window ids that fall
+//     in the tile are counted in a 16-bit LDS table; each thread patches the few penalised logits it holds;
+//   - greedy rows (temperature <= 0 or top_k == 1, sampler.cpp:19): each lane keeps its first maximum;
+//   - top-k rows: every logit is compared with a running fp32 bound tf (a lower bound of the row's k-th key) in a
+//     wave ballot; the few that pass are appended to an LDS buffer as 64-bit composites (key << 32 | ~id: integer
+//     order = ferro's candidate order, value desc then id asc, sampler.cpp:30).
+// The bound starts from tile 0's histogram and is raised from a per-row histogram of counted logits shared by the
+// row's segments (L2 atomics): any k counted logits at or above a bin make its lower edge a valid bound. The
+// buffer is compacted (entries below the bound dropped, else the exact k-th composite kept) when it could
+// overflow. Each segment publishes its candidates at or above its final bound.
 //
-// merge_kernel (one workgroup per row): gathers the segments' lists in one memory round trip, L = max of the
-// segments' k-th keys bounds the row's k-th key from below, a histogram over [L, max] gives a tight T1, the ~k
-// candidates >= T1 are rank-sorted in LDS (ferro's cand_, sampler.cpp:25-35), then the double-precision softmax
-// at temperature, min-p, top-p and the draw r = u * tot (sampler.cpp:37-49), with block scans in place of the
-// sequential sums. Verify windows (server.cpp:627-637): the last row of a stream to finish (agent-scope sc1
-// stores, a vmcnt drain and an agent-scope counter, no L2 write-back) computes the accepted prefix.
+// merge_kernel (one workgroup per row): gathers the segments' lists, L = max of the segments' bounds bounds the
+// row's k-th key from below, a histogram over [L, max] gives a tight T1, the ~k candidates >= T1 are sorted in
+// LDS (ferro's cand_, sampler.cpp:25-35; rank sort or a counting sort), then the double-precision softmax at
+// temperature, min-p, top-p and the draw r = u * tot (sampler.cpp:37-49), with scans in place of the sequential
+// sums. Rows with k > 2048 are sampled here by whole-row passes. Verify windows (server.cpp:627-637): the last
+// row of a stream to finish (agent-scope sc1 stores, a vmcnt drain and an agent-scope counter, no L2 write-back)
+// computes the accepted prefix.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -2246,8 +2247,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     __syncthreads();                               // LDS is reused by the next item
 }
 
-// Segment kernel (persistent): workgroup g handles items g, g+G, ... (item = row*nseg + segment, row-major; rows
-// sampled with k > KMAX are left to the merge kernel).
+// Segment kernel: one (row, segment) item per workgroup (rows sampled with k > KMAX are left to the merge kernel).
 // The fields a workgroup needs first come as separate leading parameters: gfx950 preloads those into SGPRs at
 // wave launch (build flag -amdgpu-kernarg-preload-count), so the first tile loads wait for no argument load.
 __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, int64_t ld, int B, int V, int nseg,
