@@ -295,6 +295,24 @@ __device__ __forceinline__ double block_sum_f64(double v, Red& r) {
     __syncthreads();
     return s;
 }
+// DPP moves of a double (two 32-bit halves); lanes without a source read 0 (bound_ctrl off, old = 0).
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROWMASK, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROWMASK, 0xF, false);
+    return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint64_t)(uint32_t)lo));
+}
+// Inclusive wave scan: row_shr 1, 2, 4, 8 inside each 16-lane row, then row_bcast 15 / 31 across rows.
+__device__ __forceinline__ double wave_scan_f64(double v) {
+    v += dpp_f64<0x111, 0xF>(v);
+    v += dpp_f64<0x112, 0xF>(v);
+    v += dpp_f64<0x114, 0xF>(v);
+    v += dpp_f64<0x118, 0xF>(v);
+    v += dpp_f64<0x142, 0xA>(v);
+    v += dpp_f64<0x143, 0xC>(v);
+    return v;
+}
 // Exclusive prefix over threads (thread order), deterministic; *total = the sum over the block.
 template <class T>
 __device__ __forceinline__ T block_excl_scan(T v, T* wsum /*NWAVES*/, T* total) {
@@ -303,7 +321,10 @@ __device__ __forceinline__ T block_excl_scan(T v, T* wsum /*NWAVES*/, T* total) 
     if constexpr (sizeof(T) == 4 && T(-1) > T(0)) {            // 32-bit unsigned: DPP scan (exact in any order)
         x = wave_incl_scan_u32(v);
         ex = x - v;
-    } else {                                                   // the fixed shuffle order of the double sums
+    } else if constexpr (sizeof(T) == 8 && T(0.5) > T(0)) {    // double: DPP scan, then wave_shr:1 (lane 0 reads 0)
+        x = wave_scan_f64(v);
+        ex = dpp_f64<0x138, 0xF>(x);
+    } else {                                                   // the fixed shuffle order of the sums
         x = v;
 #pragma unroll
         for (int o = 1; o < WAVE; o <<= 1) {
@@ -1210,24 +1231,6 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
 // softmax / min-p / top-p / draw of sampler.cpp:37-49, the sums as DPP wave scans in candidate order. LDS accesses
 // of one wave are ordered, so no further block barrier is needed: the other waves go straight to the epilogue.
 
-// DPP moves of a double (two 32-bit halves); lanes without a source read 0 (bound_ctrl off, old = 0).
-template <int CTRL, int ROWMASK>
-__device__ __forceinline__ double dpp_f64(double v) {
-    const uint64_t u = (uint64_t)__double_as_longlong(v);
-    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROWMASK, 0xF, false);
-    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROWMASK, 0xF, false);
-    return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint64_t)(uint32_t)lo));
-}
-// Inclusive wave scan: row_shr 1, 2, 4, 8 inside each 16-lane row, then row_bcast 15 / 31 across rows.
-__device__ __forceinline__ double wave_scan_f64(double v) {
-    v += dpp_f64<0x111, 0xF>(v);
-    v += dpp_f64<0x112, 0xF>(v);
-    v += dpp_f64<0x114, 0xF>(v);
-    v += dpp_f64<0x118, 0xF>(v);
-    v += dpp_f64<0x142, 0xA>(v);
-    v += dpp_f64<0x143, 0xC>(v);
-    return v;
-}
 __device__ __forceinline__ double lane_f64(double v, int lane) {   // lane: wave-uniform
     const uint64_t u = (uint64_t)__double_as_longlong(v);
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, lane);
@@ -1660,11 +1663,11 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 __syncthreads();
                 m = (int)s.count;
             }
-            if (m > k) {
+            if (m > KMAX) {                             // else the counting sort orders all m; the first k are used
                 compact_exact(m, k, s);
                 m = k;
             }
-            bin_sort_desc(m, s);                        // m <= KMAX
+            bin_sort_desc(m, s);
             top = s.cand;
             c1 = (uint32_t)m;
         }
