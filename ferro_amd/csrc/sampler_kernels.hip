@@ -749,6 +749,19 @@ __device__ __forceinline__ void load_tile(float (&x)[TPT], const float* rowp, in
         x[4 * j + 0] = t.x; x[4 * j + 1] = t.y; x[4 * j + 2] = t.z; x[4 * j + 3] = t.w;
     }
 }
+// Tile t of a segment through its buffer resource: a tile past the segment's end reads zeros without a memory
+// access, so the tile loop requests its next tiles unconditionally (straight-line loads keep the compiler's
+// memory-counter waits exact: consuming a tile waits for that tile only).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ f32x4 raw_buffer_load_f32x4(__amdgpu_buffer_rsrc_t rs, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.load.v4f32");
+__device__ __forceinline__ void load_seg_tile(float (&x)[TPT], __amdgpu_buffer_rsrc_t rs, int t) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const f32x4 v = raw_buffer_load_f32x4(rs, (j * BLOCK + (int)threadIdx.x) * 16, t * TILE * 4, 0);
+        x[4 * j + 0] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
+    }
+}
 // The model's final-logit softcap, moved into the read: l = cap * tanhf(l / cap) (model_gemma4_gpu.cpp:282-283:
 // fp32 divide, tanhf, fp32 multiply), before the penalties as in ferro, where the model caps the row first.
 template <int N>
@@ -927,44 +940,33 @@ __device__ __forceinline__ uint64_t compact_exact(int n, int k, Shared& s) {
 //   5. top-p and the draw: the first candidate (candidate order) whose cumulative mass reaches a target, by a
 //      descent over fp64 mass histograms of the keys, then the j-th smallest id among the ties at the final key.
 // Sums run in a different order than ferro's sequential loop (probabilities agree to ~1e-15 relative).
-constexpr int LPF = 2;                    // tiles in flight per large-row pass
+constexpr int LPF = 4;                    // tiles in flight per large-row pass
 constexpr int MB = 256;                   // mass histogram bins
 
-// Issue the loads of the tile at lo of a row that may end inside it (elements >= V read as 0, never used).
-__device__ __forceinline__ void load_tile_masked(float (&x)[TPT], const float* rowp, int lo, int V) {
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const int e = lo + (j * BLOCK + (int)threadIdx.x) * 4;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) x[4 * j + q] = e + q < V ? rowp[e + q] : 0.f;
-    }
-}
-
 // One pass over the whole row, LPF tiles in flight, penalties applied (the window ids are in s.ids): g(x, lo) per
-// tile, called by every thread (g may use barriers). Element i of a thread is elem_id(lo, i) when < V.
+// tile, called by every thread (g may use barriers). Element i of a thread is elem_id(lo, i) when < V. The tiles are
+// read through a buffer resource over the row (rounded up to whole float4s, which stay inside the row's ld-strided
+// allocation): loads past it return zeros without a memory access, so every tile's successor is requested
+// unconditionally and the compiler's memory-counter waits stay exact (consuming a tile waits for that tile only).
 template <class G>
 __device__ __forceinline__ void row_tiles(const Args& a, const RowCtx& rc, Shared& s, G g) {
     const int V = a.V;
     const float* rowp = a.logits + (int64_t)rc.row * a.ld;
     const int ntile = (V + TILE - 1) / TILE;
-    const int full = V / TILE;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(rowp), (short)0,
+                                                                        ((V + 3) & ~3) * 4, 0x00020000);
     float buf[LPF][TPT];
 #pragma unroll
-    for (int p = 0; p < LPF; ++p) {
-        if (p < full) load_tile(buf[p], rowp, p * TILE);
-        else if (p < ntile) load_tile_masked(buf[p], rowp, p * TILE, V);
-    }
+    for (int p = 0; p < LPF; ++p) load_seg_tile(buf[p], rs, p);
     for (int t0 = 0; t0 < ntile; t0 += LPF) {
 #pragma unroll
         for (int p = 0; p < LPF; ++p) {
             const int t = t0 + p;
-            if (t < ntile) {
-                float x[TPT];
+            float x[TPT];
 #pragma unroll
-                for (int i = 0; i < TPT; ++i) x[i] = buf[p][i];
-                const int nt = t + LPF;
-                if (nt < full) load_tile(buf[p], rowp, nt * TILE);
-                else if (nt < ntile) load_tile_masked(buf[p], rowp, nt * TILE, V);
+            for (int i = 0; i < TPT; ++i) x[i] = buf[p][i];
+            load_seg_tile(buf[p], rs, t + LPF);
+            if (t < ntile) {
                 if (rc.capped) softcap_vals(x, rc.p.softcap);
                 if (rc.pen) {
                     __syncthreads();                 // the previous tile's table reads are done
@@ -1113,12 +1115,12 @@ __device__ __forceinline__ uint64_t large_mass_select(const Args& a, const RowCt
     return large_pick(a, rc, s, klo, lo_c, j);
 }
 
-// The whole large-k sample of one row: token, kept count, optional candidate outputs (in chunks of KMAX).
-__device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Shared& s, int& tok_out, int& keep_out) {
+// The exact multi-pass selection (narrowing histograms over the keys; about 15 passes over the row): the fallback
+// of large_row when a coarse-bin step does not apply. Sets the token and the kept count.
+__device__ __forceinline__ void large_row_exact(const Args& a, const RowCtx& rc, Shared& s, int& tok_out, int& keep_out) {
     const int tid = threadIdx.x;
     const int row = rc.row;
     const fs_row_params& p = rc.p;
-    if (rc.pen) gather_window(a, rc, 0, a.V, s);
     // 1. extremes and count of the ordered elements
     uint64_t cmax = 0ull, cmin = ~0ull;
     uint32_t nv = 0u;
@@ -1191,7 +1193,14 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
     if (pick == 0ull) pick = clast;
     tok_out = (int)comp_id(pick);
     keep_out = (int)keep;
-    // optional outputs: the first min(k, kcap) candidates in candidate order, KMAX at a time
+    (void)tid;
+}
+
+// Optional outputs of a large row: the first min(k, kcap) candidates in candidate order, KMAX at a time.
+__device__ __forceinline__ void large_outputs(const Args& a, const RowCtx& rc, Shared& s, int keff, uint64_t Xk, uint32_t kk,
+                                              uint32_t kmax, float mx, double Td, double S) {
+    const int tid = threadIdx.x;
+    const int row = rc.row;
     if (a.mode != MODE_VERIFY && a.kcap > 0 && (a.cand_ids || a.cand_probs)) {
         const int mtot = keff < a.kcap ? keff : a.kcap;
         uint64_t hi_c = ~0ull;                          // this chunk: composites in [Xc, hi_c)
@@ -1223,6 +1232,296 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
             hi_c = Xc;
         }
     }
+}
+
+
+// ---- large k through coarse key bins: a few passes instead of ~15
+// Pass 1: extremes and a count histogram over LB coarse bins (key >> LB_SHIFT). Xk (the k-th composite, k < the
+// count) is narrowed inside its coarse bin. Pass 2: S (a deterministic fp64 block sum, as the exact path) and a
+// fixed-point mass histogram over the same bins (integer sums: deterministic, within 2^-44 per element). The bins'
+// masses stay in registers (thread t: descending positions PT*t ..). The top-p and draw targets each pick a coarse
+// bin from them; one pass gathers that bin's candidates into LDS, a counting sort orders them and the exact fp64
+// masses are walked in candidate order from the bin's fixed-point "above" mass. A target that does not fall inside
+// its bin's exact masses (a rounding step at the bin edge), or a bin of more than KMAX candidates, takes the exact
+// multi-pass selection instead.
+constexpr int LB = 4096;                    // coarse key bins of the large-k path
+constexpr int LB_SHIFT = 32 - 12;
+constexpr int LPT = LB / BLOCK;             // coarse bins per thread
+constexpr double FXS = 17592186044416.0;    // 2^44: fixed-point mass scale (an element's mass is <= 1)
+static_assert(LB * 8 <= CAP * 8, "the fixed-point mass histogram fits the candidate buffer");
+
+// Smallest descending position d (bin LB-1-d) at which the running total from the top reaches target, given each
+// thread's LPT values at positions LPT*t + j; *above = the total of the positions before d. -1: never reached.
+template <class T>
+__device__ __forceinline__ int desc_locate(const T (&v)[LPT], T target, T* above, T* wsum, Shared& s) {
+    const int tid = threadIdx.x;
+    T sum = T(0);
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) sum += v[j];
+    T tot;
+    T run = block_excl_scan<T>(sum, wsum, &tot);
+    int hit = 0x7fffffff;
+    T ab = T(0);
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+        if (hit == 0x7fffffff && v[j] != T(0) && run + v[j] >= target) {
+            hit = LPT * tid + j;
+            ab = run;
+        }
+        run += v[j];
+    }
+    const int d = block_min_i32(hit, s.red);
+    if (d == 0x7fffffff) return -1;
+    if (hit == d) s.red.u64b[0] = (uint64_t)ab;
+    __syncthreads();
+    *above = (T)s.red.u64b[0];
+    __syncthreads();
+    return d;
+}
+// Gathers the candidates (composite >= lo_c) of coarse bin b into s.cand[0, n) and sorts them; returns n, or -1
+// when more than KMAX (the caller falls back). Extra per-element work f(x, key, composite) for every candidate.
+template <class F>
+__device__ __forceinline__ int large_gather_bin(const Args& a, const RowCtx& rc, Shared& s, uint32_t b, uint64_t lo_c, F f) {
+    const int V = a.V;
+    if (threadIdx.x == 0) s.count = 0u;
+    __syncthreads();
+    row_tiles(a, rc, s, [&](const float (&x)[TPT], int lo) {
+#pragma unroll
+        for (int i = 0; i < TPT; ++i) {
+            const int e = elem_id(lo, i);
+            const bool ok = e < V && x[i] == x[i];
+            const uint32_t kq = key_of(x[i]);
+            const uint64_t c = comp_of(kq, (uint32_t)e);
+            const bool cand = ok && c >= lo_c;
+            if (cand) f(x[i], kq, c);
+            const bool in = cand && (kq >> LB_SHIFT) == b;
+            wave_append(in, c, s.cand, &s.count, KMAX);
+        }
+    });
+    const int n = (int)s.count;                       // row_tiles ends with a barrier
+    if (n > KMAX) return -1;
+    bin_sort_desc(n, s);
+    return n;
+}
+
+// The first of the n sorted entries s.cand[0, n) with composite >= lo_c at which above + the running exact mass
+// reaches target: its index, and the running mass there in *cum. -1: above >= target (the crossing lies in a higher
+// bin); -2: the bin's masses end below target.
+__device__ __forceinline__ int large_walk(Shared& s, int n, uint64_t lo_c, double above, double target, float mx, double Td,
+                                          double* cum) {
+    const int i0 = (int)threadIdx.x * KPT;
+    if (!(above < target)) return -1;
+    double e[KPT], run = 0.0;
+#pragma unroll
+    for (int q = 0; q < KPT; ++q) {
+        const int i = i0 + q;
+        e[q] = (i < n && s.cand[i] >= lo_c) ? mass_of(val_of(comp_key(s.cand[i])), mx, Td) : 0.0;
+        run += e[q];
+    }
+    double tot;
+    const double off = block_excl_scan<double>(run, s.red.f64, &tot);
+    double c = above + off;
+    int hit = 0x7fffffff;
+    double ch = 0.0;
+#pragma unroll
+    for (int q = 0; q < KPT; ++q) {
+        c += e[q];
+        if (hit == 0x7fffffff && i0 + q < n && e[q] > 0.0 && c >= target) { hit = i0 + q; ch = c; }
+    }
+    const int first = block_min_i32(hit, s.red);
+    if (first == 0x7fffffff) return -2;
+    if (hit == first) s.red.dmisc[2] = ch;
+    __syncthreads();
+    *cum = s.red.dmisc[2];
+    __syncthreads();
+    return first;
+}
+
+// The whole large-k sample of one row: token, kept count, optional candidate outputs (in chunks of KMAX).
+__device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Shared& s, int& tok_out, int& keep_out) {
+    const int tid = threadIdx.x;
+    const int row = rc.row;
+    const fs_row_params& p = rc.p;
+    if (rc.pen) gather_window(a, rc, 0, a.V, s);
+    // 1. extremes, count of the ordered elements, their coarse-bin counts
+    uint32_t* hc = reinterpret_cast<uint32_t*>(s.cand);
+    for (int i = tid; i < LB; i += BLOCK) hc[i] = 0u;
+    __syncthreads();
+    uint64_t cmax = 0ull, cmin = ~0ull;
+    uint32_t nv = 0u;
+    row_elems(a, rc, s, [&](float, uint32_t kq, uint64_t c) {
+        cmax = c > cmax ? c : cmax;
+        cmin = c < cmin ? c : cmin;
+        ++nv;
+        atomicAdd(&hc[kq >> LB_SHIFT], 1u);
+    });
+    cmax = block_max_u64(cmax, s.red);
+    cmin = block_min_u64(cmin, s.red);
+    uint32_t ntot;
+    (void)block_excl_scan<uint32_t>(nv, s.wsum, &ntot);
+    if (ntot == 0u) {                         // every logit NaN: no order to sample from
+        tok_out = 0;
+        keep_out = 0;
+        return;
+    }
+    const uint32_t kmax = comp_key(cmax);
+    const float mx = val_of(kmax);
+    const double Td = (double)p.temperature;
+    const int keff = (uint32_t)rc.k < ntot ? rc.k : (int)ntot;
+    uint64_t Xk = cmin;
+    if ((uint32_t)keff < ntot) {                          // the k-th composite, inside its coarse bin
+        uint32_t cv[LPT];
+#pragma unroll
+        for (int j = 0; j < LPT; ++j) cv[j] = hc[LB - 1 - (LPT * tid + j)];
+        uint32_t abk = 0u;
+        const int dk = desc_locate<uint32_t>(cv, (uint32_t)keff, &abk, s.wsum, s);
+        const uint32_t bk = (uint32_t)(LB - 1 - dk);
+        const uint32_t blo = bk << LB_SHIFT, bhi = blo | ((1u << LB_SHIFT) - 1u);
+        Xk = large_kth(a, rc, s, keff - (int)abk, 1ull, ~0ull, blo, bhi);
+    }
+    const uint32_t kk = comp_key(Xk);
+    // 2. S and the fixed-point mass histogram of the candidates
+    uint64_t* hm = reinterpret_cast<uint64_t*>(s.cand);
+    for (int i = tid; i < LB; i += BLOCK) hm[i] = 0ull;
+    __syncthreads();
+    double part = 0.0;
+    row_elems(a, rc, s, [&](float x, uint32_t kq, uint64_t c) {
+        if (c >= Xk) {
+            const double m = mass_of(x, mx, Td);
+            part += m;
+            atomicAdd(reinterpret_cast<unsigned long long*>(&hm[kq >> LB_SHIFT]), (unsigned long long)(m * FXS + 0.5));
+        }
+    });
+    const double S = block_sum_f64(part, s.red);          // its barriers also complete the histogram
+    uint64_t mv[LPT];
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) mv[j] = hm[LB - 1 - (LPT * tid + j)];
+    __syncthreads();                                      // the candidate buffer is reused below
+    // 3. min-p: the smallest key whose pr reaches pr[0] * min_p (pr[0] = 1 / S)
+    bool ok_fast = true;
+    uint64_t Xm = 0ull;
+    uint32_t km = 0xFFFFFFFFu;
+    if (p.min_p > 0.0f) {
+        const double thr = (1.0 / S) * (double)p.min_p;
+        auto ok = [&](uint32_t key) { return mass_of(val_of(key), mx, Td) / S >= thr; };
+        if (!ok(kmax)) {
+            Xm = cmax;                                    // keep >= 1
+        } else {
+            uint32_t lo = kk, hi = kmax;
+            while (lo < hi) {
+                const uint32_t mid = lo + ((hi - lo) >> 1);
+                if (ok(mid)) hi = mid; else lo = mid + 1u;
+            }
+            km = lo;
+            Xm = (uint64_t)lo << 32;
+        }
+    }
+    // 4. top-p's crossing bin, gathered with the min-p counts and masses
+    uint64_t Xc = 0ull;
+    uint32_t keep_c = 0u;
+    double tot_c = 0.0;
+    int nc = -1;                                          // top-p's bin, sorted in s.cand (-1: none)
+    uint32_t bc = 0u;
+    double above_c = 0.0;
+    uint32_t cnt_m = 0u, ca_c = 0u;
+    double sum_m = 0.0;
+    uint64_t cl_m = ~0ull;
+    const bool need_m = p.min_p > 0.0f && Xm != cmax;
+    if (p.top_p < 1.0f || need_m) {
+        const double tgt = (double)p.top_p * S;
+        uint64_t abfx = 0ull;
+        int dc = -1;
+        if (p.top_p < 1.0f) {
+            dc = desc_locate<uint64_t>(mv, (uint64_t)(tgt * FXS), &abfx, s.red.u64b, s);
+            if (dc < 0) dc = LB - 1 - (int)(kk >> LB_SHIFT);     // the total rounds below the target: last bin
+            bc = (uint32_t)(LB - 1 - dc);
+            above_c = (double)abfx / FXS;
+        }
+        const uint32_t bsel = p.top_p < 1.0f ? bc : 0xFFFFFFFFu;
+        uint32_t my_ca = 0u, my_cm = 0u;
+        double my_sm = 0.0;
+        uint64_t my_cl = ~0ull;
+        nc = large_gather_bin(a, rc, s, bsel, Xk, [&](float x, uint32_t kq, uint64_t c) {
+            if ((kq >> LB_SHIFT) > bsel && bsel != 0xFFFFFFFFu) ++my_ca;
+            if (need_m && kq >= km) {
+                ++my_cm;
+                my_sm += mass_of(x, mx, Td);
+                my_cl = c < my_cl ? c : my_cl;
+            }
+        });
+        (void)block_excl_scan<uint32_t>(my_ca, s.wsum, &ca_c);
+        if (need_m) {
+            (void)block_excl_scan<uint32_t>(my_cm, s.wsum, &cnt_m);
+            sum_m = block_sum_f64(my_sm, s.red);
+            cl_m = block_min_u64(my_cl, s.red);
+        }
+        if (p.top_p < 1.0f) {
+            if (nc < 0) {
+                ok_fast = false;
+            } else {
+                double cum = 0.0;
+                const int ic = large_walk(s, nc, Xk, above_c, tgt, mx, Td, &cum);
+                if (ic < 0) {
+                    ok_fast = false;
+                } else {
+                    Xc = s.cand[ic];
+                    keep_c = ca_c + (uint32_t)ic + 1u;
+                    tot_c = cum;
+                }
+            }
+        }
+    }
+    if (!ok_fast) {
+        large_row_exact(a, rc, s, tok_out, keep_out);
+        large_outputs(a, rc, s, keff, Xk, kk, kmax, mx, Td, S);
+        return;
+    }
+    // the kept prefix: the largest of the three thresholds (sampler.cpp:43-44)
+    uint64_t Xkeep = Xk, clast = Xk;
+    uint32_t keep = (uint32_t)keff;
+    double tot = S;
+    if (p.min_p > 0.0f && Xm > Xkeep) {
+        Xkeep = Xm;
+        if (Xm == cmax) { keep = 1u; tot = 1.0; clast = cmax; }   // mass_of(mx) = exp(0)
+        else { keep = cnt_m; tot = sum_m; clast = cl_m; }
+    }
+    if (p.top_p < 1.0f && Xc > Xkeep) {
+        Xkeep = Xc;
+        keep = keep_c;
+        tot = tot_c;
+        clast = Xc;
+    }
+    // 5. the draw r = u * tot (sampler.cpp:45-49), in mass units
+    const double u = a.u ? a.u[row] : 0.0;
+    const double r = u * tot + 0.0;
+    uint64_t abd = 0ull;
+    int dd = desc_locate<uint64_t>(mv, (uint64_t)(r * FXS), &abd, s.red.u64b, s);
+    uint64_t pick = 0ull;
+    bool drawn = false;
+    if (dd >= 0) {
+        const uint32_t bd = (uint32_t)(LB - 1 - dd);
+        int nd = -1;
+        if (nc >= 0 && bd == bc && p.top_p < 1.0f) {
+            nd = nc;                                          // the same bin is in LDS already
+        } else {
+            nd = large_gather_bin(a, rc, s, bd, Xkeep, [&](float, uint32_t, uint64_t) {});
+        }
+        if (nd >= 0) {
+            double cum = 0.0;
+            const int id = large_walk(s, nd, Xkeep, (double)abd / FXS, r, mx, Td, &cum);
+            if (id >= 0) {
+                pick = s.cand[id];
+                drawn = true;
+            } else if (id == -2 && comp_key(Xkeep) >> LB_SHIFT == bd) {
+                drawn = true;                                 // past the last kept candidate: clast
+            }
+        }
+    }
+    if (!drawn) pick = large_mass_select(a, rc, s, r, Xkeep, comp_key(Xkeep), kmax, mx, Td);
+    if (pick == 0ull) pick = clast;
+    tok_out = (int)comp_id(pick);
+    keep_out = (int)keep;
+    large_outputs(a, rc, s, keff, Xk, kk, kmax, mx, Td, S);
 }
 
 // ------------------------------------------------------------------------------------------------ one-wave finish
@@ -1843,19 +2142,6 @@ struct SegStart {
     const float* rowp;
     __amdgpu_buffer_rsrc_t rs;   // [seg_lo, seg_lo + ntiles * TILE) of the row
 };
-// Tile t of a segment through its buffer resource: a tile past the segment's end reads zeros without a memory
-// access, so the tile loop requests its next tiles unconditionally (straight-line loads keep the compiler's
-// memory-counter waits exact: consuming a tile waits for that tile only).
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-__device__ f32x4 raw_buffer_load_f32x4(__amdgpu_buffer_rsrc_t rs, int voffset, int soffset, int aux)
-    __asm("llvm.amdgcn.raw.ptr.buffer.load.v4f32");
-__device__ __forceinline__ void load_seg_tile(float (&x)[TPT], __amdgpu_buffer_rsrc_t rs, int t) {
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const f32x4 v = raw_buffer_load_f32x4(rs, (j * BLOCK + (int)threadIdx.x) * 16, t * TILE * 4, 0);
-        x[4 * j + 0] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
-    }
-}
 __device__ __forceinline__ SegStart seg_start(const Args& a, int row, int seg, float (&buf)[PF][TPT]) {
     SegStart g;
     g.seg_lo = seg * a.seg_tiles * TILE;
