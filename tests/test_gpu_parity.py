@@ -319,6 +319,31 @@ def test_large_k_candidate_chunks():
     assert nb <= 1
 
 
+def test_large_k_coarse_bins_min_p_ties():
+    """Large k through coarse key bins: top_k = 0 and 2048 < k < V (the k-th composite narrowed inside its bin),
+    top-p on and off, min-p binding and not, penalties; rows with a block of > 2048 tied logits (a bin the LDS
+    gather cannot hold: the exact multi-pass fallback) and with -inf entries."""
+    rng = np.random.default_rng(61)
+    B, V = 12, 20000
+    x = (rng.standard_normal((B, V)) * 1.5).astype(np.float32)
+    x[2, 1000:4500] = np.float32(5.0)                                # 3500 ties above the rest: top-p crosses inside
+    x[5, ::3] = np.float32(-np.inf)
+    x[7, 5000:7600] = np.float32(-0.3)
+    p = W.make_params(B, temperature=0.9, top_k=0, top_p=0.9, repetition_penalty=1.1)
+    p["top_k"][1::3] = 3000
+    p["top_k"][2::6] = 2500
+    p["top_p"][::4] = 1.0
+    p["min_p"][1::4] = 0.05
+    p["min_p"][3::4] = 0.3
+    p["top_k"][2], p["top_p"][2] = 0, 0.5
+    p["frequency_penalty"][::5] = 0.3
+    hists = [rng.integers(0, V, 400) for _ in range(B)]
+    u = rng.random(B)
+    g, o, nb = check(_case(list(x), p, hists, u, "large_k_bins"), kcap=3000)
+    say(f"large_k_bins boundary rows: {nb}")
+    assert nb <= 2
+
+
 def test_verify_large_k():
     rng = np.random.default_rng(8)
     S, M, V = 3, 4, 3000
