@@ -2816,13 +2816,14 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
         if (hipDeviceGetAttribute(&ctx->cus, hipDeviceAttributeMultiprocessorCount, ctx->device) != hipSuccess)
             return FS_E_HIP;
     }
-    // Segments: about two per CU over the whole batch; a segment streams >= 1 full tile of 4096 logits. The
-    // merge kernel handles each row's partial last tile (all of a row shorter than one tile).
+    // Segments: at most two per CU over the whole batch (all resident at once: a second round of a few
+    // workgroups would double the time), at least one per row; a segment streams >= 1 full tile of 4096 logits.
+    // The merge kernel handles each row's partial last tile (all of a row shorter than one tile).
     const int64_t tiles_row = a.V / fs::TILE;
     a.nseg = 0;
     a.seg_tiles = 1;
     if (tiles_row > 0) {
-        int64_t want = (2 * (int64_t)ctx->cus + rows - 1) / rows;
+        int64_t want = (2 * (int64_t)ctx->cus) / rows;
         if (want < 1) want = 1;
         if (want > tiles_row) want = tiles_row;
         if (want > fs::BLOCK - 1) want = fs::BLOCK - 1;   // the merge gives each list (segments + tail) a thread
