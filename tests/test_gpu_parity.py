@@ -344,6 +344,36 @@ def test_large_k_coarse_bins_min_p_ties():
     assert nb <= 2
 
 
+def test_device_logits_handoff_in_place():
+    """The producer side of the boundary (ferro copies the lm_head output to the host first,
+    model_lfm2_lm.cpp:477-480): logits computed on the device by an lm_head matmul land in a padded [B, ld] buffer
+    (ld > V, as a model's aligned output) and are sampled from that buffer in place - no host copy and no repack.
+    The oracle samples the same logits, copied to the host for it alone."""
+    torch.manual_seed(5)
+    B, d, V, ld = 16, 256, 50000, 50048
+    hidden = torch.randn(B, d, device="cuda")
+    w_head = torch.randn(d, V, device="cuda") * 0.08
+    out = torch.zeros(B, ld, device="cuda")
+    out[:, :V] = hidden @ w_head
+    fed, fed_ld, n = F.sampler._check_logits(out, V)
+    assert fed.data_ptr() == out.data_ptr() and fed_ld == ld and n == V     # the model's own buffer, unrepacked
+    rng = np.random.default_rng(17)
+    p = W.make_params(B, temperature=0.7, top_k=64, top_p=0.9, repetition_penalty=1.1)
+    p["top_k"][::4] = 0
+    p["temperature"][3] = 0.0
+    hists = [rng.integers(0, V, 128) for _ in range(B)]
+    hist = np.concatenate(hists).astype(np.int32)
+    hoff = np.concatenate([[0], np.cumsum([len(h) for h in hists])]).astype(np.int64)
+    u = rng.random(B)
+    res = F.sample_batch(out, p, u, hist=hist, hist_off=hoff, V=V, kcap=64)
+    torch.cuda.synchronize()
+    g = {k: v.cpu().numpy() for k, v in res.items() if v is not None and not k.startswith("_")}
+    w = _case(list(out[:, :V].cpu().numpy()), p, hists, u, "handoff")
+    nb = compare(g, run_oracle(w, 64), p, u, 64)
+    assert nb <= 1
+    assert F.device_error() == 0
+
+
 def test_verify_large_k():
     rng = np.random.default_rng(8)
     S, M, V = 3, 4, 3000
