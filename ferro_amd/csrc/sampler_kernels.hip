@@ -90,7 +90,6 @@ struct Args {
     int seg_tiles;                 // tiles per segment
     uint64_t* cand;                // [B*nseg][CAP]
     uint32_t* meta;                // [B*nseg][2]: lower bound of the k-th key, count
-    uint32_t* row_cnt;             // [B] segment completion counters, left at 0
     uint32_t* rhist;               // [B][RBINS] row histograms of the segments' candidates, left at 0
     uint32_t* stream_cnt;          // [n_streams] verify completion counters, left at 0
     int32_t* err;                  // device error bits
@@ -2766,7 +2765,6 @@ struct fs_context {
     uint64_t* cand = nullptr;
     size_t cand_slots = 0;     // chunk slots of CAP entries
     uint32_t* meta = nullptr;
-    uint32_t* row_cnt = nullptr;
     uint32_t* rhist = nullptr;  // [row_cap][RBINS]
     size_t row_cap = 0;
     uint32_t* stream_cnt = nullptr;
@@ -2786,11 +2784,8 @@ int grow(fs_context* c, size_t slots, size_t rows, size_t streams) {
         c->cand_slots = slots;
     }
     if (rows > c->row_cap) {
-        if (c->row_cnt) (void)hipFree(c->row_cnt);
         if (c->rhist) (void)hipFree(c->rhist);
-        c->row_cnt = nullptr; c->rhist = nullptr; c->row_cap = 0;
-        if (hipMalloc(&c->row_cnt, rows * sizeof(uint32_t)) != hipSuccess) return FS_E_NOMEM;
-        if (hipMemset(c->row_cnt, 0, rows * sizeof(uint32_t)) != hipSuccess) return FS_E_HIP;
+        c->rhist = nullptr; c->row_cap = 0;
         if (hipMalloc(&c->rhist, rows * fs::RBINS * sizeof(uint32_t)) != hipSuccess) return FS_E_NOMEM;
         if (hipMemset(c->rhist, 0, rows * fs::RBINS * sizeof(uint32_t)) != hipSuccess) return FS_E_HIP;
         c->row_cap = rows;
@@ -2836,9 +2831,9 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
     // one workgroup per (row, segment), the rows dealt to XCDS slots (segment_kernel)
     const int64_t seg_grid = items > 0 ? (int64_t)fs::XCDS * a.nseg * ((rows + fs::XCDS - 1) / fs::XCDS) : 0;
     if (seg_grid > 0x7fffffff) return FS_E_INVALID;
-    int rc = grow(ctx, (size_t)(items + rows), (size_t)rows, (size_t)(streams > 0 ? streams : 1));
+    int rc = grow(ctx, (size_t)(items > 0 ? items : 1), (size_t)rows, (size_t)(streams > 0 ? streams : 1));
     if (rc != FS_OK) return rc;
-    a.cand = ctx->cand; a.meta = ctx->meta; a.row_cnt = ctx->row_cnt; a.rhist = ctx->rhist;
+    a.cand = ctx->cand; a.meta = ctx->meta; a.rhist = ctx->rhist;
     a.stream_cnt = ctx->stream_cnt; a.err = ctx->err;
     if (seg_grid > 0) {
         hipLaunchKernelGGL(fs::segment_kernel, dim3((unsigned)seg_grid), dim3(fs::BLOCK), 0, st, a.logits, a.ld, a.B, a.V,
@@ -2872,7 +2867,6 @@ int fs_destroy(fs_context* c) {
     if (!c) return FS_E_INVALID;
     (void)hipFree(c->cand);
     (void)hipFree(c->meta);
-    (void)hipFree(c->row_cnt);
     (void)hipFree(c->rhist);
     (void)hipFree(c->stream_cnt);
     (void)hipFree(c->err);
