@@ -2,7 +2,7 @@
 """Benchmark of the gfx950 token sampler on the headline configuration:
 B=64 rows x V=262144 fp32 logits, T 0.8, top-k 64, top-p 0.95, repetition penalty 1.05 over 512-token histories.
 
-A step is one fs_sample_batch call over the whole batch (penalty -> top-k -> softmax/top-p -> draw, one fused
+A step is one fs_sample_batch call over the whole batch (penalty -> top-k -> softmax/top-p -> draw, one
 kernel) with inputs already resident in HBM. The logits rotate over enough copies (> 256 MB MALL) that every step
 streams its rows from HBM. Prints ONE JSON line with rows/s, the kernel's HBM roofline fraction (HIP events on
 the launch stream) and the CPU baseline (ferro's own sampler.cpp compiled by oracle/Makefile when present, else
@@ -185,7 +185,7 @@ def main():
                    "logit_copies_rotated": nrot},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "fs_sample_batch: fs::segment_kernel + fs::merge_kernel", "kernel_ms": kern_ms,
+                     "kernel": "fs_sample_batch: fs::segment_kernel (segments, then a merging workgroup per row)", "kernel_ms": kern_ms,
                      "algorithmic_bytes": alg_bytes},
     }
     if args.copy_calib:

@@ -1,6 +1,6 @@
 // sampler_kernels.hip - gfx950 (CDNA4) kernels of the token sampler and the C ABI of include/ferro_sampler.h.
 //
-// Two kernels per call on the caller's stream.
+// One kernel per call on the caller's stream (two when a row is shorter than one 4096-logit tile).
 //
 // segment_kernel (one 512-thread workgroup per (row, segment) item, two per CU): a row of V fp32 logits is split
 // into nseg segments of seg_tiles tiles (TILE = 4096 logits); the items are dealt to the 8 XCDs so that a row's
@@ -18,7 +18,9 @@
 // buffer is compacted (entries below the bound dropped, else the exact k-th composite kept) when it could
 // overflow. Each segment publishes its candidates at or above its final bound.
 //
-// merge_kernel (one workgroup per row): gathers the segments' lists, L = max of the segments' bounds bounds the
+// The merge (a role of the same grid: one workgroup per row after the segments, on the row's XCD; a separate
+// merge_kernel launch when rows are shorter than one tile): waits for the row's segment count in the L2, gathers
+// the segments' lists, L = max of the segments' bounds bounds the
 // row's k-th key from below, a histogram over [L, max] gives a tight T1, the ~k candidates >= T1 are sorted in
 // LDS (ferro's cand_, sampler.cpp:25-35; rank sort or a counting sort), then the double-precision softmax at
 // temperature, min-p, top-p and the draw r = u * tot (sampler.cpp:37-49), with scans in place of the sequential
@@ -137,6 +139,9 @@ __device__ __forceinline__ int32_t ld_agent(const int32_t* p) {
 }
 // Wait until this wave's vector memory operations (the sc1 stores above) have completed.
 __device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Invalidate the CU's L1 (vector cache): later loads are served by the XCD's L2, which holds what other workgroups
+// of this XCD stored or added (stores write through the L1; atomics execute in the L2).
+__device__ __forceinline__ void l1_invalidate() { asm volatile("buffer_inv sc0" ::: "memory"); }
 
 // ------------------------------------------------------------------------------------------------ wave/block
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
@@ -939,7 +944,7 @@ __device__ __forceinline__ uint64_t compact_exact(int n, int k, Shared& s) {
 //   5. top-p and the draw: the first candidate (candidate order) whose cumulative mass reaches a target, by a
 //      descent over fp64 mass histograms of the keys, then the j-th smallest id among the ties at the final key.
 // Sums run in a different order than ferro's sequential loop (probabilities agree to ~1e-15 relative).
-constexpr int LPF = 4;                    // tiles in flight per large-row pass
+constexpr int LPF = 2;                    // tiles in flight per large-row pass
 constexpr int MB = 256;                   // mass histogram bins
 
 // One pass over the whole row, LPF tiles in flight, penalties applied (the window ids are in s.ids): g(x, lo) per
@@ -1634,11 +1639,11 @@ __device__ __forceinline__ void prefetch_lists(const Args& a, int row, Pre& pre)
     pre.t0m = 0u;
     pre.cnm = 0u;
     if (nseg > 0) {
-        pre.t0m = ld_agent(&a.meta[2 * slot]);
-        pre.cnm = ld_agent(&a.meta[2 * slot + 1]);
+        pre.t0m = a.meta[2 * slot];
+        pre.cnm = a.meta[2 * slot + 1];
     }
 #pragma unroll
-    for (int q = 0; q < SPEC; ++q) pre.v[q] = nseg > 0 ? ld_agent(lst + (pre.act ? pre.r_me + q * pre.tps : 0)) : 0ull;
+    for (int q = 0; q < SPEC; ++q) pre.v[q] = nseg > 0 ? lst[pre.act ? pre.r_me + q * pre.tps : 0] : 0ull;
 }
 
 __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Shared& s, const Pre& pre) {
@@ -1825,7 +1830,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 const int m = (c0 + c1) >> 1;
                 if (s.off[m] <= g) c0 = m; else c1 = m;
             }
-            const uint64_t w = ld_agent(a.cand + ((int64_t)row * nseg + c0) * CAP + (g - s.off[c0]));
+            const uint64_t w = a.cand[((int64_t)row * nseg + c0) * CAP + (g - s.off[c0])];
             return f < total ? w : 0ull;
         };
         // gather the candidates >= L into LDS (counted past CAP), tracking their max key
@@ -1863,7 +1868,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             }
         }
         for (uint32_t i = (uint32_t)(r_me + SPEC * tps); act && i < cnm; i += (uint32_t)tps) {   // long lists
-            const uint64_t w = ld_agent(lst + i);
+            const uint64_t w = lst[i];
             const bool in = w != 0 && comp_key(w) >= L;
             if (in) kmax = comp_key(w) > kmax ? comp_key(w) : kmax;
             wave_append(in, w, s.cand, &s.count, gcap);
@@ -2535,7 +2540,44 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     __syncthreads();                               // LDS is reused by the next item
 }
 
-// Segment kernel: one (row, segment) item per workgroup (rows sampled with k > KMAX are left to the merge kernel).
+// The row's completion counter: the row histogram's last bin, which no ordered key reaches (keys of non-NaN values
+// are at most +inf's, bin 4088). Segments add 1 (an L2 atomic); the merge role polls it.
+__device__ __forceinline__ uint32_t* row_counter(const Args& a, int row) {
+    return a.rhist + (int64_t)row * RBINS + (RBINS - 1);
+}
+static_assert(((0xFF800000u >> RSHIFT) < (uint32_t)(RBINS - 1)), "the counter bin lies above every ordered key");
+constexpr uint32_t MERGE_SPINS = 1u << 20;   // bounded wait of the merge role (far above any segment's time)
+
+// Merge role of the segment grid: one workgroup per row, placed after the segments on the row's XCD (slot x of
+// the last XCDS * ceil(B / XCDS) workgroups merges rows x, x + XCDS, ...). Workgroups are dispatched in index
+// order, so the row's segments are running or done when it starts: it waits for their count (an atomic that
+// is not idempotent, so it executes in the L2 and is never folded into an L1-served load), invalidates its L1
+// and reads the lists from the L2. A wait past MERGE_SPINS flags FS_DEVERR_INTERNAL and gives up.
+__device__ __forceinline__ void merge_role(const Args& a, int mi, Shared& s) {
+    const int row = mi % XCDS + XCDS * (mi / XCDS);
+    if (row >= a.B) return;
+    uint32_t* ctr = row_counter(a, row);
+    if (threadIdx.x == 0) {
+        uint32_t spins = 0u;
+        while ((__hip_atomic_fetch_add(ctr, 0x10000u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & 0xFFFFu) <
+               (uint32_t)a.nseg) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins == MERGE_SPINS) {
+                atomicOr(a.err, FS_DEVERR_INTERNAL);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    l1_invalidate();
+    Pre pre;
+    prefetch_lists(a, row, pre);
+    if (threadIdx.x == 0) *ctr = 0u;                 // the bin is left at 0 with the rest of the row histogram
+    merge_row(a, row_ctx(a, row), s, pre);
+}
+
+// Segment kernel: one (row, segment) item per workgroup (rows sampled with k > KMAX only count themselves done),
+// then the merge role.
 // The fields a workgroup needs first come as separate leading parameters: gfx950 preloads those into SGPRs at
 // wave launch (build flag -amdgpu-kernarg-preload-count), so the first tile loads wait for no argument load.
 __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, int64_t ld, int B, int V, int nseg,
@@ -2548,6 +2590,11 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, 
     // One (row, segment) item per workgroup. Workgroup i runs on XCD i % XCDS (round-robin dispatch): slot
     // x = i % XCDS takes the rows x, x + XCDS, ..., all segments of a row in consecutive rounds, so a row's segments
     // share one XCD and its L2 (the row histogram). Slots past the last row return at once.
+    const unsigned seg_grid = (unsigned)(XCDS * a.nseg * ((a.B + XCDS - 1) / XCDS));
+    if (blockIdx.x >= seg_grid) {
+        merge_role(a, (int)(blockIdx.x - seg_grid), s);
+        return;
+    }
     const int x = (int)(blockIdx.x % (unsigned)XCDS);
     const int j = (int)(blockIdx.x / (unsigned)XCDS);
     const int q = __builtin_amdgcn_readfirstlane(j / a.nseg);    // uniform: lets the compiler use scalar loads
@@ -2557,8 +2604,10 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, 
     float buf[PF][TPT];
     const SegStart g = seg_start(a, row, seg, buf);   // the tiles are on their way before the parameters
     const RowCtx rc = row_ctx(a, row);
-    if (rc.large) return;                            // the merge kernel samples the whole row
-    process_segment(a, rc, seg, s, buf, g);
+    if (!rc.large) process_segment(a, rc, seg, s, buf, g);   // large rows: the merge role samples the whole row
+    vm_drain();                                      // the list and meta stores are in the L2
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(row_counter(a, row), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Merge kernel: one workgroup per row, after the segment kernel. The segment lists are requested first, so their
@@ -2835,10 +2884,12 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
     if (rc != FS_OK) return rc;
     a.cand = ctx->cand; a.meta = ctx->meta; a.rhist = ctx->rhist;
     a.stream_cnt = ctx->stream_cnt; a.err = ctx->err;
-    if (seg_grid > 0) {
-        hipLaunchKernelGGL(fs::segment_kernel, dim3((unsigned)seg_grid), dim3(fs::BLOCK), 0, st, a.logits, a.ld, a.B, a.V,
+    if (seg_grid > 0) {                            // the segments, then one merging workgroup per row (same grid)
+        const int64_t grid = seg_grid + (int64_t)fs::XCDS * ((rows + fs::XCDS - 1) / fs::XCDS);
+        if (grid > 0x7fffffff) return FS_E_INVALID;
+        hipLaunchKernelGGL(fs::segment_kernel, dim3((unsigned)grid), dim3(fs::BLOCK), 0, st, a.logits, a.ld, a.B, a.V,
                            a.nseg, a.seg_tiles, a.params, a.hist_off, a);
-        if (hipGetLastError() != hipSuccess) return FS_E_HIP;
+        return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
     }
     hipLaunchKernelGGL(fs::merge_kernel, dim3((unsigned)rows), dim3(fs::BLOCK), 0, st, a.nseg, a.cand, a.meta, a.rhist,
                        a.params, a);
