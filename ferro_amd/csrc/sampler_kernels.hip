@@ -2094,9 +2094,9 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
 // up, in lane order = descending bins; counts above the window are left out (fewer counts: the bound stays
 // valid).
 // The row histogram lives in the L2 of the XCD that runs the row's segments (the grid places them there): counts
-// are L2 atomics and snapshots are loads that skip the CU's L1 (sc0) and hit that L2. Every access is an increment
-// of zeroed memory or a read, so a read returns at most the row's true counts wherever the segments run - if one
-// ran on another XCD its counts would only be missing - and every bound stays valid.
+// are L2 atomics and snapshots are group-scope loads, served by that L2 or by a line the CU's L1 still holds from
+// an earlier snapshot (older counts). Every access is an increment of zeroed memory or a read, so a read returns
+// at most the row's true counts - stale, or with a segment on another XCD missing - and every bound stays valid.
 struct RowSnap {
     uint64_t w[2];
     uint32_t b0;
@@ -2109,7 +2109,7 @@ __device__ u32x4 raw_buffer_load_u32x4(__amdgpu_buffer_rsrc_t rs, int voffset, i
     __asm("llvm.amdgcn.raw.ptr.buffer.load.v4i32");
 __device__ uint32_t raw_buffer_load_u32(__amdgpu_buffer_rsrc_t rs, int voffset, int soffset, int aux)
     __asm("llvm.amdgcn.raw.ptr.buffer.load.i32");
-constexpr int AUX_SC0 = 1;               // cache policy: group scope (miss in the CU's L1, served by the XCD's L2)
+constexpr int AUX_SC0 = 1;               // cache policy sc0: group scope (the CU's L1, else the XCD's L2)
 __device__ __forceinline__ RowSnap row_snap(__amdgpu_buffer_rsrc_t rs, uint32_t tkey) {
     RowSnap r;
     r.b0 = (tkey >> RSHIFT) & ~3u;
