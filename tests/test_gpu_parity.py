@@ -374,6 +374,43 @@ def test_device_logits_handoff_in_place():
     assert F.device_error() == 0
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_randomized_sweep(seed):
+    """Seeded random batches against the oracle: B not a multiple of 8, V from 1 to ~70000 (rows shorter than a
+    tile, exact tiles, ragged tails), k from 1 to V and 0, top-p, min-p, repetition / frequency / presence
+    penalties with windows and scopes, -inf entries, and NaN in greedy rows (ferro's candidate sort is undefined with
+    NaN; its greedy scan is not). (The softcap is left out: the device's tanhf and
+    glibc's may differ by an ulp, which reorders logits one ulp apart; test_softcap_fused_read covers it.)"""
+    rng = np.random.default_rng(1000 + seed)
+    for case in range(4):
+        B = int(rng.integers(1, 40))
+        V = int(rng.choice([1, 3, 100, 4095, 4096, 4097, 12288, 20000, 65536, 70001]))
+        x = (rng.standard_normal((B, V)) * rng.uniform(0.5, 4.0)).astype(np.float32)
+        p = W.make_params(B, temperature=0.8)
+        p["temperature"] = rng.choice([0.0, 0.3, 0.8, 1.5], B)
+        p["top_k"] = rng.choice([0, 1, 5, 40, 64, 300, 2048, 3000, V + 5], B)
+        if V > 10:
+            for b in range(0, B, 5):
+                if p["temperature"][b] <= 0 or p["top_k"][b] == 1:    # NaN: defined for ferro's greedy scan only
+                    x[b, rng.integers(0, V, 3)] = np.float32(np.nan)  # (its candidate sort has no order for it)
+                x[b, rng.integers(0, V, 2)] = np.float32(-np.inf)
+            if B > 2:
+                x[2, : V // 3] = np.float32(1.25)                       # a tied block
+        p["top_p"] = rng.choice([1.0, 0.95, 0.6], B)
+        p["min_p"] = rng.choice([0.0, 0.0, 0.05], B)
+        p["repetition_penalty"] = rng.choice([1.0, 1.1, 1.3], B)
+        p["frequency_penalty"] = rng.choice([0.0, 0.0, 0.4], B)
+        p["presence_penalty"] = rng.choice([0.0, 0.2], B)
+        p["repeat_last_n"] = rng.choice([-1, 0, 16], B)
+        p["penalty_from"] = rng.choice([0, 0, 3], B)
+        hists = [rng.integers(-2, V + 2, int(rng.integers(0, 300))) for _ in range(B)]
+        u = rng.random(B)
+        kk = np.where((p["top_k"] > 0) & (p["top_k"] < V), p["top_k"], V)
+        kcap = int(min(max(int(kk.max()), 1), 2048))
+        g, o, nb = check(_case(list(x), p, hists, u, f"sweep{seed}.{case}"), kcap=kcap)
+        assert nb <= 3
+
+
 def test_verify_large_k():
     rng = np.random.default_rng(8)
     S, M, V = 3, 4, 3000
