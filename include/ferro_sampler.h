@@ -33,10 +33,11 @@ extern "C" {
 
 /* Device-side error bits (fs_device_error). */
 #define FS_DEVERR_COUNT_OVERFLOW 1   /* one token occurs > 65535 times in a penalty window */
-#define FS_DEVERR_INTERNAL 2         /* an internal invariant failed (a bug: please report) */
+#define FS_DEVERR_INTERNAL 2         /* an internal invariant failed, or a row's merge gave up waiting for its
+                                        segments (workgroups not dispatched round-robin over the XCDs by index) */
 
-/* Limits. */
-#define FS_MAX_VOCAB (1 << 30)
+/* Limits. A row is read through one buffer resource (32-bit byte range): V * 4 < 2^31. */
+#define FS_MAX_VOCAB (1 << 28)
 
 /* Per-row sampling parameters. Fields 1-5 and 8-9 are ferro's SamplerParams (src/sampler.h:12-21) with the
  * same meaning and defaults; the seed is replaced by the per-row draw u. frequency_penalty / presence_penalty
