@@ -1347,8 +1347,10 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
     const int row = rc.row;
     const fs_row_params& p = rc.p;
     if (rc.pen) gather_window(a, rc, 0, a.V, s);
-    // 1. extremes, count of the ordered elements, their coarse-bin counts
+    // 1. extremes, count of the ordered elements, their coarse-bin counts (only needed to find the k-th when k < V:
+    //    k >= V takes every ordered logit)
     uint32_t* hc = reinterpret_cast<uint32_t*>(s.cand);
+    const bool need_kth = rc.k < a.V;
     for (int i = tid; i < LB; i += BLOCK) hc[i] = 0u;
     __syncthreads();
     uint64_t cmax = 0ull, cmin = ~0ull;
@@ -1357,7 +1359,7 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
         cmax = c > cmax ? c : cmax;
         cmin = c < cmin ? c : cmin;
         ++nv;
-        atomicAdd(&hc[kq >> LB_SHIFT], 1u);
+        if (need_kth) atomicAdd(&hc[kq >> LB_SHIFT], 1u);
     });
     cmax = block_max_u64(cmax, s.red);
     cmin = block_min_u64(cmin, s.red);
