@@ -1355,12 +1355,48 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
     __syncthreads();
     uint64_t cmax = 0ull, cmin = ~0ull;
     uint32_t nv = 0u;
-    row_elems(a, rc, s, [&](float, uint32_t kq, uint64_t c) {
-        cmax = c > cmax ? c : cmax;
-        cmin = c < cmin ? c : cmin;
-        ++nv;
-        if (need_kth) atomicAdd(&hc[kq >> LB_SHIFT], 1u);
-    });
+    if (a.nseg > 0 && !need_kth) {
+        // the segments published the extremes and counts of their full tiles; the partial last tile is read here
+        for (int c = tid; c < a.nseg; c += BLOCK) {
+            const int64_t slot = (int64_t)row * a.nseg + c;
+            const uint64_t hi = a.cand[slot * CAP], lo = a.cand[slot * CAP + 1];
+            cmax = hi > cmax ? hi : cmax;
+            cmin = lo < cmin ? lo : cmin;
+            nv += a.meta[2 * slot + 1];
+        }
+        const int V = a.V;
+        const int tail_lo = (V / TILE) * TILE;
+        if (tail_lo < V) {
+            const float* rowp = a.logits + (int64_t)row * a.ld;
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(rowp), (short)0,
+                                                                                ((V + 3) & ~3) * 4, 0x00020000);
+            float x[TPT];
+            load_seg_tile(x, rs, tail_lo / TILE);
+            if (rc.capped) softcap_vals(x, rc.p.softcap);
+            if (rc.pen) {
+                __syncthreads();
+                apply_penalties(x, a, rc, tail_lo, s);
+            }
+#pragma unroll
+            for (int i = 0; i < TPT; ++i) {
+                const int e = elem_id(tail_lo, i);
+                if (e < V && x[i] == x[i]) {
+                    const uint64_t c = comp_of(key_of(x[i]), (uint32_t)e);
+                    cmax = c > cmax ? c : cmax;
+                    cmin = c < cmin ? c : cmin;
+                    ++nv;
+                }
+            }
+            __syncthreads();                              // the tail's table reads are done
+        }
+    } else {
+        row_elems(a, rc, s, [&](float, uint32_t kq, uint64_t c) {
+            cmax = c > cmax ? c : cmax;
+            cmin = c < cmin ? c : cmin;
+            ++nv;
+            if (need_kth) atomicAdd(&hc[kq >> LB_SHIFT], 1u);
+        });
+    }
     cmax = block_max_u64(cmax, s.red);
     cmin = block_min_u64(cmin, s.red);
     uint32_t ntot;
@@ -2542,6 +2578,49 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     __syncthreads();                               // LDS is reused by the next item
 }
 
+// Rows sampled with k >= V (top_k = 0 included; ferro's k = n, sampler.cpp:26): each segment streams its tiles once
+// for the row's extremes and ordered (non-NaN) count, penalties applied, and publishes them in its list slot
+// (entry 0: the largest composite, entry 1: the smallest; meta: 0, the count), so the merge's whole-row selection
+// starts at its mass pass.
+__device__ __forceinline__ void large_segment_extremes(const Args& a, const RowCtx& rc, int seg, Shared& s,
+                                                       const SegStart& g) {
+    const int tid = threadIdx.x;
+    if (rc.pen) gather_window(a, rc, g.seg_lo, g.seg_lo + g.ntiles * TILE, s);
+    uint64_t cmax = 0ull, cmin = ~0ull;
+    uint32_t nv = 0u;
+    for (int t = 0; t < g.ntiles; ++t) {                 // large rows only: one tile in flight is enough here
+        float x[TPT];
+        load_seg_tile(x, g.rs, t);
+        const int lo = g.seg_lo + t * TILE;
+        if (rc.capped) softcap_vals(x, rc.p.softcap);
+        if (rc.pen) {
+            __syncthreads();                             // the previous tile's table reads are done
+            apply_penalties(x, a, rc, lo, s);
+        }
+#pragma unroll
+        for (int i = 0; i < TPT; ++i) {
+            if (x[i] == x[i]) {
+                const uint64_t c = comp_of(key_of(x[i]), (uint32_t)elem_id(lo, i));
+                cmax = c > cmax ? c : cmax;
+                cmin = c < cmin ? c : cmin;
+                ++nv;
+            }
+        }
+    }
+    cmax = block_max_u64(cmax, s.red);
+    cmin = block_min_u64(cmin, s.red);
+    uint32_t tot;
+    (void)block_excl_scan<uint32_t>(nv, s.wsum, &tot);
+    if (tid == 0) {
+        const int64_t slot = (int64_t)rc.row * a.nseg + seg;
+        a.cand[slot * CAP] = cmax;
+        a.cand[slot * CAP + 1] = cmin;
+        a.meta[2 * slot] = 0u;
+        a.meta[2 * slot + 1] = tot;
+    }
+    __syncthreads();                                     // LDS is reused by the caller
+}
+
 // The row's completion counter: the row histogram's last bin, which no ordered key reaches (keys of non-NaN values
 // are at most +inf's, bin 4088). Segments add 1 (an L2 atomic); the merge role polls it.
 __device__ __forceinline__ uint32_t* row_counter(const Args& a, int row) {
@@ -2606,7 +2685,8 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, 
     float buf[PF][TPT];
     const SegStart g = seg_start(a, row, seg, buf);   // the tiles are on their way before the parameters
     const RowCtx rc = row_ctx(a, row);
-    if (!rc.large) process_segment(a, rc, seg, s, buf, g);   // large rows: the merge role samples the whole row
+    if (!rc.large) process_segment(a, rc, seg, s, buf, g);
+    else if (rc.k >= a.V) large_segment_extremes(a, rc, seg, s, g);   // the merge role samples the row
     vm_drain();                                      // the list and meta stores are in the L2
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_fetch_add(row_counter(a, row), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);

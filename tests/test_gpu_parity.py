@@ -344,6 +344,36 @@ def test_large_k_coarse_bins_min_p_ties():
     assert nb <= 2
 
 
+def test_large_k_extremes_from_segments_and_tail():
+    """top_k = 0 rows take their extremes and ordered count from the segments' published summaries plus the row's
+    partial last tile: the maximum or the minimum in that tail (penalised), a segment holding only -inf, a segment
+    of one repeated value, and a row shorter than one tile (no segments). Every candidate's order is compared, so
+    the softcap stays out (the device's tanhf and glibc's may differ by an ulp, reordering near-ties);
+    test_softcap_fused_read samples a top_k = 0 row with a tail through the softcap."""
+    rng = np.random.default_rng(71)
+    for V in (3 * 4096 + 37, 1000):
+        B = 6
+        x = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+        x[0, V - 3] = np.float32(14.0)                               # the maximum in the tail, penalised below
+        x[1, V - 1] = np.float32(-40.0)                              # the minimum in the tail
+        x[2, 4096:8192 if V > 8192 else V // 2] = np.float32(-np.inf)
+        x[2, V - 20] = np.float32(9.0)
+        x[3, : min(4096, V // 2)] = np.float32(1.25)
+        x[5, V - 2] = np.float32(12.0)
+        p = W.make_params(B, temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.3)
+        p["top_p"][1] = 0.9
+        p["min_p"][2] = 0.02
+        p["temperature"][3], p["top_p"][3] = 0.7, 0.95
+        p["frequency_penalty"][4], p["presence_penalty"][4] = 0.5, 0.25
+        p["frequency_penalty"][5], p["presence_penalty"][5] = 2.0, 1.0
+        hists = [rng.integers(0, V, 150) for _ in range(B)]
+        hists[0] = np.concatenate([hists[0], [V - 3] * 3])
+        hists[5] = np.concatenate([hists[5], [V - 2] * 4, [V - 1]])
+        g, o, nb = check(_case(list(x), p, hists, rng.random(B), f"large_k_tail{V}"), kcap=V)
+        say(f"large_k_tail{V} boundary rows: {nb}")
+        assert nb <= 1
+
+
 def test_device_logits_handoff_in_place():
     """The producer side of the boundary (ferro copies the lm_head output to the host first,
     model_lfm2_lm.cpp:477-480): logits computed on the device by an lm_head matmul land in a padded [B, ld] buffer
