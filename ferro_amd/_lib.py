@@ -45,6 +45,7 @@ SIGNATURES = {
     "fs_rng_next_u": (ctypes.c_int, [_P, _P, _I32]),
     "fs_rng_copy": (ctypes.c_int, [_P, _P]),
     "fs_lookup_draft": (ctypes.c_int, [_P, _I32, _P, _P, _P, _P, _I32, _P, _I32, _P, _P]),
+    "fs_hist_append": (ctypes.c_int, [_P, _I32, _P, _P, _P, _P, _P, _P, ctypes.c_int64, _P, _P]),
     "fs_drng_create": (ctypes.c_int, [_I32, _P, _P, _P]),
     "fs_drng_destroy": (ctypes.c_int, [_P]),
     "fs_drng_draw": (ctypes.c_int, [_P, _P, _P, _P, _I32, _P]),

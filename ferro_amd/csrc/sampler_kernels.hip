@@ -2765,6 +2765,64 @@ __global__ __launch_bounds__(PEN_BLOCK) void penalize_kernel(float* logits, int6
 // and the tokens after it, up to kmax and stopping before eos, are the draft.
 constexpr int LD_BLOCK = 256;
 
+// History append (the per-stream hist.push_back of each consumed token, server.cpp:342, as the decode loop at
+// server.cpp:603-606 and the verify window at server.cpp:627-637 feed them), on CSR histories and out of place: stream
+// s keeps its old ids and gains tok[row_off[s] + i], i < n_s, where n_s is count[s] (NULL: 1) clamped to its rows
+// [0, row_off[s+1] - row_off[s]]. The new offsets are old (rebased to 0) + the exclusive prefix of the n_s.
+__device__ __forceinline__ int64_t app_n(const int64_t* row_off, const int32_t* count, int s, bool* bad) {
+    const int64_t r0 = row_off ? row_off[s] : (int64_t)s;
+    const int64_t nr = row_off ? row_off[s + 1] - r0 : 1;
+    int64_t n = count ? (int64_t)count[s] : 1;
+    if (n < 0 || n > nr) {
+        *bad = true;
+        n = n < 0 ? 0 : nr;
+    }
+    return n;
+}
+
+// One workgroup: the new offsets, streams in chunks of BLOCK (carry in int64).
+__global__ __launch_bounds__(BLOCK) void hist_offsets_kernel(int S, const int64_t* hist_off, const int64_t* row_off,
+                                                             const int32_t* count, int64_t* out_off, int64_t out_cap,
+                                                             int32_t* err) {
+    __shared__ uint32_t wsum[NWAVES];
+    const int tid = threadIdx.x;
+    const int64_t h0 = hist_off[0];
+    int64_t carry = 0;
+    bool bad = false;
+    for (int c0 = 0; c0 < S; c0 += BLOCK) {
+        const int s = c0 + tid;
+        const uint32_t n = s < S ? (uint32_t)app_n(row_off, count, s, &bad) : 0u;
+        uint32_t tot;
+        const uint32_t ex = block_excl_scan<uint32_t>(n, wsum, &tot);
+        if (s < S) out_off[s] = hist_off[s] - h0 + carry + ex;
+        carry += tot;
+        __syncthreads();                                 // wsum is reused by the next chunk
+    }
+    if (tid == 0) {
+        const int64_t end = hist_off[S] - h0 + carry;
+        out_off[S] = end;
+        if (end > out_cap) atomicOr(err, FS_DEVERR_HIST_APPEND);
+    }
+    if (bad) atomicOr(err, FS_DEVERR_HIST_APPEND);
+}
+
+// One workgroup per stream: its old ids, then its appended tokens (positions >= out_cap are not written).
+__global__ __launch_bounds__(LD_BLOCK) void hist_append_kernel(const int32_t* hist, const int64_t* hist_off,
+                                                               const int32_t* tok, const int64_t* row_off,
+                                                               const int32_t* count, const int64_t* out_off,
+                                                               int32_t* out, int64_t out_cap) {
+    const int s = (int)blockIdx.x;
+    bool bad = false;
+    const int64_t n = app_n(row_off, count, s, &bad);
+    const int64_t a = hist_off[s], L = hist_off[s + 1] - a;
+    const int64_t o = out_off[s];
+    const int64_t r0 = row_off ? row_off[s] : (int64_t)s;
+    for (int64_t i = threadIdx.x; i < L + n; i += LD_BLOCK) {
+        const int64_t d = o + i;
+        if (d < out_cap) out[d] = i < L ? hist[a + i] : tok[r0 + (i - L)];
+    }
+}
+
 __global__ __launch_bounds__(LD_BLOCK) void lookup_draft_kernel(const int32_t* hist, const int64_t* hist_off,
                                                                 const int32_t* kmax_arr, const int32_t* min_n_arr,
                                                                 int eos, int32_t* draft, int draft_ld,
@@ -3074,6 +3132,27 @@ int fs_lookup_draft(fs_context* ctx, int32_t n_streams, const int32_t* d_hist, c
     if (n_streams == 0) return FS_OK;
     hipLaunchKernelGGL(fs::lookup_draft_kernel, dim3((unsigned)n_streams), dim3(fs::LD_BLOCK), 0, (hipStream_t)stream,
                        d_hist, d_hist_off, d_kmax, d_min_n, eos_id, d_draft, draft_ld, d_ndraft);
+    return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
+}
+
+int fs_hist_append(fs_context* ctx, int32_t n_streams, const int32_t* d_hist, const int64_t* d_hist_off,
+                   const int32_t* d_tok, const int64_t* d_row_off, const int32_t* d_count, int32_t* d_out_hist,
+                   int64_t out_cap, int64_t* d_out_hist_off, void* stream) {
+    if (!ctx || n_streams < 0 || !d_hist_off || !d_tok || !d_out_hist_off || out_cap < 0) return FS_E_INVALID;
+    if (out_cap > 0 && !d_out_hist) return FS_E_INVALID;
+    if (d_out_hist_off == d_hist_off || (d_out_hist && d_out_hist == d_hist)) return FS_E_INVALID;   // out of place
+    {
+        std::lock_guard<std::mutex> g(ctx->mu);
+        const int rc = grow(ctx, 1, 1, 1);               // the device error word
+        if (rc != FS_OK) return rc;
+    }
+    const hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(fs::hist_offsets_kernel, dim3(1), dim3(fs::BLOCK), 0, st, (int)n_streams, d_hist_off,
+                       d_row_off, d_count, d_out_hist_off, out_cap, ctx->err);
+    if (hipGetLastError() != hipSuccess) return FS_E_HIP;
+    if (n_streams == 0) return FS_OK;
+    hipLaunchKernelGGL(fs::hist_append_kernel, dim3((unsigned)n_streams), dim3(fs::LD_BLOCK), 0, st, d_hist,
+                       d_hist_off, d_tok, d_row_off, d_count, d_out_hist_off, d_out_hist, out_cap);
     return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
 }
 

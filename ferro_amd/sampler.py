@@ -320,6 +320,34 @@ def lookup_draft(hist, hist_off, kmax, min_n=None, eos_id=-1, draft_ld=None, ctx
     return draft, nd
 
 
+def hist_append(hist, hist_off, tok, row_off=None, count=None, out_cap=None, ctx=None, stream=None):
+    """fs_hist_append: each stream's consumed tokens pushed onto its history (server.cpp:342), on device CSR
+    histories, out of place. Stream s gains tok[row_off[s] : row_off[s] + count[s]] (row_off None: row s; count
+    None: 1 per stream; fs_verify's tok / row_off / accepted fit as they are). Returns (out_hist, out_off): out_off
+    [S+1] int64 rebased to 0; out_hist holds out_cap ids (default: room for every row of tok), of which
+    out_off[-1] are used. Stays on the device: nothing here waits for the GPU."""
+    hist_off = torch.as_tensor(hist_off, dtype=torch.int64, device="cuda")
+    dev = hist_off.device
+    S = hist_off.numel() - 1
+    hist = torch.as_tensor(hist, dtype=torch.int32, device=dev)
+    tok = torch.as_tensor(tok, dtype=torch.int32, device=dev)
+    ro = None if row_off is None else torch.as_tensor(row_off, dtype=torch.int64, device=dev)
+    cnt = None if count is None else torch.as_tensor(count, dtype=torch.int32, device=dev)
+    if ro is not None and ro.numel() != S + 1:
+        raise SamplerError(f"row_off has {ro.numel()} entries for {S} streams")
+    if cnt is not None and cnt.numel() != S:
+        raise SamplerError(f"count has {cnt.numel()} entries for {S} streams")
+    if out_cap is None:
+        out_cap = hist.numel() + tok.numel()
+    out = torch.empty(max(int(out_cap), 1), dtype=torch.int32, device=dev)
+    out_off = torch.empty(S + 1, dtype=torch.int64, device=dev)
+    ctx = ctx or Context.default(dev)
+    with ctx.lock:
+        check(lib().fs_hist_append(ctx.h, S, _ptr(hist), _ptr(hist_off), _ptr(tok), _ptr(ro), _ptr(cnt), _ptr(out),
+                                   int(out_cap), _ptr(out_off), _stream(stream)), "fs_hist_append")
+    return out, out_off
+
+
 def device_error(ctx=None, stream=None) -> int:
     ctx = ctx or Context.default()
     bits = ctypes.c_int32(0)

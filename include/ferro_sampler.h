@@ -35,6 +35,8 @@ extern "C" {
 #define FS_DEVERR_COUNT_OVERFLOW 1   /* one token occurs > 65535 times in a penalty window */
 #define FS_DEVERR_INTERNAL 2         /* an internal invariant failed, or a row's merge gave up waiting for its
                                         segments (workgroups not dispatched round-robin over the XCDs by index) */
+#define FS_DEVERR_HIST_APPEND 4      /* fs_hist_append: the new histories exceed out_cap (ids past it are not
+                                        written), or a count lies outside [0, its stream's rows] (clamped) */
 
 /* Limits. A row is read through one buffer resource (32-bit byte range): V * 4 < 2^31. */
 #define FS_MAX_VOCAB (1 << 28)
@@ -113,6 +115,18 @@ int fs_rng_copy(const fs_rng* src, fs_rng* dst);
 int fs_lookup_draft(fs_context* ctx, int32_t n_streams, const int32_t* d_hist, const int64_t* d_hist_off,
                     const int32_t* d_kmax, const int32_t* d_min_n, int32_t eos_id, int32_t* d_draft, int32_t draft_ld,
                     int32_t* d_ndraft, void* stream);
+
+/* History append: the per-stream hist.push_back of each consumed token (src/server.cpp:342, in gen_token; fed one
+ * token per stream by the decode loop, server.cpp:603-606, and the accepted prefix by the verify window,
+ * server.cpp:627-637), on device CSR histories, out of place. Stream s keeps d_hist[d_hist_off[s] ..
+ * d_hist_off[s+1]) and gains d_tok[d_row_off[s] + i] for i < d_count[s] (d_row_off NULL: row s; d_count NULL: 1
+ * per stream; fs_verify's d_tok / d_row_off / d_accepted fit as they are). Writes d_out_hist_off[0 .. n_streams]
+ * (rebased to start at 0) and d_out_hist (capacity out_cap ids); an overflow or a count outside [0, the stream's
+ * rows] sets FS_DEVERR_HIST_APPEND. The outputs must not alias the inputs. Token rewrites the host applies after
+ * sampling (gen_token's think-budget close, server.cpp:339) must be applied to d_tok first. */
+int fs_hist_append(fs_context* ctx, int32_t n_streams, const int32_t* d_hist, const int64_t* d_hist_off,
+                   const int32_t* d_tok, const int64_t* d_row_off, const int32_t* d_count, int32_t* d_out_hist,
+                   int64_t out_cap, int64_t* d_out_hist_off, void* stream);
 
 /* Device draw streams: n_streams std::mt19937_64 engines held in device memory (seeds[s] from the host; 0 =
  * random, as ferro), drawing libstdc++ generate_canonical<double,53> values - ferro::Sampler's draw stream

@@ -182,6 +182,31 @@ def lookup_draft(hist, kmax, eos=-1, min_n=2):
     return out[:d].copy()
 
 
+def hist_append(hist, hist_off, tok, row_off=None, count=None):
+    """gen_token's `j.hist.push_back(id)` (server.cpp:342) for each stream's consumed tokens, in row order: the decode
+    loop (server.cpp:603-606) consumes one token per stream, the verify window (server.cpp:627-637) its first
+    count[s] rows. CSR in, CSR out (offsets rebased to 0). Counts outside [0, the stream's rows] are clamped, as the
+    device entry point does (it also flags them)."""
+    hist = np.asarray(hist, np.int32)
+    off = np.asarray(hist_off, np.int64)
+    tok = np.asarray(tok, np.int32)
+    S = off.size - 1
+    ro = np.arange(S + 1, dtype=np.int64) if row_off is None else np.asarray(row_off, np.int64)
+    streams = []
+    for s in range(S):
+        h = list(hist[off[s]:off[s + 1]])
+        rows = int(ro[s + 1] - ro[s])
+        n = 1 if count is None else int(count[s])
+        n = min(max(n, 0), rows)
+        for i in range(n):
+            h.append(int(tok[ro[s] + i]))
+        streams.append(h)
+    out_off = np.zeros(S + 1, np.int64)
+    out_off[1:] = np.cumsum([len(h) for h in streams])
+    out = np.array([t for h in streams for t in h], np.int32)
+    return out, out_off
+
+
 def canonical(x):
     return float(lib().fso_canonical(x))
 

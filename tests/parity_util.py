@@ -6,6 +6,8 @@ sequential sums put u*tot, top_p or the min-p threshold within 1e-6 of a boundar
 """
 import numpy as np
 
+from oracle import oracle as O
+
 PROB_RTOL = 1e-5
 BOUNDARY = 1e-6
 
@@ -48,3 +50,23 @@ def compare(gpu, ora, params, u, kcap):
                             f"{ora['keep'][b]} away from any boundary"
         nb += int(at_edge)
     return nb
+
+
+def oracle_decode_loop(rows_per_step, params, seeds, hist0):
+    """Each step samples every stream's row with the stream's current history (oracle sampler, the stream's own
+    mt19937_64 draws; greedy rows draw nothing, sampler.cpp:19-23), then appends the tokens with O.hist_append."""
+    S = len(seeds)
+    engines = [O.MT64(int(sd)) for sd in seeds]
+    hist = np.concatenate([np.asarray(h, np.int32) for h in hist0]) if S else np.zeros(0, np.int32)
+    off = np.concatenate([[0], np.cumsum([len(h) for h in hist0])]).astype(np.int64)
+    toks = []
+    for x in rows_per_step:
+        t = np.zeros(S, np.int32)
+        for s in range(S):
+            p = params[s]
+            greedy = p["temperature"] <= 0 or p["top_k"] == 1
+            u = 0.0 if greedy else O.canonical(engines[s].next())
+            t[s] = O.sample(x[s], hist[off[s]:off[s + 1]], p, u)[0]
+        hist, off = O.hist_append(hist, off, t)
+        toks.append(t)
+    return np.stack(toks), hist, off

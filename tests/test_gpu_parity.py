@@ -17,7 +17,7 @@ torch = pytest.importorskip("torch")
 from oracle import oracle as O  # noqa: E402
 from ferro_amd import workloads as W  # noqa: E402
 import ferro_amd as F  # noqa: E402
-from parity_util import compare  # noqa: E402
+from parity_util import compare, oracle_decode_loop  # noqa: E402
 
 NT = min(16, os.cpu_count() or 1)
 
@@ -705,3 +705,72 @@ def test_lookup_draft_matches_oracle():
         np.testing.assert_array_equal(draft[s_, :nd[s_]], want)
         hits += len(want) > 0
     assert hits >= 10
+
+
+def test_device_decode_loop_with_history_append():
+    """Decode steps entirely on the device: fs_drng_draw, fs_sample_batch over the device histories, then
+    fs_hist_append (gen_token's push_back, server.cpp:342) feeding the next step. Tokens and the final histories
+    equal the oracle's loop (sample each stream, then append)."""
+    rng = np.random.default_rng(505)
+    S, V, steps = 6, 5000, 10
+    p = W.make_params(S, temperature=0.8, top_k=40, top_p=0.9, repetition_penalty=1.4)
+    p["temperature"][1] = 0.0
+    p["top_k"][2] = 0
+    p["repeat_last_n"][3] = 6
+    p["frequency_penalty"][4], p["presence_penalty"][4] = 0.5, 0.3
+    seeds = [101, 202, 303, 404, 505, 606]
+    hist0 = [list(rng.integers(0, V, int(rng.integers(0, 40)))) for _ in range(S)]
+    hist0[5] = []
+    rows = [(rng.standard_normal((S, V)) * 2.5).astype(np.float32) for _ in range(steps)]
+    want, want_hist, want_off = oracle_decode_loop(rows, p, seeds, hist0)
+    d = F.DeviceRng(np.array(seeds, np.uint64))
+    hist = torch.from_numpy(np.concatenate([np.asarray(h, np.int32) for h in hist0])).cuda()
+    off = torch.from_numpy(np.concatenate([[0], np.cumsum([len(h) for h in hist0])]).astype(np.int64)).cuda()
+    got = []
+    for k in range(steps):
+        say(f"decode step {k}")
+        u = d.draw(p)
+        tok = F.sample_batch(torch.from_numpy(rows[k]).cuda(), p, u, hist=hist, hist_off=off)["tok"]
+        got.append(tok)
+        hist, off = F.hist_append(hist, off, tok)
+    np.testing.assert_array_equal(torch.stack(got).cpu().numpy(), want)
+    o = off.cpu().numpy()
+    np.testing.assert_array_equal(o, want_off)
+    np.testing.assert_array_equal(hist[:o[-1]].cpu().numpy(), want_hist)
+    assert F.device_error() == 0
+
+
+def test_history_append_verify_window_and_limits():
+    """fs_hist_append fed fs_verify's outputs as they are (tok, row_off, accepted): each stream gains its accepted
+    prefix. Counts outside [0, rows] are clamped and flagged; an output past out_cap is not written and flagged."""
+    rng = np.random.default_rng(9)
+    Sn, M, V = 4, 5, 3000
+    x = (rng.standard_normal((Sn * M, V)) * 3).astype(np.float32)
+    rows = rng.integers(0, V, Sn * M).astype(np.int32)
+    row_off = np.arange(0, Sn * M + 1, M, dtype=np.int64)
+    x[np.arange(Sn * M - 1), rows[1:]] += 30.0
+    x[2 * M + 1, rows[2 * M + 2]] -= 60.0                            # stream 2 rejects its second draft
+    p = W.make_params(Sn, temperature=0.0)
+    hists = [rng.integers(0, V, int(n)).astype(np.int32) for n in (0, 7, 30, 3)]
+    h = np.concatenate(hists)
+    ho = np.concatenate([[0], np.cumsum([len(a) for a in hists])]).astype(np.int64)
+    tok, acc = F.verify(torch.from_numpy(x).cuda(), rows, row_off, p, hist=h, hist_off=ho)
+    out, oo = F.hist_append(torch.from_numpy(h).cuda(), torch.from_numpy(ho).cuda(), tok, row_off=row_off, count=acc)
+    wh, wo = O.hist_append(h, ho, tok.cpu().numpy(), row_off=row_off, count=acc.cpu().numpy())
+    np.testing.assert_array_equal(oo.cpu().numpy(), wo)
+    np.testing.assert_array_equal(out[:wo[-1]].cpu().numpy(), wh)
+    assert acc.cpu().numpy()[2] == 2 and F.device_error() == 0
+    # counts out of range: clamped, flagged
+    bad = np.array([-1, 9, 2, 5], np.int32)
+    out, oo = F.hist_append(torch.from_numpy(h).cuda(), torch.from_numpy(ho).cuda(), tok, row_off=row_off, count=bad)
+    wh, wo = O.hist_append(h, ho, tok.cpu().numpy(), row_off=row_off, count=bad)
+    np.testing.assert_array_equal(oo.cpu().numpy(), wo)
+    np.testing.assert_array_equal(out[:wo[-1]].cpu().numpy(), wh)
+    assert F.device_error() == 4
+    # capacity: the first out_cap ids are written, the offsets are complete, the overflow is flagged
+    cap = int(wo[-1]) - 3
+    out, oo = F.hist_append(torch.from_numpy(h).cuda(), torch.from_numpy(ho).cuda(), tok, row_off=row_off, count=bad,
+                            out_cap=cap)
+    np.testing.assert_array_equal(oo.cpu().numpy(), wo)
+    np.testing.assert_array_equal(out[:cap].cpu().numpy(), wh[:cap])
+    assert F.device_error() == 4

@@ -16,6 +16,7 @@ import pytest
 
 from oracle import oracle as O
 from ferro_amd import workloads as W
+from parity_util import oracle_decode_loop
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "sampler_golden.npz")
 
@@ -238,3 +239,46 @@ def test_lookup_draft_known_answers():
     assert list(O.lookup_draft([5], 4)) == [] and list(O.lookup_draft([], 4)) == []
     assert list(O.lookup_draft([5, 5], 4)) == []      # n = min(4, L-1) = 1 < min_n
     assert list(O.lookup_draft([1, 2, 1, 2], 0)) == []  # kmax = 0: nothing to draft
+
+
+def test_hist_append_known_answers():
+    """gen_token's push_back (server.cpp:342) on CSR histories: one token per stream (the decode loop), the accepted
+    prefix of a verify window (server.cpp:627-637), empty histories, counts clamped to the stream's rows."""
+    out, off = O.hist_append([1, 2, 3, 9], [0, 3, 3, 4], [7, 8, 6])
+    assert list(off) == [0, 4, 5, 7] and list(out) == [1, 2, 3, 7, 8, 9, 6]
+    # verify window: stream rows [0, 3) and [3, 5), accepted 2 and 1 -> tokens 10, 11 and 13
+    out, off = O.hist_append([5, 6], [0, 1, 2], [10, 11, 12, 13, 14], row_off=[0, 3, 5], count=[2, 1])
+    assert list(off) == [0, 3, 5] and list(out) == [5, 10, 11, 6, 13]
+    # rebased input offsets, count 0, a count past the stream's rows (clamped)
+    out, off = O.hist_append([0, 0, 4, 4], [2, 3, 4], [1, 2, 3], row_off=[0, 1, 3], count=[0, 9])
+    assert list(off) == [0, 1, 4] and list(out) == [4, 4, 2, 3]
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built (needs /root/reference)")
+def test_decode_loop_with_append_matches_reference():
+    """The oracle's decode loop (sample, then append) against ferro's own Sampler objects, one per stream, each fed
+    its growing history the way gen_token keeps it (hist.push_back, server.cpp:342)."""
+    rng = np.random.default_rng(404)
+    S, V, steps = 5, 700, 12
+    params = W.make_params(S, temperature=0.9, top_k=40, top_p=0.9, repetition_penalty=1.3)
+    params["temperature"][1] = 0.0
+    params["top_k"][3] = 0
+    params["repeat_last_n"][4] = 8
+    seeds = [11, 22, 33, 44, 55]
+    hist0 = [list(rng.integers(0, V, int(rng.integers(0, 30)))) for _ in range(S)]
+    rows = [(rng.standard_normal((S, V)) * 2).astype(np.float32) for _ in range(steps)]
+    toks, _, _ = oracle_decode_loop(rows, params, seeds, hist0)
+    R = O.ref()
+    for s in range(S):
+        p = np.ascontiguousarray(params[s:s + 1], O.PARAMS_DTYPE)
+        h = [int(t) for t in hist0[s]]
+        obj = R.ref_sampler_new(O._ptr(p), seeds[s])
+        try:
+            for k in range(steps):
+                x = rows[k][s].copy()
+                hh = np.asarray(h, np.int32)
+                t = R.ref_sampler_sample(obj, O._ptr(x), V, O._ptr(hh), hh.size)
+                assert t == toks[k, s], (s, k)
+                h.append(t)
+        finally:
+            R.ref_sampler_free(obj)
