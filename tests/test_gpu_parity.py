@@ -774,3 +774,33 @@ def test_history_append_verify_window_and_limits():
     np.testing.assert_array_equal(oo.cpu().numpy(), wo)
     np.testing.assert_array_equal(out[:cap].cpu().numpy(), wh[:cap])
     assert F.device_error() == 4
+
+
+def test_history_append_many_streams():
+    """fs_hist_append over 1500 streams (the offset scan runs in chunks of 512 with a carry): ragged histories,
+    empty ones, rows of 0-6 per stream and random accepted counts, against the oracle; and no streams at all."""
+    rng = np.random.default_rng(77)
+    S = 1500
+    lens = rng.integers(0, 40, S)
+    lens[::7] = 0
+    h = rng.integers(0, 100000, int(lens.sum())).astype(np.int32)
+    ho = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    nrows = rng.integers(0, 7, S)
+    row_off = np.concatenate([[0], np.cumsum(nrows)]).astype(np.int64)
+    tok = rng.integers(0, 100000, int(row_off[-1])).astype(np.int32)
+    cnt = np.array([rng.integers(0, r + 1) for r in nrows], np.int32)
+    out, oo = F.hist_append(torch.from_numpy(h).cuda(), torch.from_numpy(ho).cuda(), torch.from_numpy(tok).cuda(),
+                            row_off=row_off, count=cnt)
+    wh, wo = O.hist_append(h, ho, tok, row_off=row_off, count=cnt)
+    np.testing.assert_array_equal(oo.cpu().numpy(), wo)
+    np.testing.assert_array_equal(out[:wo[-1]].cpu().numpy(), wh)
+    # one token per stream (decode), on a sub-view whose offsets do not start at 0
+    out, oo = F.hist_append(torch.from_numpy(h).cuda(), torch.from_numpy(ho[5:]).cuda(),
+                            torch.from_numpy(tok[:S - 5]).cuda())
+    wh, wo = O.hist_append(h, ho[5:], tok[:S - 5])
+    np.testing.assert_array_equal(oo.cpu().numpy(), wo)
+    np.testing.assert_array_equal(out[:wo[-1]].cpu().numpy(), wh)
+    out, oo = F.hist_append(torch.zeros(0, dtype=torch.int32).cuda(), torch.zeros(1, dtype=torch.int64).cuda(),
+                            torch.zeros(0, dtype=torch.int32).cuda())
+    assert oo.cpu().numpy().tolist() == [0]
+    assert F.device_error() == 0
