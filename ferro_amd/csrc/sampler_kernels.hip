@@ -3139,7 +3139,7 @@ int fs_hist_append(fs_context* ctx, int32_t n_streams, const int32_t* d_hist, co
                    const int32_t* d_tok, const int64_t* d_row_off, const int32_t* d_count, int32_t* d_out_hist,
                    int64_t out_cap, int64_t* d_out_hist_off, void* stream) {
     if (!ctx || n_streams < 0 || !d_hist_off || !d_out_hist_off || out_cap < 0) return FS_E_INVALID;
-    if (n_streams > 0 && !d_tok) return FS_E_INVALID;
+    if (n_streams > 0 && (!d_tok || !d_hist)) return FS_E_INVALID;
     if (out_cap > 0 && !d_out_hist) return FS_E_INVALID;
     if (d_out_hist_off == d_hist_off || (d_out_hist && d_out_hist == d_hist)) return FS_E_INVALID;   // out of place
     {

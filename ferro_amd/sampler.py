@@ -330,6 +330,8 @@ def hist_append(hist, hist_off, tok, row_off=None, count=None, out_cap=None, ctx
     dev = hist_off.device
     S = hist_off.numel() - 1
     hist = torch.as_tensor(hist, dtype=torch.int32, device=dev)
+    if hist.numel() == 0:
+        hist = torch.zeros(1, dtype=torch.int32, device=dev)     # every history empty: a valid pointer, never read
     tok = torch.as_tensor(tok, dtype=torch.int32, device=dev)
     ro = None if row_off is None else torch.as_tensor(row_off, dtype=torch.int64, device=dev)
     cnt = None if count is None else torch.as_tensor(count, dtype=torch.int32, device=dev)

@@ -122,8 +122,8 @@ int fs_lookup_draft(fs_context* ctx, int32_t n_streams, const int32_t* d_hist, c
  * d_hist_off[s+1]) and gains d_tok[d_row_off[s] + i] for i < d_count[s] (d_row_off NULL: row s; d_count NULL: 1
  * per stream; fs_verify's d_tok / d_row_off / d_accepted fit as they are). Writes d_out_hist_off[0 .. n_streams]
  * (rebased to start at 0) and d_out_hist (capacity out_cap ids); an overflow or a count outside [0, the stream's
- * rows] sets FS_DEVERR_HIST_APPEND. The outputs must not alias the inputs; d_tok may be NULL only with no
- * streams. Token rewrites the host applies after sampling (gen_token's think-budget close, server.cpp:339) must be
+ * rows] sets FS_DEVERR_HIST_APPEND. The outputs must not alias the inputs; d_hist and d_tok may be NULL
+ * only with no streams. Token rewrites the host applies after sampling (gen_token's think-budget close, server.cpp:339) must be
  * applied to d_tok first. */
 int fs_hist_append(fs_context* ctx, int32_t n_streams, const int32_t* d_hist, const int64_t* d_hist_off,
                    const int32_t* d_tok, const int64_t* d_row_off, const int32_t* d_count, int32_t* d_out_hist,

@@ -61,6 +61,8 @@ def test_invalid_arguments_rejected_without_device():
     assert L.fs_hist_append(h, 1, fake, fake, fake, None, None, None, 4, P(48), None) == _lib.FS_E_INVALID
     assert L.fs_hist_append(h, 1, fake, P(48), fake, None, None, P(32), 4, P(48), None) == _lib.FS_E_INVALID
     assert L.fs_hist_append(h, 1, fake, fake, fake, None, None, fake, 4, P(48), None) == _lib.FS_E_INVALID
+    assert L.fs_hist_append(h, 1, None, fake, fake, None, None, P(32), 4, P(48), None) == _lib.FS_E_INVALID
+    assert L.fs_hist_append(h, 1, fake, fake, None, None, None, P(32), 4, P(48), None) == _lib.FS_E_INVALID
     # misaligned logits / ld not a multiple of 4 / ld < V / V < 1
     assert L.fs_sample_batch(h, P(4), 8, 1, 8, None, None, fake, None, fake, 0, None, None, None, None) \
         == _lib.FS_E_INVALID

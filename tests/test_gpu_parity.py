@@ -803,4 +803,7 @@ def test_history_append_many_streams():
     out, oo = F.hist_append(torch.zeros(0, dtype=torch.int32).cuda(), torch.zeros(1, dtype=torch.int64).cuda(),
                             torch.zeros(0, dtype=torch.int32).cuda())
     assert oo.cpu().numpy().tolist() == [0]
+    out, oo = F.hist_append(torch.zeros(0, dtype=torch.int32).cuda(), torch.zeros(4, dtype=torch.int64).cuda(),
+                            torch.tensor([5, 6, 7], dtype=torch.int32).cuda())      # streams, all histories empty
+    assert oo.cpu().numpy().tolist() == [0, 1, 2, 3] and out[:3].cpu().numpy().tolist() == [5, 6, 7]
     assert F.device_error() == 0
