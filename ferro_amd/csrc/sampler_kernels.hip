@@ -57,7 +57,7 @@ constexpr int HBITS = 11;
 constexpr int NBINS = 1 << HBITS;         // threshold histograms
 constexpr int SMALL = 512;                // rank-sort capacity of the merge
 constexpr int MAX_SEGS = 1024;            // segments per row
-constexpr int SPEC = 8;                   // merge gather: loads in flight per thread per round
+constexpr int SPEC = 2;                   // merge gather: loads in flight per thread per round
 constexpr int FAST_SEGS = 64;             // merge fast path: a wave reads every list's bound and count
 static_assert(SPEC * BLOCK + SMALL + 2 * WAVE + 4 * 2 * WAVE / 2 <= CAP, "merge fast path: list, ranks and finish buffers fit");
 constexpr int RBITS = 12;                 // row histogram: bins of the top key bits, shared by a row's segments
@@ -1662,6 +1662,7 @@ struct Pre {
     uint32_t t0m, cnm;
     uint64_t v[SPEC];
     double u;                              // the row's draw (requested with the lists)
+    float l0;                              // the row's first logit (a NaN there is ferro's greedy answer)
 };
 
 __device__ __forceinline__ void prefetch_lists(const Args& a, int row, Pre& pre) {
@@ -1674,6 +1675,7 @@ __device__ __forceinline__ void prefetch_lists(const Args& a, int row, Pre& pre)
     const int64_t slot = (int64_t)row * nseg + pre.c_me;
     const uint64_t* lst = a.cand + slot * CAP;
     pre.u = a.u ? ld_const(a.u + row) : 0.0;
+    pre.l0 = ld_const(a.logits + (int64_t)row * a.ld);
     pre.t0m = 0u;
     pre.cnm = 0u;
     if (nseg > 0) {
@@ -1682,6 +1684,139 @@ __device__ __forceinline__ void prefetch_lists(const Args& a, int row, Pre& pre)
     }
 #pragma unroll
     for (int q = 0; q < SPEC; ++q) pre.v[q] = nseg > 0 ? lst[pre.act ? pre.r_me + q * pre.tps : 0] : 0ull;
+}
+
+// Softmax at temperature, min-p, top-p and the draw (sampler.cpp:37-49) over k <= WAVE candidates held by one wave:
+// lane i holds candidate i in ferro's order (0 past k). Sums are DPP wave scans in candidate order. Writes the
+// optional candidate outputs; returns the token and the kept count.
+__device__ __forceinline__ void wave_softmax(const Args& a, const RowCtx& rc, uint64_t v, int k, double u, int& tok_out,
+                                             int& keep_out) {
+    const int lane = lane_id();
+    const int row = rc.row;
+    const fs_row_params& p = rc.p;
+    const float mx = val_of(comp_key(read_lane(v, 0)));
+    const double Td = (double)p.temperature;
+    double e = 0.0;
+    if (lane < k) {
+        const float d = val_of(comp_key(v)) - mx;        // fp32 subtraction, as ferro
+        e = exp((double)d / Td);
+    }
+    const double sum = lane_f64(wave_scan_f64(e), WAVE - 1);   // lanes >= k hold 0
+    const double pr = e / sum;
+    const double cum = wave_scan_f64(pr);                 // ferro's running c (sampler.cpp:44,47)
+    int keep_m = k;
+    if (p.min_p > 0.0f) {                                 // keep = 1 + the last index with pr >= pr[0]*min_p
+        const double thr = lane_f64(pr, 0) * (double)p.min_p;
+        const uint64_t mm = __ballot(lane < k && pr >= thr);
+        keep_m = mm ? 64 - __clzll((long long)mm) : 1;
+    }
+    int keep = keep_m;
+    if (p.top_p < 1.0f) {
+        const uint64_t mm = __ballot(lane < keep_m && cum >= (double)p.top_p);
+        if (mm) {
+            const int first = __ffsll((unsigned long long)mm) - 1;
+            keep = first + 1 < keep_m ? first + 1 : keep_m;
+        }
+    }
+    const double tot = lane_f64(cum, keep - 1);
+    const double rr = u * tot + 0.0;
+    const uint64_t hm = __ballot(lane < keep && rr <= cum);
+    const int at = hm ? __ffsll((unsigned long long)hm) - 1 : keep - 1;
+    tok_out = (int)comp_id(read_lane(v, at));
+    keep_out = keep;
+    if (a.mode != MODE_VERIFY) {
+        const int m = k < a.kcap ? k : a.kcap;
+        if (lane < m) {
+            if (a.cand_ids) a.cand_ids[(int64_t)row * a.kcap + lane] = (int32_t)comp_id(v);
+            if (a.cand_probs) a.cand_probs[(int64_t)row * a.kcap + lane] = pr;
+        }
+    }
+}
+
+// The short merge: rows with no partial tail tile whose segment lists lie inside the prefetched windows.
+//   - greedy rows: the largest of the segments' maxima (wave 0; lanes < nseg hold entry 0 of every list);
+//   - k <= WAVE: the candidates at or above L (the largest of the lists' bounds; at least k of the row's logits reach
+//     every bound) go into LDS (one LDS atomic per wave); when there are at most 2 * BLOCK / 4 of them the block ranks
+//     them (P threads per candidate, each comparing with 1/P of the list), places the first k by rank, and wave 0
+//     finishes the row.
+// Returns false, after a barrier and with nothing written, when the row does not fit (the general merge then runs).
+constexpr int FRANK = BLOCK / 2;          // largest candidate count the short merge ranks
+__device__ __forceinline__ bool merge_fast(const Args& a, const RowCtx& rc, Shared& s, const Pre& pre, int& tok,
+                                           int& keep) {
+    const int tid = threadIdx.x;
+    const int k = rc.k;
+    if (a.nseg > FAST_SEGS) return false;
+    const uint32_t cmax = wave_max(pre.cnm);
+    if (cmax > (uint32_t)(SPEC * pre.tps)) return false;        // uniform: every wave holds every list's meta
+    if (rc.greedy) {
+        if (tid < WAVE) {
+            uint64_t best = (pre.act && pre.r_me == 0) ? pre.v[0] : 0ull;   // each segment's best (entry 0)
+            best = wave_max(best);
+            tok = best != 0ull ? (int)comp_id(best) : 0;      // nothing above -inf / NaN: ferro's scan stays at 0
+            if (pre.l0 != pre.l0) tok = 0;                    // ferro's scan never moves off a NaN at index 0
+            keep = 1;
+            if (tid == 0 && a.mode != MODE_VERIFY) {
+                if (a.cand_ids && a.kcap > 0) a.cand_ids[(int64_t)rc.row * a.kcap] = tok;
+                if (a.cand_probs && a.kcap > 0) a.cand_probs[(int64_t)rc.row * a.kcap] = 1.0;
+            }
+        }
+        return true;
+    }
+    if (k > WAVE) return false;
+    const uint32_t L = wave_max(pre.t0m);
+    // the candidates >= L into LDS: one atomic per wave for all of a thread's entries
+    {
+        uint64_t bal[SPEC];
+        uint32_t tot = 0u;
+#pragma unroll
+        for (int q = 0; q < SPEC; ++q) {
+            const uint64_t w = pre.v[q];
+            const bool in = pre.act && (uint32_t)(pre.r_me + q * pre.tps) < pre.cnm && w != 0ull && comp_key(w) >= L;
+            bal[q] = __ballot(in);
+            tot += (uint32_t)__popcll(bal[q]);
+        }
+        if (tid == 0) s.count = 0u;
+        __syncthreads();
+        if (tot != 0u) {
+            uint32_t base = 0u;
+            if (lane_id() == 0) base = atomicAdd(&s.count, tot);
+            base = (uint32_t)__builtin_amdgcn_readlane((int)base, 0);
+#pragma unroll
+            for (int q = 0; q < SPEC; ++q) {
+                if ((bal[q] >> lane_id()) & 1ull) s.cand[base + mbcnt(bal[q])] = pre.v[q];
+                base += (uint32_t)__popcll(bal[q]);
+            }
+        }
+    }
+    __syncthreads();
+    const int n = (int)s.count;
+    if (n < k || n > FRANK) {                                    // uniform
+        __syncthreads();
+        return false;
+    }
+    // ranks: P threads per candidate (c = tid % per), part q compares candidate c with entries [q*span, (q+1)*span)
+    const int P = n <= BLOCK / 4 ? 4 : 2;
+    const int per = BLOCK / P;
+    const int span = (n + P - 1) / P;
+    const int c = tid % per, q = tid / per;
+    uint32_t* rk = reinterpret_cast<uint32_t*>(s.cand + FRANK);            // [BLOCK]
+    uint64_t* sorted = s.cand + FRANK + BLOCK / 2;                        // [WAVE]
+    if (c < n) {
+        const uint64_t me = s.cand[c];
+        const int j0 = q * span, j1 = j0 + span < n ? j0 + span : n;
+        uint32_t r = 0u;
+        for (int j = j0; j < j1; ++j) r += s.cand[j] > me ? 1u : 0u;
+        rk[q * per + c] = r;
+    }
+    __syncthreads();
+    if (tid < n) {
+        uint32_t r = 0u;
+        for (int qq = 0; qq < P; ++qq) r += rk[qq * per + tid];
+        if (r < (uint32_t)k) sorted[r] = s.cand[tid];
+    }
+    __syncthreads();
+    if (tid < WAVE) wave_softmax(a, rc, tid < k ? sorted[tid] : 0ull, k, pre.u, tok, keep);
+    return true;
 }
 
 __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Shared& s, const Pre& pre) {
@@ -1694,8 +1829,11 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
     int k = rc.k;
     int tok = 0, keep = 1;
 
+    bool fast = false;
     if (rc.large) {
         large_row(a, rc, s, tok, keep);
+    } else if (ntail == 0 && (fast = merge_fast(a, rc, s, pre, tok, keep))) {
+        // the short merge wrote the row's outputs
     } else {
     // ---- the row's tail: loads first, then its penalty pass (the same arithmetic as the segment kernel)
     constexpr int TT = TILE / BLOCK;                  // tail logits per thread: element tail_lo + r*BLOCK + tid
@@ -1766,10 +1904,6 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             const uint32_t L = wave_max(pre.t0m);
             const uint32_t cmax = wave_max(pre.cnm);
             if (cmax <= (uint32_t)(SPEC * pre.tps)) {
-                {                                     // the segments' row histogram is spent: leave it at 0
-                    uint4* rz = reinterpret_cast<uint4*>(a.rhist + (int64_t)row * RBINS);
-                    for (int i = tid; i < RBINS / 4; i += BLOCK) rz[i] = make_uint4(0u, 0u, 0u, 0u);
-                }
                 for (int i = tid; i < NBINS; i += BLOCK) s.bins()[i] = 0u;
                 if (tid == 0) { s.count = 0u; s.nids = 0u; }
                 __syncthreads();
@@ -1910,10 +2044,6 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             const bool in = w != 0 && comp_key(w) >= L;
             if (in) kmax = comp_key(w) > kmax ? comp_key(w) : kmax;
             wave_append(in, w, s.cand, &s.count, gcap);
-        }
-        {                                           // the segments' row histogram is spent: leave it at 0
-            uint4* rz = reinterpret_cast<uint4*>(a.rhist + (int64_t)row * RBINS);
-            for (int i = tid; i < RBINS / 4; i += BLOCK) rz[i] = make_uint4(0u, 0u, 0u, 0u);
         }
         for (int i = tid; i < NBINS; i += BLOCK) s.bins()[i] = 0u;
         uint32_t kmin = L;
@@ -2097,6 +2227,10 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
         }
         }                                             // general path
     }
+    }
+    if (!rc.large && !rc.greedy && nseg > 0) {         // the segments' row histogram is spent: leave it at 0
+        uint4* rz = reinterpret_cast<uint4*>(a.rhist + (int64_t)row * RBINS);
+        for (int i = tid; i < RBINS / 4; i += BLOCK) rz[i] = make_uint4(0u, 0u, 0u, 0u);
     }
     if (a.mode != MODE_VERIFY) {
         if (tid == 0) {
