@@ -1805,7 +1805,12 @@ __device__ __forceinline__ bool merge_fast(const Args& a, const RowCtx& rc, Shar
         const uint64_t me = s.cand[c];
         const int j0 = q * span, j1 = j0 + span < n ? j0 + span : n;
         uint32_t r = 0u;
-        for (int j = j0; j < j1; ++j) r += s.cand[j] > me ? 1u : 0u;
+        int j = j0;
+        for (; j + 4 <= j1; j += 4) {                  // four LDS reads in flight per step
+            const uint64_t e0 = s.cand[j], e1 = s.cand[j + 1], e2 = s.cand[j + 2], e3 = s.cand[j + 3];
+            r += (e0 > me ? 1u : 0u) + (e1 > me ? 1u : 0u) + (e2 > me ? 1u : 0u) + (e3 > me ? 1u : 0u);
+        }
+        for (; j < j1; ++j) r += s.cand[j] > me ? 1u : 0u;
         rk[q * per + c] = r;
     }
     __syncthreads();
@@ -2771,6 +2776,7 @@ constexpr uint32_t MERGE_SPINS = 1u << 20;   // bounded wait of the merge role (
 __device__ __forceinline__ void merge_role(const Args& a, int mi, Shared& s) {
     const int row = mi % XCDS + XCDS * (mi / XCDS);
     if (row >= a.B) return;
+    const RowCtx rc = row_ctx(a, row);               // the row's inputs are read while the segments run
     uint32_t* ctr = row_counter(a, row);
     if (threadIdx.x == 0) {
         uint32_t spins = 0u;
@@ -2788,7 +2794,7 @@ __device__ __forceinline__ void merge_role(const Args& a, int mi, Shared& s) {
     Pre pre;
     prefetch_lists(a, row, pre);
     if (threadIdx.x == 0) *ctr = 0u;                 // the bin is left at 0 with the rest of the row histogram
-    merge_row(a, row_ctx(a, row), s, pre);
+    merge_row(a, rc, s, pre);
 }
 
 // Segment kernel: one (row, segment) item per workgroup (rows sampled with k > KMAX only count themselves done),
