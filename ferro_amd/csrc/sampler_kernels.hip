@@ -445,13 +445,15 @@ __device__ __forceinline__ uint32_t hist_threshold(const uint32_t* bins, uint32_
 
 // Exact k-th largest composite among the candidates a visitor yields (all distinct, 0 = absent; 1 <= k <= count).
 // Radix select from the top byte: 8 passes of a 256-bin LDS histogram. each(f) calls f(c) for every candidate the
-// calling thread holds.
+// calling thread holds. With last_shift = 32 it stops after the key bytes: the result is the k-th largest key (low
+// word 0), which at least k candidates reach.
 template <class Each>
-__device__ __forceinline__ uint64_t radix_kth(Each each, int k, uint32_t* hist256, uint32_t* wsum, Red& r) {
+__device__ __forceinline__ uint64_t radix_kth(Each each, int k, uint32_t* hist256, uint32_t* wsum, Red& r,
+                                              int last_shift = 0) {
     uint64_t prefix = 0, mask = 0;
     int kk = k;
     const int tid = threadIdx.x;
-    for (int shift = 56; shift >= 0; shift -= 8) {
+    for (int shift = 56; shift >= last_shift; shift -= 8) {
         if (tid < 256) hist256[tid] = 0;
         __syncthreads();
         each([&](uint64_t c) {
@@ -2526,8 +2528,20 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 counted = m;
             }
             if (m < 0 || short_room(n)) {
-                raise_key(comp_key(compact_exact(n, k, s)));
-                n = k;
+                // the entries at or above the k-th largest key (a radix select over the key bytes: 4 passes of an
+                // 8-bit LDS histogram); if ties at that key leave too little room, exactly the k largest composites
+                int nn = n;
+                auto each = [&](auto&& f) { for (int i = tid; i < nn; i += BLOCK) f(s.cand[i]); };
+                uint64_t X = radix_kth(each, k, s.bins(), s.wsum, s.red, 32);
+                const int m2 = keep_from(nn, X, s);
+                if (m2 >= 0) nn = m2;
+                if (m2 < 0 || short_room(nn)) {
+                    X = radix_kth(each, k, s.bins(), s.wsum, s.red);
+                    (void)keep_from(nn, X, s);   // exactly k (composites are distinct)
+                    nn = k;
+                }
+                raise_key(comp_key(X));
+                n = nn;
                 counted = n;               // the survivors are left uncounted (fewer counts: bounds stay valid)
             }
         }
@@ -2538,12 +2552,31 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     RowSnap snap1;                     // the row histogram after tile 0 (segments of >= 3 tiles)
     for (int pass = 0; pass < 2; ++pass) {
         const bool safe = pass == 1;
+        // k <= 64: tile 0's candidates are appended at tile 1, after the first row bound (its penalised logits wait in
+        // the candidate buffer's tail; each thread reads back its own). Rows with the per-tile count table, and rows
+        // with larger k (whose tile-0 bound lets through half a tile or more), append at once.
+        const bool defer0 = topk && !safe && ntiles >= 2 && !slowpen && k <= WAVE;
         bool overflow = false;
         int R = 1;
-        // ---- tile 0 (peeled: the initial threshold is computed here)
+        // ---- tile 0 (peeled: the initial threshold is computed here). Its logits are staged in the candidate
+        // buffer's tail (tile 0's own appends, at most one tile, stay below it) so that tile PF is requested as soon
+        // as tile 0 arrives: the tile's bound computation (two barriers) and appends then run with PF tiles in flight.
         {
-            float (&x)[TPT] = buf[0];
+            float x[TPT];
             const int lo = seg_lo;
+            {
+                float4* st = reinterpret_cast<float4*>(s.cand + (CAP - TILE / 2));
+                static_assert(TILE + TILE / 2 <= CAP, "tile 0's appends stay below its stage");
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+                    st[j * BLOCK + tid] = make_float4(buf[0][4 * j], buf[0][4 * j + 1], buf[0][4 * j + 2], buf[0][4 * j + 3]);
+                load_seg_tile(buf[0], g.rs, PF);
+#pragma unroll
+                for (int j = 0; j < NV; ++j) {
+                    const float4 v = st[j * BLOCK + tid];
+                    x[4 * j] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
+                }
+            }
             if (rc.capped) softcap_vals(x, rc.p.softcap);
             if (slowpen) apply_penalties(x, a, rc, lo, s);
             if (fastpen) bitmap_pen(x, lo);
@@ -2558,10 +2591,17 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     // counts: every bound read from them stays valid).
                     uint32_t kq[TPT];
                     uint32_t m1 = 0u;
+                    if (k > WAVE) {
 #pragma unroll
-                    for (int i = 0; i < TPT; ++i) {
-                        kq[i] = key_of(x[i]);
-                        m1 = kq[i] > m1 ? kq[i] : m1;
+                        for (int i = 0; i < TPT; ++i) {
+                            kq[i] = key_of(x[i]);
+                            m1 = kq[i] > m1 ? kq[i] : m1;
+                        }
+                    } else {                             // the lane's largest logit (fmaxf passes over NaN)
+                        float fm = x[0];
+#pragma unroll
+                        for (int i = 1; i < TPT; ++i) fm = fmaxf(fm, x[i]);
+                        m1 = key_of(fm);
                     }
                     const uint32_t wm = wave_max(m1);
                     if (lane_id() == 0) atomicMax(&s.tmax, wm);
@@ -2588,9 +2628,15 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                         if (c != 0u) __hip_atomic_fetch_add(rh + rc0 + tid, c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                     }
                 }
-                topk_append(x, lo);
+                if (defer0) {                            // the penalised tile waits in its stage for tile 1
+                    float4* st = reinterpret_cast<float4*>(s.cand + (CAP - TILE / 2));
+#pragma unroll
+                    for (int j = 0; j < NV; ++j)
+                        st[j * BLOCK + tid] = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
+                } else {
+                    topk_append(x, lo);
+                }
             }
-            load_seg_tile(x, g.rs, PF);
             if (topk) {
                 lastn = 0;
                 const int n = check(1, safe);
@@ -2637,8 +2683,21 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     if (p == 0 && take1) raise_key(row_bound(snap1, k));
                     if (p == 0 && dpend) raise_key(row_bound(snapd, k));
                     if (p == 1 && snap) raise_key(row_bound(snap2, k));
-                    if (rc.greedy) greedy_update(x, tt);
-                    else topk_append(x, lo);
+                    if (rc.greedy) {
+                        greedy_update(x, tt);
+                    } else {
+                        if (p == 0 && defer0 && t0 == 1) {
+                            float x0[TPT];
+                            const float4* st = reinterpret_cast<const float4*>(s.cand + (CAP - TILE / 2));
+#pragma unroll
+                            for (int j = 0; j < NV; ++j) {
+                                const float4 v = st[j * BLOCK + tid];
+                                x0[4 * j] = v.x; x0[4 * j + 1] = v.y; x0[4 * j + 2] = v.z; x0[4 * j + 3] = v.w;
+                            }
+                            topk_append(x0, seg_lo);
+                        }
+                        topk_append(x, lo);
+                    }
                 }
                 // past the end: zeros, no memory access. The first tile of an iteration requests its successor
                 // after the check and the row snapshot: the snapshot is then taken at the next tile with that
