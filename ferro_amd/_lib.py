@@ -19,6 +19,7 @@ FS_E_HIP = -2
 FS_E_NOMEM = -3
 FS_E_DEVICE = -4
 FS_DEVERR_COUNT_OVERFLOW = 1
+FS_DEVERR_INTERNAL = 2
 
 # fs_row_params (include/ferro_sampler.h); field order follows ferro's SamplerParams (src/sampler.h:12-21).
 PARAMS_DTYPE = np.dtype([
@@ -40,6 +41,7 @@ SIGNATURES = {
     "fs_verify": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P]),
     "fs_penalize_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P]),
     "fs_device_error": (ctypes.c_int, [_P, _P, _P]),
+    "fs_set_wait_limit": (ctypes.c_int, [_P, ctypes.c_uint32]),
     "fs_rng_create": (ctypes.c_int, [ctypes.c_uint64, _P]),
     "fs_rng_destroy": (ctypes.c_int, [_P]),
     "fs_rng_next_u": (ctypes.c_int, [_P, _P, _I32]),

@@ -95,6 +95,8 @@ struct Args {
     uint32_t* rhist;               // [B][RBINS] row histograms of the segments' candidates, left at 0
     uint32_t* stream_cnt;          // [n_streams] verify completion counters, left at 0
     int32_t* err;                  // device error bits
+    int32_t* dirty;                // nonzero: a merge gave up waiting; the row histograms and counters may be stale
+    uint32_t merge_spins;          // bounded wait of the merge role (polls)
 };
 
 // ------------------------------------------------------------------------------------------------ keys
@@ -576,6 +578,7 @@ struct Shared {
     uint32_t tmax;                     // segment kernel: the largest key of tile 0
     uint32_t rc64[WAVE];               // segment kernel: tile-0 counts in the 64 coarse bins up to tmax's
     uint32_t nids;
+    uint32_t misc_alone;               // merge role: the row is computed from its logits alone
     Red red;
     __device__ __forceinline__ uint32_t* cnt() { return scr; }
     __device__ __forceinline__ uint32_t* bins() { return scr + TILE / 2; }
@@ -1344,7 +1347,8 @@ __device__ __forceinline__ int large_walk(Shared& s, int n, uint64_t lo_c, doubl
 }
 
 // The whole large-k sample of one row: token, kept count, optional candidate outputs (in chunks of KMAX).
-__device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Shared& s, int& tok_out, int& keep_out) {
+__device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Shared& s, int& tok_out, int& keep_out,
+                                          bool seg_summaries = true) {
     const int tid = threadIdx.x;
     const int row = rc.row;
     const fs_row_params& p = rc.p;
@@ -1357,7 +1361,7 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
     __syncthreads();
     uint64_t cmax = 0ull, cmin = ~0ull;
     uint32_t nv = 0u;
-    if (a.nseg > 0 && !need_kth) {
+    if (a.nseg > 0 && !need_kth && seg_summaries) {
         // the segments published the extremes and counts of their full tiles; the partial last tile is read here
         for (int c = tid; c < a.nseg; c += BLOCK) {
             const int64_t slot = (int64_t)row * a.nseg + c;
@@ -1405,11 +1409,21 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
     (void)block_excl_scan<uint32_t>(nv, s.wsum, &ntot);
     if (ntot == 0u) {                         // every logit NaN: no order to sample from
         tok_out = 0;
-        keep_out = 0;
+        keep_out = rc.greedy ? 1 : 0;
         return;
     }
     const uint32_t kmax = comp_key(cmax);
     const float mx = val_of(kmax);
+    if (rc.greedy) {                          // ferro's scan (sampler.cpp:19-23): the first maximum above -inf,
+        tok_out = mx > -__builtin_huge_valf() ? (int)comp_id(cmax) : 0;       // never moving off a NaN at index 0
+        if (ld_const(a.logits + (int64_t)row * a.ld) != ld_const(a.logits + (int64_t)row * a.ld)) tok_out = 0;
+        keep_out = 1;
+        if (tid == 0 && a.mode != MODE_VERIFY && a.kcap > 0) {
+            if (a.cand_ids) a.cand_ids[(int64_t)row * a.kcap] = tok_out;
+            if (a.cand_probs) a.cand_probs[(int64_t)row * a.kcap] = 1.0;
+        }
+        return;
+    }
     const double Td = (double)p.temperature;
     const int keff = (uint32_t)rc.k < ntot ? rc.k : (int)ntot;
     uint64_t Xk = cmin;
@@ -1826,7 +1840,7 @@ __device__ __forceinline__ bool merge_fast(const Args& a, const RowCtx& rc, Shar
     return true;
 }
 
-__device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Shared& s, const Pre& pre) {
+__device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Shared& s, const Pre& pre, bool alone = false) {
     const int tid = threadIdx.x;
     const int row = rc.row;
     const int V = a.V;
@@ -1837,8 +1851,8 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
     int tok = 0, keep = 1;
 
     bool fast = false;
-    if (rc.large) {
-        large_row(a, rc, s, tok, keep);
+    if (rc.large || alone) {
+        large_row(a, rc, s, tok, keep, !alone);     // alone: the whole row from the logits, no segment output
     } else if (ntail == 0 && (fast = merge_fast(a, rc, s, pre, tok, keep))) {
         // the short merge wrote the row's outputs
     } else {
@@ -2235,7 +2249,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
         }                                             // general path
     }
     }
-    if (!rc.large && !rc.greedy && nseg > 0) {         // the segments' row histogram is spent: leave it at 0
+    if (!rc.large && !rc.greedy && nseg > 0 && !alone) {   // the segments' row histogram is spent: leave it at 0
         uint4* rz = reinterpret_cast<uint4*>(a.rhist + (int64_t)row * RBINS);
         for (int i = tid; i < RBINS / 4; i += BLOCK) rz[i] = make_uint4(0u, 0u, 0u, 0u);
     }
@@ -2831,24 +2845,40 @@ constexpr uint32_t MERGE_SPINS = 1u << 20;   // bounded wait of the merge role (
 // the last XCDS * ceil(B / XCDS) workgroups merges rows x, x + XCDS, ...). Workgroups are dispatched in index
 // order, so the row's segments are running or done when it starts: it waits for their count (an atomic that
 // is not idempotent, so it executes in the L2 and is never folded into an L1-served load), invalidates its L1
-// and reads the lists from the L2. A wait past MERGE_SPINS flags FS_DEVERR_INTERNAL and gives up.
+// and reads the lists from the L2. The wait is bounded (a.merge_spins polls): past it FS_DEVERR_INTERNAL is
+// raised, the context is marked dirty and the row is computed from its logits alone (exact, one workgroup); a
+// dirty context computes every row that way until fs_device_error clears the workspace.
 __device__ __forceinline__ void merge_role(const Args& a, int mi, Shared& s) {
     const int row = mi % XCDS + XCDS * (mi / XCDS);
     if (row >= a.B) return;
     const RowCtx rc = row_ctx(a, row);               // the row's inputs are read while the segments run
     uint32_t* ctr = row_counter(a, row);
     if (threadIdx.x == 0) {
+        // A context left dirty by an earlier give-up: its row histograms and counters may hold a late segment's
+        // additions, so no segment output is trusted and the row is computed from its logits alone. Otherwise a
+        // bounded wait for the row's segments; past it the context is marked dirty (a segment that finishes later
+        // still adds to this row's counter and histogram) and this row, too, is computed alone.
+        uint32_t alone = ld_agent(a.dirty) != 0 ? 1u : 0u;
         uint32_t spins = 0u;
-        while ((__hip_atomic_fetch_add(ctr, 0x10000u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & 0xFFFFu) <
-               (uint32_t)a.nseg) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins == MERGE_SPINS) {
+        while (!alone &&
+               (__hip_atomic_fetch_add(ctr, 0x10000u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & 0xFFFFu) <
+                   (uint32_t)a.nseg) {
+            if (++spins >= a.merge_spins) {
                 atomicOr(a.err, FS_DEVERR_INTERNAL);
+                __hip_atomic_store(a.dirty, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                alone = 1u;
                 break;
             }
+            __builtin_amdgcn_s_sleep(1);
         }
+        s.misc_alone = alone;
     }
     __syncthreads();
+    if (s.misc_alone) {
+        Pre none = {};
+        merge_row(a, rc, s, none, true);
+        return;
+    }
     l1_invalidate();
     Pre pre;
     prefetch_lists(a, row, pre);
@@ -3157,7 +3187,8 @@ struct fs_context {
     size_t row_cap = 0;
     uint32_t* stream_cnt = nullptr;
     size_t stream_cap = 0;
-    int32_t* err = nullptr;
+    int32_t* err = nullptr;        // [0]: error bits; [1]: dirty (a merge gave up; see fs_device_error)
+    uint32_t merge_spins = fs::MERGE_SPINS;
 };
 
 namespace {
@@ -3186,8 +3217,8 @@ int grow(fs_context* c, size_t slots, size_t rows, size_t streams) {
         c->stream_cap = streams;
     }
     if (!c->err) {
-        if (hipMalloc(&c->err, sizeof(int32_t)) != hipSuccess) return FS_E_NOMEM;
-        if (hipMemset(c->err, 0, sizeof(int32_t)) != hipSuccess) return FS_E_HIP;
+        if (hipMalloc(&c->err, 2 * sizeof(int32_t)) != hipSuccess) return FS_E_NOMEM;
+        if (hipMemset(c->err, 0, 2 * sizeof(int32_t)) != hipSuccess) return FS_E_HIP;
     }
     return FS_OK;
 }
@@ -3222,7 +3253,7 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
     int rc = grow(ctx, (size_t)(items > 0 ? items : 1), (size_t)rows, (size_t)(streams > 0 ? streams : 1));
     if (rc != FS_OK) return rc;
     a.cand = ctx->cand; a.meta = ctx->meta; a.rhist = ctx->rhist;
-    a.stream_cnt = ctx->stream_cnt; a.err = ctx->err;
+    a.stream_cnt = ctx->stream_cnt; a.err = ctx->err; a.dirty = ctx->err + 1; a.merge_spins = ctx->merge_spins;
     if (seg_grid > 0) {                            // the segments, then one merging workgroup per row (same grid)
         const int64_t grid = seg_grid + (int64_t)fs::XCDS * ((rows + fs::XCDS - 1) / fs::XCDS);
         if (grid > 0x7fffffff) return FS_E_INVALID;
@@ -3360,9 +3391,27 @@ int fs_device_error(fs_context* ctx, void* stream, int32_t* bits) {
     if (!ctx || !bits) return FS_E_INVALID;
     *bits = 0;
     if (!ctx->err) return FS_OK;
+    std::lock_guard<std::mutex> g(ctx->mu);
     if (hipStreamSynchronize((hipStream_t)stream) != hipSuccess) return FS_E_HIP;
-    if (hipMemcpy(bits, ctx->err, sizeof(int32_t), hipMemcpyDeviceToHost) != hipSuccess) return FS_E_HIP;
-    if (hipMemset(ctx->err, 0, sizeof(int32_t)) != hipSuccess) return FS_E_HIP;
+    int32_t h[2] = {0, 0};
+    if (hipMemcpy(h, ctx->err, sizeof(h), hipMemcpyDeviceToHost) != hipSuccess) return FS_E_HIP;
+    *bits = h[0];
+    if (h[1] != 0) {
+        // a merge gave up: the segments it did not wait for have finished by now (the stream is idle), so the
+        // row histograms and counters are cleared and the context leaves its compute-alone mode
+        if (ctx->rhist && hipMemset(ctx->rhist, 0, ctx->row_cap * fs::RBINS * sizeof(uint32_t)) != hipSuccess)
+            return FS_E_HIP;
+        if (ctx->stream_cnt && hipMemset(ctx->stream_cnt, 0, ctx->stream_cap * sizeof(uint32_t)) != hipSuccess)
+            return FS_E_HIP;
+    }
+    if (hipMemset(ctx->err, 0, sizeof(h)) != hipSuccess) return FS_E_HIP;
+    return FS_OK;
+}
+
+int fs_set_wait_limit(fs_context* ctx, uint32_t polls) {
+    if (!ctx) return FS_E_INVALID;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    ctx->merge_spins = polls ? polls : fs::MERGE_SPINS;
     return FS_OK;
 }
 

@@ -100,6 +100,10 @@ class Context:
             except Exception:
                 pass
 
+    def set_wait_limit(self, polls: int) -> None:
+        """fs_set_wait_limit: the merge's bounded wait for a row's segments (0 = default)."""
+        check(lib().fs_set_wait_limit(self.h, int(polls)), "fs_set_wait_limit")
+
     @classmethod
     def default(cls, device=None) -> "Context":
         dev = torch.device("cuda", torch.cuda.current_device() if device is None else torch.device(device).index or 0)

@@ -34,7 +34,10 @@ extern "C" {
 /* Device-side error bits (fs_device_error). */
 #define FS_DEVERR_COUNT_OVERFLOW 1   /* one token occurs > 65535 times in a penalty window */
 #define FS_DEVERR_INTERNAL 2         /* an internal invariant failed, or a row's merge gave up waiting for its
-                                        segments (workgroups not dispatched round-robin over the XCDs by index) */
+                                        segments (workgroups not dispatched round-robin over the XCDs by index, or
+                                        a wait limit below the segments' time). The row was then computed alone from
+                                        its logits (the token is exact); the context stays in that slower mode until
+                                        fs_device_error, which clears its workspace */
 #define FS_DEVERR_HIST_APPEND 4      /* fs_hist_append: the new histories exceed out_cap (ids past it are not
                                         written), or a count lies outside [0, its stream's rows] (clamped) */
 
@@ -156,8 +159,13 @@ int fs_drng_error(fs_drng* r, void* stream, int32_t* bits);
 int fs_penalize_batch(fs_context* ctx, float* d_logits, int64_t ld, int32_t B, int32_t V, const int32_t* d_hist,
                       const int64_t* d_hist_off, const fs_row_params* d_params, void* stream);
 
-/* Waits for `stream`, then returns and clears the device error bits (FS_DEVERR_*) kernels of this context set. */
+/* Waits for `stream`, then returns and clears the device error bits (FS_DEVERR_*) kernels of this context set; after
+ * FS_DEVERR_INTERNAL it also clears the context's workspace (row histograms and counters). */
 int fs_device_error(fs_context* ctx, void* stream, int32_t* bits);
+
+/* The merge's bounded wait for a row's segments, in polls (0 = the default, 2^20: far above any segment's time).
+ * A smaller limit makes merges give up (FS_DEVERR_INTERNAL) and compute their rows alone: a test of that path. */
+int fs_set_wait_limit(fs_context* ctx, uint32_t polls);
 
 /* Static description of the error code. */
 const char* fs_strerror(int code);
