@@ -2088,6 +2088,13 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
         __syncthreads();
         uint32_t c1;
         const uint32_t T1 = hist_threshold(s.bins(), L, sh, k, &c1, s.wsum, s.red);
+        if (c1 < (uint32_t)k) {
+            // Fewer than k candidates: with L = 0 (no bound above NaN's key) every number of the row is a candidate,
+            // so the row holds fewer than k numbers and samples over them (NaN is never a candidate); with L > 0 the
+            // bounds promised k, an invariant failure. Never read past the list.
+            if (tid == 0 && L != 0u) atomicOr(a.err, FS_DEVERR_INTERNAL);
+            k = (int)c1;
+        }
         // the c1 >= k candidates with key >= T1 contain the top k: sort them
         uint64_t* top;
         bool wave_done = false;                   // wave 0 finished the row (k <= 64, c1 <= 128)
@@ -2113,7 +2120,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 }
             }
             __syncthreads();
-            if (c1 <= (uint32_t)(2 * WAVE) && k <= WAVE) {
+            if (c1 <= (uint32_t)(2 * WAVE) && k <= WAVE && k > 0) {
                 uint32_t* rk = reinterpret_cast<uint32_t*>(small_out + 2 * WAVE);   // past wave_finish's buffers
                 block_ranks(small_in, (int)c1, rk);
                 if (tid < WAVE) wave_finish(a, rc, small_in, rk, k, pre.u, reinterpret_cast<double*>(small_out), tok, keep);
@@ -2164,10 +2171,14 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             c1 = (uint32_t)m;
         }
         if (!wave_done) {
-            if (c1 < (uint32_t)k) {                       // impossible by construction; never read past the list
+            if (c1 < (uint32_t)k) {                       // c1 >= k after the clamp above; never read past the list
                 if (tid == 0) atomicOr(a.err, FS_DEVERR_INTERNAL);
                 k = (int)c1;
             }
+            if (k == 0) {                                 // every logit NaN: token 0, nothing kept
+                tok = 0;
+                keep = 0;
+            } else {
 
             // ---- softmax at temperature, min-p, top-p, draw (sampler.cpp:37-49), k <= KMAX
             const fs_row_params& p = rc.p;
@@ -2245,6 +2256,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                         if (i0 + q < m) a.cand_probs[(int64_t)row * a.kcap + i0 + q] = pr[q];
                 }
             }
+            }                                             // k > 0
         }
         }                                             // general path
     }

@@ -63,7 +63,17 @@ def params_array(params) -> np.ndarray:
 
 
 def _ptr(t):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    """Device pointer of a tensor the C ABI reads or writes as a packed array."""
+    if t is None:
+        return None
+    if not t.is_contiguous():
+        raise SamplerError("a non-contiguous tensor cannot be passed as a packed array")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _dev(x, dtype, device):
+    """An input array or tensor as a packed device tensor of `dtype` (a strided view is copied, not misread)."""
+    return torch.as_tensor(x, dtype=dtype, device=device).contiguous()
 
 
 def _stream(stream=None):
@@ -75,7 +85,7 @@ def _dev_params(params, device) -> torch.Tensor:
     if isinstance(params, torch.Tensor):
         if params.dtype != torch.uint8 or params.numel() % PARAMS_DTYPE.itemsize:
             raise SamplerError("params tensor must be uint8 bytes of fs_row_params records")
-        return params.to(device)
+        return params.to(device).contiguous()
     a = params_array(params)
     return torch.from_numpy(a.view(np.uint8).copy()).to(device)
 
@@ -169,7 +179,7 @@ class DeviceRng:
         ro = None
         rows = self.n
         if row_off is not None:
-            ro = torch.as_tensor(row_off, dtype=torch.int64, device=self._dev)
+            ro = _dev(row_off, torch.int64, self._dev)
             if ro.numel() != self.n + 1:
                 raise SamplerError("row_off must have n_streams+1 entries")
             rows = int(ro[-1].item())
@@ -181,7 +191,7 @@ class DeviceRng:
 
     def skip(self, counts, params, stream=None) -> None:
         p = _dev_params(params, self._dev)
-        c = torch.as_tensor(counts, dtype=torch.int32, device=self._dev)
+        c = _dev(counts, torch.int32, self._dev)
         if c.numel() != self.n:
             raise SamplerError("one count per stream")
         check(lib().fs_drng_skip(self.h, _ptr(c), _ptr(p), _stream(stream)), "fs_drng_skip")
@@ -215,8 +225,8 @@ def _check_logits(logits: torch.Tensor, V: int | None):
 def _hist_tensors(hist, hist_off, B, device):
     if hist is None:
         return None, None
-    hist = torch.as_tensor(hist, dtype=torch.int32, device=device)
-    hist_off = torch.as_tensor(hist_off, dtype=torch.int64, device=device)
+    hist = _dev(hist, torch.int32, device)
+    hist_off = _dev(hist_off, torch.int64, device)
     if hist_off.numel() != B + 1:
         raise SamplerError("hist_off must have B+1 entries")
     return hist, hist_off
@@ -231,7 +241,7 @@ def sample_batch(logits, params, u, hist=None, hist_off=None, V=None, kcap=0, ct
     p = _dev_params(params, dev)
     if p.numel() != B * PARAMS_DTYPE.itemsize:
         raise SamplerError("one params record per row")
-    u = torch.as_tensor(u, dtype=torch.float64, device=dev)
+    u = _dev(u, torch.float64, dev)
     hist, hist_off = _hist_tensors(hist, hist_off, B, dev)
     tok = torch.empty(B, dtype=torch.int32, device=dev)
     keep = torch.empty(B, dtype=torch.int32, device=dev)
@@ -266,13 +276,13 @@ def verify(logits, rows, row_off, params, u=None, hist=None, hist_off=None, eos_
     logits, ld, n = _check_logits(logits, V)
     R = logits.shape[0]
     dev = logits.device
-    rows = torch.as_tensor(rows, dtype=torch.int32, device=dev)
-    row_off = torch.as_tensor(row_off, dtype=torch.int64, device=dev)
+    rows = _dev(rows, torch.int32, dev)
+    row_off = _dev(row_off, torch.int64, dev)
     S = row_off.numel() - 1
     p = _dev_params(params, dev)
     if p.numel() != S * PARAMS_DTYPE.itemsize:
         raise SamplerError("one params record per stream")
-    u = torch.as_tensor(np.zeros(R) if u is None else u, dtype=torch.float64, device=dev)
+    u = _dev(np.zeros(R) if u is None else u, torch.float64, dev)
     hist, hist_off = _hist_tensors(hist, hist_off, S, dev)
     tok = torch.empty(R, dtype=torch.int32, device=dev)
     acc = torch.empty(S, dtype=torch.int32, device=dev)
@@ -307,13 +317,12 @@ def penalize_batch(logits, params, hist=None, hist_off=None, V=None, ctx=None, s
 
 def lookup_draft(hist, hist_off, kmax, min_n=None, eos_id=-1, draft_ld=None, ctx=None, stream=None):
     """fs_lookup_draft: prompt-lookup drafts per stream (server.cpp:552-564). Returns (draft [S, draft_ld], n [S])."""
-    hist_off = torch.as_tensor(hist_off, dtype=torch.int64, device="cuda")
+    hist_off = _dev(hist_off, torch.int64, "cuda")
     S = hist_off.numel() - 1
     dev = hist_off.device
-    hist = torch.as_tensor(hist, dtype=torch.int32, device=dev)
-    km = torch.as_tensor(np.broadcast_to(np.asarray(kmax, np.int32), (S,)).copy(), device=dev)
-    mn = None if min_n is None else torch.as_tensor(np.broadcast_to(np.asarray(min_n, np.int32), (S,)).copy(),
-                                                     device=dev)
+    hist = _dev(hist, torch.int32, dev)
+    km = _dev(np.broadcast_to(np.asarray(kmax, np.int32), (S,)).copy(), torch.int32, dev)
+    mn = None if min_n is None else _dev(np.broadcast_to(np.asarray(min_n, np.int32), (S,)).copy(), torch.int32, dev)
     ld = int(draft_ld if draft_ld is not None else max(int(km.max().item()) if S else 1, 1))
     draft = torch.zeros((S, ld), dtype=torch.int32, device=dev)
     nd = torch.zeros(S, dtype=torch.int32, device=dev)
@@ -330,15 +339,15 @@ def hist_append(hist, hist_off, tok, row_off=None, count=None, out_cap=None, ctx
     None: 1 per stream; fs_verify's tok / row_off / accepted fit as they are). Returns (out_hist, out_off): out_off
     [S+1] int64 rebased to 0; out_hist holds out_cap ids (default: room for every row of tok), of which
     out_off[-1] are used. Stays on the device: nothing here waits for the GPU."""
-    hist_off = torch.as_tensor(hist_off, dtype=torch.int64, device="cuda")
+    hist_off = _dev(hist_off, torch.int64, "cuda")
     dev = hist_off.device
     S = hist_off.numel() - 1
-    hist = torch.as_tensor(hist, dtype=torch.int32, device=dev)
+    hist = _dev(hist, torch.int32, dev)
     if hist.numel() == 0:
         hist = torch.zeros(1, dtype=torch.int32, device=dev)     # every history empty: a valid pointer, never read
-    tok = torch.as_tensor(tok, dtype=torch.int32, device=dev)
-    ro = None if row_off is None else torch.as_tensor(row_off, dtype=torch.int64, device=dev)
-    cnt = None if count is None else torch.as_tensor(count, dtype=torch.int32, device=dev)
+    tok = _dev(tok, torch.int32, dev)
+    ro = None if row_off is None else _dev(row_off, torch.int64, dev)
+    cnt = None if count is None else _dev(count, torch.int32, dev)
     if ro is not None and ro.numel() != S + 1:
         raise SamplerError(f"row_off has {ro.numel()} entries for {S} streams")
     if cnt is not None and cnt.numel() != S:

@@ -64,8 +64,13 @@ int fso_penalize(float* row, int n, const int32_t* hist, int64_t hlen, const fso
 /* ------------------------------------------------------------------ candidate order: sampler.cpp:30 */
 typedef struct { float v; int32_t id; } cand_t;
 
-/* a precedes b: larger logit first, equal logits (-0 == +0) by lower id. */
+/* a precedes b: larger logit first, equal logits (-0 == +0) by lower id. NaN: ferro's comparator (sampler.cpp:30)
+ * is not a strict weak order with a NaN in the row, so std::partial_sort's result is unspecified there; this build
+ * ranks NaN below every number (NaNs by lower id) and never makes it a candidate (see fso_sample). Rows without a
+ * NaN are unaffected. */
 static int better(const cand_t* a, const cand_t* b) {
+    const int an = a->v != a->v, bn = b->v != b->v;
+    if (an || bn) return an && bn ? a->id < b->id : bn;
     return a->v > b->v || (a->v == b->v && a->id < b->id);
 }
 static int cmp_cand(const void* pa, const void* pb) {
@@ -118,7 +123,15 @@ int fso_sample(float* row, int n, const int32_t* hist, int64_t hlen, const fso_p
         if (ncand_out) *ncand_out = 1;
         return best;
     }
-    const int k = (p->top_k > 0 && p->top_k < n) ? p->top_k : n;   /* sampler.cpp:26 */
+    int k = (p->top_k > 0 && p->top_k < n) ? p->top_k : n;   /* sampler.cpp:26 */
+    int nnum = 0;                                              /* NaN policy: candidates are numbers only */
+    for (int i = 0; i < n; ++i) nnum += row[i] == row[i];
+    if (nnum == 0) {                                           /* every logit NaN: token 0, nothing kept */
+        if (keep_out) *keep_out = 0;
+        if (ncand_out) *ncand_out = 0;
+        return 0;
+    }
+    if (k > nnum) k = nnum;
     cand_t* c = top_k_sorted(row, n, k);
     /* softmax at temperature: the difference is a float op, then double divide and exp (sampler.cpp:37-41) */
     const float mx = c[0].v;

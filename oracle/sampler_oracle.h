@@ -10,6 +10,10 @@
  *   - frequency / presence penalties (not in ferro) follow the llama.cpp convention,
  *     l -= cnt * freq + (cnt > 0) * pres, applied after the repetition step over the same window; with
  *     freq = pres = 0 the row is unchanged bit for bit.
+ * One policy where ferro's result is unspecified: with a NaN logit in a sampled row, ferro's candidate
+ * comparator (sampler.cpp:30) is no strict weak order. Here NaN ranks below every number and is never a
+ * candidate: k becomes min(k, the row's count of numbers); a row of NaNs only gives token 0 and keeps 0. Rows
+ * without a NaN are unaffected. Parity on NaN rows is therefore pinned to this policy, not to ferro.
  */
 #pragma once
 #include <stdint.h>

@@ -27,11 +27,22 @@ def boundary_row(probs, keep, u, top_p, min_p):
     return bool(np.any(np.abs(u * tot - c[:max(keep, 1)]) <= BOUNDARY))
 
 
+class Parity(int):
+    """Rows of a comparison whose draw lies near a cumulative boundary (the int value), with .diverged: the rows
+    among them whose token or kept count actually differs from the oracle's."""
+
+    def __new__(cls, near, diverged):
+        obj = super().__new__(cls, near)
+        obj.diverged = diverged
+        return obj
+
+
 def compare(gpu, ora, params, u, kcap):
-    """gpu / ora: dicts with tok, keep, cand_ids, cand_probs ([B, kcap]) and ora ncand. Returns #boundary rows;
-    asserts everything else."""
+    """gpu / ora: dicts with tok, keep, cand_ids, cand_probs ([B, kcap]) and ora ncand. Returns a Parity: the rows
+    near a boundary and, of those, the ones that differ; asserts everything else."""
     B = len(ora["tok"])
     nb = 0
+    nd = 0
     for b in range(B):
         p = params[b]
         m = min(int(ora["ncand"][b]), kcap)
@@ -48,8 +59,9 @@ def compare(gpu, ora, params, u, kcap):
         if gpu["tok"][b] != ora["tok"][b] or gpu["keep"][b] != ora["keep"][b]:
             assert at_edge, f"row {b}: tok {gpu['tok'][b]} vs {ora['tok'][b]}, keep {gpu['keep'][b]} vs " \
                             f"{ora['keep'][b]} away from any boundary"
+            nd += 1
         nb += int(at_edge)
-    return nb
+    return Parity(nb, nd)
 
 
 def oracle_decode_loop(rows_per_step, params, seeds, hist0):

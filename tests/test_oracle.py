@@ -282,3 +282,32 @@ def test_decode_loop_with_append_matches_reference():
                 h.append(t)
         finally:
             R.ref_sampler_free(obj)
+
+
+def test_nan_policy_numbers_only():
+    """The oracle's NaN policy (ferro's comparator is no strict weak order with a NaN, so its candidates are
+    unspecified there): NaN ranks below every number and is never a candidate. Checked against a brute-force sort
+    of the numbers: the candidates are the first min(k, #numbers) numbers (value desc, id asc), softmax over them;
+    a row of NaNs only gives token 0 with nothing kept."""
+    rng = np.random.default_rng(5)
+    for trial in range(40):
+        V = int(rng.integers(2, 300))
+        x = (rng.standard_normal(V) * 2).astype(np.float32)
+        x[rng.random(V) < rng.uniform(0.05, 0.9)] = np.nan
+        k = int(rng.choice([1, 3, 40, 0, V + 5]))
+        p = O.make_params(temperature=0.7, top_k=k, top_p=1.0, repetition_penalty=1.0)
+        tok, ids, probs, keep, ncand = O.sample(x, [], p[0], 0.37, kcap=V)
+        num = [i for i in range(V) if x[i] == x[i]]
+        if not num:
+            assert (tok, keep, ncand) == (0, 0, 0)
+            continue
+        if k == 1:
+            continue                                   # greedy: ferro's scan, defined with NaN (never moves onto it)
+        order = sorted(num, key=lambda i: (-float(x[i]), i))
+        kk = min(k if 0 < k < V else V, len(num))
+        assert ncand == kk
+        np.testing.assert_array_equal(ids, order[:kk])
+        mx = np.float32(x[order[0]])
+        e = np.array([np.exp(np.float64(np.float32(x[i] - mx)) / np.float64(np.float32(0.7))) for i in order[:kk]])
+        np.testing.assert_allclose(probs, e / e.sum(), rtol=1e-13)
+        assert x[tok] == x[tok]                        # a number is drawn
