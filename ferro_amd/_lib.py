@@ -18,6 +18,7 @@ FS_E_INVALID = -1
 FS_E_HIP = -2
 FS_E_NOMEM = -3
 FS_E_DEVICE = -4
+FS_E_LIMIT = -5
 FS_DEVERR_COUNT_OVERFLOW = 1
 FS_DEVERR_INTERNAL = 2
 
@@ -37,6 +38,7 @@ SIGNATURES = {
     "fs_create": (ctypes.c_int, [_P]),
     "fs_destroy": (ctypes.c_int, [_P]),
     "fs_sample_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P]),
+    "fs_sample_batch_static": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P]),
     "fs_argmax_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P]),
     "fs_verify": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P]),
     "fs_penalize_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P]),

@@ -3201,6 +3201,7 @@ struct fs_context {
     size_t stream_cap = 0;
     int32_t* err = nullptr;        // [0]: error bits; [1]: dirty (a merge gave up; see fs_device_error)
     uint32_t merge_spins = fs::MERGE_SPINS;
+    int static_dev = -1;       // device whose static workspace fs_sample_batch_static used with this context
 };
 
 namespace {
@@ -3235,21 +3236,16 @@ int grow(fs_context* c, size_t slots, size_t rows, size_t streams) {
     return FS_OK;
 }
 
-int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream_t st) {
-    std::lock_guard<std::mutex> g(ctx->mu);
-    if (ctx->device < 0) {
-        if (hipGetDevice(&ctx->device) != hipSuccess) return FS_E_HIP;
-        if (hipDeviceGetAttribute(&ctx->cus, hipDeviceAttributeMultiprocessorCount, ctx->device) != hipSuccess)
-            return FS_E_HIP;
-    }
-    // Segments: at most two per CU over the whole batch (all resident at once: a second round of a few
-    // workgroups would double the time), at least one per row; a segment streams >= 1 full tile of 4096 logits.
-    // The merge kernel handles each row's partial last tile (all of a row shorter than one tile).
+// Segments: at most two per CU over the whole batch (all resident at once: a second round of a few workgroups
+// would double the time), at least one per row; a segment streams >= 1 full tile of 4096 logits. The merge
+// handles each row's partial last tile (all of a row shorter than one tile). Sets a.nseg / a.seg_tiles and the
+// workspace the call needs (items = (row, segment) slots).
+int plan(int cus, fs::Args& a, int64_t rows, int64_t& items, int64_t& seg_grid) {
     const int64_t tiles_row = a.V / fs::TILE;
     a.nseg = 0;
     a.seg_tiles = 1;
     if (tiles_row > 0) {
-        int64_t want = (2 * (int64_t)ctx->cus) / rows;
+        int64_t want = (2 * (int64_t)cus) / rows;
         if (want < 1) want = 1;
         if (want > tiles_row) want = tiles_row;
         if (want > fs::BLOCK - 1) want = fs::BLOCK - 1;   // the merge gives each list (segments + tail) a thread
@@ -3257,15 +3253,16 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
         a.nseg = (int)((tiles_row + a.seg_tiles - 1) / a.seg_tiles);
     }
     if (a.nseg > fs::MAX_SEGS) return FS_E_INVALID;
-    const int64_t items = rows * a.nseg;
+    items = rows * a.nseg;
     if (items > 0x7fffffff) return FS_E_INVALID;
     // one workgroup per (row, segment), the rows dealt to XCDS slots (segment_kernel)
-    const int64_t seg_grid = items > 0 ? (int64_t)fs::XCDS * a.nseg * ((rows + fs::XCDS - 1) / fs::XCDS) : 0;
+    seg_grid = items > 0 ? (int64_t)fs::XCDS * a.nseg * ((rows + fs::XCDS - 1) / fs::XCDS) : 0;
     if (seg_grid > 0x7fffffff) return FS_E_INVALID;
-    int rc = grow(ctx, (size_t)(items > 0 ? items : 1), (size_t)rows, (size_t)(streams > 0 ? streams : 1));
-    if (rc != FS_OK) return rc;
-    a.cand = ctx->cand; a.meta = ctx->meta; a.rhist = ctx->rhist;
-    a.stream_cnt = ctx->stream_cnt; a.err = ctx->err; a.dirty = ctx->err + 1; a.merge_spins = ctx->merge_spins;
+    return FS_OK;
+}
+
+// Launches the sampling grid on a bound workspace (a.cand / meta / rhist / stream_cnt / err / dirty).
+int launch_planned(const fs::Args& a, int64_t rows, int64_t seg_grid, hipStream_t st) {
     if (seg_grid > 0) {                            // the segments, then one merging workgroup per row (same grid)
         const int64_t grid = seg_grid + (int64_t)fs::XCDS * ((rows + fs::XCDS - 1) / fs::XCDS);
         if (grid > 0x7fffffff) return FS_E_INVALID;
@@ -3277,6 +3274,84 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
                        a.params, a);
     return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
 }
+
+int device_of(fs_context* ctx) {
+    if (ctx->device < 0) {
+        if (hipGetDevice(&ctx->device) != hipSuccess) return FS_E_HIP;
+        if (hipDeviceGetAttribute(&ctx->cus, hipDeviceAttributeMultiprocessorCount, ctx->device) != hipSuccess)
+            return FS_E_HIP;
+    }
+    return FS_OK;
+}
+
+int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream_t st) {
+    std::lock_guard<std::mutex> g(ctx->mu);
+    int rc = device_of(ctx);
+    if (rc != FS_OK) return rc;
+    int64_t items = 0, seg_grid = 0;
+    rc = plan(ctx->cus, a, rows, items, seg_grid);
+    if (rc != FS_OK) return rc;
+    rc = grow(ctx, (size_t)(items > 0 ? items : 1), (size_t)rows, (size_t)(streams > 0 ? streams : 1));
+    if (rc != FS_OK) return rc;
+    a.cand = ctx->cand; a.meta = ctx->meta; a.rhist = ctx->rhist;
+    a.stream_cnt = ctx->stream_cnt; a.err = ctx->err; a.dirty = ctx->err + 1; a.merge_spins = ctx->merge_spins;
+    return launch_planned(a, rows, seg_grid, st);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------------------ static workspace
+// fs_sample_batch_static's workspace: one file-scope device array per GPU, held until the process ends, so the
+// call allocates nothing. Layout (bytes): error word and dirty flag | meta [ST_SLOTS][2] | row histograms
+// [ST_ROWS][RBINS] | candidate lists [ST_SLOTS][CAP]. The row histograms (counters included) must be zero when a
+// call starts; the kernels leave them so, and the first call on a device clears them with a fill kernel (no
+// hipMemsetAsync: the call may be recorded into a graph).
+constexpr int64_t ST_ROWS = 512;                                  // rows per call
+constexpr int64_t ST_SLOTS = 512;                                 // (row, segment) slots per call
+constexpr size_t ST_ERR_OFF = 0;                                  // int32 [2]: error bits, dirty
+constexpr size_t ST_META_OFF = 256;
+constexpr size_t ST_RHIST_OFF = ST_META_OFF + ((ST_SLOTS * 2 * sizeof(uint32_t) + 255) / 256) * 256;
+constexpr size_t ST_CAND_OFF = ST_RHIST_OFF + (size_t)ST_ROWS * fs::RBINS * sizeof(uint32_t);
+constexpr size_t ST_BYTES = ST_CAND_OFF + (size_t)ST_SLOTS * fs::CAP * sizeof(uint64_t);   // 33.8 MB
+
+static __device__ __align__(256) unsigned char scratch[ST_BYTES];
+
+namespace fs {
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0u;
+}
+}  // namespace fs
+
+namespace {
+
+constexpr int ST_MAX_DEVICES = 64;
+std::mutex g_static_mu;
+unsigned char* g_static_ptr[ST_MAX_DEVICES] = {};   // the device address of `scratch` on each device
+
+// The static workspace of the current device: its address from hipGetSymbolAddress (the array's name is not a
+// device address in host code), once per device; the first call also zeroes the error words and row histograms
+// on `st`, ahead of its own launch.
+int static_workspace(int dev, hipStream_t st, unsigned char** out) {
+    if (dev < 0 || dev >= ST_MAX_DEVICES) return FS_E_INVALID;
+    std::lock_guard<std::mutex> g(g_static_mu);
+    if (!g_static_ptr[dev]) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return FS_E_HIP;
+        unsigned char* base = (unsigned char*)ptr;
+        hipLaunchKernelGGL(fs::zero_words_kernel, dim3(1), dim3(256), 0, st, (uint32_t*)(base + ST_ERR_OFF),
+                           (int64_t)(ST_META_OFF / 4));
+        hipLaunchKernelGGL(fs::zero_words_kernel, dim3(1024), dim3(256), 0, st, (uint32_t*)(base + ST_RHIST_OFF),
+                           (int64_t)ST_ROWS * fs::RBINS);
+        if (hipGetLastError() != hipSuccess) return FS_E_HIP;
+        g_static_ptr[dev] = base;
+    }
+    *out = g_static_ptr[dev];
+    return FS_OK;
+}
+
+}  // namespace
+
+namespace {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -3319,6 +3394,43 @@ int fs_sample_batch(fs_context* ctx, const float* d_logits, int64_t ld, int32_t 
     a.u = d_u; a.tok = d_tok; a.kcap = kcap; a.cand_ids = d_cand_ids; a.cand_probs = d_cand_probs; a.keep = d_keep;
     a.mode = fs::MODE_SAMPLE; a.eos = -1;
     return launch(ctx, a, B, 0, (hipStream_t)stream);
+}
+
+int fs_sample_batch_static(fs_context* ctx, const float* d_logits, int64_t ld, int32_t B, int32_t V,
+                           const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params,
+                           const double* d_u, int32_t* d_tok, int32_t kcap, int32_t* d_cand_ids, double* d_cand_probs,
+                           int32_t* d_keep, void* stream) {
+    if (!ctx || !d_params || !d_tok || kcap < 0 || ((d_cand_ids || d_cand_probs) && kcap == 0)) return FS_E_INVALID;
+    int rc = check_rows(d_logits, ld, B, V);
+    if (rc != FS_OK) return rc;
+    if (B == 0) return FS_OK;
+    if (B > ST_ROWS) return FS_E_LIMIT;
+    fs::Args a = {};
+    a.logits = d_logits; a.ld = ld; a.B = B; a.V = V; a.hist = d_hist; a.hist_off = d_hist_off; a.params = d_params;
+    a.u = d_u; a.tok = d_tok; a.kcap = kcap; a.cand_ids = d_cand_ids; a.cand_probs = d_cand_probs; a.keep = d_keep;
+    a.mode = fs::MODE_SAMPLE; a.eos = -1;
+    const hipStream_t st = (hipStream_t)stream;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    rc = device_of(ctx);
+    if (rc != FS_OK) return rc;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return FS_E_HIP;
+    if (ctx->static_dev >= 0 && ctx->static_dev != dev) return FS_E_INVALID;   // a context stays on one device
+    int64_t items = 0, seg_grid = 0;
+    rc = plan(ctx->cus, a, B, items, seg_grid);
+    if (rc != FS_OK) return rc;
+    if (items > ST_SLOTS) return FS_E_LIMIT;
+    unsigned char* base = nullptr;
+    rc = static_workspace(dev, st, &base);
+    if (rc != FS_OK) return rc;
+    ctx->static_dev = dev;
+    a.err = (int32_t*)(base + ST_ERR_OFF); a.dirty = a.err + 1;
+    a.meta = (uint32_t*)(base + ST_META_OFF);
+    a.rhist = (uint32_t*)(base + ST_RHIST_OFF);
+    a.cand = (uint64_t*)(base + ST_CAND_OFF);
+    a.stream_cnt = nullptr;                          // sampling mode has no verify streams
+    a.merge_spins = ctx->merge_spins;
+    return launch_planned(a, B, seg_grid, st);
 }
 
 int fs_argmax_batch(fs_context* ctx, const float* d_logits, int64_t ld, int32_t B, int32_t V, const int32_t* d_hist,
@@ -3402,21 +3514,40 @@ int fs_hist_append(fs_context* ctx, int32_t n_streams, const int32_t* d_hist, co
 int fs_device_error(fs_context* ctx, void* stream, int32_t* bits) {
     if (!ctx || !bits) return FS_E_INVALID;
     *bits = 0;
-    if (!ctx->err) return FS_OK;
     std::lock_guard<std::mutex> g(ctx->mu);
+    if (!ctx->err && ctx->static_dev < 0) return FS_OK;
     if (hipStreamSynchronize((hipStream_t)stream) != hipSuccess) return FS_E_HIP;
-    int32_t h[2] = {0, 0};
-    if (hipMemcpy(h, ctx->err, sizeof(h), hipMemcpyDeviceToHost) != hipSuccess) return FS_E_HIP;
-    *bits = h[0];
-    if (h[1] != 0) {
-        // a merge gave up: the segments it did not wait for have finished by now (the stream is idle), so the
-        // row histograms and counters are cleared and the context leaves its compute-alone mode
-        if (ctx->rhist && hipMemset(ctx->rhist, 0, ctx->row_cap * fs::RBINS * sizeof(uint32_t)) != hipSuccess)
-            return FS_E_HIP;
-        if (ctx->stream_cnt && hipMemset(ctx->stream_cnt, 0, ctx->stream_cap * sizeof(uint32_t)) != hipSuccess)
-            return FS_E_HIP;
+    if (ctx->err) {
+        int32_t h[2] = {0, 0};
+        if (hipMemcpy(h, ctx->err, sizeof(h), hipMemcpyDeviceToHost) != hipSuccess) return FS_E_HIP;
+        *bits |= h[0];
+        if (h[1] != 0) {
+            // a merge gave up: the segments it did not wait for have finished by now (the stream is idle), so the
+            // row histograms and counters are cleared and the context leaves its compute-alone mode
+            if (ctx->rhist && hipMemset(ctx->rhist, 0, ctx->row_cap * fs::RBINS * sizeof(uint32_t)) != hipSuccess)
+                return FS_E_HIP;
+            if (ctx->stream_cnt && hipMemset(ctx->stream_cnt, 0, ctx->stream_cap * sizeof(uint32_t)) != hipSuccess)
+                return FS_E_HIP;
+        }
+        if (hipMemset(ctx->err, 0, sizeof(h)) != hipSuccess) return FS_E_HIP;
     }
-    if (hipMemset(ctx->err, 0, sizeof(h)) != hipSuccess) return FS_E_HIP;
+    if (ctx->static_dev >= 0) {
+        // the device's static workspace (fs_sample_batch_static), shared by every context on the device
+        unsigned char* base = nullptr;
+        {
+            std::lock_guard<std::mutex> gs(g_static_mu);
+            base = g_static_ptr[ctx->static_dev];
+        }
+        if (base) {
+            int32_t h[2] = {0, 0};
+            if (hipMemcpy(h, base + ST_ERR_OFF, sizeof(h), hipMemcpyDeviceToHost) != hipSuccess) return FS_E_HIP;
+            *bits |= h[0];
+            if (h[1] != 0 &&
+                hipMemset(base + ST_RHIST_OFF, 0, (size_t)ST_ROWS * fs::RBINS * sizeof(uint32_t)) != hipSuccess)
+                return FS_E_HIP;
+            if (hipMemset(base + ST_ERR_OFF, 0, sizeof(h)) != hipSuccess) return FS_E_HIP;
+        }
+    }
     return FS_OK;
 }
 
@@ -3540,6 +3671,7 @@ const char* fs_strerror(int code) {
         case FS_E_HIP: return "HIP runtime error";
         case FS_E_NOMEM: return "device allocation failed";
         case FS_E_DEVICE: return "device-side error";
+        case FS_E_LIMIT: return "batch exceeds the static workspace of fs_sample_batch_static";
         default: return "unknown error";
     }
 }

@@ -30,6 +30,7 @@ extern "C" {
 #define FS_E_HIP (-2)       /* a HIP runtime call failed */
 #define FS_E_NOMEM (-3)     /* workspace allocation failed */
 #define FS_E_DEVICE (-4)    /* a kernel reported a row it could not process (see fs_device_error) */
+#define FS_E_LIMIT (-5)     /* fs_sample_batch_static: the batch exceeds its static workspace */
 
 /* Device-side error bits (fs_device_error). */
 #define FS_DEVERR_COUNT_OVERFLOW 1   /* one token occurs > 65535 times in a penalty window */
@@ -81,6 +82,19 @@ int fs_sample_batch(fs_context* ctx, const float* d_logits, int64_t ld, int32_t 
                     const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params,
                     const double* d_u, int32_t* d_tok, int32_t kcap, int32_t* d_cand_ids, double* d_cand_probs,
                     int32_t* d_keep, void* stream);
+
+/* fs_sample_batch without any allocation. No counterpart in the reference: it is for callers that cannot allocate
+ * device memory during a call - code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * Same arguments, semantics and outputs as fs_sample_batch; ctx only carries settings (fs_set_wait_limit) and
+ * error reporting (fs_device_error reads and clears this workspace's error bits too). The workspace is one static
+ * device array per GPU (33.8 MB, held until the process ends), shared by every context on that GPU: calls that
+ * overlap in time on one GPU race (serialise them on one stream). Limits: B <= 512 rows and at most 512
+ * (row, segment) slots, i.e. 2 per compute unit on MI355X; beyond them the call returns FS_E_LIMIT and launches
+ * nothing. The first call on a device also enqueues a clear of the workspace on `stream`. */
+int fs_sample_batch_static(fs_context* ctx, const float* d_logits, int64_t ld, int32_t B, int32_t V,
+                           const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params,
+                           const double* d_u, int32_t* d_tok, int32_t kcap, int32_t* d_cand_ids, double* d_cand_probs,
+                           int32_t* d_keep, void* stream);
 
 /* Greedy batch: argmax after penalties, lowest index on ties (sampler.cpp:19-23). d_params may be NULL (no
  * penalties); otherwise only the penalty fields are read and every row is treated as greedy. */
@@ -160,7 +174,8 @@ int fs_penalize_batch(fs_context* ctx, float* d_logits, int64_t ld, int32_t B, i
                       const int64_t* d_hist_off, const fs_row_params* d_params, void* stream);
 
 /* Waits for `stream`, then returns and clears the device error bits (FS_DEVERR_*) kernels of this context set; after
- * FS_DEVERR_INTERNAL it also clears the context's workspace (row histograms and counters). */
+ * FS_DEVERR_INTERNAL it also clears the context's workspace (row histograms and counters). A context that has
+ * called fs_sample_batch_static also reports and clears the bits of its device's static workspace. */
 int fs_device_error(fs_context* ctx, void* stream, int32_t* bits);
 
 /* The merge's bounded wait for a row's segments, in polls (0 = the default, 2^20: far above any segment's time).
