@@ -1,12 +1,17 @@
 #!/usr/bin/env python3
-"""Benchmark of the gfx950 token sampler on the headline configuration:
-B=64 rows x V=262144 fp32 logits, T 0.8, top-k 64, top-p 0.95, repetition penalty 1.05 over 512-token histories.
+"""Benchmark of the gfx950 token sampler. The default workload is the headline configuration (BASELINE.json
+configs[2]): B=64 rows x V=262144 fp32 logits, T 0.8, top-k 64, top-p 0.95, repetition penalty 1.05 over 512-token
+histories. --workload cfg1..cfg5 measures each configuration of BASELINE.json (cfg4 through fs_verify), topk0 the
+headline rows with top_k = 0 (every token a candidate); --workload all prints one line per workload.
 
-A step is one fs_sample_batch call over the whole batch (penalty -> top-k -> softmax/top-p -> draw, one
-kernel) with inputs already resident in HBM. The logits rotate over enough copies (> 256 MB MALL) that every step
-streams its rows from HBM. Prints ONE JSON line with rows/s, the kernel's HBM roofline fraction (HIP events on
-the launch stream) and the CPU baseline (ferro's own sampler.cpp compiled by oracle/Makefile when present, else
-the oracle restatement) timed on this host's cores on a bounded sample of the same rows.
+A step is one fs_sample_batch (fs_verify for cfg4) call over the whole batch (penalty -> top-k -> softmax/top-p ->
+draw, one kernel) with inputs already resident in HBM. The logits rotate over enough copies (> 256 MB MALL) that
+every step streams its rows from HBM. Each line carries rows/s, the kernel's HBM roofline fraction (HIP events on
+the launch stream), the HBM traffic of the committed rocprofv3 PMC summary for that workload, and the CPU baseline
+(ferro's own sampler.cpp compiled by oracle/Makefile where it supports the workload's parameters, else the oracle
+restatement) timed on this host's cores on a bounded sample of the same rows. The CPU leg also checks the GPU's
+tokens: rows whose token differs from the reference are counted, and so are the rows whose draw lies within 1e-6 of
+a cumulative boundary (where a different summation order may legitimately pick the neighbouring token).
 """
 import argparse
 import ctypes
@@ -24,101 +29,170 @@ sys.path.insert(0, ROOT)
 METRIC = "sampled rows/s + logits HBM GB/s (% of peak), top-k/top-p, B=64, V=262144"
 HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 << 20
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "sample_kernel_cfg3_traffic.md")
+KERNEL = "fs::segment_kernel"
+
+# workload -> (constructor name in ferro_amd.workloads, entry point, description)
+WORKLOADS = {
+    "cfg1": ("config1", "sample", "cfg1_single_row: B=1 x V=65536 fp32, N(0,2) + 8 spikes, T 0.7, top-k 40, "
+                                  "top-p 0.95, repetition 1.1 over a 64-token history"),
+    "cfg2": ("config2", "sample", "cfg2_greedy_freq_pres: B=8 x V=65536 fp32, greedy, frequency 0.5 / presence 0.3 "
+                                  "over 256-token Zipf histories, 1% forced ties"),
+    "cfg3": ("config3", "sample", "cfg3_gemma_serving: B=64 x V=262144 fp32, T 0.8, top-k 64, top-p 0.95, "
+                                  "repetition 1.05 over 512-token histories"),
+    "cfg4": ("config4", "verify", "cfg4_spec_verify: 16 streams x 17 rows = 272 x V=65536 fp32, greedy, "
+                                  "per-position argmax + accepted prefix per stream (fs_verify)"),
+    "cfg5": ("config5", "sample", "cfg5_heterogeneous: B=256 x V=262144 fp32, per-row T / top-k (1..2048) / top-p / "
+                                  "repetition, frequency and presence penalties over 1024-token histories"),
+    "topk0": ("config3_all_tokens", "sample", "cfg3_all_tokens: cfg3's rows with top_k = 0 (every token a "
+                                              "candidate: the whole-row path)"),
+}
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def read_traffic():
+def read_traffic(name):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, calibrated)."""
     try:
-        txt = open(TRAFFIC_FILE).read()
+        txt = open(os.path.join(ROOT, "profiles", f"sample_kernel_{name}_traffic.md")).read()
     except OSError:
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", txt)
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(w, gpu_tok, budget_s):
-    """Rows of the same workload through ferro's CPU sampler on 1 core, repeated up to ~budget_s seconds."""
-    from oracle import oracle as O
-    kind = "reference" if O.ref_available() else "port"
-    rows_done, t_used, mism = 0, 0.0, 0
-    B = w.B
-    chunk = 8
-    b = 0
-    while t_used < budget_s:
-        sl = slice(b, b + chunk)
-        x = np.ascontiguousarray(w.logits[sl]).copy()
-        off = w.hist_off[b:b + chunk + 1] - w.hist_off[b]
-        h = w.hist[w.hist_off[b]:w.hist_off[b + chunk]]
-        t0 = time.perf_counter()
-        if kind == "reference":
-            tok = O.ref_sample_batch(x, h, off, w.params[sl], w.seeds[sl], nthreads=1, inplace=True)
-        else:
-            tok = O.sample_batch(x, h, off, w.params[sl], w.u[sl], nthreads=1)["tok"]
-        t_used += time.perf_counter() - t0
-        mism += int((tok != gpu_tok[sl]).sum())
-        rows_done += x.shape[0]
-        b = (b + chunk) % B
-    out = dict(value=rows_done / t_used, unit="rows/s", cores=1, kind=kind,
-               sample=f"{rows_done} rows of the same B={w.B} x V={w.V} workload (rows cycled), serial on 1 core "
-                      f"as ferro's server samples them ({t_used:.1f} s)",
-               token_mismatches_vs_gpu=mism)
-    if kind == "reference":
-        out["all_cores"] = cpu_all_cores(w, budget_s / 3)
-    return out
-
-
-def cpu_all_cores(w, budget_s):
-    """Upper bound for a CPU server: the whole batch's rows spread over this host's cores (rows are independent),
-    through ferro's own sampler, repeated up to ~budget_s seconds."""
-    from oracle import oracle as O
+def n_cores():
     try:
         avail = len(os.sched_getaffinity(0))
     except AttributeError:
         avail = os.cpu_count() or 1
-    nth = max(1, min(16, avail))                  # a GPU box's CPU share is 16 cores per GPU
+    return max(1, min(16, avail))                  # a GPU box's CPU share is 16 cores per GPU
+
+
+def uses_extension(w):
+    """ferro's SamplerParams has no frequency/presence penalty (sampler.h:12-21): such rows run on the port."""
+    return bool((w.params["frequency_penalty"] != 0).any() or (w.params["presence_penalty"] != 0).any())
+
+
+def verify_rows(w):
+    """cfg4 as ferro's server samples it (server.cpp:627-637): row r of stream s with the stream's history plus the
+    drafts fed before it; returns per-row CSR histories and per-row params."""
+    hs, prm = [], []
+    for s in range(len(w.row_off) - 1):
+        r0, r1 = int(w.row_off[s]), int(w.row_off[s + 1])
+        base = w.hist[w.hist_off[s]:w.hist_off[s + 1]]
+        for r in range(r1 - r0):
+            hs.append(np.concatenate([base, w.rows[r0 + 1:r0 + 1 + r]]).astype(np.int32))
+            prm.append(w.params[s])
+    off = np.zeros(len(hs) + 1, np.int64)
+    off[1:] = np.cumsum([len(h) for h in hs])
+    return np.concatenate(hs), off, np.array(prm, dtype=w.params.dtype)
+
+
+def accepted_prefix(tok, rows, row_off, eos=-1):
+    """The verification rule (server.cpp:627-637): 1 + leading rows whose token equals the next draft."""
+    acc = np.zeros(len(row_off) - 1, np.int32)
+    for s in range(len(row_off) - 1):
+        r0, m = int(row_off[s]), int(row_off[s + 1] - row_off[s])
+        a = 0
+        for r in range(m):
+            a = r + 1
+            if eos >= 0 and tok[r0 + r] == eos:
+                break
+            if r + 1 < m and tok[r0 + r] == rows[r0 + r + 1]:
+                continue
+            break
+        acc[s] = a
+    return acc
+
+
+def cpu_baseline(w, entry, gpu_tok, gpu_acc, budget_s):
+    """Rows of the same workload through ferro's CPU sampler (or the oracle port where ferro lacks a parameter) on
+    1 core, serial per row as ferro's server samples them, repeated up to ~budget_s seconds; then the whole batch
+    once more, untimed, to count the GPU's token mismatches and the rows near a cumulative boundary."""
+    from oracle import oracle as O
+    if entry == "verify":
+        hist, hoff, params = verify_rows(w)
+    else:
+        hist, hoff, params = w.hist, w.hist_off, w.params
+    kind = "reference" if O.ref_available() and not uses_extension(w) else "port"
+    B = w.B
+    chunk = min(8, B)
+    rows_done, t_used, b = 0, 0.0, 0
+    while t_used < budget_s:
+        e = min(b + chunk, B)
+        sl = slice(b, e)
+        x = np.ascontiguousarray(w.logits[sl]).copy()
+        off = hoff[b:e + 1] - hoff[b]
+        h = hist[hoff[b]:hoff[e]]
+        t0 = time.perf_counter()
+        if kind == "reference":
+            O.ref_sample_batch(x, h, off, params[sl], w.seeds[sl], nthreads=1, inplace=True)
+        else:
+            O.sample_batch(x, h, off, params[sl], w.u[sl], nthreads=1)
+        t_used += time.perf_counter() - t0
+        rows_done += e - b
+        b = e % B
+    out = dict(value=rows_done / t_used, unit="rows/s", cores=1, kind=kind,
+               sample=f"{rows_done} rows of the same B={B} x V={w.V} workload (rows cycled), serial on 1 core "
+                      f"as ferro's server samples them ({t_used:.1f} s)" +
+                      ("; ferro has no frequency/presence penalty, so the oracle port ran" if kind == "port" else ""))
+    nth = n_cores()
+    if kind == "reference":
+        ref_tok = O.ref_sample_batch(w.logits, hist, hoff, params, w.seeds, nthreads=nth)
+        out["all_cores"] = cpu_all_cores(w, hist, hoff, params, budget_s / 3, min(nth, B))
+    else:
+        ref_tok = None
+    # parity leg (untimed): the oracle's candidate probabilities locate the rows near a cumulative boundary
+    kmax = int(np.where(params["top_k"] <= 0, w.V, np.minimum(params["top_k"], w.V)).max())
+    ora = O.sample_batch(w.logits, hist, hoff, params, w.u, kcap=min(kmax, w.V), nthreads=nth)
+    ref_tok = ora["tok"] if ref_tok is None else ref_tok
+    diff = np.nonzero(gpu_tok != ref_tok)[0]
+    near = []
+    for r in range(B):
+        p = params[r]
+        if p["temperature"] <= 0 or p["top_k"] == 1:
+            continue
+        nc = int(ora["ncand"][r])
+        if O.near_boundary(ora["cand_probs"][r, :nc], int(ora["keep"][r]), float(w.u[r]), float(p["top_p"]),
+                           float(p["min_p"])):
+            near.append(r)
+    out["parity"] = dict(rows=B, token_mismatches_vs_cpu=int(len(diff)), rows_near_boundary=len(near),
+                         mismatches_near_boundary=int(np.isin(diff, near).sum()),
+                         oracle_vs_reference_mismatches=int((ora["tok"] != ref_tok).sum()) if kind == "reference"
+                         else None)
+    if entry == "verify":
+        out["parity"]["accepted_mismatches_vs_cpu"] = int(
+            (accepted_prefix(ref_tok, w.rows, w.row_off) != gpu_acc).sum())
+    return out
+
+
+def cpu_all_cores(w, hist, hoff, params, budget_s, nth):
+    """Upper bound for a CPU server: the whole batch's rows spread over this host's cores (rows are independent),
+    through ferro's own sampler, repeated up to ~budget_s seconds."""
+    from oracle import oracle as O
     rows_done, t_used = 0, 0.0
     while t_used < budget_s:
         x = np.ascontiguousarray(w.logits).copy()
         t0 = time.perf_counter()
-        O.ref_sample_batch(x, w.hist, w.hist_off, w.params, w.seeds, nthreads=nth, inplace=True)
+        O.ref_sample_batch(x, hist, hoff, params, w.seeds, nthreads=nth, inplace=True)
         t_used += time.perf_counter() - t0
         rows_done += w.B
     return dict(value=rows_done / t_used, unit="rows/s", cores=nth,
                 sample=f"{rows_done} rows (the B={w.B} batch repeated), rows spread over {nth} threads ({t_used:.1f} s)")
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=["cfg3", "cfg5"], default="cfg3",
-                    help="cfg3 (default): the headline; cfg5: the heterogeneous B=256 batch, for profiling")
-    ap.add_argument("--copy-calib", action="store_true",
-                    help="after the timed steps, run plain 256 MiB device copies (counter calibration for rocprofv3)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU: the sampler path is built and measured on a single MI355X "
-              f"(--gpus {args.gpus} is not supported in this build)", file=sys.stderr)
-        sys.exit(2)
-
-    import torch
+def run_workload(name, args, torch):
     from ferro_amd import workloads as W
     from ferro_amd import _lib
     from ferro_amd.sampler import Context
 
+    ctor, entry, desc = WORKLOADS[name]
     t0 = time.time()
-    w = W.config3() if args.workload == "cfg3" else W.config5()
+    w = getattr(W, ctor)()
     log(f"workload {w.name}: B={w.B} V={w.V} generated in {time.time() - t0:.1f}s")
     dev = torch.device("cuda", 0)
-    torch.cuda.set_device(dev)
     nrot = max(2, -(-2 * MALL_BYTES // w.logits.nbytes))
     base = torch.from_numpy(w.logits).to(dev)
     bufs = [base] + [base.clone() for _ in range(nrot - 1)]
@@ -133,18 +207,28 @@ def main():
     stream = torch.cuda.current_stream()
     sh = ctypes.c_void_p(stream.cuda_stream)
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
-    fixed = (w.B, w.V, P(hist), P(hoff), P(params), P(u), P(tok), 0, None, None, P(keep), sh)
+    if entry == "verify":
+        rows = torch.from_numpy(w.rows).to(dev)
+        roff = torch.from_numpy(w.row_off).to(dev)
+        S = len(w.row_off) - 1
+        acc = torch.empty(S, dtype=torch.int32, device=dev)
+        fixed = (S, w.B, w.V, P(rows), P(roff), P(hist), P(hoff), P(params), P(u), -1, P(tok), P(acc), sh)
+        call, what = L.fs_verify, "fs_verify"
+    else:
+        acc = None
+        fixed = (w.B, w.V, P(hist), P(hoff), P(params), P(u), P(tok), 0, None, None, P(keep), sh)
+        call, what = L.fs_sample_batch, "fs_sample_batch"
 
     def step(i):
-        x = bufs[i % nrot]
-        rc = L.fs_sample_batch(ctx.h, P(x), w.V, *fixed)
+        rc = call(ctx.h, P(bufs[i % nrot]), w.V, *fixed)
         if rc != 0:
-            raise RuntimeError(f"fs_sample_batch returned {rc}")
+            raise RuntimeError(f"{what} returned {rc}")
 
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
     gpu_tok = tok.cpu().numpy().copy()
+    gpu_acc = acc.cpu().numpy().copy() if acc is not None else None
 
     K = args.steps
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
@@ -155,15 +239,15 @@ def main():
         step(i)
         ev[i][1].record(stream)
     torch.cuda.synchronize()
-    t_end = time.perf_counter()
-    wall = t_end - t_start
+    wall = time.perf_counter() - t_start
     kern_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
     if not np.array_equal(tok.cpu().numpy(), gpu_tok):
         raise RuntimeError("tokens changed between steps on identical inputs")
+    if F_device_error(L, ctx, sh) != 0:
+        raise RuntimeError("device error bits set after the timed steps")
 
     alg_bytes = w.algorithmic_bytes()
     achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
-    traffic = read_traffic()
     out = {
         "metric": METRIC,
         "value": w.B * K / wall,
@@ -176,17 +260,15 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded: 90% N(0,1.5) + 10% 4*Student-t(3) logits, Zipf(1.1) histories)",
-        "config": {"workload": ("cfg3_gemma_serving: B=64 x V=262144 fp32, T 0.8, top-k 64, top-p 0.95, "
-                                "repetition 1.05 over 512-token histories") if args.workload == "cfg3" else
-                               ("cfg5_heterogeneous: B=256 x V=262144 fp32, per-row T / top-k (1..2048) / top-p / "
-                                "repetition, frequency and presence penalties over 1024-token histories"),
-                   "B": w.B, "V": w.V,
-                   "logit_copies_rotated": nrot},
+        "data": "synthetic (seeded; BASELINE.json's logit, history and parameter distributions for this config)",
+        "config": {"workload": desc, "B": w.B, "V": w.V, "entry_point": what, "logit_copies_rotated": nrot},
+        "value_note": ("rows/s over the wall clock of K back-to-back calls from Python (ctypes launch included); "
+                       "roofline.kernel_ms is the HIP-event time of one call on its stream"),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "fs_sample_batch: fs::segment_kernel (segments, then a merging workgroup per row)", "kernel_ms": kern_ms,
-                     "algorithmic_bytes": alg_bytes},
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(name),
+                     "kernel": f"{what}: {KERNEL} (segments, then a merging workgroup per row, one grid)",
+                     "kernel_ms": kern_ms, "algorithmic_bytes": alg_bytes,
+                     "algorithmic_bytes_note": "4*V per row (one read of the fp32 row) + 4 per history id"},
     }
     if args.copy_calib:
         src = torch.empty(64 << 20, dtype=torch.float32, device=dev)   # 256 MiB
@@ -196,8 +278,41 @@ def main():
         torch.cuda.synchronize()
         log("copy calibration: 5 copies of 268435456 bytes")
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(w, gpu_tok, args.cpu_seconds)
-    print(json.dumps(out), flush=True)
+        out["cpu_baseline"] = cpu_baseline(w, entry, gpu_tok, gpu_acc, args.cpu_seconds)
+    del bufs
+    torch.cuda.empty_cache()
+    return out
+
+
+def F_device_error(L, ctx, sh):
+    bits = ctypes.c_int32(0)
+    rc = L.fs_device_error(ctx.h, sh, ctypes.byref(bits))
+    return bits.value if rc == 0 else -1
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=list(WORKLOADS) + ["all"], default="cfg3",
+                    help="cfg3 (default): the headline; cfg1..cfg5: BASELINE.json's configurations; topk0: cfg3 with "
+                         "top_k = 0; all: one line per workload")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="after the timed steps, run plain 256 MiB device copies (counter calibration for rocprofv3)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the sampler path is built and measured on a single MI355X "
+              f"(--gpus {args.gpus} is not supported in this build)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    torch.cuda.set_device(torch.device("cuda", 0))
+    names = list(WORKLOADS) if args.workload == "all" else [args.workload]
+    for name in names:
+        print(json.dumps(run_workload(name, args, torch)), flush=True)
 
 
 if __name__ == "__main__":

@@ -196,3 +196,12 @@ def config5(seed: int = 5, B: int = 256, V: int = 262144, H: int = 1024) -> Work
 
 
 CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}
+
+
+def config3_all_tokens(seed: int = 3, B: int = 64, V: int = 262144) -> Workload:
+    """cfg3's rows and parameters with top_k = 0: every token is a candidate (ferro's k = n, sampler.h:14,
+    sampler.cpp:26-27), the whole-row path."""
+    w = config3(seed, B, V)
+    w.params["top_k"] = 0
+    w.name = "cfg3_all_tokens"
+    return w

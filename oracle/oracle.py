@@ -244,3 +244,24 @@ def ref_sample_batch(logits, hist, hist_off, params, seeds, nthreads=1, inplace=
                        _ptr(np.ascontiguousarray(params, PARAMS_DTYPE)),
                        _ptr(np.ascontiguousarray(seeds, np.uint64)), _ptr(tok), nthreads)
     return tok
+
+
+# ---------------------------------------------------------------------------------------------- parity bar
+BOUNDARY = 1e-6
+
+
+def near_boundary(probs, keep, u, top_p, min_p):
+    """True if a sequential-vs-parallel summation difference could flip keep or the drawn index of a row: the
+    oracle's candidate probabilities `probs` (candidate order), its kept count, the draw u, top_p and min_p put
+    u*tot, top_p or the min-p threshold within 1e-6 (relative) of a cumulative boundary (sampler.cpp:43-49)."""
+    c = np.cumsum(probs)
+    if len(c) == 0:
+        return False
+    if top_p < 1.0 and np.any(np.abs(c - np.float64(np.float32(top_p))) <= BOUNDARY):
+        return True
+    if min_p > 0.0:
+        thr = probs[0] * np.float64(np.float32(min_p))
+        if np.any(np.abs(probs - thr) <= BOUNDARY * max(thr, 1e-300)):
+            return True
+    tot = c[max(keep, 1) - 1]
+    return bool(np.any(np.abs(u * tot - c[:max(keep, 1)]) <= BOUNDARY))

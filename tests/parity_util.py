@@ -9,22 +9,10 @@ import numpy as np
 from oracle import oracle as O
 
 PROB_RTOL = 1e-5
-BOUNDARY = 1e-6
+BOUNDARY = O.BOUNDARY
 
 
-def boundary_row(probs, keep, u, top_p, min_p):
-    """True if a sequential-vs-parallel summation difference could flip keep or the drawn index of this row."""
-    c = np.cumsum(probs)
-    if len(c) == 0:
-        return False
-    if top_p < 1.0 and np.any(np.abs(c - np.float64(np.float32(top_p))) <= BOUNDARY):
-        return True
-    if min_p > 0.0:
-        thr = probs[0] * np.float64(np.float32(min_p))
-        if np.any(np.abs(probs - thr) <= BOUNDARY * max(thr, 1e-300)):
-            return True
-    tot = c[max(keep, 1) - 1]
-    return bool(np.any(np.abs(u * tot - c[:max(keep, 1)]) <= BOUNDARY))
+boundary_row = O.near_boundary
 
 
 class Parity(int):
