@@ -284,6 +284,68 @@ def run_workload(name, args, torch):
     return out
 
 
+# Stage breakdown by ablation: the same rows and call, with stages switched off one at a time (parameter overrides
+# applied to every row). Differences between the lines price the penalty pass, the top-k select and the
+# softmax / top-p / draw; the greedy line with no penalty is the streaming read plus an argmax.
+BREAKDOWN = [
+    ("full", {}),
+    ("no penalty", {"repetition_penalty": 1.0, "frequency_penalty": 0.0, "presence_penalty": 0.0}),
+    ("no top-p (softmax + draw over k)", {"top_p": 1.0}),
+    ("no penalty, no top-p", {"repetition_penalty": 1.0, "frequency_penalty": 0.0, "presence_penalty": 0.0,
+                              "top_p": 1.0}),
+    ("greedy (argmax) with penalty", {"temperature": 0.0}),
+    ("greedy (argmax), no penalty: stream + argmax", {"temperature": 0.0, "repetition_penalty": 1.0,
+                                                      "frequency_penalty": 0.0, "presence_penalty": 0.0}),
+]
+
+
+def run_breakdown(name, args, torch):
+    """One JSON line: the HIP-event time per call of each ablation variant of the workload."""
+    from ferro_amd import workloads as W
+    from ferro_amd import _lib
+    from ferro_amd.sampler import Context
+
+    ctor, entry, desc = WORKLOADS[name]
+    if entry != "sample":
+        raise SystemExit("--breakdown applies to fs_sample_batch workloads")
+    w = getattr(W, ctor)()
+    dev = torch.device("cuda", 0)
+    nrot = max(2, -(-2 * MALL_BYTES // w.logits.nbytes))
+    base = torch.from_numpy(w.logits).to(dev)
+    bufs = [base] + [base.clone() for _ in range(nrot - 1)]
+    hist = torch.from_numpy(w.hist).to(dev)
+    hoff = torch.from_numpy(w.hist_off).to(dev)
+    u = torch.from_numpy(w.u).to(dev)
+    tok = torch.empty(w.B, dtype=torch.int32, device=dev)
+    ctx = Context.default(dev)
+    L = _lib.lib()
+    stream = torch.cuda.current_stream()
+    sh = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    out = []
+    for label, over in BREAKDOWN:
+        prm = w.params.copy()
+        for f, v in over.items():
+            prm[f] = v
+        params = torch.from_numpy(prm.view(np.uint8).copy()).to(dev)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        for i in range(args.warmup + args.steps):
+            if i >= args.warmup:
+                ev[i - args.warmup][0].record(stream)
+            rc = L.fs_sample_batch(ctx.h, P(bufs[i % nrot]), w.V, w.B, w.V, P(hist), P(hoff), P(params), P(u), P(tok),
+                                   0, None, None, None, sh)
+            if rc != 0:
+                raise RuntimeError(f"fs_sample_batch returned {rc}")
+            if i >= args.warmup:
+                ev[i - args.warmup][1].record(stream)
+        torch.cuda.synchronize()
+        ms = float(np.median([a.elapsed_time(b) for a, b in ev]))
+        out.append({"variant": label, "us_per_call": ms * 1e3,
+                    "GB_per_s": w.algorithmic_bytes() / (ms * 1e-3) / 1e9})
+    return {"breakdown": desc, "B": w.B, "V": w.V, "steps": args.steps, "timing": "median HIP-event time per call",
+            "variants": out}
+
+
 def F_device_error(L, ctx, sh):
     bits = ctypes.c_int32(0)
     rc = L.fs_device_error(ctx.h, sh, ctypes.byref(bits))
@@ -300,6 +362,8 @@ def main():
     ap.add_argument("--workload", choices=list(WORKLOADS) + ["all"], default="cfg3",
                     help="cfg3 (default): the headline; cfg1..cfg5: BASELINE.json's configurations; topk0: cfg3 with "
                          "top_k = 0; all: one line per workload")
+    ap.add_argument("--breakdown", action="store_true",
+                    help="instead of the bench line: per-stage ablation timings of the workload (one JSON line)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="after the timed steps, run plain 256 MiB device copies (counter calibration for rocprofv3)")
     args = ap.parse_args()
@@ -312,7 +376,11 @@ def main():
     torch.cuda.set_device(torch.device("cuda", 0))
     names = list(WORKLOADS) if args.workload == "all" else [args.workload]
     for name in names:
-        print(json.dumps(run_workload(name, args, torch)), flush=True)
+        if args.breakdown:
+            if WORKLOADS[name][1] == "sample":
+                print(json.dumps(run_breakdown(name, args, torch)), flush=True)
+        else:
+            print(json.dumps(run_workload(name, args, torch)), flush=True)
 
 
 if __name__ == "__main__":

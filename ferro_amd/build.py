@@ -9,6 +9,8 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 SRC = os.path.join(PKG, "csrc", "sampler_kernels.hip")
 LIB = os.path.join(PKG, "libferro_sampler.so")
+# the same source with phase timestamps compiled in (-DFS_TRACE, fs_trace_set): read by ferro_amd/trace_phases.py
+TRACE_LIB = os.path.join(PKG, "libferro_sampler_trace.so")
 # C++ drop-in test driver (tests/cpp): host code over include/ferro_sampler.hpp, linked against LIB
 SHIM_SRC = os.path.join(ROOT, "tests", "cpp", "shim_replay.cpp")
 SHIM_BIN = os.path.join(ROOT, "tests", "cpp", "shim_replay")
@@ -39,8 +41,20 @@ def _run(cmd, what, verbose):
         raise RuntimeError(f"{cmd[0]} failed ({r.returncode}) building {what}")
 
 
-def build(verbose: bool = False) -> str:
-    _run([HIPCC, *FLAGS, "-o", LIB, SRC], LIB, verbose)
+def build(verbose: bool = False, trace: bool = True) -> str:
+    jobs = [([HIPCC, *FLAGS, "-o", LIB, SRC], LIB)]
+    if trace:
+        jobs.append(([HIPCC, *FLAGS, "-DFS_TRACE", "-o", TRACE_LIB, SRC], TRACE_LIB))
+    procs = []
+    for cmd, what in jobs:                         # the two libraries compile side by side
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True), cmd, what))
+    for p, cmd, what in procs:
+        out, _ = p.communicate()
+        if p.returncode != 0:
+            sys.stderr.write(out)
+            raise RuntimeError(f"{cmd[0]} failed ({p.returncode}) building {what}")
     if os.path.exists(SHIM_SRC):
         _run(["g++", "-O2", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROOT, "include"),
               "-I" + os.path.join(ROCM, "include"), SHIM_SRC, "-o", SHIM_BIN, "-L" + PKG, "-lferro_sampler",

@@ -97,7 +97,33 @@ struct Args {
     int32_t* err;                  // device error bits
     int32_t* dirty;                // nonzero: a merge gave up waiting; the row histograms and counters may be stale
     uint32_t merge_spins;          // bounded wait of the merge role (polls)
+    uint64_t* trace;               // FS_TRACE builds: per-workgroup phase timestamps (NULL: none)
 };
+
+// Phase timestamps (FS_TRACE builds only; the product library compiles these to nothing): thread 0 of a workgroup
+// keeps the constant 100 MHz clock (s_memrealtime) of phase i in LDS (no memory store, so no wait on the memory
+// counter in the middle of the kernel) and writes them to trace[blockIdx * TRACE_W + i] at its end; slots 5-7 hold
+// the role (1 segment, 2 merge), the row and the segment.
+constexpr int TRACE_W = 8;
+#ifdef FS_TRACE
+#define FS_MARK(i)                                                                                        \
+    do {                                                                                                  \
+        if (threadIdx.x == 0) s.trace_t[(i)] = __builtin_amdgcn_s_memrealtime();                          \
+    } while (0)
+#define FS_TAG(i, v)                                                                                      \
+    do {                                                                                                  \
+        if (threadIdx.x == 0) s.trace_t[(i)] = (uint64_t)(v);                                            \
+    } while (0)
+#define FS_FLUSH()                                                                                        \
+    do {                                                                                                  \
+        if (threadIdx.x == 0 && a.trace)                                                                  \
+            for (int i_ = 0; i_ < TRACE_W; ++i_) a.trace[(int64_t)blockIdx.x * TRACE_W + i_] = s.trace_t[i_]; \
+    } while (0)
+#else
+#define FS_MARK(i) do {} while (0)
+#define FS_TAG(i, v) do {} while (0)
+#define FS_FLUSH() do {} while (0)
+#endif
 
 // ------------------------------------------------------------------------------------------------ keys
 // Order-preserving map fp32 -> u32: larger float -> larger key; -0 and +0 share a key (sampler.cpp:30 compares
@@ -579,6 +605,9 @@ struct Shared {
     uint32_t rc64[WAVE];               // segment kernel: tile-0 counts in the 64 coarse bins up to tmax's
     uint32_t nids;
     uint32_t misc_alone;               // merge role: the row is computed from its logits alone
+#ifdef FS_TRACE
+    uint64_t trace_t[8];               // this workgroup's phase timestamps (written to a.trace at its end)
+#endif
     Red red;
     __device__ __forceinline__ uint32_t* cnt() { return scr; }
     __device__ __forceinline__ uint32_t* bins() { return scr + TILE / 2; }
@@ -1805,6 +1834,7 @@ __device__ __forceinline__ bool merge_fast(const Args& a, const RowCtx& rc, Shar
         }
     }
     __syncthreads();
+    FS_MARK(2);
     const int n = (int)s.count;
     if (n < k || n > FRANK) {                                    // uniform
         __syncthreads();
@@ -1836,6 +1866,7 @@ __device__ __forceinline__ bool merge_fast(const Args& a, const RowCtx& rc, Shar
         if (r < (uint32_t)k) sorted[r] = s.cand[tid];
     }
     __syncthreads();
+    FS_MARK(3);
     if (tid < WAVE) wave_softmax(a, rc, tid < k ? sorted[tid] : 0ull, k, pre.u, tok, keep);
     return true;
 }
@@ -2597,6 +2628,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 for (int j = 0; j < NV; ++j)
                     st[j * BLOCK + tid] = make_float4(buf[0][4 * j], buf[0][4 * j + 1], buf[0][4 * j + 2], buf[0][4 * j + 3]);
                 load_seg_tile(buf[0], g.rs, PF);
+                if (!safe) FS_MARK(1);
 #pragma unroll
                 for (int j = 0; j < NV; ++j) {
                     const float4 v = st[j * BLOCK + tid];
@@ -2679,6 +2711,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
             } else if (slowpen) {
                 __syncthreads();                         // penalty-table reads of this tile are done
             }
+            if (!safe) FS_MARK(2);
         }
         // ---- tiles 1.. (PF in flight; tile t is in buf[t % 2]). Iterations start at odd tiles, so the order in
         // which the two buffers were requested is the same on entry and around the back edge.
@@ -2768,6 +2801,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         __syncthreads();
     }
     if (topk && spending) row_take(sb0, scnt);
+    FS_MARK(3);
 
     // ---- publish this segment's candidates (read by the merge kernel after this kernel completes)
     const int nseg = a.nseg;
@@ -2863,6 +2897,7 @@ constexpr uint32_t MERGE_SPINS = 1u << 20;   // bounded wait of the merge role (
 __device__ __forceinline__ void merge_role(const Args& a, int mi, Shared& s) {
     const int row = mi % XCDS + XCDS * (mi / XCDS);
     if (row >= a.B) return;
+    FS_TAG(5, 2); FS_TAG(6, row); FS_TAG(7, 0);
     const RowCtx rc = row_ctx(a, row);               // the row's inputs are read while the segments run
     uint32_t* ctr = row_counter(a, row);
     if (threadIdx.x == 0) {
@@ -2885,6 +2920,7 @@ __device__ __forceinline__ void merge_role(const Args& a, int mi, Shared& s) {
         }
         s.misc_alone = alone;
     }
+    FS_MARK(1);
     __syncthreads();
     if (s.misc_alone) {
         Pre none = {};
@@ -2913,8 +2949,12 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, 
     // x = i % XCDS takes the rows x, x + XCDS, ..., all segments of a row in consecutive rounds, so a row's segments
     // share one XCD and its L2 (the row histogram). Slots past the last row return at once.
     const unsigned seg_grid = (unsigned)(XCDS * a.nseg * ((a.B + XCDS - 1) / XCDS));
+    FS_MARK(0);
+    FS_TAG(1, 0); FS_TAG(2, 0); FS_TAG(3, 0); FS_TAG(5, 0);
     if (blockIdx.x >= seg_grid) {
         merge_role(a, (int)(blockIdx.x - seg_grid), s);
+        FS_MARK(4);
+        FS_FLUSH();
         return;
     }
     const int x = (int)(blockIdx.x % (unsigned)XCDS);
@@ -2923,6 +2963,7 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, 
     const int seg = j - q * a.nseg;
     const int row = x + XCDS * q;
     if (row >= a.B) return;
+    FS_TAG(5, 1); FS_TAG(6, row); FS_TAG(7, seg);
     float buf[PF][TPT];
     const SegStart g = seg_start(a, row, seg, buf);   // the tiles are on their way before the parameters
     const RowCtx rc = row_ctx(a, row);
@@ -2931,6 +2972,8 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, 
     vm_drain();                                      // the list and meta stores are in the L2
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_fetch_add(row_counter(a, row), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    FS_MARK(4);
+    FS_FLUSH();
 }
 
 // Merge kernel: one workgroup per row, after the segment kernel. The segment lists are requested first, so their
@@ -3202,6 +3245,8 @@ struct fs_context {
     int32_t* err = nullptr;        // [0]: error bits; [1]: dirty (a merge gave up; see fs_device_error)
     uint32_t merge_spins = fs::MERGE_SPINS;
     int static_dev = -1;       // device whose static workspace fs_sample_batch_static used with this context
+    uint64_t* trace = nullptr; // FS_TRACE builds: phase timestamps, trace_cap entries (fs_trace_set)
+    int64_t trace_cap = 0;
 };
 
 namespace {
@@ -3295,6 +3340,13 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
     if (rc != FS_OK) return rc;
     a.cand = ctx->cand; a.meta = ctx->meta; a.rhist = ctx->rhist;
     a.stream_cnt = ctx->stream_cnt; a.err = ctx->err; a.dirty = ctx->err + 1; a.merge_spins = ctx->merge_spins;
+    a.trace = nullptr;
+#ifdef FS_TRACE
+    {
+        const int64_t grid = seg_grid > 0 ? seg_grid + (int64_t)fs::XCDS * ((rows + fs::XCDS - 1) / fs::XCDS) : rows;
+        if (ctx->trace && grid * fs::TRACE_W <= ctx->trace_cap) a.trace = ctx->trace;   // else: untraced
+    }
+#endif
     return launch_planned(a, rows, seg_grid, st);
 }
 
@@ -3663,6 +3715,18 @@ int fs_drng_error(fs_drng* r, void* stream, int32_t* bits) {
     if (hipMemset(r->err, 0, sizeof(int32_t)) != hipSuccess) return FS_E_HIP;
     return FS_OK;
 }
+
+#ifdef FS_TRACE
+// Trace builds only (not in the product library): phase timestamps of the next sampling grids into d_buf (cap
+// entries, TRACE_W per workgroup); a grid larger than the buffer runs untraced.
+int fs_trace_set(fs_context* ctx, uint64_t* d_buf, int64_t cap) {
+    if (!ctx || cap < 0) return FS_E_INVALID;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    ctx->trace = d_buf;
+    ctx->trace_cap = d_buf ? cap : 0;
+    return FS_OK;
+}
+#endif
 
 const char* fs_strerror(int code) {
     switch (code) {

@@ -1,0 +1,178 @@
+#!/usr/bin/env python3
+"""Per-phase timeline of one sampling call, from the trace build of the library.
+
+libferro_sampler_trace.so is the same source compiled with -DFS_TRACE (ferro_amd/build.py builds it beside the
+product library): thread 0 of every workgroup stores the GPU's constant 100 MHz clock at its phase boundaries.
+Segment workgroups (one per (row, segment) item): 0 start, 1 tile 0 arrived, 2 tile 0 done (penalty, first bound,
+appends, check), 3 last tile done, 4 list published and counted. Merging workgroups (one per row): 0 start, 1 the
+row's segments seen done, 2 candidates gathered (short merge), 3 candidates ranked (short merge), 4 row finished.
+
+Usage (on a GPU):  python ferro_amd/trace_phases.py --workload cfg3 [--calls 5]
+Prints a markdown table: when each phase happens (µs from the first workgroup's start; min / median / max over the
+workgroups, median over the traced calls) and how long it takes per workgroup.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import os
+import sys
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+TRACE_LIB = os.path.join(PKG, "libferro_sampler_trace.so")
+TRACE_W = 8
+TICK_US = 0.01                                    # s_memrealtime: 100 MHz
+
+
+def load():
+    from ferro_amd._lib import SIGNATURES
+    if not os.path.exists(TRACE_LIB):
+        raise RuntimeError(f"{TRACE_LIB} is missing: build it with `python ferro_amd/build.py`")
+    L = ctypes.CDLL(TRACE_LIB)
+    for name, (res, args) in SIGNATURES.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    L.fs_trace_set.restype = ctypes.c_int
+    L.fs_trace_set.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+    return L
+
+
+def one_call(L, ctx, w, entry, bufs, dev_in, trace, i, torch):
+    P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    x = bufs[i % len(bufs)]
+    if entry == "verify":
+        rc = L.fs_verify(ctx, P(x), w.V, len(w.row_off) - 1, w.B, w.V, P(dev_in["rows"]), P(dev_in["roff"]),
+                         P(dev_in["hist"]), P(dev_in["hoff"]), P(dev_in["params"]), P(dev_in["u"]), -1,
+                         P(dev_in["tok"]), P(dev_in["acc"]), st)
+    else:
+        rc = L.fs_sample_batch(ctx, P(x), w.V, w.B, w.V, P(dev_in["hist"]), P(dev_in["hoff"]), P(dev_in["params"]),
+                               P(dev_in["u"]), P(dev_in["tok"]), 0, None, None, P(dev_in["keep"]), st)
+    if rc != 0:
+        raise RuntimeError(f"call returned {rc}")
+
+
+def phases(tr):
+    """tr: [grid, TRACE_W] uint64 of one call -> dict of per-workgroup arrays (µs from the first start)."""
+    role = tr[:, 5]
+    t0 = tr[role > 0, 0].min()
+    rel = (tr[:, :5].astype(np.int64) - np.int64(t0)) * TICK_US
+    seg, mer = role == 1, role == 2
+    out = {"seg": rel[seg], "seg_row": tr[seg, 6], "mer": rel[mer], "mer_row": tr[mer, 6],
+           "mer_set": tr[mer, :5] != 0}
+    return out
+
+
+def summarize(calls, seg_tiles):
+    def stat(vals):
+        v = np.asarray(vals, float)
+        return (np.min(v), np.median(v), np.max(v)) if v.size else (np.nan,) * 3
+
+    rows = []
+
+    def add(name, per_call, per_wg):
+        """per_call: list over calls of arrays (times); per_wg: list over calls of arrays (durations)."""
+        t = np.median(np.array([stat(c) for c in per_call]), axis=0) if per_call else (np.nan,) * 3
+        d = np.median([np.median(c) for c in per_wg]) if per_wg and all(len(c) for c in per_wg) else np.nan
+        rows.append((name, *t, d))
+
+    S = [c["seg"] for c in calls]
+    M = [c["mer"] for c in calls]
+    add("segment start", [s[:, 0] for s in S], [])
+    add("segment: tile 0 arrived", [s[:, 1] for s in S], [s[:, 1] - s[:, 0] for s in S])
+    add("segment: tile 0 done (penalty, bound, appends)", [s[:, 2] for s in S], [s[:, 2] - s[:, 1] for s in S])
+    add(f"segment: last tile done ({seg_tiles - 1} more tiles)", [s[:, 3] for s in S],
+        [(s[:, 3] - s[:, 2]) / max(seg_tiles - 1, 1) for s in S])
+    add("segment: list published, counted done", [s[:, 4] for s in S], [s[:, 4] - s[:, 3] for s in S])
+    add("merge start", [m[:, 0] for m in M], [])
+    waits = []
+    for c in calls:
+        last = {}
+        for r, t in zip(c["seg_row"], c["seg"][:, 4]):
+            last[int(r)] = max(last.get(int(r), -1e9), t)
+        waits.append(np.array([m[1] - last.get(int(r), m[1]) for r, m in zip(c["mer_row"], c["mer"])]))
+    add("merge: row's segments seen done", [m[:, 1] for m in M], waits)
+    fast = [c["mer_set"][:, 2] & c["mer_set"][:, 3] for c in calls]
+    add("merge: candidates gathered (short merge)", [m[f, 2] for m, f in zip(M, fast)],
+        [m[f, 2] - m[f, 1] for m, f in zip(M, fast)])
+    add("merge: candidates ranked (short merge)", [m[f, 3] for m, f in zip(M, fast)],
+        [m[f, 3] - m[f, 2] for m, f in zip(M, fast)])
+    add("merge: row finished (softmax, top-p, draw, outputs)", [m[:, 4] for m in M],
+        [m[f, 4] - m[f, 3] for m, f in zip(M, fast)])
+    span = np.median([max(c["seg"][:, 4].max(), c["mer"][:, 4].max()) for c in calls])
+    return rows, span
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--workload", default="cfg3")
+    ap.add_argument("--calls", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=20)
+    args = ap.parse_args()
+
+    import torch
+    import bench
+    from ferro_amd import workloads as W
+
+    ctor, entry, desc = bench.WORKLOADS[args.workload]
+    w = getattr(W, ctor)()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    L = load()
+    ctx = ctypes.c_void_p()
+    if L.fs_create(ctypes.byref(ctx)) != 0:
+        raise RuntimeError("fs_create failed")
+    nrot = max(2, -(-2 * bench.MALL_BYTES // w.logits.nbytes))
+    base = torch.from_numpy(w.logits).to(dev)
+    bufs = [base] + [base.clone() for _ in range(nrot - 1)]
+    dev_in = dict(params=torch.from_numpy(w.params.view(np.uint8).copy()).to(dev),
+                  hist=torch.from_numpy(w.hist).to(dev), hoff=torch.from_numpy(w.hist_off).to(dev),
+                  u=torch.from_numpy(w.u).to(dev), tok=torch.empty(w.B, dtype=torch.int32, device=dev),
+                  keep=torch.empty(w.B, dtype=torch.int32, device=dev))
+    if entry == "verify":
+        dev_in.update(rows=torch.from_numpy(w.rows).to(dev), roff=torch.from_numpy(w.row_off).to(dev),
+                      acc=torch.empty(len(w.row_off) - 1, dtype=torch.int32, device=dev))
+    cap = 1 << 20
+    trace = torch.zeros(cap, dtype=torch.int64, device=dev)
+    for i in range(args.warmup):
+        one_call(L, ctx, w, entry, bufs, dev_in, trace, i, torch)
+    calls = []
+    for c in range(args.calls):
+        trace.zero_()
+        torch.cuda.synchronize()
+        if L.fs_trace_set(ctx, ctypes.c_void_p(trace.data_ptr()), cap) != 0:
+            raise RuntimeError("fs_trace_set failed")
+        one_call(L, ctx, w, entry, bufs, dev_in, trace, args.warmup + c, torch)
+        torch.cuda.synchronize()
+        L.fs_trace_set(ctx, None, 0)
+        tr = trace.cpu().numpy().view(np.uint64).reshape(-1, TRACE_W)
+        used = tr[:, 5] > 0
+        n = int(np.nonzero(used)[0].max()) + 1 if used.any() else 0
+        if n == 0:
+            raise RuntimeError("nothing traced (grid larger than the trace buffer?)")
+        calls.append(phases(tr[:n]))
+        one_call(L, ctx, w, entry, bufs, dev_in, trace, args.warmup + c + 1, torch)   # untraced spacer
+    tiles_row = w.V // 4096
+    segs = int(np.median([len(c["seg"]) for c in calls]) / max(w.B, 1))
+    seg_tiles = -(-tiles_row // max(segs, 1))
+    rows, span = summarize(calls, seg_tiles)
+    print(f"Phase timeline of one call, {desc} ({len(calls[0]['seg'])} segment workgroups of {seg_tiles} tiles, "
+          f"{len(calls[0]['mer'])} merging workgroups); µs from the first workgroup's start, median over "
+          f"{args.calls} traced calls:\n")
+    print("| phase | first | median | last | per workgroup (median) |")
+    print("|---|---|---|---|---|")
+    for name, lo, med, hi, d in rows:
+        f = lambda v: "" if np.isnan(v) else f"{v:.2f}"  # noqa: E731
+        print(f"| {name} | {f(lo)} | {f(med)} | {f(hi)} | {f(d)} |")
+    print(f"\nFirst workgroup start to last workgroup end: {span:.2f} µs")
+
+
+if __name__ == "__main__":
+    main()
