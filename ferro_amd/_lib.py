@@ -42,6 +42,7 @@ SIGNATURES = {
     "fs_argmax_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P]),
     "fs_verify": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P]),
     "fs_penalize_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P]),
+    "fs_softcap_batch": (ctypes.c_int, [_P, _P, _I64, ctypes.c_float, _P]),
     "fs_device_error": (ctypes.c_int, [_P, _P, _P]),
     "fs_set_wait_limit": (ctypes.c_int, [_P, ctypes.c_uint32]),
     "fs_rng_create": (ctypes.c_int, [ctypes.c_uint64, _P]),

@@ -800,12 +800,108 @@ __device__ __forceinline__ void load_seg_tile(float (&x)[TPT], __amdgpu_buffer_r
         x[4 * j + 0] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
     }
 }
+// tanhf as the host C library computes it where ferro runs (glibc's float tanh, which follows Sun's fdlibm
+// s_tanh.c / s_expm1.c in single precision): tanh(x) = -e/(e+2) with e = expm1(-2|x|) for |x| < 1,
+// 1 - 2/(expm1(2|x|)+2) for 1 <= |x| < 22, +-1 beyond; expm1 reduces x = k ln2 + r (ln2 split into a 24-bit-exact
+// hi part and a lo part), approximates expm1(r) by fdlibm's rational scheme (the degree-5 polynomial in r^2/2 with
+// fdlibm's Q1..Q5 rounded to float) and rescales by 2^k. Every operation is a separately rounded IEEE fp32 add,
+// multiply or divide (no contraction), so the result is bit-identical to the host's: the GPU test checks all 2^32
+// inputs against the C library.
+__device__ __forceinline__ float f_of(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ float host_expm1f(float x) {
+    const float ln2_hi = f_of(0x3f317180u), ln2_lo = f_of(0x3717f7d1u), invln2 = f_of(0x3fb8aa3bu);
+    const float Q1 = f_of(0xbd088889u), Q2 = f_of(0x3ad00d01u), Q3 = f_of(0xb8a670cdu), Q4 = f_of(0x36867e54u),
+                Q5 = f_of(0xb457edbbu);
+    const float huge = 1.0e+30f, tiny = 1.0e-30f;
+    uint32_t hx = __float_as_uint(x);
+    const bool neg = (hx & 0x80000000u) != 0u;
+    hx &= 0x7fffffffu;
+    if (hx >= 0x4195b844u) {                           // |x| >= 27 ln2
+        if (hx >= 0x42b17218u) {                       // |x| >= 88.72: NaN, +-inf, overflow
+            if (hx > 0x7f800000u) return __fadd_rn(x, x);
+            if (hx == 0x7f800000u) return neg ? -1.0f : x;
+            if (x > f_of(0x42b17180u)) return __fmul_rn(huge, huge);
+        }
+        if (neg) return __fsub_rn(tiny, 1.0f);        // expm1 = -1 (inexact)
+    }
+    float c = 0.0f;
+    int k = 0;
+    if (hx > 0x3eb17218u) {                            // |x| > ln2 / 2: reduce
+        float hi, lo;
+        if (hx < 0x3F851592u) {                        // |x| < 1.5 ln2: k = +-1
+            hi = neg ? __fadd_rn(x, ln2_hi) : __fsub_rn(x, ln2_hi);
+            lo = neg ? -ln2_lo : ln2_lo;
+            k = neg ? -1 : 1;
+        } else {
+            k = (int)__fadd_rn(__fmul_rn(invln2, x), neg ? -0.5f : 0.5f);   // truncation toward zero
+            const float t = (float)k;
+            hi = __fsub_rn(x, __fmul_rn(t, ln2_hi));   // t * ln2_hi is exact
+            lo = __fmul_rn(t, ln2_lo);
+        }
+        x = __fsub_rn(hi, lo);
+        c = __fsub_rn(__fsub_rn(hi, x), lo);
+    } else if (hx < 0x33000000u) {                     // |x| < 2^-25: x
+        const float t = __fadd_rn(huge, x);
+        return __fsub_rn(x, __fsub_rn(t, __fadd_rn(huge, x)));
+    }
+    const float hfx = __fmul_rn(0.5f, x);
+    const float hxs = __fmul_rn(x, hfx);
+    const float r1 = __fadd_rn(1.0f, __fmul_rn(hxs, __fadd_rn(Q1, __fmul_rn(hxs, __fadd_rn(Q2, __fmul_rn(hxs,
+                     __fadd_rn(Q3, __fmul_rn(hxs, __fadd_rn(Q4, __fmul_rn(hxs, Q5)))))))))) ;
+    float t = __fsub_rn(3.0f, __fmul_rn(r1, hfx));
+    float e = __fmul_rn(hxs, __fdiv_rn(__fsub_rn(r1, t), __fsub_rn(6.0f, __fmul_rn(x, t))));
+    if (k == 0) return __fsub_rn(x, __fsub_rn(__fmul_rn(x, e), hxs));
+    const float twopk = f_of(0x3f800000u + ((uint32_t)k << 23));
+    e = __fsub_rn(__fmul_rn(x, __fsub_rn(e, c)), c);
+    e = __fsub_rn(e, hxs);
+    if (k == -1) return __fsub_rn(__fmul_rn(0.5f, __fsub_rn(x, e)), 0.5f);
+    if (k == 1) {
+        if (x < -0.25f) return __fmul_rn(-2.0f, __fsub_rn(e, __fadd_rn(x, 0.5f)));
+        return __fadd_rn(1.0f, __fmul_rn(2.0f, __fsub_rn(x, e)));
+    }
+    float y;
+    if (k <= -2 || k > 56) {
+        y = __fsub_rn(1.0f, __fsub_rn(e, x));
+        y = k == 128 ? __fmul_rn(__fmul_rn(y, 2.0f), f_of(0x7f000000u)) : __fmul_rn(y, twopk);
+        return __fsub_rn(y, 1.0f);
+    }
+    if (k < 23) {
+        t = f_of(0x3f800000u - (0x1000000u >> k));    // 1 - 2^-k
+        y = __fmul_rn(__fsub_rn(t, __fsub_rn(e, x)), twopk);
+    } else {
+        t = f_of((uint32_t)(0x7f - k) << 23);          // 2^-k
+        y = __fmul_rn(__fadd_rn(__fsub_rn(x, __fadd_rn(e, t)), 1.0f), twopk);
+    }
+    return y;
+}
+__device__ __forceinline__ float host_tanhf(float x) {
+    const uint32_t jx = __float_as_uint(x);
+    const uint32_t ix = jx & 0x7fffffffu;
+    const bool neg = (jx & 0x80000000u) != 0u;
+    if (ix >= 0x7f800000u) return neg ? __fsub_rn(__fdiv_rn(1.0f, x), 1.0f) : __fadd_rn(__fdiv_rn(1.0f, x), 1.0f);
+    float z;
+    if (ix < 0x41b00000u) {                            // |x| < 22
+        if (ix < 0x24000000u) return __fmul_rn(x, __fadd_rn(1.0f, x));   // |x| < 2^-55
+        if (ix >= 0x3f800000u) {                       // |x| >= 1
+            const float t = host_expm1f(__fmul_rn(2.0f, fabsf(x)));
+            z = __fsub_rn(1.0f, __fdiv_rn(2.0f, __fadd_rn(t, 2.0f)));
+        } else {
+            const float t = host_expm1f(__fmul_rn(-2.0f, fabsf(x)));
+            z = __fdiv_rn(-t, __fadd_rn(t, 2.0f));
+        }
+    } else {
+        z = __fsub_rn(1.0f, 1.0e-30f);                 // +-1 (inexact)
+    }
+    return neg ? -z : z;
+}
 // The model's final-logit softcap, moved into the read: l = cap * tanhf(l / cap) (model_gemma4_gpu.cpp:282-283:
-// fp32 divide, tanhf, fp32 multiply), before the penalties as in ferro, where the model caps the row first.
+// fp32 divide, the host C library's tanhf, fp32 multiply), before the penalties as in ferro, where the model caps
+// the row first. Bit-identical to the host loop.
+__device__ __forceinline__ float softcap_one(float l, float cap) { return __fmul_rn(cap, host_tanhf(__fdiv_rn(l, cap))); }
 template <int N>
 __device__ __forceinline__ void softcap_vals(float (&x)[N], float cap) {
 #pragma unroll
-    for (int i = 0; i < N; ++i) x[i] = __fmul_rn(cap, tanhf(__fdiv_rn(x[i], cap)));
+    for (int i = 0; i < N; ++i) x[i] = softcap_one(x[i], cap);
 }
 // element id of this thread's i-th logit of the tile starting at lo
 __device__ __forceinline__ int elem_id(int lo, int i) { return lo + ((i >> 2) * BLOCK + (int)threadIdx.x) * 4 + (i & 3); }
@@ -2989,6 +3085,12 @@ __global__ __launch_bounds__(BLOCK) void merge_kernel(int nseg, uint64_t* cand, 
     merge_row(a, row_ctx(a, row), s, pre);
 }
 
+// fs_softcap_batch: the sampler's fused final-logit cap as a standalone elementwise pass.
+__global__ __launch_bounds__(256) void softcap_kernel(const float* in, float* out, int64_t n, float cap) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        out[i] = softcap_one(in[i], cap);
+}
+
 // In-place penalty pass (fs_penalize_batch): ferro's sample() leaves its host row penalised (sampler.cpp:11-18),
 // and a caller that reads the row back afterwards (lm_cli.cpp:353) sees those values. One workgroup per
 // (row, 8192-id chunk): the window's ids that fall in the chunk are counted in a 16-bit LDS table, then every
@@ -3528,6 +3630,16 @@ int fs_penalize_batch(fs_context* ctx, float* d_logits, int64_t ld, int32_t B, i
     }
     hipLaunchKernelGGL(fs::penalize_kernel, dim3((unsigned)(B * nchunk)), dim3(fs::PEN_BLOCK), 0, (hipStream_t)stream,
                        d_logits, ld, V, d_hist, d_hist_off, d_params, (int)nchunk, ctx->err);
+    return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
+}
+
+int fs_softcap_batch(const float* d_in, float* d_out, int64_t n, float cap, void* stream) {
+    if (n < 0 || (n > 0 && (!d_in || !d_out)) || !(cap > 0.0f)) return FS_E_INVALID;
+    if (n == 0) return FS_OK;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(fs::softcap_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, d_in, d_out, n,
+                       cap);
     return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
 }
 

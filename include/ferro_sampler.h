@@ -173,6 +173,12 @@ int fs_drng_error(fs_drng* r, void* stream, int32_t* bits);
 int fs_penalize_batch(fs_context* ctx, float* d_logits, int64_t ld, int32_t B, int32_t V, const int32_t* d_hist,
                       const int64_t* d_hist_off, const fs_row_params* d_params, void* stream);
 
+/* Gemma 4's final-logit softcap as the sampler applies it (fs_row_params.softcap): d_out[i] = cap * tanhf(d_in[i] /
+ * cap), the host loop of model_gemma4_gpu.cpp:282-283, bit-identical to it on a glibc host (its float tanh is
+ * restated on the device). For callers that need the capped logits themselves (log-probabilities); sampling does
+ * not (the cap is fused into its read). In place when d_out == d_in; cap > 0. */
+int fs_softcap_batch(const float* d_in, float* d_out, int64_t n, float cap, void* stream);
+
 /* Waits for `stream`, then returns and clears the device error bits (FS_DEVERR_*) kernels of this context set; after
  * FS_DEVERR_INTERNAL it also clears the context's workspace (row histograms and counters). A context that has
  * called fs_sample_batch_static also reports and clears the bits of its device's static workspace. */

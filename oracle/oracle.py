@@ -79,6 +79,8 @@ def lib():
         L.fso_mt64_seed.argtypes = [_P, ctypes.c_uint64]
         L.fso_mt64_next.restype = ctypes.c_uint64
         L.fso_mt64_next.argtypes = [_P]
+        L.fso_softcap.restype = None
+        L.fso_softcap.argtypes = [_P, _P, ctypes.c_int64, ctypes.c_float, ctypes.c_int]
         L.fso_canonical.restype = ctypes.c_double
         L.fso_canonical.argtypes = [ctypes.c_uint64]
         _lib = L
@@ -107,6 +109,14 @@ def ref():
 
 
 # ---------------------------------------------------------------------------------------------- oracle calls
+def softcap(x, cap, nthreads=1):
+    """The model's host softcap loop (model_gemma4_gpu.cpp:282-283) on a copy of x (float32)."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().fso_softcap(_ptr(x), _ptr(out), x.size, float(cap), int(nthreads))
+    return out
+
+
 def penalize(row, hist, params):
     row = np.ascontiguousarray(row, np.float32).copy()
     hist = np.ascontiguousarray(hist, np.int32)

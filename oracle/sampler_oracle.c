@@ -295,3 +295,26 @@ int fso_lookup_draft(const int32_t* h, int64_t L, int kmax, int32_t eos, int min
     }
     return 0;
 }
+
+/* ------------------------------------------------------------------ Gemma 4 softcap: model_gemma4_gpu.cpp:282-283 */
+/* out[i] = cap * tanhf(in[i] / cap), the model's host loop verbatim in arithmetic (the C library's tanhf), over
+ * nthreads threads. */
+typedef struct { const float* in; float* out; int64_t lo, hi; float cap; } cap_job;
+static void* cap_worker(void* p) {
+    const cap_job* j = (const cap_job*)p;
+    for (int64_t i = j->lo; i < j->hi; ++i) j->out[i] = j->cap * tanhf(j->in[i] / j->cap);
+    return 0;
+}
+void fso_softcap(const float* in, float* out, int64_t n, float cap, int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 64) nthreads = 64;
+    cap_job jobs[64];
+    pthread_t th[64];
+    for (int t = 0; t < nthreads; ++t) {
+        cap_job j = { in, out, n * t / nthreads, n * (t + 1) / nthreads, cap };
+        jobs[t] = j;
+    }
+    for (int t = 1; t < nthreads; ++t) pthread_create(&th[t], 0, cap_worker, &jobs[t]);
+    cap_worker(&jobs[0]);
+    for (int t = 1; t < nthreads; ++t) pthread_join(th[t], 0);
+}

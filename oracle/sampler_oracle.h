@@ -48,6 +48,9 @@ int fso_sample(float* row, int n, const int32_t* hist, int64_t hlen, const fso_p
 
 /* Batch over rows (row b = logits + b*ld, history CSR hist[hist_off[b] .. hist_off[b+1])), rows spread over
  * nthreads POSIX threads. Per-row outputs as fso_sample with leading dimension kcap. Rows are penalised in place. */
+/* The model's final-logit softcap (model_gemma4_gpu.cpp:282-283): out[i] = cap * tanhf(in[i] / cap). */
+void fso_softcap(const float* in, float* out, int64_t n, float cap, int nthreads);
+
 void fso_sample_batch(float* logits, int64_t ld, int B, int n, const int32_t* hist, const int64_t* hist_off,
                       const fso_params* params, const double* u, int32_t* tok, int32_t* cand_ids,
                       double* cand_probs, int kcap, int32_t* keep, int32_t* ncand, int nthreads);

@@ -4,6 +4,7 @@ Full configuration sizes are used where the oracle finishes in seconds (all five
 reference's own code paths allow: empty histories, windows and scopes, out-of-range history ids, ties (incl.
 -0/+0 and all-equal rows), top_k >= V, V = 1, V not a multiple of 4, NaN at index 0 for greedy.
 """
+import ctypes
 import os
 import sys
 
@@ -348,9 +349,7 @@ def test_large_k_coarse_bins_min_p_ties():
 def test_large_k_extremes_from_segments_and_tail():
     """top_k = 0 rows take their extremes and ordered count from the segments' published summaries plus the row's
     partial last tile: the maximum or the minimum in that tail (penalised), a segment holding only -inf, a segment
-    of one repeated value, and a row shorter than one tile (no segments). Every candidate's order is compared, so
-    the softcap stays out (the device's tanhf and glibc's may differ by an ulp, reordering near-ties);
-    test_softcap_fused_read samples a top_k = 0 row with a tail through the softcap."""
+    of one repeated value, and a row shorter than one tile (no segments). Every candidate's order is compared."""
     rng = np.random.default_rng(71)
     for V in (3 * 4096 + 37, 1000):
         B = 6
@@ -409,9 +408,9 @@ def test_device_logits_handoff_in_place():
 def test_randomized_sweep(seed):
     """Seeded random batches against the oracle: B not a multiple of 8, V from 1 to ~70000 (rows shorter than a
     tile, exact tiles, ragged tails), k from 1 to V and 0, top-p, min-p, repetition / frequency / presence
-    penalties with windows and scopes, -inf entries, and NaN in greedy rows (ferro's candidate sort is undefined with
-    NaN; its greedy scan is not). (The softcap is left out: the device's tanhf and
-    glibc's may differ by an ulp, which reorders logits one ulp apart; test_softcap_fused_read covers it.)"""
+    penalties with windows and scopes, -inf entries, NaN in greedy rows (ferro's candidate sort is undefined with
+    NaN; its greedy scan is not), and the Gemma 4 softcap on unclipped rows (the device restates the host C
+    library's tanhf bit for bit, so capped rows are held to the same exact bar)."""
     rng = np.random.default_rng(1000 + seed)
     for case in range(4):
         B = int(rng.integers(1, 40))
@@ -434,6 +433,7 @@ def test_randomized_sweep(seed):
         p["presence_penalty"] = rng.choice([0.0, 0.2], B)
         p["repeat_last_n"] = rng.choice([-1, 0, 16], B)
         p["penalty_from"] = rng.choice([0, 0, 3], B)
+        p["softcap"] = rng.choice([0.0, 0.0, 30.0, 2.5], B)
         hists = [rng.integers(-2, V + 2, int(rng.integers(0, 300))) for _ in range(B)]
         u = rng.random(B)
         kk = np.where((p["top_k"] > 0) & (p["top_k"] < V), p["top_k"], V)
@@ -656,27 +656,70 @@ def test_device_draws_replay_reference_streams():
             hists[s_].append(int(tok[s_]))
 
 
-def test_softcap_fused_read():
+@pytest.mark.parametrize("seed", [30, 31, 32])
+def test_softcap_fused_read(seed):
     """Gemma 4's final-logit softcap (cap 30) fused into the read, on every path: top-k, greedy, large k, penalties,
-    and a row tail; probabilities to 1e-5 against the oracle (glibc tanhf, as ferro's model code)."""
-    rng = np.random.default_rng(30)
+    and a row tail, on unclipped logits (saturating ones and +-inf included), to the same exact bar as uncapped rows:
+    the device's tanhf is the host C library's, restated (model_gemma4_gpu.cpp:282-283 caps the host row with it)."""
+    rng = np.random.default_rng(seed)
     V = 262144 + 77
     B = 8
-    # |x| <= 150: no logit saturates tanhf (where two libm implementations may round differently)
-    x = np.clip(W.mixture_logits(rng, B, V) * np.float32(3.0), -150.0, 150.0).astype(np.float32)
+    x = (W.mixture_logits(rng, B, V) * np.float32(rng.uniform(1.0, 40.0))).astype(np.float32)
+    x[0, rng.integers(0, V, 50)] = np.float32(1e4)                 # saturated: every one of them caps to 30
+    x[5, rng.integers(0, V, 5)] = np.float32(np.inf)
+    x[6, rng.integers(0, V, 5)] = np.float32(-np.inf)
     p = W.make_params(B, temperature=0.8, top_k=64, top_p=0.95, repetition_penalty=1.05)
     p["softcap"] = 30.0
     p["temperature"][1] = 0.0
     p["top_k"][2] = 0
+    p["top_k"][7] = 1500
     p["frequency_penalty"][3], p["presence_penalty"][3] = 0.4, 0.2
     hists = [rng.integers(0, V, 300) for _ in range(B)]
-    g, o, nb = check(_case(list(x), p, hists, rng.random(B), "softcap"), kcap=64)
-    assert nb == 0
+    g, o, nb = check(_case(list(x), p, hists, rng.random(B), f"softcap{seed}"), kcap=64)
+    assert nb <= 1
     t2 = F.argmax_batch(torch.from_numpy(x).cuda(), params=p, hist=np.concatenate(hists).astype(np.int32),
                         hist_off=np.concatenate([[0], np.cumsum([len(h) for h in hists])]).astype(np.int64))
     np.testing.assert_array_equal(t2.cpu().numpy(), [O.sample(x[b], hists[b], O.make_params(
         temperature=0.0, repetition_penalty=1.05, softcap=30.0, frequency_penalty=float(p["frequency_penalty"][b]),
         presence_penalty=float(p["presence_penalty"][b])))[0] for b in range(B)])
+
+
+def test_softcap_matches_host_libm_on_every_float():
+    """fs_softcap_batch (the sampler's fused cap) against the model's host loop, cap * tanhf(x / cap) with the C
+    library's tanhf (model_gemma4_gpu.cpp:282-283): bit-identical on all 2^32 float inputs at cap 1 (tanhf itself),
+    and on 2^26 random bit patterns at caps 30 and 0.375. NaN inputs give NaN (payloads are not compared)."""
+    from ferro_amd._lib import lib
+    L = lib()
+    chunk = 1 << 27
+    dev = torch.device("cuda", 0)
+    d_in = torch.empty(chunk, dtype=torch.int32, device=dev)
+    d_out = torch.empty(chunk, dtype=torch.float32, device=dev)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    base = np.arange(chunk, dtype=np.uint32)
+    nth = min(16, os.cpu_count() or 1)
+    bad = 0
+
+    def run(bits, cap):
+        n = bits.size
+        d_in[:n].copy_(torch.from_numpy(bits.view(np.int32)))
+        rc = L.fs_softcap_batch(ctypes.c_void_p(d_in.data_ptr()), ctypes.c_void_p(d_out.data_ptr()), n,
+                                ctypes.c_float(cap), st)
+        assert rc == 0
+        ref = torch.from_numpy(O.softcap(bits.view(np.float32), cap, nth).view(np.int32)).to(dev)
+        got = d_out[:n].view(torch.int32)
+        differ = (got != ref) & ~(torch.isnan(d_out[:n]) & torch.isnan(ref.view(torch.float32)))
+        return int(differ.sum().item())
+
+    for c in range((1 << 32) // chunk):
+        bad += run(base + np.uint32(c * chunk), 1.0)
+    say(f"softcap cap 1: {bad} of 2^32 inputs differ from the host C library")
+    assert bad == 0
+    rng = np.random.default_rng(5)
+    for cap in (30.0, 0.375):
+        bits = rng.integers(0, 1 << 32, 1 << 26, dtype=np.uint64).astype(np.uint32)
+        n = run(bits, cap)
+        say(f"softcap cap {cap}: {n} of 2^26 random inputs differ")
+        assert n == 0
 
 
 def test_lookup_draft_matches_oracle():
