@@ -93,6 +93,7 @@ struct Args {
     uint64_t* cand;                // [B*nseg][CAP]
     uint32_t* meta;                // [B*nseg][2]: lower bound of the k-th key, count
     uint32_t* rhist;               // [B][RBINS] row histograms of the segments' candidates, left at 0
+    uint64_t* rmass;               // [B][4096] fixed-point mass histograms of large rows' candidates, left at 0
     uint32_t* stream_cnt;          // [n_streams] verify completion counters, left at 0
     int32_t* err;                  // device error bits
     int32_t* dirty;                // nonzero: a merge gave up waiting; the row histograms and counters may be stale
@@ -808,100 +809,79 @@ __device__ __forceinline__ void load_seg_tile(float (&x)[TPT], __amdgpu_buffer_r
 // multiply or divide (no contraction), so the result is bit-identical to the host's: the GPU test checks all 2^32
 // inputs against the C library.
 __device__ __forceinline__ float f_of(uint32_t u) { return __uint_as_float(u); }
-__device__ __forceinline__ float host_expm1f(float x) {
+// Straight-line form (every case computed, the result selected): no branches, so the eight-wide unrolled reads
+// that call it stay one basic block each. Selecting between separately computed IEEE results changes none of them.
+__device__ __forceinline__ float host_tanhf(float x) {
     const float ln2_hi = f_of(0x3f317180u), ln2_lo = f_of(0x3717f7d1u), invln2 = f_of(0x3fb8aa3bu);
     const float Q1 = f_of(0xbd088889u), Q2 = f_of(0x3ad00d01u), Q3 = f_of(0xb8a670cdu), Q4 = f_of(0x36867e54u),
                 Q5 = f_of(0xb457edbbu);
-    const float huge = 1.0e+30f, tiny = 1.0e-30f;
-    uint32_t hx = __float_as_uint(x);
-    const bool neg = (hx & 0x80000000u) != 0u;
-    hx &= 0x7fffffffu;
-    if (hx >= 0x4195b844u) {                           // |x| >= 27 ln2
-        if (hx >= 0x42b17218u) {                       // |x| >= 88.72: NaN, +-inf, overflow
-            if (hx > 0x7f800000u) return __fadd_rn(x, x);
-            if (hx == 0x7f800000u) return neg ? -1.0f : x;
-            if (x > f_of(0x42b17180u)) return __fmul_rn(huge, huge);
-        }
-        if (neg) return __fsub_rn(tiny, 1.0f);        // expm1 = -1 (inexact)
-    }
-    float c = 0.0f;
-    int k = 0;
-    if (hx > 0x3eb17218u) {                            // |x| > ln2 / 2: reduce
-        float hi, lo;
-        if (hx < 0x3F851592u) {                        // |x| < 1.5 ln2: k = +-1
-            hi = neg ? __fadd_rn(x, ln2_hi) : __fsub_rn(x, ln2_hi);
-            lo = neg ? -ln2_lo : ln2_lo;
-            k = neg ? -1 : 1;
-        } else {
-            k = (int)__fadd_rn(__fmul_rn(invln2, x), neg ? -0.5f : 0.5f);   // truncation toward zero
-            const float t = (float)k;
-            hi = __fsub_rn(x, __fmul_rn(t, ln2_hi));   // t * ln2_hi is exact
-            lo = __fmul_rn(t, ln2_lo);
-        }
-        x = __fsub_rn(hi, lo);
-        c = __fsub_rn(__fsub_rn(hi, x), lo);
-    } else if (hx < 0x33000000u) {                     // |x| < 2^-25: x
-        const float t = __fadd_rn(huge, x);
-        return __fsub_rn(x, __fsub_rn(t, __fadd_rn(huge, x)));
-    }
-    const float hfx = __fmul_rn(0.5f, x);
-    const float hxs = __fmul_rn(x, hfx);
+    const uint32_t jx = __float_as_uint(x), ix = jx & 0x7fffffffu;
+    const bool neg = (jx >> 31) != 0u;
+    const float ax = __uint_as_float(ix);
+    const bool big = ix >= 0x3f800000u;                     // |x| >= 1: tanh = 1 - 2/(expm1(2|x|)+2)
+    const float y = big ? __fmul_rn(2.0f, ax) : __fmul_rn(-2.0f, ax);   // expm1's argument, in (-2, 44) for |x| < 22
+    const uint32_t hy = __float_as_uint(y) & 0x7fffffffu;
+    const bool yneg = !big;
+    // expm1(y): y = k ln2 + r (|y| > ln2 / 2; k = +-1 below 1.5 ln2)
+    const bool red = hy > 0x3eb17218u;
+    const bool near = hy < 0x3F851592u;
+    const float hiA = yneg ? __fadd_rn(y, ln2_hi) : __fsub_rn(y, ln2_hi);
+    const float loA = yneg ? -ln2_lo : ln2_lo;
+    const int kB = (int)__fadd_rn(__fmul_rn(invln2, y), yneg ? -0.5f : 0.5f);   // truncation toward zero
+    const float tB = (float)kB;
+    const float hiB = __fsub_rn(y, __fmul_rn(tB, ln2_hi));   // tB * ln2_hi is exact
+    const float loB = __fmul_rn(tB, ln2_lo);
+    const int k = red ? (near ? (yneg ? -1 : 1) : kB) : 0;
+    const float hi = near ? hiA : hiB, lo = near ? loA : loB;
+    const float xr = red ? __fsub_rn(hi, lo) : y;
+    const float c = red ? __fsub_rn(__fsub_rn(hi, xr), lo) : 0.0f;
+    const float hfx = __fmul_rn(0.5f, xr);
+    const float hxs = __fmul_rn(xr, hfx);
     const float r1 = __fadd_rn(1.0f, __fmul_rn(hxs, __fadd_rn(Q1, __fmul_rn(hxs, __fadd_rn(Q2, __fmul_rn(hxs,
-                     __fadd_rn(Q3, __fmul_rn(hxs, __fadd_rn(Q4, __fmul_rn(hxs, Q5)))))))))) ;
-    float t = __fsub_rn(3.0f, __fmul_rn(r1, hfx));
-    float e = __fmul_rn(hxs, __fdiv_rn(__fsub_rn(r1, t), __fsub_rn(6.0f, __fmul_rn(x, t))));
-    if (k == 0) return __fsub_rn(x, __fsub_rn(__fmul_rn(x, e), hxs));
-    const float twopk = f_of(0x3f800000u + ((uint32_t)k << 23));
-    e = __fsub_rn(__fmul_rn(x, __fsub_rn(e, c)), c);
-    e = __fsub_rn(e, hxs);
-    if (k == -1) return __fsub_rn(__fmul_rn(0.5f, __fsub_rn(x, e)), 0.5f);
-    if (k == 1) {
-        if (x < -0.25f) return __fmul_rn(-2.0f, __fsub_rn(e, __fadd_rn(x, 0.5f)));
-        return __fadd_rn(1.0f, __fmul_rn(2.0f, __fsub_rn(x, e)));
-    }
-    float y;
-    if (k <= -2 || k > 56) {
-        y = __fsub_rn(1.0f, __fsub_rn(e, x));
-        y = k == 128 ? __fmul_rn(__fmul_rn(y, 2.0f), f_of(0x7f000000u)) : __fmul_rn(y, twopk);
-        return __fsub_rn(y, 1.0f);
-    }
-    if (k < 23) {
-        t = f_of(0x3f800000u - (0x1000000u >> k));    // 1 - 2^-k
-        y = __fmul_rn(__fsub_rn(t, __fsub_rn(e, x)), twopk);
-    } else {
-        t = f_of((uint32_t)(0x7f - k) << 23);          // 2^-k
-        y = __fmul_rn(__fadd_rn(__fsub_rn(x, __fadd_rn(e, t)), 1.0f), twopk);
-    }
-    return y;
-}
-__device__ __forceinline__ float host_tanhf(float x) {
-    const uint32_t jx = __float_as_uint(x);
-    const uint32_t ix = jx & 0x7fffffffu;
-    const bool neg = (jx & 0x80000000u) != 0u;
-    if (ix >= 0x7f800000u) return neg ? __fsub_rn(__fdiv_rn(1.0f, x), 1.0f) : __fadd_rn(__fdiv_rn(1.0f, x), 1.0f);
-    float z;
-    if (ix < 0x41b00000u) {                            // |x| < 22
-        if (ix < 0x24000000u) return __fmul_rn(x, __fadd_rn(1.0f, x));   // |x| < 2^-55
-        if (ix >= 0x3f800000u) {                       // |x| >= 1
-            const float t = host_expm1f(__fmul_rn(2.0f, fabsf(x)));
-            z = __fsub_rn(1.0f, __fdiv_rn(2.0f, __fadd_rn(t, 2.0f)));
-        } else {
-            const float t = host_expm1f(__fmul_rn(-2.0f, fabsf(x)));
-            z = __fdiv_rn(-t, __fadd_rn(t, 2.0f));
-        }
-    } else {
-        z = __fsub_rn(1.0f, 1.0e-30f);                 // +-1 (inexact)
-    }
-    return neg ? -z : z;
+                     __fadd_rn(Q3, __fmul_rn(hxs, __fadd_rn(Q4, __fmul_rn(hxs, Q5))))))))));
+    const float t = __fsub_rn(3.0f, __fmul_rn(r1, hfx));
+    const float e = __fmul_rn(hxs, __fdiv_rn(__fsub_rn(r1, t), __fsub_rn(6.0f, __fmul_rn(xr, t))));
+    const float R0 = __fsub_rn(xr, __fsub_rn(__fmul_rn(xr, e), hxs));                       // k = 0
+    const float e2 = __fsub_rn(__fsub_rn(__fmul_rn(xr, __fsub_rn(e, c)), c), hxs);
+    const float Rm1 = __fsub_rn(__fmul_rn(0.5f, __fsub_rn(xr, e2)), 0.5f);                 // k = -1
+    const float R1 = xr < -0.25f ? __fmul_rn(-2.0f, __fsub_rn(e2, __fadd_rn(xr, 0.5f)))    // k = 1
+                                 : __fadd_rn(1.0f, __fmul_rn(2.0f, __fsub_rn(xr, e2)));
+    const int kc = k < -126 ? -126 : (k > 127 ? 127 : k);
+    const float twopk = f_of(0x3f800000u + ((uint32_t)kc << 23));
+    const float RL = __fsub_rn(__fmul_rn(__fsub_rn(1.0f, __fsub_rn(e2, xr)), twopk), 1.0f);  // k <= -2 or k > 56
+    const int ks = k < 0 ? 0 : (k > 31 ? 31 : k);
+    const float RS = __fmul_rn(__fsub_rn(f_of(0x3f800000u - (0x1000000u >> ks)), __fsub_rn(e2, xr)), twopk);   // 1 - 2^-k
+    const int kt = k < 0 ? 0 : (k > 126 ? 126 : k);
+    const float RB = __fmul_rn(__fadd_rn(__fsub_rn(xr, __fadd_rn(e2, f_of((uint32_t)(0x7f - kt) << 23))), 1.0f), twopk);
+    float em = k == 0 ? R0 : k == -1 ? Rm1 : k == 1 ? R1 : (k <= -2 || k > 56) ? RL : k < 23 ? RS : RB;
+    const float huge = 1.0e+30f;
+    if (hy < 0x33000000u) em = __fsub_rn(y, __fsub_rn(__fadd_rn(huge, y), __fadd_rn(huge, y)));   // |y| < 2^-25
+    // tanh from expm1
+    float z = big ? __fsub_rn(1.0f, __fdiv_rn(2.0f, __fadd_rn(em, 2.0f))) : __fdiv_rn(-em, __fadd_rn(em, 2.0f));
+    if (ix >= 0x41b00000u) z = __fsub_rn(1.0f, 1.0e-30f);      // |x| >= 22: +-1 (inexact)
+    float r = neg ? -z : z;
+    if (ix < 0x24000000u) r = __fmul_rn(x, __fadd_rn(1.0f, x));  // |x| < 2^-55
+    if (ix >= 0x7f800000u)                                       // +-inf, NaN
+        r = neg ? __fsub_rn(__fdiv_rn(1.0f, x), 1.0f) : __fadd_rn(__fdiv_rn(1.0f, x), 1.0f);
+    return r;
 }
 // The model's final-logit softcap, moved into the read: l = cap * tanhf(l / cap) (model_gemma4_gpu.cpp:282-283:
 // fp32 divide, the host C library's tanhf, fp32 multiply), before the penalties as in ferro, where the model caps
 // the row first. Bit-identical to the host loop.
 __device__ __forceinline__ float softcap_one(float l, float cap) { return __fmul_rn(cap, host_tanhf(__fdiv_rn(l, cap))); }
+// A rolled loop: one copy of the cap per call site (there are dozens, all unrolled eight-wide otherwise), for capped
+// rows only; the element is picked and put back by index.
 template <int N>
 __device__ __forceinline__ void softcap_vals(float (&x)[N], float cap) {
+#pragma unroll 1
+    for (int i = 0; i < N; ++i) {
+        float v = x[0];
 #pragma unroll
-    for (int i = 0; i < N; ++i) x[i] = softcap_one(x[i], cap);
+        for (int j = 1; j < N; ++j) v = i == j ? x[j] : v;
+        v = softcap_one(v, cap);
+#pragma unroll
+        for (int j = 0; j < N; ++j) x[j] = i == j ? v : x[j];
+    }
 }
 // element id of this thread's i-th logit of the tile starting at lo
 __device__ __forceinline__ int elem_id(int lo, int i) { return lo + ((i >> 2) * BLOCK + (int)threadIdx.x) * 4 + (i & 3); }
@@ -1471,9 +1451,19 @@ __device__ __forceinline__ int large_walk(Shared& s, int n, uint64_t lo_c, doubl
     return first;
 }
 
-// The whole large-k sample of one row: token, kept count, optional candidate outputs (in chunks of KMAX).
+// What a large row's optional candidate outputs need (large_outputs), left by large_row or large_segment.
+struct LargeOut {
+    bool valid;
+    int keff;
+    uint64_t Xk;
+    uint32_t kmax;
+    double S;
+};
+
+// The whole large-k sample of one row: token and kept count; lo describes the candidates for the optional outputs.
 __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Shared& s, int& tok_out, int& keep_out,
-                                          bool seg_summaries = true) {
+                                          LargeOut& lo) {
+    lo.valid = false;
     const int tid = threadIdx.x;
     const int row = rc.row;
     const fs_row_params& p = rc.p;
@@ -1486,48 +1476,12 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
     __syncthreads();
     uint64_t cmax = 0ull, cmin = ~0ull;
     uint32_t nv = 0u;
-    if (a.nseg > 0 && !need_kth && seg_summaries) {
-        // the segments published the extremes and counts of their full tiles; the partial last tile is read here
-        for (int c = tid; c < a.nseg; c += BLOCK) {
-            const int64_t slot = (int64_t)row * a.nseg + c;
-            const uint64_t hi = a.cand[slot * CAP], lo = a.cand[slot * CAP + 1];
-            cmax = hi > cmax ? hi : cmax;
-            cmin = lo < cmin ? lo : cmin;
-            nv += a.meta[2 * slot + 1];
-        }
-        const int V = a.V;
-        const int tail_lo = (V / TILE) * TILE;
-        if (tail_lo < V) {
-            const float* rowp = a.logits + (int64_t)row * a.ld;
-            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(rowp), (short)0,
-                                                                                ((V + 3) & ~3) * 4, 0x00020000);
-            float x[TPT];
-            load_seg_tile(x, rs, tail_lo / TILE);
-            if (rc.capped) softcap_vals(x, rc.p.softcap);
-            if (rc.pen) {
-                __syncthreads();
-                apply_penalties(x, a, rc, tail_lo, s);
-            }
-#pragma unroll
-            for (int i = 0; i < TPT; ++i) {
-                const int e = elem_id(tail_lo, i);
-                if (e < V && x[i] == x[i]) {
-                    const uint64_t c = comp_of(key_of(x[i]), (uint32_t)e);
-                    cmax = c > cmax ? c : cmax;
-                    cmin = c < cmin ? c : cmin;
-                    ++nv;
-                }
-            }
-            __syncthreads();                              // the tail's table reads are done
-        }
-    } else {
-        row_elems(a, rc, s, [&](float, uint32_t kq, uint64_t c) {
-            cmax = c > cmax ? c : cmax;
-            cmin = c < cmin ? c : cmin;
-            ++nv;
-            if (need_kth) atomicAdd(&hc[kq >> LB_SHIFT], 1u);
-        });
-    }
+    row_elems(a, rc, s, [&](float, uint32_t kq, uint64_t c) {
+        cmax = c > cmax ? c : cmax;
+        cmin = c < cmin ? c : cmin;
+        ++nv;
+        if (need_kth) atomicAdd(&hc[kq >> LB_SHIFT], 1u);
+    });
     cmax = block_max_u64(cmax, s.red);
     cmin = block_min_u64(cmin, s.red);
     uint32_t ntot;
@@ -1654,9 +1608,9 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
             }
         }
     }
+    lo.valid = true; lo.keff = keff; lo.Xk = Xk; lo.kmax = kmax; lo.S = S;
     if (!ok_fast) {
         large_row_exact(a, rc, s, tok_out, keep_out);
-        large_outputs(a, rc, s, keff, Xk, kk, kmax, mx, Td, S);
         return;
     }
     // the kept prefix: the largest of the three thresholds (sampler.cpp:43-44)
@@ -1704,9 +1658,34 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
     if (pick == 0ull) pick = clast;
     tok_out = (int)comp_id(pick);
     keep_out = (int)keep;
-    large_outputs(a, rc, s, keff, Xk, kk, kmax, mx, Td, S);
 }
 
+// Large rows sampled by their segments together (large_segment, below): the list slot's scalars and the row barrier.
+// Slot layout: each phase's scalars in a 128-byte line of their own, then three gather regions of whole lines. A
+// segment reads another segment's line only after the barrier that follows its writing, and never earlier in the
+// call, so no line it reads can be stale in its L1.
+constexpr int LLINE = 16;                      // composites per 128-byte line
+constexpr int LSC = 5 * LLINE;                 // scalar lines at the head of a large-row segment's list slot
+constexpr int LLR = ((CAP - LSC) / 3) / LLINE * LLINE;   // capacity of each of its three gather regions
+enum LargeSlot : int {
+    LS_MAX = 0, LS_MIN, LS_NV,                                   // P1: largest / smallest composite, ordered count
+    LS_SHI = LLINE, LS_NBK,                                      // P2: fp64 mass of the candidates above bk; bin bk's count
+    LS_NBC = 2 * LLINE, LS_CA, LS_CNTM, LS_SUMM, LS_CLM,         // P3: bin bc's count, candidates above bc, min-p's
+    LS_NBD = 3 * LLINE,                                          // P4: bin bd's count
+    LS_TOK = 4 * LLINE, LS_XK, LS_S, LS_KEFF, LS_STATUS          // segment 0: token | keep << 32, Xk, S, keff | kmax << 32, 1 = done
+};
+static_assert(LS_STATUS < LSC, "the scalars fit the slot head");
+static_assert(LSC + 3 * LLR <= CAP, "three gather regions after the scalars");
+
+// The row barrier counter: the row histogram's bin RBINS - 2, above every ordered key (bins <= 4088) like the
+// completion counter. Low 15 bits: arrivals; bit 15: the row is abandoned.
+__device__ __forceinline__ uint32_t* row_sync_ctr(const Args& a, int row) {
+    return a.rhist + (int64_t)row * RBINS + (RBINS - 2);
+}
+constexpr uint32_t ROW_ABANDONED = 0x8000u;
+__device__ __forceinline__ void row_abandon(const Args& a, int row) {
+    if (threadIdx.x == 0) __hip_atomic_fetch_or(row_sync_ctr(a, row), ROW_ABANDONED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 // ------------------------------------------------------------------------------------------------ one-wave finish
 // For k <= 64 once the block has narrowed the row to c1 <= 128 candidates (composites, all distinct, containing the
 // top k) and ranked them (block_ranks): wave 0 places them (lane i = candidate i in ferro's order) and runs the
@@ -1978,8 +1957,35 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
     int tok = 0, keep = 1;
 
     bool fast = false;
-    if (rc.large || alone) {
-        large_row(a, rc, s, tok, keep, !alone);     // alone: the whole row from the logits, no segment output
+    LargeOut lo;
+    lo.valid = false;
+    bool whole = rc.large || alone;                   // sampled as a whole row: by the segments together or here
+    bool from_segs = false;
+    if (rc.large && !alone && nseg > 0) {
+        // the row's segments sampled it together (large_segment): segment 0's slot holds the result unless the row
+        // was abandoned (then it is sampled here alone, exactly)
+        const uint64_t* s0 = a.cand + (int64_t)row * nseg * CAP;
+        const uint32_t sc = *reinterpret_cast<volatile const uint32_t*>(row_sync_ctr(a, row));   // not read before
+        if (!(sc & ROW_ABANDONED) && s0[LS_STATUS] == 1ull) {
+            const uint64_t tk = s0[LS_TOK];
+            tok = (int)(uint32_t)tk;
+            keep = (int)(tk >> 32);
+            const uint64_t kw = s0[LS_KEFF];
+            lo.valid = keep > 0;
+            lo.keff = (int)(uint32_t)kw;
+            lo.Xk = s0[LS_XK];
+            lo.kmax = (uint32_t)(kw >> 32);
+            lo.S = __longlong_as_double((long long)s0[LS_S]);
+            from_segs = true;
+        }
+    }
+    if (whole) {
+        if (!from_segs) large_row(a, rc, s, tok, keep, lo);          // from the logits alone
+        if (lo.valid && a.mode != MODE_VERIFY && a.kcap > 0 && (a.cand_ids || a.cand_probs)) {
+            if (rc.pen && from_segs) gather_window(a, rc, 0, a.V, s);   // the output passes apply the penalties
+            large_outputs(a, rc, s, lo.keff, lo.Xk, comp_key(lo.Xk), lo.kmax, val_of(lo.kmax),
+                          (double)rc.p.temperature, lo.S);
+        }
     } else if (ntail == 0 && (fast = merge_fast(a, rc, s, pre, tok, keep))) {
         // the short merge wrote the row's outputs
     } else {
@@ -2388,9 +2394,13 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
         }                                             // general path
     }
     }
-    if (!rc.large && !rc.greedy && nseg > 0 && !alone) {   // the segments' row histogram is spent: leave it at 0
+    if (!rc.greedy && nseg > 0 && !alone) {           // the segments' row histogram is spent: leave it at 0
         uint4* rz = reinterpret_cast<uint4*>(a.rhist + (int64_t)row * RBINS);
         for (int i = tid; i < RBINS / 4; i += BLOCK) rz[i] = make_uint4(0u, 0u, 0u, 0u);
+        if (rc.large) {                                // and a large row's mass histogram
+            uint4* mz = reinterpret_cast<uint4*>(a.rmass + (int64_t)row * LB);
+            for (int i = tid; i < LB / 2; i += BLOCK) mz[i] = make_uint4(0u, 0u, 0u, 0u);
+        }
     }
     if (a.mode != MODE_VERIFY) {
         if (tid == 0) {
@@ -2932,47 +2942,439 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     __syncthreads();                               // LDS is reused by the next item
 }
 
-// Rows sampled with k >= V (top_k = 0 included; ferro's k = n, sampler.cpp:26): each segment streams its tiles once
-// for the row's extremes and ordered (non-NaN) count, penalties applied, and publishes them in its list slot
-// (entry 0: the largest composite, entry 1: the smallest; meta: 0, the count), so the merge's whole-row selection
-// starts at its mass pass.
-__device__ __forceinline__ void large_segment_extremes(const Args& a, const RowCtx& rc, int seg, Shared& s,
-                                                       const SegStart& g) {
-    const int tid = threadIdx.x;
-    if (rc.pen) gather_window(a, rc, g.seg_lo, g.seg_lo + g.ntiles * TILE, s);
-    uint64_t cmax = 0ull, cmin = ~0ull;
-    uint32_t nv = 0u;
-    for (int t = 0; t < g.ntiles; ++t) {                 // large rows only: one tile in flight is enough here
-        float x[TPT];
-        load_seg_tile(x, g.rs, t);
-        const int lo = g.seg_lo + t * TILE;
-        if (rc.capped) softcap_vals(x, rc.p.softcap);
-        if (rc.pen) {
-            __syncthreads();                             // the previous tile's table reads are done
-            apply_penalties(x, a, rc, lo, s);
+// ------------------------------------------------------------------------------------------------ large k, split
+// Rows sampled with k > KMAX (top_k = 0 included: ferro's k = n, sampler.cpp:26) are sampled by the row's segment
+// workgroups together: the passes of large_row (the one-workgroup version, kept as the fallback) each run over
+// every segment at once, and the segments meet at row barriers between them. After each barrier every segment reads
+// the others' published partial results and computes the same row-wide decision (the same inputs in the same
+// order), so no workgroup waits for a coordinator:
+//   P1 extremes, ordered count and (k < V) coarse-bin counts (added to the row histogram) -> the k-th's coarse bin bk;
+//   P2 the masses exp((v - mx) / T) of the candidates above bk (fp64 partial sums, fixed-point mass histogram added
+//      to the row's in the workspace) and bin bk's elements gathered -> the exact k-th Xk, S and the mass histogram;
+//   P3 top-p's crossing bin bc gathered, with min-p's counts and masses -> the kept prefix and its total;
+//   P4 the draw's bin bd gathered, unless it is bc (already sorted in LDS) -> the token.
+// Segment 0 publishes the token and what the merge needs for the optional candidate outputs. A bin too large for
+// one sort, a target outside its bin's exact masses, or a barrier that waits too long abandons the row (a flag on
+// the barrier counter); the merging workgroup then samples it alone with large_row (exact).
+// Arrive and wait until `target` arrivals (every segment of the row at this barrier). This workgroup's stores and
+// atomics complete first (vmcnt(0)); after the wait its L1 is invalidated at agent scope (buffer_inv sc1; device
+// memory's L2 lines are kept), so the others' published data is read from the XCD's L2. The poll is an atomic that is not idempotent (it executes in the L2). Bounded: past
+// a.merge_spins polls the row is abandoned. Returns false when the row is abandoned.
+__device__ __forceinline__ bool row_sync(const Args& a, int row, uint32_t target, Shared& s) {
+    vm_drain();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t* c = row_sync_ctr(a, row);
+        __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        uint32_t ok = 1u, spins = 0u;
+        for (;;) {
+            const uint32_t v = __hip_atomic_fetch_add(c, 0x10000u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (v & ROW_ABANDONED) { ok = 0u; break; }
+            if ((v & 0x7FFFu) >= target) break;
+            if (++spins >= a.merge_spins) {
+                __hip_atomic_fetch_or(c, ROW_ABANDONED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                ok = 0u;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
         }
+        s.red.misc[4] = ok;
+    }
+    __syncthreads();
+    const bool ok = s.red.misc[4] != 0u;
+    asm volatile("buffer_inv sc1" ::: "memory");         // drop this CU's L1 lines (agent scope)
+    __syncthreads();                                     // misc[4] is reused by the next barrier
+    return ok;
+}
+
+// One pass over a large-row segment's tiles [lo0, hi) (the last segment also takes the row's partial tile), two
+// tiles in flight, softcap and penalties applied: f(x, key, composite) per ordered element. Ends with a barrier.
+template <class F>
+__device__ __forceinline__ void seg_elems(const Args& a, const RowCtx& rc, Shared& s, int lo0, int hi, F f) {
+    const float* rowp = a.logits + (int64_t)rc.row * a.ld;
+    const int nt = (hi - lo0 + TILE - 1) / TILE;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(rowp + lo0), (short)0,
+                                                                        ((hi - lo0 + 3) & ~3) * 4, 0x00020000);
+    float buf[LPF][TPT];
 #pragma unroll
-        for (int i = 0; i < TPT; ++i) {
-            if (x[i] == x[i]) {
-                const uint64_t c = comp_of(key_of(x[i]), (uint32_t)elem_id(lo, i));
-                cmax = c > cmax ? c : cmax;
-                cmin = c < cmin ? c : cmin;
-                ++nv;
+    for (int p = 0; p < LPF; ++p) load_seg_tile(buf[p], rs, p);
+    for (int t0 = 0; t0 < nt; t0 += LPF) {
+#pragma unroll
+        for (int p = 0; p < LPF; ++p) {
+            const int t = t0 + p;
+            float x[TPT];
+#pragma unroll
+            for (int i = 0; i < TPT; ++i) x[i] = buf[p][i];
+            load_seg_tile(buf[p], rs, t + LPF);
+            if (t < nt) {
+                const int lo = lo0 + t * TILE;
+                if (rc.capped) softcap_vals(x, rc.p.softcap);
+                if (rc.pen) {
+                    __syncthreads();                     // the previous tile's table reads are done
+                    apply_penalties(x, a, rc, lo, s);
+                }
+#pragma unroll
+                for (int i = 0; i < TPT; ++i) {
+                    const int e = elem_id(lo, i);
+                    const bool ok = e < hi && x[i] == x[i];
+                    const uint32_t kq = key_of(x[i]);
+                    f(ok, x[i], kq, comp_of(kq, (uint32_t)e));
+                }
             }
         }
     }
+    __syncthreads();
+}
+
+// The gathered lists of one region of every segment of the row, concatenated into s.cand[0, n) and sorted in
+// candidate order (descending composites). Returns n, or -1 when a list overflowed or they exceed KMAX together.
+// Called after a row barrier (the lists are in the L2; this workgroup's L1 is invalidated).
+__device__ __forceinline__ int load_lists(const Args& a, int row, int region, int cnt_slot, Shared& s) {
+    const int tid = threadIdx.x, nseg = a.nseg;
+    const uint64_t* base = a.cand + (int64_t)row * nseg * CAP;
+    uint32_t mine = 0u;
+    bool over = false;
+    for (int j = tid; j < nseg; j += BLOCK) {
+        const uint64_t c = base[(int64_t)j * CAP + cnt_slot];
+        over |= c > (uint64_t)LLR;
+    }
+    // offsets: thread j < nseg holds list j's count (nseg < BLOCK, kept so by the host)
+    if (tid < nseg) {
+        const uint64_t c = base[(int64_t)tid * CAP + cnt_slot];
+        mine = c > (uint64_t)LLR ? 0u : (uint32_t)c;
+    }
+    uint32_t tot;
+    const uint32_t off = block_excl_scan<uint32_t>(mine, s.wsum, &tot);
+    const bool any_over = block_max_u32(over ? 1u : 0u, s.red) != 0u;
+    if (any_over || tot > (uint32_t)KMAX) return -1;    // uniform
+    if (tid < nseg) s.off[tid] = off;
+    if (tid == 0) s.off[nseg] = tot;
+    __syncthreads();
+    for (uint32_t f = tid; f < tot; f += BLOCK) {        // flat index -> (list, position)
+        int c0 = 0, c1 = nseg;
+        while (c1 - c0 > 1) {
+            const int m = (c0 + c1) >> 1;
+            if (s.off[m] <= f) c0 = m; else c1 = m;
+        }
+        s.cand[f] = base[(int64_t)c0 * CAP + LSC + region * LLR + (f - s.off[c0])];
+    }
+    __syncthreads();
+    bin_sort_desc((int)tot, s);
+    return (int)tot;
+}
+
+// A row-wide sum over the segments' published scalar (fp64 bits at cnt_slot), in a fixed order (deterministic).
+__device__ __forceinline__ double sum_slots_f64(const Args& a, int row, int sl, Shared& s) {
+    const uint64_t* base = a.cand + (int64_t)row * a.nseg * CAP;
+    double v = 0.0;
+    for (int j = threadIdx.x; j < a.nseg; j += BLOCK) v += __longlong_as_double((long long)base[(int64_t)j * CAP + sl]);
+    return block_sum_f64(v, s.red);
+}
+__device__ __forceinline__ uint64_t sum_slots_u64(const Args& a, int row, int sl, Shared& s) {
+    const uint64_t* base = a.cand + (int64_t)row * a.nseg * CAP;
+    uint64_t v = 0ull;
+    for (int j = threadIdx.x; j < a.nseg; j += BLOCK) v += base[(int64_t)j * CAP + sl];
+    uint64_t tot;
+    (void)block_excl_scan<uint64_t>(v, s.red.u64b, &tot);
+    return tot;
+}
+
+// This segment's part of a large row (see above).
+__device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, int seg, Shared& s, const SegStart& g) {
+    const int tid = threadIdx.x;
+    const int row = rc.row, nseg = a.nseg;
+    const fs_row_params& p = rc.p;
+    const int lo0 = g.seg_lo;
+    const int hi = seg == nseg - 1 ? a.V : lo0 + g.ntiles * TILE;      // the last segment takes the partial tile
+    uint64_t* my = a.cand + ((int64_t)row * nseg + seg) * CAP;
+    const uint64_t* slot0 = a.cand + (int64_t)row * nseg * CAP;
+    if (ld_agent(a.dirty) != 0) return;                 // a dirty context: the merge samples the row alone
+    if (seg == 0 && tid == 0) my[LS_STATUS] = 0ull;
+    if (rc.pen) gather_window(a, rc, lo0, hi, s);
+    // ---- P1: extremes, ordered count, coarse-bin counts of the k-th's search (k < V)
+    const bool need_kth = rc.k < a.V;
+    uint32_t* hc = reinterpret_cast<uint32_t*>(s.cand);  // [LB]
+    if (need_kth) {
+        for (int i = tid; i < LB; i += BLOCK) hc[i] = 0u;
+        __syncthreads();
+    }
+    uint64_t cmax = 0ull, cmin = ~0ull;
+    uint32_t nv = 0u;
+    seg_elems(a, rc, s, lo0, hi, [&](bool ok, float, uint32_t kq, uint64_t c) {
+        if (ok) {
+            cmax = c > cmax ? c : cmax;
+            cmin = c < cmin ? c : cmin;
+            ++nv;
+            if (need_kth) atomicAdd(&hc[kq >> LB_SHIFT], 1u);
+        }
+    });
+    FS_MARK(1);                                          // P1 streamed
     cmax = block_max_u64(cmax, s.red);
     cmin = block_min_u64(cmin, s.red);
-    uint32_t tot;
-    (void)block_excl_scan<uint32_t>(nv, s.wsum, &tot);
-    if (tid == 0) {
-        const int64_t slot = (int64_t)rc.row * a.nseg + seg;
-        a.cand[slot * CAP] = cmax;
-        a.cand[slot * CAP + 1] = cmin;
-        a.meta[2 * slot] = 0u;
-        a.meta[2 * slot + 1] = tot;
+    uint32_t nseg_v;
+    (void)block_excl_scan<uint32_t>(nv, s.wsum, &nseg_v);
+    uint32_t* rh = a.rhist + (int64_t)row * RBINS;
+    if (need_kth)
+        for (int i = tid; i < LB; i += BLOCK)
+            if (hc[i] != 0u) __hip_atomic_fetch_add(rh + i, hc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (tid == 0) { my[LS_MAX] = cmax; my[LS_MIN] = cmin; my[LS_NV] = nseg_v; }
+    if (!row_sync(a, row, (uint32_t)nseg, s)) return;
+    // row-wide: extremes, count; the k-th's coarse bin from the row histogram
+    {
+        uint64_t mx_ = 0ull, mn_ = ~0ull, nv_ = 0ull;
+        for (int j = tid; j < nseg; j += BLOCK) {
+            const uint64_t* sl = a.cand + ((int64_t)row * nseg + j) * CAP;
+            mx_ = sl[LS_MAX] > mx_ ? sl[LS_MAX] : mx_;
+            mn_ = sl[LS_MIN] < mn_ ? sl[LS_MIN] : mn_;
+            nv_ += sl[LS_NV];
+        }
+        cmax = block_max_u64(mx_, s.red);
+        cmin = block_min_u64(mn_, s.red);
+        uint64_t t_;
+        (void)block_excl_scan<uint64_t>(nv_, s.red.u64b, &t_);
+        nv = (uint32_t)t_;
     }
-    __syncthreads();                                     // LDS is reused by the caller
+    const uint32_t ntot = nv;
+    if (ntot == 0u) {                                    // every logit NaN: no order to sample from
+        if (seg == 0 && tid == 0) { my[LS_TOK] = 0ull; my[LS_STATUS] = 1ull; }
+        return;
+    }
+    const uint32_t kmax = comp_key(cmax);
+    const float mx = val_of(kmax);
+    const double Td = (double)p.temperature;
+    const int keff = (uint32_t)rc.k < ntot ? rc.k : (int)ntot;
+    uint32_t bk = 0xFFFFFFFFu, abk = 0u;                 // the k-th's coarse bin (none: every element a candidate)
+    if ((uint32_t)keff < ntot) {
+        uint32_t cv[LPT];
+#pragma unroll
+        for (int j = 0; j < LPT; ++j) {
+            const int b = LB - 1 - (LPT * tid + j);
+            cv[j] = b <= (int)(0xFF800000u >> LB_SHIFT) ? rh[b] : 0u;   // the counters above the keys are not counts
+        }
+        const int dk = desc_locate<uint32_t>(cv, (uint32_t)keff, &abk, s.wsum, s);
+        if (dk < 0) { row_abandon(a, row); return; }    // uniform (the counts disagree with ntot: never expected)
+        bk = (uint32_t)(LB - 1 - dk);
+    }
+    // ---- P2: candidate masses above bk, bin bk gathered
+    uint64_t* hm = reinterpret_cast<uint64_t*>(s.cand);  // [LB] fixed-point masses
+    for (int i = tid; i < LB; i += BLOCK) hm[i] = 0ull;
+    if (tid == 0) s.count = 0u;
+    __syncthreads();
+    // An element whose mass exp((v - mx) / T) is below e^-32 (1.3e-14) adds 0 to the fixed-point histogram (2^-44
+    // units) and at most 262144 * 1.3e-14 to S (>= 1) altogether: it takes a single-precision exp (relative error
+    // ~1e-7 of a negligible term) instead of the fp64 one, so S stays within ~1e-14 relative of the exact sum.
+    double part = 0.0;
+    float part_tiny = 0.0f;
+    const float inv_tf = 1.0f / p.temperature;
+    uint64_t* regA = my + LSC;
+    seg_elems(a, rc, s, lo0, hi, [&](bool ok, float x, uint32_t kq, uint64_t c) {
+        const uint32_t b = kq >> LB_SHIFT;
+        if (ok && (bk == 0xFFFFFFFFu || b > bk)) {
+            const float d = x - mx;                      // fp32 subtraction, as ferro
+            const float zf = d * inv_tf;
+            if (!(zf < -32.0f)) {                    // (NaN, from inf - inf, stays on the exact path)
+                const double m = exp((double)d / Td);
+                part += m;
+                atomicAdd(reinterpret_cast<unsigned long long*>(&hm[b]), (unsigned long long)(m * FXS + 0.5));
+            } else {
+                part_tiny += __expf(zf);
+            }
+        }
+        wave_append(ok && b == bk, c, regA, &s.count, (uint32_t)LLR);
+    });
+    part += (double)part_tiny;
+    FS_MARK(2);                                          // P2 streamed
+    const double shi = block_sum_f64(part, s.red);      // its barriers also complete the LDS histogram
+    uint64_t* rm = a.rmass + (int64_t)row * LB;
+    for (int i = tid; i < LB; i += BLOCK)
+        if (hm[i] != 0ull) __hip_atomic_fetch_add(rm + i, hm[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (tid == 0) {
+        my[LS_SHI] = (uint64_t)__double_as_longlong(shi);
+        my[LS_NBK] = s.count;
+    }
+    if (!row_sync(a, row, 2u * (uint32_t)nseg, s)) return;
+    double S = sum_slots_f64(a, row, LS_SHI, s);
+    uint64_t Xk = cmin;
+    uint64_t fx_bk = 0ull;                               // fixed-point mass of bin bk's candidates
+    if (bk != 0xFFFFFFFFu) {
+        const int n = load_lists(a, row, 0, LS_NBK, s);
+        const int need = keff - (int)abk;                // >= 1: the k-th lies in bin bk
+        if (n < need || need < 1) { row_abandon(a, row); return; }   // uniform
+        Xk = s.cand[need - 1];
+        double sb = 0.0;
+        uint64_t fb = 0ull;
+        for (int i = tid; i < need; i += BLOCK) {
+            const double m = mass_of(val_of(comp_key(s.cand[i])), mx, Td);
+            sb += m;
+            fb += (uint64_t)(m * FXS + 0.5);
+        }
+        S += block_sum_f64(sb, s.red);
+        uint64_t t_;
+        (void)block_excl_scan<uint64_t>(fb, s.red.u64b, &t_);
+        fx_bk = t_;
+    }
+    FS_MARK(3);                                          // past the second barrier: S and Xk known
+    const uint32_t kk = comp_key(Xk);
+    uint64_t mv[LPT];                                    // the candidates' mass histogram, descending positions
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+        const int b = LB - 1 - (LPT * tid + j);
+        mv[j] = rm[b] + ((uint32_t)b == bk ? fx_bk : 0ull);
+    }
+    // min-p: the smallest key whose pr reaches pr[0] * min_p (pr[0] = 1 / S): a search over keys, no pass
+    uint64_t Xm = 0ull;
+    uint32_t km = 0xFFFFFFFFu;
+    if (p.min_p > 0.0f) {
+        const double thr = (1.0 / S) * (double)p.min_p;
+        auto okm = [&](uint32_t key) { return mass_of(val_of(key), mx, Td) / S >= thr; };
+        if (!okm(kmax)) {
+            Xm = cmax;
+        } else {
+            uint32_t lo = kk, h = kmax;
+            while (lo < h) {
+                const uint32_t mid = lo + ((h - lo) >> 1);
+                if (okm(mid)) h = mid; else lo = mid + 1u;
+            }
+            km = lo;
+            Xm = (uint64_t)lo << 32;
+        }
+    }
+    const bool need_m = p.min_p > 0.0f && Xm != cmax;
+    // ---- P3: top-p's crossing bin gathered, with min-p's counts and masses
+    uint64_t Xc = 0ull;
+    uint32_t keep_c = 0u, cnt_m = 0u;
+    double tot_c = 0.0, sum_m = 0.0;
+    uint64_t cl_m = ~0ull;
+    int nc = -1;
+    uint32_t bc = 0xFFFFFFFFu;
+    uint32_t nsync = 2u;
+    if (p.top_p < 1.0f || need_m) {
+        const double tgt = (double)p.top_p * S;
+        double above_c = 0.0;
+        if (p.top_p < 1.0f) {
+            uint64_t abfx = 0ull;
+            int dc = desc_locate<uint64_t>(mv, (uint64_t)(tgt * FXS), &abfx, s.red.u64b, s);
+            if (dc < 0) dc = LB - 1 - (int)(kk >> LB_SHIFT);   // the total rounds below the target: the last bin
+            bc = (uint32_t)(LB - 1 - dc);
+            above_c = (double)abfx / FXS;
+        }
+        uint32_t my_ca = 0u, my_cm = 0u;
+        double my_sm = 0.0;
+        uint64_t my_cl = ~0ull;
+        if (tid == 0) s.count = 0u;
+        __syncthreads();
+        uint64_t* regB = my + LSC + LLR;
+        seg_elems(a, rc, s, lo0, hi, [&](bool ok, float x, uint32_t kq, uint64_t c) {
+            const bool cand = ok && c >= Xk;
+            if (cand && bc != 0xFFFFFFFFu && (kq >> LB_SHIFT) > bc) ++my_ca;
+            if (cand && need_m && kq >= km) {
+                ++my_cm;
+                my_sm += mass_of(x, mx, Td);
+                my_cl = c < my_cl ? c : my_cl;
+            }
+            wave_append(cand && (kq >> LB_SHIFT) == bc, c, regB, &s.count, (uint32_t)LLR);
+        });
+        uint32_t ca_t, cm_t;
+        (void)block_excl_scan<uint32_t>(my_ca, s.wsum, &ca_t);
+        (void)block_excl_scan<uint32_t>(my_cm, s.wsum, &cm_t);
+        const double sm_t = block_sum_f64(my_sm, s.red);
+        const uint64_t cl_t = block_min_u64(my_cl, s.red);
+        if (tid == 0) {
+            my[LS_NBC] = s.count;
+            my[LS_CA] = ca_t;
+            my[LS_CNTM] = cm_t;
+            my[LS_SUMM] = (uint64_t)__double_as_longlong(sm_t);
+            my[LS_CLM] = cl_t;
+        }
+        nsync = 3u;
+        if (!row_sync(a, row, 3u * (uint32_t)nseg, s)) return;
+        const uint32_t ca_c = (uint32_t)sum_slots_u64(a, row, LS_CA, s);
+        if (need_m) {
+            cnt_m = (uint32_t)sum_slots_u64(a, row, LS_CNTM, s);
+            sum_m = sum_slots_f64(a, row, LS_SUMM, s);
+            uint64_t c_ = ~0ull;
+            for (int j = tid; j < nseg; j += BLOCK) {
+                const uint64_t v = a.cand[((int64_t)row * nseg + j) * CAP + LS_CLM];
+                c_ = v < c_ ? v : c_;
+            }
+            cl_m = block_min_u64(c_, s.red);
+        }
+        if (p.top_p < 1.0f) {
+            nc = load_lists(a, row, 1, LS_NBC, s);
+            if (nc < 0) { row_abandon(a, row); return; }
+            double cum = 0.0;
+            const int ic = large_walk(s, nc, Xk, above_c, tgt, mx, Td, &cum);
+            if (ic < 0) { row_abandon(a, row); return; }   // outside the bin's exact masses: the exact path
+            Xc = s.cand[ic];
+            keep_c = ca_c + (uint32_t)ic + 1u;
+            tot_c = cum;
+        }
+    }
+    // the kept prefix: the largest of the three thresholds (sampler.cpp:43-44)
+    uint64_t Xkeep = Xk, clast = Xk;
+    uint32_t keep = (uint32_t)keff;
+    double tot = S;
+    if (p.min_p > 0.0f && Xm > Xkeep) {
+        Xkeep = Xm;
+        if (Xm == cmax) { keep = 1u; tot = 1.0; clast = cmax; }
+        else { keep = cnt_m; tot = sum_m; clast = cl_m; }
+    }
+    if (p.top_p < 1.0f && Xc > Xkeep) {
+        Xkeep = Xc;
+        keep = keep_c;
+        tot = tot_c;
+        clast = Xc;
+    }
+    // ---- P4: the draw r = u * tot (sampler.cpp:45-49) in its coarse bin
+    const double u = a.u ? a.u[rc.row] : 0.0;
+    const double r = u * tot + 0.0;
+    if (!(r > 0.0)) {                                    // r = 0: ferro's first candidate (r <= pr[0], sampler.cpp:48)
+        if (seg == 0 && tid == 0) {
+            my[LS_TOK] = (uint64_t)comp_id(cmax) | ((uint64_t)keep << 32);
+            my[LS_XK] = Xk;
+            my[LS_S] = (uint64_t)__double_as_longlong(S);
+            my[LS_KEFF] = (uint64_t)keff | ((uint64_t)kmax << 32);
+            my[LS_STATUS] = 1ull;
+        }
+        return;
+    }
+    uint64_t abd = 0ull;
+    const int dd = desc_locate<uint64_t>(mv, (uint64_t)(r * FXS), &abd, s.red.u64b, s);
+    if (dd < 0) { row_abandon(a, row); return; }
+    const uint32_t bd = (uint32_t)(LB - 1 - dd);
+    int nd;
+    if (nc >= 0 && bd == bc) {
+        nd = nc;                                         // the same bin is sorted in LDS already
+    } else {
+        if (tid == 0) s.count = 0u;
+        __syncthreads();
+        uint64_t* regC = my + LSC + 2 * LLR;
+        seg_elems(a, rc, s, lo0, hi, [&](bool ok, float, uint32_t kq, uint64_t c) {
+            wave_append(ok && c >= Xkeep && (kq >> LB_SHIFT) == bd, c, regC, &s.count, (uint32_t)LLR);
+        });
+        if (tid == 0) my[LS_NBD] = s.count;
+        if (!row_sync(a, row, (nsync + 1u) * (uint32_t)nseg, s)) return;
+        nd = load_lists(a, row, 2, LS_NBD, s);
+        if (nd < 0) { row_abandon(a, row); return; }
+    }
+    double cum = 0.0;
+    const int id = large_walk(s, nd, Xkeep, (double)abd / FXS, r, mx, Td, &cum);
+    uint64_t pick = 0ull;
+    if (id >= 0) {
+        pick = s.cand[id];
+    } else if (!(id == -2 && comp_key(Xkeep) >> LB_SHIFT == bd)) {
+        row_abandon(a, row);                             // a rounding step at the bin edge: the exact path
+        return;
+    }
+    if (pick == 0ull) pick = clast;                      // past the last kept candidate
+    if (seg == 0 && tid == 0) {
+        my[LS_TOK] = (uint64_t)comp_id(pick) | ((uint64_t)keep << 32);
+        my[LS_XK] = Xk;
+        my[LS_S] = (uint64_t)__double_as_longlong(S);
+        my[LS_KEFF] = (uint64_t)keff | ((uint64_t)kmax << 32);
+        my[LS_STATUS] = 1ull;
+    }
+    (void)slot0;
 }
 
 // The row's completion counter: the row histogram's last bin, which no ordered key reaches (keys of non-NaN values
@@ -3018,16 +3420,14 @@ __device__ __forceinline__ void merge_role(const Args& a, int mi, Shared& s) {
     }
     FS_MARK(1);
     __syncthreads();
-    if (s.misc_alone) {
-        Pre none = {};
-        merge_row(a, rc, s, none, true);
-        return;
+    const bool alone = s.misc_alone != 0u;
+    Pre pre = {};
+    if (!alone) {
+        l1_invalidate();
+        prefetch_lists(a, row, pre);
+        if (threadIdx.x == 0) *ctr = 0u;             // the bin is left at 0 with the rest of the row histogram
     }
-    l1_invalidate();
-    Pre pre;
-    prefetch_lists(a, row, pre);
-    if (threadIdx.x == 0) *ctr = 0u;                 // the bin is left at 0 with the rest of the row histogram
-    merge_row(a, rc, s, pre);
+    merge_row(a, rc, s, pre, alone);                 // one call site: the merge code is inlined once
 }
 
 // Segment kernel: one (row, segment) item per workgroup (rows sampled with k > KMAX only count themselves done),
@@ -3064,7 +3464,7 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, 
     const SegStart g = seg_start(a, row, seg, buf);   // the tiles are on their way before the parameters
     const RowCtx rc = row_ctx(a, row);
     if (!rc.large) process_segment(a, rc, seg, s, buf, g);
-    else if (rc.k >= a.V) large_segment_extremes(a, rc, seg, s, g);   // the merge role samples the row
+    else large_segment(a, rc, seg, s, g);           // the row's segments sample it together
     vm_drain();                                      // the list and meta stores are in the L2
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_fetch_add(row_counter(a, row), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -3341,6 +3741,7 @@ struct fs_context {
     size_t cand_slots = 0;     // chunk slots of CAP entries
     uint32_t* meta = nullptr;
     uint32_t* rhist = nullptr;  // [row_cap][RBINS]
+    uint64_t* rmass = nullptr;  // [row_cap][LB]
     size_t row_cap = 0;
     uint32_t* stream_cnt = nullptr;
     size_t stream_cap = 0;
@@ -3364,9 +3765,12 @@ int grow(fs_context* c, size_t slots, size_t rows, size_t streams) {
     }
     if (rows > c->row_cap) {
         if (c->rhist) (void)hipFree(c->rhist);
-        c->rhist = nullptr; c->row_cap = 0;
+        if (c->rmass) (void)hipFree(c->rmass);
+        c->rhist = nullptr; c->rmass = nullptr; c->row_cap = 0;
         if (hipMalloc(&c->rhist, rows * fs::RBINS * sizeof(uint32_t)) != hipSuccess) return FS_E_NOMEM;
         if (hipMemset(c->rhist, 0, rows * fs::RBINS * sizeof(uint32_t)) != hipSuccess) return FS_E_HIP;
+        if (hipMalloc(&c->rmass, rows * fs::LB * sizeof(uint64_t)) != hipSuccess) return FS_E_NOMEM;
+        if (hipMemset(c->rmass, 0, rows * fs::LB * sizeof(uint64_t)) != hipSuccess) return FS_E_HIP;
         c->row_cap = rows;
     }
     if (streams > c->stream_cap) {
@@ -3440,7 +3844,7 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
     if (rc != FS_OK) return rc;
     rc = grow(ctx, (size_t)(items > 0 ? items : 1), (size_t)rows, (size_t)(streams > 0 ? streams : 1));
     if (rc != FS_OK) return rc;
-    a.cand = ctx->cand; a.meta = ctx->meta; a.rhist = ctx->rhist;
+    a.cand = ctx->cand; a.meta = ctx->meta; a.rhist = ctx->rhist; a.rmass = ctx->rmass;
     a.stream_cnt = ctx->stream_cnt; a.err = ctx->err; a.dirty = ctx->err + 1; a.merge_spins = ctx->merge_spins;
     a.trace = nullptr;
 #ifdef FS_TRACE
@@ -3457,16 +3861,17 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
 // ------------------------------------------------------------------------------------------------ static workspace
 // fs_sample_batch_static's workspace: one file-scope device array per GPU, held until the process ends, so the
 // call allocates nothing. Layout (bytes): error word and dirty flag | meta [ST_SLOTS][2] | row histograms
-// [ST_ROWS][RBINS] | candidate lists [ST_SLOTS][CAP]. The row histograms (counters included) must be zero when a
-// call starts; the kernels leave them so, and the first call on a device clears them with a fill kernel (no
-// hipMemsetAsync: the call may be recorded into a graph).
+// [ST_ROWS][RBINS] | large rows' mass histograms [ST_ROWS][LB] | candidate lists [ST_SLOTS][CAP]. The row and mass
+// histograms (counters included) must be zero when a call starts; the kernels leave them so, and the first call on a
+// device clears them with a fill kernel (no hipMemsetAsync: the call may be recorded into a graph).
 constexpr int64_t ST_ROWS = 512;                                  // rows per call
 constexpr int64_t ST_SLOTS = 512;                                 // (row, segment) slots per call
 constexpr size_t ST_ERR_OFF = 0;                                  // int32 [2]: error bits, dirty
 constexpr size_t ST_META_OFF = 256;
 constexpr size_t ST_RHIST_OFF = ST_META_OFF + ((ST_SLOTS * 2 * sizeof(uint32_t) + 255) / 256) * 256;
-constexpr size_t ST_CAND_OFF = ST_RHIST_OFF + (size_t)ST_ROWS * fs::RBINS * sizeof(uint32_t);
-constexpr size_t ST_BYTES = ST_CAND_OFF + (size_t)ST_SLOTS * fs::CAP * sizeof(uint64_t);   // 33.8 MB
+constexpr size_t ST_RMASS_OFF = ST_RHIST_OFF + (size_t)ST_ROWS * fs::RBINS * sizeof(uint32_t);
+constexpr size_t ST_CAND_OFF = ST_RMASS_OFF + (size_t)ST_ROWS * fs::LB * sizeof(uint64_t);
+constexpr size_t ST_BYTES = ST_CAND_OFF + (size_t)ST_SLOTS * fs::CAP * sizeof(uint64_t);   // 50.6 MB
 
 static __device__ __align__(256) unsigned char scratch[ST_BYTES];
 
@@ -3495,7 +3900,7 @@ int static_workspace(int dev, hipStream_t st, unsigned char** out) {
         hipLaunchKernelGGL(fs::zero_words_kernel, dim3(1), dim3(256), 0, st, (uint32_t*)(base + ST_ERR_OFF),
                            (int64_t)(ST_META_OFF / 4));
         hipLaunchKernelGGL(fs::zero_words_kernel, dim3(1024), dim3(256), 0, st, (uint32_t*)(base + ST_RHIST_OFF),
-                           (int64_t)ST_ROWS * fs::RBINS);
+                           (int64_t)((ST_CAND_OFF - ST_RHIST_OFF) / 4));   // row and mass histograms
         if (hipGetLastError() != hipSuccess) return FS_E_HIP;
         g_static_ptr[dev] = base;
     }
@@ -3530,6 +3935,7 @@ int fs_destroy(fs_context* c) {
     (void)hipFree(c->cand);
     (void)hipFree(c->meta);
     (void)hipFree(c->rhist);
+    (void)hipFree(c->rmass);
     (void)hipFree(c->stream_cnt);
     (void)hipFree(c->err);
     delete c;
@@ -3581,6 +3987,7 @@ int fs_sample_batch_static(fs_context* ctx, const float* d_logits, int64_t ld, i
     a.err = (int32_t*)(base + ST_ERR_OFF); a.dirty = a.err + 1;
     a.meta = (uint32_t*)(base + ST_META_OFF);
     a.rhist = (uint32_t*)(base + ST_RHIST_OFF);
+    a.rmass = (uint64_t*)(base + ST_RMASS_OFF);
     a.cand = (uint64_t*)(base + ST_CAND_OFF);
     a.stream_cnt = nullptr;                          // sampling mode has no verify streams
     a.merge_spins = ctx->merge_spins;
@@ -3690,6 +4097,8 @@ int fs_device_error(fs_context* ctx, void* stream, int32_t* bits) {
             // row histograms and counters are cleared and the context leaves its compute-alone mode
             if (ctx->rhist && hipMemset(ctx->rhist, 0, ctx->row_cap * fs::RBINS * sizeof(uint32_t)) != hipSuccess)
                 return FS_E_HIP;
+            if (ctx->rmass && hipMemset(ctx->rmass, 0, ctx->row_cap * fs::LB * sizeof(uint64_t)) != hipSuccess)
+                return FS_E_HIP;
             if (ctx->stream_cnt && hipMemset(ctx->stream_cnt, 0, ctx->stream_cap * sizeof(uint32_t)) != hipSuccess)
                 return FS_E_HIP;
         }
@@ -3706,8 +4115,7 @@ int fs_device_error(fs_context* ctx, void* stream, int32_t* bits) {
             int32_t h[2] = {0, 0};
             if (hipMemcpy(h, base + ST_ERR_OFF, sizeof(h), hipMemcpyDeviceToHost) != hipSuccess) return FS_E_HIP;
             *bits |= h[0];
-            if (h[1] != 0 &&
-                hipMemset(base + ST_RHIST_OFF, 0, (size_t)ST_ROWS * fs::RBINS * sizeof(uint32_t)) != hipSuccess)
+            if (h[1] != 0 && hipMemset(base + ST_RHIST_OFF, 0, ST_CAND_OFF - ST_RHIST_OFF) != hipSuccess)
                 return FS_E_HIP;
             if (hipMemset(base + ST_ERR_OFF, 0, sizeof(h)) != hipSuccess) return FS_E_HIP;
         }

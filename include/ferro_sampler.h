@@ -87,7 +87,7 @@ int fs_sample_batch(fs_context* ctx, const float* d_logits, int64_t ld, int32_t 
  * device memory during a call - code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
  * Same arguments, semantics and outputs as fs_sample_batch; ctx only carries settings (fs_set_wait_limit) and
  * error reporting (fs_device_error reads and clears this workspace's error bits too). The workspace is one static
- * device array per GPU (33.8 MB, held until the process ends), shared by every context on that GPU: calls that
+ * device array per GPU (50.3 MB, held until the process ends), shared by every context on that GPU: calls that
  * overlap in time on one GPU race (serialise them on one stream). Limits: B <= 512 rows and at most 512
  * (row, segment) slots, i.e. 2 per compute unit on MI355X; beyond them the call returns FS_E_LIMIT and launches
  * nothing. The first call on a device also enqueues a clear of the workspace on `stream`. */
