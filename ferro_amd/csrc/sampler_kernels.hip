@@ -103,9 +103,9 @@ struct Args {
 
 // Phase timestamps (FS_TRACE builds only; the product library compiles these to nothing): thread 0 of a workgroup
 // keeps the constant 100 MHz clock (s_memrealtime) of phase i in LDS (no memory store, so no wait on the memory
-// counter in the middle of the kernel) and writes them to trace[blockIdx * TRACE_W + i] at its end; slots 5-7 hold
+// counter in the middle of the kernel) and writes them to trace[blockIdx * TRACE_W + i] at its end; slots 13-15 hold
 // the role (1 segment, 2 merge), the row and the segment.
-constexpr int TRACE_W = 8;
+constexpr int TRACE_W = 16;
 #ifdef FS_TRACE
 #define FS_MARK(i)                                                                                        \
     do {                                                                                                  \
@@ -607,7 +607,7 @@ struct Shared {
     uint32_t nids;
     uint32_t misc_alone;               // merge role: the row is computed from its logits alone
 #ifdef FS_TRACE
-    uint64_t trace_t[8];               // this workgroup's phase timestamps (written to a.trace at its end)
+    uint64_t trace_t[16];              // this workgroup's phase timestamps (written to a.trace at its end)
 #endif
     Red red;
     __device__ __forceinline__ uint32_t* cnt() { return scr; }
@@ -2957,8 +2957,10 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
 // one sort, a target outside its bin's exact masses, or a barrier that waits too long abandons the row (a flag on
 // the barrier counter); the merging workgroup then samples it alone with large_row (exact).
 // Arrive and wait until `target` arrivals (every segment of the row at this barrier). This workgroup's stores and
-// atomics complete first (vmcnt(0)); after the wait its L1 is invalidated at agent scope (buffer_inv sc1; device
-// memory's L2 lines are kept), so the others' published data is read from the XCD's L2. The poll is an atomic that is not idempotent (it executes in the L2). Bounded: past
+// atomics complete first (vmcnt(0)). No cache maintenance follows: what the others published lies in lines that no
+// workgroup of the row reads before this barrier (their own lines per phase, see the slot layout), so this CU's L1
+// holds no copy of them and the loads are served by the XCD's L2. (An agent-scope invalidate, buffer_inv sc1, cost
+// about 10 us per barrier here.) The poll is an atomic that is not idempotent (it executes in the L2). Bounded: past
 // a.merge_spins polls the row is abandoned. Returns false when the row is abandoned.
 __device__ __forceinline__ bool row_sync(const Args& a, int row, uint32_t target, Shared& s) {
     vm_drain();
@@ -2982,15 +2984,16 @@ __device__ __forceinline__ bool row_sync(const Args& a, int row, uint32_t target
     }
     __syncthreads();
     const bool ok = s.red.misc[4] != 0u;
-    asm volatile("buffer_inv sc1" ::: "memory");         // drop this CU's L1 lines (agent scope)
     __syncthreads();                                     // misc[4] is reused by the next barrier
     return ok;
 }
 
 // One pass over a large-row segment's tiles [lo0, hi) (the last segment also takes the row's partial tile), two
 // tiles in flight, softcap and penalties applied: f(x, key, composite) per ordered element. Ends with a barrier.
+// bmp: a repetition penalty alone, from a bitmap of the window's ids over the segment (bit i = id lo0 + i; a
+// thread's four consecutive logits share a word), else the per-tile count table (s.ids holds the window's ids).
 template <class F>
-__device__ __forceinline__ void seg_elems(const Args& a, const RowCtx& rc, Shared& s, int lo0, int hi, F f) {
+__device__ __forceinline__ void seg_elems(const Args& a, const RowCtx& rc, Shared& s, int lo0, int hi, bool bmp, F f) {
     const float* rowp = a.logits + (int64_t)rc.row * a.ld;
     const int nt = (hi - lo0 + TILE - 1) / TILE;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(rowp + lo0), (short)0,
@@ -3009,7 +3012,22 @@ __device__ __forceinline__ void seg_elems(const Args& a, const RowCtx& rc, Share
             if (t < nt) {
                 const int lo = lo0 + t * TILE;
                 if (rc.capped) softcap_vals(x, rc.p.softcap);
-                if (rc.pen) {
+                if (rc.pen && bmp) {
+                    const uint32_t* bm = reinterpret_cast<const uint32_t*>(s.ids);
+                    const float rp = rc.p.repetition_penalty;
+#pragma unroll
+                    for (int j = 0; j < NV; ++j) {
+                        const uint32_t rel = (uint32_t)(lo - lo0) + (uint32_t)(j * BLOCK + (int)threadIdx.x) * 4u;
+                        const uint32_t nib = (bm[rel >> 5] >> (rel & 31u)) & 0xFu;
+                        if (nib != 0u) {
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                const float l = x[4 * j + q];
+                                if ((nib >> q) & 1u) x[4 * j + q] = l > 0.0f ? __fdiv_rn(l, rp) : __fmul_rn(l, rp);
+                            }
+                        }
+                    }
+                } else if (rc.pen) {
                     __syncthreads();                     // the previous tile's table reads are done
                     apply_penalties(x, a, rc, lo, s);
                 }
@@ -3090,7 +3108,21 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
     const uint64_t* slot0 = a.cand + (int64_t)row * nseg * CAP;
     if (ld_agent(a.dirty) != 0) return;                 // a dirty context: the merge samples the row alone
     if (seg == 0 && tid == 0) my[LS_STATUS] = 0ull;
-    if (rc.pen) gather_window(a, rc, lo0, hi, s);
+    // Penalties: a repetition penalty alone as an exact bitmap of the window's ids over this segment (in s.ids, built
+    // once for every pass), frequency / presence with the per-tile count table over the gathered window.
+    const bool bmpen = rc.pen && rc.rep_on && !rc.fp_on && ((hi - lo0 + TILE - 1) / TILE) * TILE <= 32 * WIDS;
+    if (bmpen) {
+        uint32_t* bm = reinterpret_cast<uint32_t*>(s.ids);
+        for (int i = tid; i < WIDS; i += BLOCK) bm[i] = 0u;
+        __syncthreads();
+        for (int64_t i = rc.b + tid; i < rc.len; i += BLOCK) {
+            const int id = hist_at(a, rc, i);
+            if (id >= lo0 && id < hi) atomicOr(&bm[(uint32_t)(id - lo0) >> 5], 1u << ((uint32_t)(id - lo0) & 31u));
+        }
+        __syncthreads();
+    } else if (rc.pen) {
+        gather_window(a, rc, lo0, hi, s);
+    }
     // ---- P1: extremes, ordered count, coarse-bin counts of the k-th's search (k < V)
     const bool need_kth = rc.k < a.V;
     uint32_t* hc = reinterpret_cast<uint32_t*>(s.cand);  // [LB]
@@ -3100,7 +3132,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
     }
     uint64_t cmax = 0ull, cmin = ~0ull;
     uint32_t nv = 0u;
-    seg_elems(a, rc, s, lo0, hi, [&](bool ok, float, uint32_t kq, uint64_t c) {
+    seg_elems(a, rc, s, lo0, hi, bmpen, [&](bool ok, float, uint32_t kq, uint64_t c) {
         if (ok) {
             cmax = c > cmax ? c : cmax;
             cmin = c < cmin ? c : cmin;
@@ -3119,6 +3151,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
             if (hc[i] != 0u) __hip_atomic_fetch_add(rh + i, hc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (tid == 0) { my[LS_MAX] = cmax; my[LS_MIN] = cmin; my[LS_NV] = nseg_v; }
     if (!row_sync(a, row, (uint32_t)nseg, s)) return;
+    FS_MARK(5);                                          // past the first barrier
     // row-wide: extremes, count; the k-th's coarse bin from the row histogram
     {
         uint64_t mx_ = 0ull, mn_ = ~0ull, nv_ = 0ull;
@@ -3156,6 +3189,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
         bk = (uint32_t)(LB - 1 - dk);
     }
     // ---- P2: candidate masses above bk, bin bk gathered
+    FS_MARK(6);                                          // P2 starts
     uint64_t* hm = reinterpret_cast<uint64_t*>(s.cand);  // [LB] fixed-point masses
     for (int i = tid; i < LB; i += BLOCK) hm[i] = 0ull;
     if (tid == 0) s.count = 0u;
@@ -3167,7 +3201,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
     float part_tiny = 0.0f;
     const float inv_tf = 1.0f / p.temperature;
     uint64_t* regA = my + LSC;
-    seg_elems(a, rc, s, lo0, hi, [&](bool ok, float x, uint32_t kq, uint64_t c) {
+    seg_elems(a, rc, s, lo0, hi, bmpen, [&](bool ok, float x, uint32_t kq, uint64_t c) {
         const uint32_t b = kq >> LB_SHIFT;
         if (ok && (bk == 0xFFFFFFFFu || b > bk)) {
             const float d = x - mx;                      // fp32 subtraction, as ferro
@@ -3193,6 +3227,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
         my[LS_NBK] = s.count;
     }
     if (!row_sync(a, row, 2u * (uint32_t)nseg, s)) return;
+    FS_MARK(7);                                          // past the second barrier
     double S = sum_slots_f64(a, row, LS_SHI, s);
     uint64_t Xk = cmin;
     uint64_t fx_bk = 0ull;                               // fixed-point mass of bin bk's candidates
@@ -3247,6 +3282,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
     uint64_t cl_m = ~0ull;
     int nc = -1;
     uint32_t bc = 0xFFFFFFFFu;
+    uint32_t bd_pred = 0xFFFFFFFFu;                      // the draw's bin, when P3 can gather it too
     uint32_t nsync = 2u;
     if (p.top_p < 1.0f || need_m) {
         const double tgt = (double)p.top_p * S;
@@ -3257,14 +3293,29 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
             if (dc < 0) dc = LB - 1 - (int)(kk >> LB_SHIFT);   // the total rounds below the target: the last bin
             bc = (uint32_t)(LB - 1 - dc);
             above_c = (double)abfx / FXS;
+            if (p.min_p <= 0.0f) {
+                // Without min-p the kept total lies in [tgt, min(S, tgt + the largest mass in bin bc)] (top-p keeps
+                // through the crossing candidate, sampler.cpp:44). When the draw u * tot falls in one coarse bin over
+                // that whole range, this pass gathers that bin too and no draw pass is needed.
+                const uint32_t top_key = ((bc << LB_SHIFT) | ((1u << LB_SHIFT) - 1u)) < kmax
+                                             ? ((bc << LB_SHIFT) | ((1u << LB_SHIFT) - 1u)) : kmax;
+                const double mhi = mass_of(val_of(top_key), mx, Td);
+                const double thi = tgt + mhi < S ? tgt + mhi : S;
+                const double u0 = a.u ? a.u[rc.row] : 0.0;
+                uint64_t ab_;
+                const int d0 = desc_locate<uint64_t>(mv, (uint64_t)(u0 * tgt * (1.0 - 1e-12) * FXS), &ab_, s.red.u64b, s);
+                const int d1 = desc_locate<uint64_t>(mv, (uint64_t)(u0 * thi * (1.0 + 1e-12) * FXS), &ab_, s.red.u64b, s);
+                if (d0 >= 0 && d0 == d1 && (uint32_t)(LB - 1 - d0) != bc) bd_pred = (uint32_t)(LB - 1 - d0);
+            }
         }
         uint32_t my_ca = 0u, my_cm = 0u;
         double my_sm = 0.0;
         uint64_t my_cl = ~0ull;
-        if (tid == 0) s.count = 0u;
+        if (tid == 0) { s.count = 0u; s.tmax = 0u; }
         __syncthreads();
         uint64_t* regB = my + LSC + LLR;
-        seg_elems(a, rc, s, lo0, hi, [&](bool ok, float x, uint32_t kq, uint64_t c) {
+        uint64_t* regC = my + LSC + 2 * LLR;
+        seg_elems(a, rc, s, lo0, hi, bmpen, [&](bool ok, float x, uint32_t kq, uint64_t c) {
             const bool cand = ok && c >= Xk;
             if (cand && bc != 0xFFFFFFFFu && (kq >> LB_SHIFT) > bc) ++my_ca;
             if (cand && need_m && kq >= km) {
@@ -3273,6 +3324,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
                 my_cl = c < my_cl ? c : my_cl;
             }
             wave_append(cand && (kq >> LB_SHIFT) == bc, c, regB, &s.count, (uint32_t)LLR);
+            wave_append(cand && (kq >> LB_SHIFT) == bd_pred, c, regC, &s.tmax, (uint32_t)LLR);
         });
         uint32_t ca_t, cm_t;
         (void)block_excl_scan<uint32_t>(my_ca, s.wsum, &ca_t);
@@ -3285,9 +3337,12 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
             my[LS_CNTM] = cm_t;
             my[LS_SUMM] = (uint64_t)__double_as_longlong(sm_t);
             my[LS_CLM] = cl_t;
+            my[LS_NBD] = s.tmax;
         }
+        FS_MARK(8);                                      // P3 streamed
         nsync = 3u;
         if (!row_sync(a, row, 3u * (uint32_t)nseg, s)) return;
+        FS_MARK(9);                                      // past the third barrier
         const uint32_t ca_c = (uint32_t)sum_slots_u64(a, row, LS_CA, s);
         if (need_m) {
             cnt_m = (uint32_t)sum_slots_u64(a, row, LS_CNTM, s);
@@ -3345,15 +3400,20 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
     int nd;
     if (nc >= 0 && bd == bc) {
         nd = nc;                                         // the same bin is sorted in LDS already
+    } else if (bd == bd_pred) {
+        nd = load_lists(a, row, 2, LS_NBD, s);           // gathered by P3
+        if (nd < 0) { row_abandon(a, row); return; }
     } else {
         if (tid == 0) s.count = 0u;
         __syncthreads();
         uint64_t* regC = my + LSC + 2 * LLR;
-        seg_elems(a, rc, s, lo0, hi, [&](bool ok, float, uint32_t kq, uint64_t c) {
+        seg_elems(a, rc, s, lo0, hi, bmpen, [&](bool ok, float, uint32_t kq, uint64_t c) {
             wave_append(ok && c >= Xkeep && (kq >> LB_SHIFT) == bd, c, regC, &s.count, (uint32_t)LLR);
         });
         if (tid == 0) my[LS_NBD] = s.count;
+        FS_MARK(10);                                     // P4 streamed
         if (!row_sync(a, row, (nsync + 1u) * (uint32_t)nseg, s)) return;
+        FS_MARK(11);                                     // past the last barrier
         nd = load_lists(a, row, 2, LS_NBD, s);
         if (nd < 0) { row_abandon(a, row); return; }
     }
@@ -3395,7 +3455,7 @@ constexpr uint32_t MERGE_SPINS = 1u << 20;   // bounded wait of the merge role (
 __device__ __forceinline__ void merge_role(const Args& a, int mi, Shared& s) {
     const int row = mi % XCDS + XCDS * (mi / XCDS);
     if (row >= a.B) return;
-    FS_TAG(5, 2); FS_TAG(6, row); FS_TAG(7, 0);
+    FS_TAG(13, 2); FS_TAG(14, row); FS_TAG(15, 0);
     const RowCtx rc = row_ctx(a, row);               // the row's inputs are read while the segments run
     uint32_t* ctr = row_counter(a, row);
     if (threadIdx.x == 0) {
@@ -3446,7 +3506,8 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, 
     // share one XCD and its L2 (the row histogram). Slots past the last row return at once.
     const unsigned seg_grid = (unsigned)(XCDS * a.nseg * ((a.B + XCDS - 1) / XCDS));
     FS_MARK(0);
-    FS_TAG(1, 0); FS_TAG(2, 0); FS_TAG(3, 0); FS_TAG(5, 0);
+    for (int i_ = 1; i_ < 13; ++i_) FS_TAG(i_, 0);
+    FS_TAG(13, 0);
     if (blockIdx.x >= seg_grid) {
         merge_role(a, (int)(blockIdx.x - seg_grid), s);
         FS_MARK(4);
@@ -3459,7 +3520,7 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, 
     const int seg = j - q * a.nseg;
     const int row = x + XCDS * q;
     if (row >= a.B) return;
-    FS_TAG(5, 1); FS_TAG(6, row); FS_TAG(7, seg);
+    FS_TAG(13, 1); FS_TAG(14, row); FS_TAG(15, seg);
     float buf[PF][TPT];
     const SegStart g = seg_start(a, row, seg, buf);   // the tiles are on their way before the parameters
     const RowCtx rc = row_ctx(a, row);

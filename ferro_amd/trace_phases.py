@@ -6,6 +6,7 @@ product library): thread 0 of every workgroup stores the GPU's constant 100 MHz 
 Segment workgroups (one per (row, segment) item): 0 start, 1 tile 0 arrived, 2 tile 0 done (penalty, first bound,
 appends, check), 3 last tile done, 4 list published and counted. Merging workgroups (one per row): 0 start, 1 the
 row's segments seen done, 2 candidates gathered (short merge), 3 candidates ranked (short merge), 4 row finished.
+Slots 5-11 time the large-row passes of the segments (see sampler_kernels.hip); slots 13-15 tag role, row, segment.
 
 Usage (on a GPU):  python ferro_amd/trace_phases.py --workload cfg3 [--calls 5]
 Prints a markdown table: when each phase happens (µs from the first workgroup's start; min / median / max over the
@@ -26,7 +27,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 TRACE_LIB = os.path.join(PKG, "libferro_sampler_trace.so")
-TRACE_W = 8
+TRACE_W = 16
 TICK_US = 0.01                                    # s_memrealtime: 100 MHz
 
 
@@ -61,11 +62,11 @@ def one_call(L, ctx, w, entry, bufs, dev_in, trace, i, torch):
 
 def phases(tr):
     """tr: [grid, TRACE_W] uint64 of one call -> dict of per-workgroup arrays (µs from the first start)."""
-    role = tr[:, 5]
+    role = tr[:, 13]
     t0 = tr[role > 0, 0].min()
     rel = (tr[:, :5].astype(np.int64) - np.int64(t0)) * TICK_US
     seg, mer = role == 1, role == 2
-    out = {"seg": rel[seg], "seg_row": tr[seg, 6], "mer": rel[mer], "mer_row": tr[mer, 6],
+    out = {"seg": rel[seg], "seg_row": tr[seg, 14], "mer": rel[mer], "mer_row": tr[mer, 14],
            "mer_set": tr[mer, :5] != 0}
     return out
 
@@ -153,7 +154,7 @@ def main():
         torch.cuda.synchronize()
         L.fs_trace_set(ctx, None, 0)
         tr = trace.cpu().numpy().view(np.uint64).reshape(-1, TRACE_W)
-        used = tr[:, 5] > 0
+        used = tr[:, 13] > 0
         n = int(np.nonzero(used)[0].max()) + 1 if used.any() else 0
         if n == 0:
             raise RuntimeError("nothing traced (grid larger than the trace buffer?)")
