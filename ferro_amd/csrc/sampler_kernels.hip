@@ -869,6 +869,13 @@ __device__ __forceinline__ float host_tanhf(float x) {
 // fp32 divide, the host C library's tanhf, fp32 multiply), before the penalties as in ferro, where the model caps
 // the row first. Bit-identical to the host loop.
 __device__ __forceinline__ float softcap_one(float l, float cap) { return __fmul_rn(cap, host_tanhf(__fdiv_rn(l, cap))); }
+// Unrolled, for the streaming loop of the segment path (its three call sites): a rolled loop there changes the
+// allocation of the tile registers and slows every row, capped or not.
+template <int N>
+__device__ __forceinline__ void softcap_vals_unrolled(float (&x)[N], float cap) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] = softcap_one(x[i], cap);
+}
 // A rolled loop: one copy of the cap per call site (there are dozens, all unrolled eight-wide otherwise), for capped
 // rows only; the element is picked and put back by index.
 template <int N>
@@ -2741,7 +2748,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     x[4 * j] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
                 }
             }
-            if (rc.capped) softcap_vals(x, rc.p.softcap);
+            if (rc.capped) softcap_vals_unrolled(x, rc.p.softcap);
             if (slowpen) apply_penalties(x, a, rc, lo, s);
             if (fastpen) bitmap_pen(x, lo);
             if (rc.greedy) {
@@ -2842,7 +2849,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 const bool live = tt < ntiles && !overflow;
                 if (live) {
                     const int lo = seg_lo + tt * TILE;
-                    if (rc.capped) softcap_vals(x, rc.p.softcap);
+                    if (rc.capped) softcap_vals_unrolled(x, rc.p.softcap);
                     if (slowpen) apply_penalties(x, a, rc, lo, s);
                     if (fastpen) bitmap_pen(x, lo);
                     if (p == 0 && take1) raise_key(row_bound(snap1, k));
