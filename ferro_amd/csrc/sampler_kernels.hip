@@ -88,7 +88,8 @@ struct Args {
     int eos;
     int32_t* accepted;
     int mode;
-    int nseg;                      // segments per row
+    int nseg;                      // segments per row (the default layout)
+    int balance;                   // nonzero: each XCD splits its workgroups among its rows by the rows' cost
     int seg_tiles;                 // tiles per segment
     uint64_t* cand;                // [B*nseg][CAP]
     uint32_t* meta;                // [B*nseg][2]: lower bound of the k-th key, count
@@ -712,7 +713,13 @@ struct RowCtx {
     int k;
     int64_t hA0, lenA, lenB, b, len;     // window [b, len) over the concatenated history
     const int32_t* segB;
+    // the row's segments: nseg of st tiles each (the last may be shorter); segment s publishes in list slot
+    // lx + XCDS * (lbase + s) (the index of the segment workgroup that streams it)
+    int nseg, st, lbase, lx;
 };
+__device__ __forceinline__ int64_t slot_of(const RowCtx& rc, int seg) {
+    return (int64_t)rc.lx + (int64_t)XCDS * (int64_t)(rc.lbase + seg);
+}
 
 // Inputs that no kernel writes (params, history offsets, verify row offsets) are read through the constant address
 // space, so uniform indices become scalar loads (lgkmcnt) and never wait behind the vector loads in flight.
@@ -729,6 +736,10 @@ __device__ __forceinline__ RowCtx row_ctx(const Args& a, int row) {
     RowCtx rc;
     rc.row = row;
     rc.pidx = row;
+    rc.nseg = a.nseg;
+    rc.st = a.seg_tiles;
+    rc.lx = row % XCDS;
+    rc.lbase = (row / XCDS) * a.nseg;
     rc.hA0 = 0; rc.lenA = 0; rc.lenB = 0;
     rc.segB = nullptr;
     if (a.mode == MODE_VERIFY) {
@@ -794,10 +805,11 @@ __device__ __forceinline__ void load_tile(float (&x)[TPT], const float* rowp, in
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ f32x4 raw_buffer_load_f32x4(__amdgpu_buffer_rsrc_t rs, int voffset, int soffset, int aux)
     __asm("llvm.amdgcn.raw.ptr.buffer.load.v4f32");
+template <int AUX = 0>
 __device__ __forceinline__ void load_seg_tile(float (&x)[TPT], __amdgpu_buffer_rsrc_t rs, int t) {
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const f32x4 v = raw_buffer_load_f32x4(rs, (j * BLOCK + (int)threadIdx.x) * 16, t * TILE * 4, 0);
+        const f32x4 v = raw_buffer_load_f32x4(rs, (j * BLOCK + (int)threadIdx.x) * 16, t * TILE * 4, AUX);
         x[4 * j + 0] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
     }
 }
@@ -1792,14 +1804,15 @@ struct Pre {
     float l0;                              // the row's first logit (a NaN there is ferro's greedy answer)
 };
 
-__device__ __forceinline__ void prefetch_lists(const Args& a, int row, Pre& pre) {
-    const int nseg = a.nseg;
+__device__ __forceinline__ void prefetch_lists(const Args& a, const RowCtx& rc, Pre& pre) {
+    const int row = rc.row;
+    const int nseg = rc.nseg;
     const int tid = threadIdx.x;
     pre.tps = nseg > 0 ? BLOCK / nseg : 0;    // >= 1: the host keeps nseg < BLOCK
     pre.c_me = nseg > 0 ? tid % nseg : 0;
     pre.r_me = nseg > 0 ? tid / nseg : 0;
     pre.act = nseg > 0 && pre.r_me < pre.tps;
-    const int64_t slot = (int64_t)row * nseg + pre.c_me;
+    const int64_t slot = slot_of(rc, pre.c_me);
     const uint64_t* lst = a.cand + slot * CAP;
     pre.u = a.u ? ld_const(a.u + row) : 0.0;
     pre.l0 = ld_const(a.logits + (int64_t)row * a.ld);
@@ -1872,7 +1885,7 @@ __device__ __forceinline__ bool merge_fast(const Args& a, const RowCtx& rc, Shar
                                            int& keep) {
     const int tid = threadIdx.x;
     const int k = rc.k;
-    if (a.nseg > FAST_SEGS) return false;
+    if (rc.nseg > FAST_SEGS) return false;
     const uint32_t cmax = wave_max(pre.cnm);
     if (cmax > (uint32_t)(SPEC * pre.tps)) return false;        // uniform: every wave holds every list's meta
     if (rc.greedy) {
@@ -1957,10 +1970,11 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
     const int tid = threadIdx.x;
     const int row = rc.row;
     const int V = a.V;
-    const int nseg = a.nseg;
+    const int nseg = rc.nseg;
     const int tail_lo = (V / TILE) * TILE;            // the segment kernel streamed [0, tail_lo)
     const int ntail = V - tail_lo;                    // < TILE logits left for this kernel
     int k = rc.k;
+    (void)nseg;
     int tok = 0, keep = 1;
 
     bool fast = false;
@@ -1971,7 +1985,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
     if (rc.large && !alone && nseg > 0) {
         // the row's segments sampled it together (large_segment): segment 0's slot holds the result unless the row
         // was abandoned (then it is sampled here alone, exactly)
-        const uint64_t* s0 = a.cand + (int64_t)row * nseg * CAP;
+        const uint64_t* s0 = a.cand + slot_of(rc, 0) * CAP;
         const uint32_t sc = *reinterpret_cast<volatile const uint32_t*>(row_sync_ctr(a, row));   // not read before
         if (!(sc & ROW_ABANDONED) && s0[LS_STATUS] == 1ull) {
             const uint64_t tk = s0[LS_TOK];
@@ -2137,7 +2151,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
         const int tps = pre.tps, c_me = pre.c_me, r_me = pre.r_me;
         const bool act = pre.act;
         const uint32_t cnm = pre.cnm;
-        const uint64_t* lst = a.cand + ((int64_t)row * nseg + c_me) * CAP;
+        const uint64_t* lst = a.cand + slot_of(rc, c_me) * CAP;
         if (act && r_me == 0) s.off[c_me] = cnm;
         if (tid == 0) s.count = 0u;
         // one reduction: L (bit 63 set when a list is longer than its prefetched window, or the lists' total may
@@ -2163,7 +2177,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 const int m = (c0 + c1) >> 1;
                 if (s.off[m] <= g) c0 = m; else c1 = m;
             }
-            const uint64_t w = a.cand[((int64_t)row * nseg + c0) * CAP + (g - s.off[c0])];
+            const uint64_t w = a.cand[slot_of(rc, c0) * CAP + (g - s.off[c0])];
             return f < total ? w : 0ull;
         };
         // gather the candidates >= L into LDS (counted past CAP), tracking their max key
@@ -2495,16 +2509,19 @@ struct SegStart {
     const float* rowp;
     __amdgpu_buffer_rsrc_t rs;   // [seg_lo, seg_lo + ntiles * TILE) of the row
 };
-__device__ __forceinline__ SegStart seg_start(const Args& a, int row, int seg, float (&buf)[PF][TPT]) {
+// spec: the balanced layout may still move this workgroup, and its loads are then overwritten before use. They are
+// marked volatile (aux bit 31) so that the compiler keeps them at kernel entry instead of sinking them past the layout.
+template <bool SPEC = false>
+__device__ __forceinline__ SegStart seg_start(const Args& a, int row, int seg, int st, float (&buf)[PF][TPT]) {
     SegStart g;
-    g.seg_lo = seg * a.seg_tiles * TILE;
-    const int left = a.V / TILE - seg * a.seg_tiles;                // full tiles left in the row
-    g.ntiles = left < a.seg_tiles ? left : a.seg_tiles;             // >= 1
+    g.seg_lo = seg * st * TILE;
+    const int left = a.V / TILE - seg * st;                         // full tiles left in the row
+    g.ntiles = left < st ? left : st;                               // >= 1
     g.rowp = a.logits + (int64_t)row * a.ld;
     g.rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(g.rowp + g.seg_lo), (short)0, g.ntiles * TILE * 4,
                                              0x00020000);
 #pragma unroll
-    for (int p = 0; p < PF; ++p) load_seg_tile(buf[p], g.rs, p);
+    for (int p = 0; p < PF; ++p) load_seg_tile<SPEC ? (int)0x80000000 : 0>(buf[p], g.rs, p);
     return g;
 }
 
@@ -2917,8 +2934,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     FS_MARK(3);
 
     // ---- publish this segment's candidates (read by the merge kernel after this kernel completes)
-    const int nseg = a.nseg;
-    const int slot = rc.row * nseg + seg;
+    const int64_t slot = slot_of(rc, seg);
     uint64_t* gout = a.cand + (int64_t)slot * CAP;
     if (rc.greedy) {
         uint64_t best = 0ull;
@@ -3054,18 +3070,17 @@ __device__ __forceinline__ void seg_elems(const Args& a, const RowCtx& rc, Share
 // The gathered lists of one region of every segment of the row, concatenated into s.cand[0, n) and sorted in
 // candidate order (descending composites). Returns n, or -1 when a list overflowed or they exceed KMAX together.
 // Called after a row barrier (the lists are in the L2; this workgroup's L1 is invalidated).
-__device__ __forceinline__ int load_lists(const Args& a, int row, int region, int cnt_slot, Shared& s) {
-    const int tid = threadIdx.x, nseg = a.nseg;
-    const uint64_t* base = a.cand + (int64_t)row * nseg * CAP;
+__device__ __forceinline__ int load_lists(const Args& a, const RowCtx& rc, int region, int cnt_slot, Shared& s) {
+    const int tid = threadIdx.x, nseg = rc.nseg;
     uint32_t mine = 0u;
     bool over = false;
     for (int j = tid; j < nseg; j += BLOCK) {
-        const uint64_t c = base[(int64_t)j * CAP + cnt_slot];
+        const uint64_t c = a.cand[slot_of(rc, j) * CAP + cnt_slot];
         over |= c > (uint64_t)LLR;
     }
     // offsets: thread j < nseg holds list j's count (nseg < BLOCK, kept so by the host)
     if (tid < nseg) {
-        const uint64_t c = base[(int64_t)tid * CAP + cnt_slot];
+        const uint64_t c = a.cand[slot_of(rc, tid) * CAP + cnt_slot];
         mine = c > (uint64_t)LLR ? 0u : (uint32_t)c;
     }
     uint32_t tot;
@@ -3081,7 +3096,7 @@ __device__ __forceinline__ int load_lists(const Args& a, int row, int region, in
             const int m = (c0 + c1) >> 1;
             if (s.off[m] <= f) c0 = m; else c1 = m;
         }
-        s.cand[f] = base[(int64_t)c0 * CAP + LSC + region * LLR + (f - s.off[c0])];
+        s.cand[f] = a.cand[slot_of(rc, c0) * CAP + LSC + region * LLR + (f - s.off[c0])];
     }
     __syncthreads();
     bin_sort_desc((int)tot, s);
@@ -3089,16 +3104,14 @@ __device__ __forceinline__ int load_lists(const Args& a, int row, int region, in
 }
 
 // A row-wide sum over the segments' published scalar (fp64 bits at cnt_slot), in a fixed order (deterministic).
-__device__ __forceinline__ double sum_slots_f64(const Args& a, int row, int sl, Shared& s) {
-    const uint64_t* base = a.cand + (int64_t)row * a.nseg * CAP;
+__device__ __forceinline__ double sum_slots_f64(const Args& a, const RowCtx& rc, int sl, Shared& s) {
     double v = 0.0;
-    for (int j = threadIdx.x; j < a.nseg; j += BLOCK) v += __longlong_as_double((long long)base[(int64_t)j * CAP + sl]);
+    for (int j = threadIdx.x; j < rc.nseg; j += BLOCK) v += __longlong_as_double((long long)a.cand[slot_of(rc, j) * CAP + sl]);
     return block_sum_f64(v, s.red);
 }
-__device__ __forceinline__ uint64_t sum_slots_u64(const Args& a, int row, int sl, Shared& s) {
-    const uint64_t* base = a.cand + (int64_t)row * a.nseg * CAP;
+__device__ __forceinline__ uint64_t sum_slots_u64(const Args& a, const RowCtx& rc, int sl, Shared& s) {
     uint64_t v = 0ull;
-    for (int j = threadIdx.x; j < a.nseg; j += BLOCK) v += base[(int64_t)j * CAP + sl];
+    for (int j = threadIdx.x; j < rc.nseg; j += BLOCK) v += a.cand[slot_of(rc, j) * CAP + sl];
     uint64_t tot;
     (void)block_excl_scan<uint64_t>(v, s.red.u64b, &tot);
     return tot;
@@ -3107,12 +3120,11 @@ __device__ __forceinline__ uint64_t sum_slots_u64(const Args& a, int row, int sl
 // This segment's part of a large row (see above).
 __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, int seg, Shared& s, const SegStart& g) {
     const int tid = threadIdx.x;
-    const int row = rc.row, nseg = a.nseg;
+    const int row = rc.row, nseg = rc.nseg;
     const fs_row_params& p = rc.p;
     const int lo0 = g.seg_lo;
     const int hi = seg == nseg - 1 ? a.V : lo0 + g.ntiles * TILE;      // the last segment takes the partial tile
-    uint64_t* my = a.cand + ((int64_t)row * nseg + seg) * CAP;
-    const uint64_t* slot0 = a.cand + (int64_t)row * nseg * CAP;
+    uint64_t* my = a.cand + slot_of(rc, seg) * CAP;
     if (ld_agent(a.dirty) != 0) return;                 // a dirty context: the merge samples the row alone
     if (seg == 0 && tid == 0) my[LS_STATUS] = 0ull;
     // Penalties: a repetition penalty alone as an exact bitmap of the window's ids over this segment (in s.ids, built
@@ -3163,7 +3175,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
     {
         uint64_t mx_ = 0ull, mn_ = ~0ull, nv_ = 0ull;
         for (int j = tid; j < nseg; j += BLOCK) {
-            const uint64_t* sl = a.cand + ((int64_t)row * nseg + j) * CAP;
+            const uint64_t* sl = a.cand + slot_of(rc, j) * CAP;
             mx_ = sl[LS_MAX] > mx_ ? sl[LS_MAX] : mx_;
             mn_ = sl[LS_MIN] < mn_ ? sl[LS_MIN] : mn_;
             nv_ += sl[LS_NV];
@@ -3235,11 +3247,11 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
     }
     if (!row_sync(a, row, 2u * (uint32_t)nseg, s)) return;
     FS_MARK(7);                                          // past the second barrier
-    double S = sum_slots_f64(a, row, LS_SHI, s);
+    double S = sum_slots_f64(a, rc, LS_SHI, s);
     uint64_t Xk = cmin;
     uint64_t fx_bk = 0ull;                               // fixed-point mass of bin bk's candidates
     if (bk != 0xFFFFFFFFu) {
-        const int n = load_lists(a, row, 0, LS_NBK, s);
+        const int n = load_lists(a, rc, 0, LS_NBK, s);
         const int need = keff - (int)abk;                // >= 1: the k-th lies in bin bk
         if (n < need || need < 1) { row_abandon(a, row); return; }   // uniform
         Xk = s.cand[need - 1];
@@ -3350,19 +3362,19 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
         nsync = 3u;
         if (!row_sync(a, row, 3u * (uint32_t)nseg, s)) return;
         FS_MARK(9);                                      // past the third barrier
-        const uint32_t ca_c = (uint32_t)sum_slots_u64(a, row, LS_CA, s);
+        const uint32_t ca_c = (uint32_t)sum_slots_u64(a, rc, LS_CA, s);
         if (need_m) {
-            cnt_m = (uint32_t)sum_slots_u64(a, row, LS_CNTM, s);
-            sum_m = sum_slots_f64(a, row, LS_SUMM, s);
+            cnt_m = (uint32_t)sum_slots_u64(a, rc, LS_CNTM, s);
+            sum_m = sum_slots_f64(a, rc, LS_SUMM, s);
             uint64_t c_ = ~0ull;
             for (int j = tid; j < nseg; j += BLOCK) {
-                const uint64_t v = a.cand[((int64_t)row * nseg + j) * CAP + LS_CLM];
+                const uint64_t v = a.cand[slot_of(rc, j) * CAP + LS_CLM];
                 c_ = v < c_ ? v : c_;
             }
             cl_m = block_min_u64(c_, s.red);
         }
         if (p.top_p < 1.0f) {
-            nc = load_lists(a, row, 1, LS_NBC, s);
+            nc = load_lists(a, rc, 1, LS_NBC, s);
             if (nc < 0) { row_abandon(a, row); return; }
             double cum = 0.0;
             const int ic = large_walk(s, nc, Xk, above_c, tgt, mx, Td, &cum);
@@ -3408,7 +3420,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
     if (nc >= 0 && bd == bc) {
         nd = nc;                                         // the same bin is sorted in LDS already
     } else if (bd == bd_pred) {
-        nd = load_lists(a, row, 2, LS_NBD, s);           // gathered by P3
+        nd = load_lists(a, rc, 2, LS_NBD, s);           // gathered by P3
         if (nd < 0) { row_abandon(a, row); return; }
     } else {
         if (tid == 0) s.count = 0u;
@@ -3421,7 +3433,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
         FS_MARK(10);                                     // P4 streamed
         if (!row_sync(a, row, (nsync + 1u) * (uint32_t)nseg, s)) return;
         FS_MARK(11);                                     // past the last barrier
-        nd = load_lists(a, row, 2, LS_NBD, s);
+        nd = load_lists(a, rc, 2, LS_NBD, s);
         if (nd < 0) { row_abandon(a, row); return; }
     }
     double cum = 0.0;
@@ -3441,7 +3453,88 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
         my[LS_KEFF] = (uint64_t)keff | ((uint64_t)kmax << 32);
         my[LS_STATUS] = 1ull;
     }
-    (void)slot0;
+}
+
+// ------------------------------------------------------------------------------------------------ row layout
+// By default every row has nseg segments of seg_tiles tiles. With a.balance, each XCD splits its W workgroups among
+// its R rows (x, x + XCDS, ...) by the rows' cost per tile, so that rows with a large k, which cost up to three
+// times a greedy row per tile, get more segments and a mixed batch's rows finish together. Every workgroup of the
+// XCD computes the same split from the same parameters with integer arithmetic. Costs (per tile, relative to a
+// greedy row = 100; measured on MI355X on uniform B=256 x V=262144 batches): k = 64 119, k = 256 158, k = 2048
+// 292, whole-row sampling (k > 2048) about 400; frequency/presence penalties x1.25, a repetition penalty x1.05.
+// What the cost needs of a row's parameters: two 16-byte buffer loads (temperature, top_k, top_p, min_p; repetition,
+// frequency, presence, repeat_last_n). A segment workgroup requests them before its first tiles, behind a scheduling
+// barrier, so that waiting for them (vector loads complete in order) does not wait for the tiles.
+struct CostIn {
+    float t, rep, fq, pr;
+    int tk;
+};
+__device__ __forceinline__ CostIn cost_in(const Args& a, int row) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<fs_row_params*>(a.params), (short)0,
+                                                                        a.B * (int)sizeof(fs_row_params), 0x00020000);
+    const u32x4 lo = raw_buffer_load_u32x4(rs, row * (int)sizeof(fs_row_params), 0, 0);
+    const u32x4 hi = raw_buffer_load_u32x4(rs, row * (int)sizeof(fs_row_params) + 16, 0, 0);
+    CostIn c;
+    c.t = __uint_as_float(lo.x); c.tk = (int)lo.y;
+    c.rep = __uint_as_float(hi.x); c.fq = __uint_as_float(hi.y); c.pr = __uint_as_float(hi.z);
+    return c;
+}
+__device__ __forceinline__ uint32_t row_cost(const Args& a, const CostIn& in) {
+    const float t = in.t, rep = in.rep, fq = in.fq, pr = in.pr;
+    const int tk = in.tk;
+    if (t <= 0.0f || tk == 1) return 100u;
+    const int k = (tk > 0 && tk < a.V) ? tk : a.V;
+    float c;
+    if (k > KMAX) {
+        c = 400.0f;
+    } else {
+        const float l = __log2f((float)k);
+        c = k <= 64 ? 100.0f + 3.0f * l : (k <= 256 ? 119.0f + 19.5f * (l - 6.0f) : 158.0f + 44.7f * (l - 8.0f));
+    }
+    if (fq != 0.0f || pr != 0.0f) c *= 1.25f;
+    else if (rep != 1.0f) c *= 1.05f;
+    return (uint32_t)c;
+}
+// Lane r < R: row x + XCDS * r gets n segments (at most its tiles), its first workgroup being base among the XCD's W.
+// in: lane r's row parameters (cost_in of row x + XCDS * r, or of row x past R).
+__device__ __forceinline__ CostIn xcd_cost_in(const Args& a, int x) {
+    const int R = (a.B - x + XCDS - 1) / XCDS;
+    return cost_in(a, x + XCDS * (lane_id() < R ? lane_id() : 0));
+}
+__device__ __forceinline__ void xcd_layout(const Args& a, int x, const CostIn& in, uint32_t& n, uint32_t& base) {
+    const int lane = lane_id();
+    const int R = (a.B - x + XCDS - 1) / XCDS;          // rows on this XCD (1 <= R <= WAVE: the host checks B)
+    const uint32_t W = (uint32_t)(a.nseg * ((a.B + XCDS - 1) / XCDS));
+    const uint32_t tiles_row = (uint32_t)(a.V / TILE);
+    const uint32_t w = lane < R ? row_cost(a, in) : 0u;  // lane r: row x + XCDS r's cost
+    const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_scan_u32(w), WAVE - 1);
+    const uint32_t spare = W - (uint32_t)R;
+    const uint32_t num = spare * w;
+    const uint32_t tq = tot > 0u ? tot : 1u;            // >= 100 per row
+    const uint32_t f = num / tq, rem = num % tq;
+    n = lane < R ? 1u + f : 0u;
+    const uint32_t left = W - (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_scan_u32(n), WAVE - 1);
+    uint32_t rank = 0u;                                  // the largest remainders get the leftover workgroups
+    for (int s2 = 0; s2 < R; ++s2) {
+        const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)rem, s2);
+        rank += (r2 > rem || (r2 == rem && s2 < lane)) ? 1u : 0u;
+    }
+    if (lane < R && rank < left) n += 1u;
+    const uint32_t cap = tiles_row < (uint32_t)(BLOCK - 1) ? tiles_row : (uint32_t)(BLOCK - 1);
+    if (n > cap) n = cap;                                // workgroups past a row's tiles stay idle
+    base = wave_incl_scan_u32(n) - n;
+}
+// The layout of row x + XCDS * q into rc (merging workgroups): its lane q of xcd_layout.
+__device__ __forceinline__ void row_layout(const Args& a, RowCtx& rc) {
+    if (!a.balance || rc.nseg == 0) return;
+    uint32_t n, base;
+    xcd_layout(a, rc.lx, xcd_cost_in(a, rc.lx), n, base);
+    const int q = rc.row / XCDS;
+    const uint32_t nq = (uint32_t)__builtin_amdgcn_readlane((int)n, q);
+    const uint32_t st = ((uint32_t)(a.V / TILE) + nq - 1u) / nq;
+    rc.st = (int)st;
+    rc.nseg = (int)(((uint32_t)(a.V / TILE) + st - 1u) / st);
+    rc.lbase = __builtin_amdgcn_readlane((int)base, q);
 }
 
 // The row's completion counter: the row histogram's last bin, which no ordered key reaches (keys of non-NaN values
@@ -3463,7 +3556,8 @@ __device__ __forceinline__ void merge_role(const Args& a, int mi, Shared& s) {
     const int row = mi % XCDS + XCDS * (mi / XCDS);
     if (row >= a.B) return;
     FS_TAG(13, 2); FS_TAG(14, row); FS_TAG(15, 0);
-    const RowCtx rc = row_ctx(a, row);               // the row's inputs are read while the segments run
+    RowCtx rc = row_ctx(a, row);                     // the row's inputs are read while the segments run
+    row_layout(a, rc);
     uint32_t* ctr = row_counter(a, row);
     if (threadIdx.x == 0) {
         // A context left dirty by an earlier give-up: its row histograms and counters may hold a late segment's
@@ -3474,7 +3568,7 @@ __device__ __forceinline__ void merge_role(const Args& a, int mi, Shared& s) {
         uint32_t spins = 0u;
         while (!alone &&
                (__hip_atomic_fetch_add(ctr, 0x10000u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & 0xFFFFu) <
-                   (uint32_t)a.nseg) {
+                   (uint32_t)rc.nseg) {
             if (++spins >= a.merge_spins) {
                 atomicOr(a.err, FS_DEVERR_INTERNAL);
                 __hip_atomic_store(a.dirty, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -3491,7 +3585,7 @@ __device__ __forceinline__ void merge_role(const Args& a, int mi, Shared& s) {
     Pre pre = {};
     if (!alone) {
         l1_invalidate();
-        prefetch_lists(a, row, pre);
+        prefetch_lists(a, rc, pre);
         if (threadIdx.x == 0) *ctr = 0u;             // the bin is left at 0 with the rest of the row histogram
     }
     merge_row(a, rc, s, pre, alone);                 // one call site: the merge code is inlined once
@@ -3523,14 +3617,45 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, 
     }
     const int x = (int)(blockIdx.x % (unsigned)XCDS);
     const int j = (int)(blockIdx.x / (unsigned)XCDS);
-    const int q = __builtin_amdgcn_readfirstlane(j / a.nseg);    // uniform: lets the compiler use scalar loads
-    const int seg = j - q * a.nseg;
-    const int row = x + XCDS * q;
-    if (row >= a.B) return;
-    FS_TAG(13, 1); FS_TAG(14, row); FS_TAG(15, seg);
+    int q = __builtin_amdgcn_readfirstlane(j / a.nseg);          // uniform: lets the compiler use scalar loads
+    int seg = j - q * a.nseg;
+    int row = x + XCDS * q;
+    if (row >= a.B && !a.balance) return;
     float buf[PF][TPT];
-    const SegStart g = seg_start(a, row, seg, buf);   // the tiles are on their way before the parameters
-    const RowCtx rc = row_ctx(a, row);
+    // the layout's parameter loads come first, then the default layout's tiles, then the row's parameters; a balanced
+    // layout that moves this workgroup requests its own tiles and parameters
+    CostIn cin = {};
+    if (a.balance) cin = xcd_cost_in(a, x);
+    __builtin_amdgcn_sched_barrier(0);
+    SegStart g = a.balance ? seg_start<true>(a, row < a.B ? row : a.B - 1, seg, a.seg_tiles, buf)
+                           : seg_start<false>(a, row < a.B ? row : a.B - 1, seg, a.seg_tiles, buf);
+    RowCtx rc = row_ctx(a, row < a.B ? row : a.B - 1);
+    int st = a.seg_tiles, nsr = a.nseg, lbase = q * a.nseg;
+    if (a.balance) {
+        uint32_t n, base;
+        xcd_layout(a, x, cin, n, base);
+        const uint64_t mine = __ballot((uint32_t)j >= base && (uint32_t)j < base + n);
+        if (mine == 0ull) return;                        // past the XCD's rows (or a capped row's tiles): idle
+        const int r = __ffsll((unsigned long long)mine) - 1;
+        const uint32_t nr = (uint32_t)__builtin_amdgcn_readlane((int)n, r);
+        lbase = __builtin_amdgcn_readlane((int)base, r);
+        st = (int)(((uint32_t)(a.V / TILE) + nr - 1u) / nr);
+        nsr = (a.V / TILE + st - 1) / st;
+        const int nseg_r = __builtin_amdgcn_readfirstlane(j - lbase);
+        if (nseg_r >= nsr) return;                       // the row's tiles are covered by its first nsr workgroups
+        if (r != q || nseg_r != seg || st != a.seg_tiles) {
+            const bool moved_row = r != q || row >= a.B;
+            q = r;
+            seg = nseg_r;
+            row = x + XCDS * q;
+            g = seg_start(a, row, seg, st, buf);
+            if (moved_row) rc = row_ctx(a, row);
+        }
+    }
+    FS_TAG(13, 1); FS_TAG(14, row); FS_TAG(15, seg);
+    rc.st = st;
+    rc.nseg = nsr;
+    rc.lbase = lbase;
     if (!rc.large) process_segment(a, rc, seg, s, buf, g);
     else large_segment(a, rc, seg, s, g);           // the row's segments sample it together
     vm_drain();                                      // the list and meta stores are in the L2
@@ -3549,8 +3674,9 @@ __global__ __launch_bounds__(BLOCK) void merge_kernel(int nseg, uint64_t* cand, 
     a.nseg = nseg; a.cand = cand; a.meta = meta; a.rhist = rhist; a.params = params;
     const int row = __builtin_amdgcn_readfirstlane((int)blockIdx.x);
     Pre pre;
-    prefetch_lists(a, row, pre);
-    merge_row(a, row_ctx(a, row), s, pre);
+    const RowCtx rc = row_ctx(a, row);
+    prefetch_lists(a, rc, pre);
+    merge_row(a, rc, s, pre);
 }
 
 // fs_softcap_batch: the sampler's fused final-logit cap as a standalone elementwise pass.
@@ -3874,9 +4000,16 @@ int plan(int cus, fs::Args& a, int64_t rows, int64_t& items, int64_t& seg_grid) 
     if (a.nseg > fs::MAX_SEGS) return FS_E_INVALID;
     items = rows * a.nseg;
     if (items > 0x7fffffff) return FS_E_INVALID;
-    // one workgroup per (row, segment), the rows dealt to XCDS slots (segment_kernel)
+    // one workgroup per (row, segment), the rows dealt to XCDS slots (segment_kernel); each segment workgroup's
+    // list slot is its index, so the workspace holds seg_grid slots
     seg_grid = items > 0 ? (int64_t)fs::XCDS * a.nseg * ((rows + fs::XCDS - 1) / fs::XCDS) : 0;
     if (seg_grid > 0x7fffffff) return FS_E_INVALID;
+    items = seg_grid;
+    // balanced layouts (sampling, >= 2 segments per row, >= 2 rows on some XCD, <= WAVE rows per XCD)
+    // Balanced layouts: sampling, >= 2 segments per row, 16 to WAVE rows per XCD. Computing the layout delays every
+    // workgroup by about 2 us, which pays on large mixed batches (cfg5 -20 us) but not on small ones.
+    a.balance = (a.mode == fs::MODE_SAMPLE && a.nseg >= 2 && (rows + fs::XCDS - 1) / fs::XCDS >= 16 &&
+                 (rows + fs::XCDS - 1) / fs::XCDS <= fs::WAVE) ? 1 : 0;
     return FS_OK;
 }
 
