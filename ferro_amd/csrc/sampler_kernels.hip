@@ -116,6 +116,12 @@ constexpr int TRACE_W = 16;
     do {                                                                                                  \
         if (threadIdx.x == 0) s.trace_t[(i)] = (uint64_t)(v);                                            \
     } while (0)
+// the latest of the workgroup's waves to reach phase i (lane 0 of each wave)
+#define FS_MARKW(i)                                                                                       \
+    do {                                                                                                  \
+        if (lane_id() == 0) atomicMax((unsigned long long*)&s.trace_t[(i)],                               \
+                                      (unsigned long long)__builtin_amdgcn_s_memrealtime());              \
+    } while (0)
 #define FS_FLUSH()                                                                                        \
     do {                                                                                                  \
         if (threadIdx.x == 0 && a.trace)                                                                  \
@@ -124,6 +130,7 @@ constexpr int TRACE_W = 16;
 #else
 #define FS_MARK(i) do {} while (0)
 #define FS_TAG(i, v) do {} while (0)
+#define FS_MARKW(i) do {} while (0)
 #define FS_FLUSH() do {} while (0)
 #endif
 
@@ -935,6 +942,91 @@ __device__ __forceinline__ void apply_penalties(float (&x)[TPT], const Args& a, 
     for (int j = 0; j < NV; ++j) {
         const int local = (j * BLOCK + tid) * 4;
         const uint2 c2 = *reinterpret_cast<const uint2*>(&s.cnt()[local >> 1]);
+        if ((c2.x | c2.y) != 0u) {
+            const uint32_t cc[4] = {c2.x & 0xFFFFu, c2.x >> 16, c2.y & 0xFFFFu, c2.y >> 16};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (cc[q] != 0u) {
+                    float l = x[4 * j + q];
+                    if (rc.rep_on) l = l > 0.0f ? __fdiv_rn(l, rp) : __fmul_rn(l, rp);
+                    if (rc.fp_on) l = __fsub_rn(l, __fadd_rn(__fmul_rn((float)cc[q], fq), pr));
+                    x[4 * j + q] = l;
+                }
+            }
+        }
+    }
+}
+
+// The segment's window ids s.ids[0, nids) (nids <= WIDS, gathered by gather_window) reordered by tile, a counting
+// sort: the ids of the segment's tile t are s.ids[t > 0 ? s.off[t - 1] : 0, s.off[t]) (s.off holds the bucket ends;
+// ntiles <= 2 * BLOCK). Ends with a barrier.
+__device__ __forceinline__ void bucket_window(int seg_lo, int ntiles, Shared& s) {
+    const int tid = threadIdx.x;
+    const int n = (int)s.nids;
+    constexpr int Q = WIDS / BLOCK;
+    int id[Q], tl[Q];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int i = tid + q * BLOCK;
+        id[q] = i < n ? s.ids[i] : 0;
+        tl[q] = i < n ? (id[q] - seg_lo) / TILE : -1;
+    }
+    for (int t = tid; t < ntiles; t += BLOCK) s.off[t] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+        if (tl[q] >= 0) atomicAdd(&s.off[tl[q]], 1u);
+    __syncthreads();
+    const uint32_t c0 = 2 * tid < ntiles ? s.off[2 * tid] : 0u;
+    const uint32_t c1 = 2 * tid + 1 < ntiles ? s.off[2 * tid + 1] : 0u;
+    uint32_t tot;
+    const uint32_t base = block_excl_scan<uint32_t>(c0 + c1, s.wsum, &tot);   // its barriers end the reads above
+    if (2 * tid < ntiles) s.off[2 * tid] = base;                              // bucket starts
+    if (2 * tid + 1 < ntiles) s.off[2 * tid + 1] = base + c0;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+        if (tl[q] >= 0) s.ids[atomicAdd(&s.off[tl[q]], 1u)] = id[q];         // the starts advance to the ends
+    __syncthreads();
+}
+
+// Penalty pass on one tile (the tt-th of the segment, starting at lo) in registers, wave by wave: the ids of the
+// tile's bucket (bucket_window) that fall on this wave's logits are counted in the wave's own 16-bit table, then
+// each lane patches its counted logits. Element lo + e belongs to wave (e % (4 * BLOCK)) / (4 * WAVE), at index
+// (e / (4 * BLOCK)) * 4 * WAVE + e % (4 * WAVE) of its table (lane l's four logits of float4 j sit at
+// j * 4 * WAVE + 4 * l). A wave's LDS accesses complete in order, so no barrier is needed; tiles holding no window
+// id skip the pass. Same arithmetic as apply_penalties.
+__device__ __forceinline__ void wave_penalties(float (&x)[TPT], const Args& a, const RowCtx& rc, int lo, int tt,
+                                               Shared& s) {
+    static_assert(NV * 4 * WAVE * NWAVES == TILE, "a tile is the waves' float4 columns");
+    static_assert(WIDS < 0xFFFF, "16-bit counts");
+    const int b0 = tt > 0 ? (int)s.off[tt - 1] : 0, b1 = (int)s.off[tt];
+    if (b0 == b1) return;                                // uniform: no window id in this tile
+    const int lane = lane_id();
+    const uint32_t w = threadIdx.x / WAVE;
+    uint32_t* tb = s.cnt() + w * (NV * 4 * WAVE / 2);    // NV * 4 * WAVE 16-bit counts (all waves: TILE / 2 words)
+    // Every table access is a 32-bit access of tb, with compiler barriers between the clear, the counts and the
+    // reads: the hardware keeps a wave's LDS accesses in order, but vector-typed accesses are not ordered by the
+    // compiler against the 32-bit atomics (no barrier here does it).
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        tb[2 * (j * WAVE + lane)] = 0u;
+        tb[2 * (j * WAVE + lane) + 1] = 0u;
+    }
+    __asm__ volatile("" ::: "memory");
+    // at most WIDS ids in the segment: a 16-bit count cannot overflow
+    for (int i = b0 + lane; i < b1; i += WAVE) {
+        const uint32_t e = (uint32_t)(s.ids[i] - lo);   // < TILE
+        if ((e % (4u * BLOCK)) / (4u * WAVE) == w) {
+            const uint32_t idx = (e / (4u * BLOCK)) * (4u * WAVE) + e % (4u * WAVE);
+            atomicAdd(&tb[idx >> 1], 1u << ((idx & 1u) * 16u));
+        }
+    }
+    __asm__ volatile("" ::: "memory");
+    const float rp = rc.p.repetition_penalty, fq = rc.p.frequency_penalty, pr = rc.p.presence_penalty;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint2 c2 = make_uint2(tb[2 * (j * WAVE + lane)], tb[2 * (j * WAVE + lane) + 1]);
         if ((c2.x | c2.y) != 0u) {
             const uint32_t cc[4] = {c2.x & 0xFFFFu, c2.x >> 16, c2.y & 0xFFFFu, c2.y >> 16};
 #pragma unroll
@@ -2550,16 +2642,34 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         const int64_t i = rc.b + q * BLOCK + tid;
         wid[q] = (rc.pen && i < rc.len) ? hist_at(a, rc, i) : -1;
     }
+    // Tile 0 is staged in the candidate buffer's tail (tile 0's own appends, at most one tile, stay below it) and
+    // tile PF requested in its registers as soon as tile 0 arrives: tile 0's bound computation (two barriers) and
+    // appends then run with PF tiles in flight. (Staging it before the penalty set-up, so that tile PF is requested
+    // earlier still, measured slower: cfg3 +1.1 us, cfg5 +1.5 us.)
+    float4* const stage0 = reinterpret_cast<float4*>(s.cand + (CAP - TILE / 2));
+    static_assert(TILE + TILE / 2 <= CAP, "tile 0's appends stay below its stage");
+    auto stage_tile0 = [&]() {
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            stage0[j * BLOCK + tid] = make_float4(buf[0][4 * j], buf[0][4 * j + 1], buf[0][4 * j + 2], buf[0][4 * j + 3]);
+        load_seg_tile(buf[0], g.rs, PF);
+    };
     // Penalties. With a repetition penalty alone (sampler.cpp:11-18) only membership in the window matters: an
     // exact bitmap of the segment's window ids (bmp, in the merge's offset array, unused by this kernel) is built
     // once, and a thread's four consecutive logits share one bitmap word, so each tile costs two LDS reads and no
-    // barrier. Frequency / presence penalties need counts: a per-tile count table (apply_penalties).
+    // barrier. Frequency / presence penalties need counts: the segment's window ids bucketed by tile once, then
+    // counted wave by wave (wave_penalties; segments of >= 4 tiles), else a per-tile count table (apply_penalties).
     const int seg_hi = seg_lo + ntiles * TILE;
     const bool fastpen = rc.pen && rc.rep_on && !rc.fp_on && seg_hi - seg_lo <= 32 * (MAX_SEGS + 1);
     const bool slowpen = rc.pen && !fastpen;
     uint32_t* bmp = s.off;
     const float rp = rc.p.repetition_penalty;
     if (slowpen) gather_window(a, rc, seg_lo, seg_hi, s);
+    // counts (frequency / presence): the window's ids bucketed by tile once, then counted per wave (no barriers);
+    // a window with more than WIDS ids in the segment keeps the per-tile table (apply_penalties)
+    const bool wavepen = slowpen && s.nids <= (uint32_t)WIDS && ntiles >= 4 && ntiles <= 2 * BLOCK;
+    const bool tablepen = slowpen && !wavepen;
+    if (wavepen) bucket_window(seg_lo, ntiles, s);
     if (fastpen) {
         for (int i = tid; i <= MAX_SEGS; i += BLOCK) bmp[i] = 0u;
         __syncthreads();
@@ -2625,9 +2735,11 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         const int first = block_min_i32(hit, s.red);
         if (first < BLOCK) raise_key((rb0 + (uint32_t)(BLOCK - 1 - first)) << RSHIFT);
     };
-    // Top-k buffer discipline: after tile 0 the buffer is checked (barrier) only every R tiles, R sized so the
-    // expected appends fill at most half the headroom; an overflow (appends past CAP are dropped) is detected at
-    // the next check and the segment is streamed again in safe mode (a check after every tile).
+    // Top-k buffer discipline: after tile 0 the buffer is checked (barrier) every R tiles, R sized so the expected
+    // appends fill at most half the headroom, and rows with k > 64 also at every iteration's first tile, where their
+    // new entries are counted into the row histogram (the other segments' bounds tighten sooner: fewer appends row
+    // wide); an overflow (appends past CAP are dropped) is detected at the next check and the segment is streamed
+    // again in safe mode (a check after every tile).
     auto greedy_update = [&](const float (&x)[TPT], int tt) {
         const int sb = tt * TPT;
 #pragma unroll
@@ -2670,9 +2782,9 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     // waves' tkeys can differ (each wave takes its own row bounds), so each wave histograms the entries it reads
     // relative to its own tkey in its own 64 bins (in bins(), free between checks) and adds them to the row at
     // that base; a wave's LDS accesses complete in order, so no barrier is needed.
-    // Entry: a barrier since the last append (a check); the next check's barrier ends the bins' use.
-    auto count_row = [&](int from) {
-        const int nb = (int)s.count;
+    // Entry: nb = the buffer's count, read by every wave after a barrier that followed the last append and before
+    // any wave appends again; the next check's barrier ends the bins' use.
+    auto count_row = [&](int from, int nb) {
         const uint32_t rb = tkey >> RSHIFT;
         uint32_t* wb = s.bins() + (tid / WAVE) * WAVE;
         wb[lane_id()] = 0u;
@@ -2701,13 +2813,14 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     auto check = [&](int tiles, bool strict) -> int {
         __syncthreads();
         int n = (int)s.count;
+        __syncthreads();                               // every wave holds the same count before any appends again
         int rate = (n - lastn) / (tiles > 0 ? tiles : 1);
         rate = rate > 341 ? rate : 341;
         auto short_room = [&](int m) {
             return m > k && (strict || k <= 4 * WAVE ? m > CAP - TILE : CAP - m < 3 * rate);
         };
         if (n <= CAP && short_room(n)) {
-            if (dyncount && !strict) count_row(counted);   // before the order changes (not in safe mode)
+            if (dyncount && !strict) count_row(counted, n);   // before the order changes (not in safe mode)
             raise_key(block_max_u32(tkey, s.red));          // its barriers also end count_row's use of bins()
             const int m = keep_from(n, (uint64_t)tkey << 32, s);
             if (m >= 0) {
@@ -2742,31 +2855,25 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         // k <= 64: tile 0's candidates are appended at tile 1, after the first row bound (its penalised logits wait in
         // the candidate buffer's tail; each thread reads back its own). Rows with the per-tile count table, and rows
         // with larger k (whose tile-0 bound lets through half a tile or more), append at once.
-        const bool defer0 = topk && !safe && ntiles >= 2 && !slowpen && k <= WAVE;
+        const bool defer0 = topk && !safe && ntiles >= 2 && !tablepen && k <= WAVE;
         bool overflow = false;
         int R = 1;
-        // ---- tile 0 (peeled: the initial threshold is computed here). Its logits are staged in the candidate
-        // buffer's tail (tile 0's own appends, at most one tile, stay below it) so that tile PF is requested as soon
-        // as tile 0 arrives: the tile's bound computation (two barriers) and appends then run with PF tiles in flight.
+        // ---- tile 0 (peeled: the initial threshold is computed here), through its stage
         {
             float x[TPT];
             const int lo = seg_lo;
             {
-                float4* st = reinterpret_cast<float4*>(s.cand + (CAP - TILE / 2));
-                static_assert(TILE + TILE / 2 <= CAP, "tile 0's appends stay below its stage");
-#pragma unroll
-                for (int j = 0; j < NV; ++j)
-                    st[j * BLOCK + tid] = make_float4(buf[0][4 * j], buf[0][4 * j + 1], buf[0][4 * j + 2], buf[0][4 * j + 3]);
-                load_seg_tile(buf[0], g.rs, PF);
-                if (!safe) FS_MARK(1);
+                stage_tile0();
+                if (!safe) { FS_MARK(1); }
 #pragma unroll
                 for (int j = 0; j < NV; ++j) {
-                    const float4 v = st[j * BLOCK + tid];
+                    const float4 v = stage0[j * BLOCK + tid];
                     x[4 * j] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
                 }
             }
             if (rc.capped) softcap_vals_unrolled(x, rc.p.softcap);
-            if (slowpen) apply_penalties(x, a, rc, lo, s);
+            if (tablepen) apply_penalties(x, a, rc, lo, s);
+            if (wavepen) wave_penalties(x, a, rc, lo, 0, s);
             if (fastpen) bitmap_pen(x, lo);
             if (rc.greedy) {
                 greedy_update(x, 0);
@@ -2817,10 +2924,9 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     }
                 }
                 if (defer0) {                            // the penalised tile waits in its stage for tile 1
-                    float4* st = reinterpret_cast<float4*>(s.cand + (CAP - TILE / 2));
 #pragma unroll
                     for (int j = 0; j < NV; ++j)
-                        st[j * BLOCK + tid] = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
+                        stage0[j * BLOCK + tid] = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
                 } else {
                     topk_append(x, lo);
                 }
@@ -2838,10 +2944,10 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     scnt = row_read(sb0);
                     spending = true;
                 }
-            } else if (slowpen) {
+            } else if (tablepen) {
                 __syncthreads();                         // penalty-table reads of this tile are done
             }
-            if (!safe) FS_MARK(2);
+            if (!safe) { FS_MARK(2); FS_MARKW(5); }
         }
         // ---- tiles 1.. (PF in flight; tile t is in buf[t % 2]). Iterations start at odd tiles, so the order in
         // which the two buffers were requested is the same on entry and around the back edge.
@@ -2867,7 +2973,8 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 if (live) {
                     const int lo = seg_lo + tt * TILE;
                     if (rc.capped) softcap_vals_unrolled(x, rc.p.softcap);
-                    if (slowpen) apply_penalties(x, a, rc, lo, s);
+                    if (tablepen) apply_penalties(x, a, rc, lo, s);
+                    if (wavepen) wave_penalties(x, a, rc, lo, tt, s);
                     if (fastpen) bitmap_pen(x, lo);
                     if (p == 0 && take1) raise_key(row_bound(snap1, k));
                     if (p == 0 && dpend) raise_key(row_bound(snapd, k));
@@ -2877,10 +2984,9 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     } else {
                         if (p == 0 && defer0 && t0 == 1) {
                             float x0[TPT];
-                            const float4* st = reinterpret_cast<const float4*>(s.cand + (CAP - TILE / 2));
 #pragma unroll
                             for (int j = 0; j < NV; ++j) {
-                                const float4 v = st[j * BLOCK + tid];
+                                const float4 v = stage0[j * BLOCK + tid];
                                 x0[4 * j] = v.x; x0[4 * j + 1] = v.y; x0[4 * j + 2] = v.z; x0[4 * j + 3] = v.w;
                             }
                             topk_append(x0, seg_lo);
@@ -2895,20 +3001,22 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                 if (live) {
                     if (topk) {
                         bool checked = false;
-                        if (++since >= R || slowpen) {
+                        if (++since >= R || tablepen || (dynrow && p == 0)) {
                             overflow = check(since, safe) > CAP;   // uniform: every thread read the same count
                             since = 0;
                             checked = true;
                         }
-                        if (p == 0 && checked && dynrow && !overflow && t0 + PF < ntiles) count_row(counted);
+                        if (p == 0 && checked && dynrow && !overflow && t0 + PF < ntiles) count_row(counted, lastn);
                         if (p == 0) dpend = dynrow && !overflow && t0 + PF < ntiles;
                         if (p == 0 && snap) snap2 = row_snap(rsr, tkey);
                         if (p == 1 && count2 && !overflow) {
                             // second count: the buffered logits of tiles 1-4
                             __syncthreads();
-                            count_row(0);
+                            const int nb = (int)s.count;
+                            __syncthreads();
+                            count_row(0, nb);
                         }
-                    } else if (slowpen) {
+                    } else if (tablepen) {
                         __syncthreads();                 // penalty-table reads of this tile are done
                     }
                 }
@@ -2916,8 +3024,10 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     snapd = row_snap(rsh, tkey);
                     load_seg_tile(x, g.rs, tt + PF);
                 }
+                if (!safe && tt < 8) FS_MARKW(5 + tt);
             }
         }
+
         if (!topk) break;
         if (!overflow) overflow = check(since, true) > CAP;
         if (!overflow) break;
@@ -2961,6 +3071,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
             a.meta[2 * slot] = tkey;              // at least k of the row's logits reach it
             a.meta[2 * slot + 1] = tot;
         }
+
     }
     __syncthreads();                               // LDS is reused by the next item
 }

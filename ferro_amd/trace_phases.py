@@ -6,7 +6,8 @@ product library): thread 0 of every workgroup stores the GPU's constant 100 MHz 
 Segment workgroups (one per (row, segment) item): 0 start, 1 tile 0 arrived, 2 tile 0 done (penalty, first bound,
 appends, check), 3 last tile done, 4 list published and counted. Merging workgroups (one per row): 0 start, 1 the
 row's segments seen done, 2 candidates gathered (short merge), 3 candidates ranked (short merge), 4 row finished.
-Slots 5-11 time the large-row passes of the segments (see sampler_kernels.hip); slots 13-15 tag role, row, segment.
+Slots 5-12 of a segment workgroup: on the fused path, when the slowest of its waves finished tiles 0-7; on the
+large-k path, the row passes (see sampler_kernels.hip). Slots 13-15 tag role, row, segment.
 
 Usage (on a GPU):  python ferro_amd/trace_phases.py --workload cfg3 [--calls 5]
 Prints a markdown table: when each phase happens (µs from the first workgroup's start; min / median / max over the
@@ -66,8 +67,9 @@ def phases(tr):
     t0 = tr[role > 0, 0].min()
     rel = (tr[:, :5].astype(np.int64) - np.int64(t0)) * TICK_US
     seg, mer = role == 1, role == 2
+    tiles = (tr[:, 5:13].astype(np.int64) - np.int64(t0)) * TICK_US
     out = {"seg": rel[seg], "seg_row": tr[seg, 14], "mer": rel[mer], "mer_row": tr[mer, 14],
-           "mer_set": tr[mer, :5] != 0}
+           "mer_set": tr[mer, :5] != 0, "seg_tiles": tiles[seg], "seg_tiles_set": tr[seg, 5:13] != 0}
     return out
 
 
@@ -89,6 +91,11 @@ def summarize(calls, seg_tiles):
     add("segment start", [s[:, 0] for s in S], [])
     add("segment: tile 0 arrived", [s[:, 1] for s in S], [s[:, 1] - s[:, 0] for s in S])
     add("segment: tile 0 done (penalty, bound, appends)", [s[:, 2] for s in S], [s[:, 2] - s[:, 1] for s in S])
+    for t in range(1, min(seg_tiles, 8)):
+        ok = [c["seg_tiles_set"][:, t] for c in calls]
+        if all(o.any() for o in ok):
+            add(f"segment: tile {t} done (slowest wave)", [c["seg_tiles"][o, t] for c, o in zip(calls, ok)],
+                [c["seg_tiles"][o, t] - c["seg_tiles"][o, t - 1] for c, o in zip(calls, ok)])
     add(f"segment: last tile done ({seg_tiles - 1} more tiles)", [s[:, 3] for s in S],
         [(s[:, 3] - s[:, 2]) / max(seg_tiles - 1, 1) for s in S])
     add("segment: list published, counted done", [s[:, 4] for s in S], [s[:, 4] - s[:, 3] for s in S])
