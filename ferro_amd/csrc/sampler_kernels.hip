@@ -631,8 +631,8 @@ struct Shared {
 // hold the next power of two >= m entries). cnt and start hold NB counters each; tmp holds m entries.
 constexpr int BIN_SORT_MAX = 48;
 template <int NB>
-__device__ __forceinline__ void bin_sort_desc(uint64_t* a, int m, uint64_t* tmp, uint32_t* cnt, uint32_t* start,
-                                              Red& red, uint32_t* wsum) {
+__device__ __forceinline__ uint32_t bin_sort_desc(uint64_t* a, int m, uint64_t* tmp, uint32_t* cnt, uint32_t* start,
+                                                  Red& red, uint32_t* wsum) {
     constexpr int EPT = KMAX / BLOCK;            // entries per thread
     constexpr int BPT = NB / BLOCK;              // bins per thread
     static_assert(BPT >= 1 && NB == BPT * BLOCK, "whole bins per thread");
@@ -652,7 +652,7 @@ __device__ __forceinline__ void bin_sort_desc(uint64_t* a, int m, uint64_t* tmp,
     for (int q = 0; q < BPT; ++q) cnt[q * BLOCK + tid] = 0u;
     cmn = block_min_u64(cmn, red);               // its barriers also order the zeroed counts
     cmx = block_max_u64(cmx, red);
-    if (m <= 1) return;
+    if (m <= 1) return 0u;
     int sh = 0;                                  // composites cmn..cmx map to bins NB-1..0
     while (((cmx - cmn) >> sh) >= (uint64_t)NB) ++sh;
     uint32_t bin[EPT], slot[EPT];
@@ -687,7 +687,7 @@ __device__ __forceinline__ void bin_sort_desc(uint64_t* a, int m, uint64_t* tmp,
         for (int i = m + tid; i < np; i += BLOCK) a[i] = 0ull;
         __syncthreads();
         bitonic_desc(a, np);
-        return;
+        return big;
     }
 #pragma unroll
     for (int q = 0; q < EPT; ++q)
@@ -697,17 +697,22 @@ __device__ __forceinline__ void bin_sort_desc(uint64_t* a, int m, uint64_t* tmp,
     for (int q = 0; q < EPT; ++q) {
         if (q * BLOCK + tid < m) {
             const uint32_t b0 = start[bin[q]], n = cnt[bin[q]];
-            uint32_t r = 0u;
-            for (uint32_t j = 0; j < n; ++j) r += tmp[b0 + j] > v[q] ? 1u : 0u;
+            uint32_t r = 0u, j = 0u;
+            for (; j + 4u <= n; j += 4u) {              // four LDS reads in flight per step
+                const uint64_t t0 = tmp[b0 + j], t1 = tmp[b0 + j + 1], t2 = tmp[b0 + j + 2], t3 = tmp[b0 + j + 3];
+                r += (t0 > v[q] ? 1u : 0u) + (t1 > v[q] ? 1u : 0u) + (t2 > v[q] ? 1u : 0u) + (t3 > v[q] ? 1u : 0u);
+            }
+            for (; j < n; ++j) r += tmp[b0 + j] > v[q] ? 1u : 0u;
             a[b0 + r] = v[q];
         }
     }
     __syncthreads();
+    return big;                                  // the largest bin (> BIN_SORT_MAX: the bitonic network sorted)
 }
 // The candidate buffer's first m <= KMAX entries, with the second KMAX entries as the scatter area.
-__device__ __forceinline__ void bin_sort_desc(int m, Shared& s) {
+__device__ __forceinline__ uint32_t bin_sort_desc(int m, Shared& s) {
     static_assert(TILE / 2 >= NBINS && 2 * KMAX <= CAP, "counts in cnt(), starts in bins(), scatter after the input");
-    bin_sort_desc<NBINS>(s.cand, m, s.cand + KMAX, s.cnt(), s.bins(), s.red, s.wsum);
+    return bin_sort_desc<NBINS>(s.cand, m, s.cand + KMAX, s.cnt(), s.bins(), s.red, s.wsum);
 }
 static_assert((TILE / 2 + NBINS) / 2 >= KMAX, "the stage holds a compacted top k");
 
@@ -2306,15 +2311,27 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 }
             }
         }
-        for (uint32_t i = (uint32_t)(r_me + SPEC * tps); act && i < cnm; i += (uint32_t)tps) {   // long lists
-            const uint64_t w = lst[i];
-            const bool in = w != 0 && comp_key(w) >= L;
-            if (in) kmax = comp_key(w) > kmax ? comp_key(w) : kmax;
-            wave_append(in, w, s.cand, &s.count, gcap);
+        // long lists: the entries past the prefetched window, LL loads in flight per thread and round (a list of
+        // k ~ 2048 entries then costs one or two L2 round trips instead of one per tps entries)
+        constexpr int LL = 8;
+        for (uint32_t i0 = (uint32_t)(r_me + SPEC * tps); act && i0 < cnm; i0 += (uint32_t)(LL * tps)) {
+            uint64_t w[LL];
+#pragma unroll
+            for (int q = 0; q < LL; ++q) {
+                const uint32_t i = i0 + (uint32_t)(q * tps);
+                w[q] = i < cnm ? lst[i] : 0ull;
+            }
+#pragma unroll
+            for (int q = 0; q < LL; ++q) {
+                const bool in = w[q] != 0 && comp_key(w[q]) >= L;
+                if (in) kmax = comp_key(w[q]) > kmax ? comp_key(w[q]) : kmax;
+                wave_append(in, w[q], s.cand, &s.count, gcap);
+            }
         }
         for (int i = tid; i < NBINS; i += BLOCK) s.bins()[i] = 0u;
         uint32_t kmin = L;
         block_minmax_u32(kmin, kmax, s.red);
+        FS_MARK(5);                                 // general merge: candidates >= L gathered
         const uint32_t n = s.count;
         const bool in_lds = n <= gcap;
         // T1: tight threshold from a histogram of the candidates' keys over [L, kmax]
@@ -2334,6 +2351,8 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
         __syncthreads();
         uint32_t c1;
         const uint32_t T1 = hist_threshold(s.bins(), L, sh, k, &c1, s.wsum, s.red);
+        FS_MARK(6);                                 // T1 known
+        FS_TAG(9, c1); FS_TAG(10, n); FS_TAG(11, in_lds ? 1 : 0);
         if (c1 < (uint32_t)k) {
             // Fewer than k candidates: with L = 0 (no bound above NaN's key) every number of the row is a candidate,
             // so the row holds fewer than k numbers and samples over them (NaN is never a candidate); with L > 0 the
@@ -2408,14 +2427,21 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 __syncthreads();
                 m = (int)s.count;
             }
+            if (in_lds) {                               // the c1 >= k entries at or above T1 hold the top k
+                const int mt = keep_from(m, (uint64_t)T1 << 32, s);
+                if (mt >= 0) m = mt;
+            }
             if (m > KMAX) {                             // else the counting sort orders all m; the first k are used
                 compact_exact(m, k, s);
                 m = k;
             }
-            bin_sort_desc(m, s);
+            const uint32_t big = bin_sort_desc(m, s);
+            FS_TAG(12, big);
+            (void)big;
             top = s.cand;
             c1 = (uint32_t)m;
         }
+        FS_MARK(7);                                 // the top candidates sorted
         if (!wave_done) {
             if (c1 < (uint32_t)k) {                       // c1 >= k after the clamp above; never read past the list
                 if (tid == 0) atomicOr(a.err, FS_DEVERR_INTERNAL);
@@ -2444,6 +2470,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 }
             }
             const double sum = block_sum_f64(part, s.red);
+            FS_MARK(8);                                 // exp and their sum
             double pr[KPT];
     #pragma unroll
             for (int q = 0; q < KPT; ++q) pr[q] = e[q] / sum;
