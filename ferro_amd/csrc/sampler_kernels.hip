@@ -934,8 +934,9 @@ __device__ __forceinline__ void apply_penalties(float (&x)[TPT], const Args& a, 
         }
     };
     const int nids = (int)s.nids;
-    for (int i = tid; i < nids && i < WIDS; i += BLOCK) count_id(s.ids[i]);
-    if (nids > WIDS)                                  // long window: rescan it from memory
+    if (nids <= WIDS)                                 // the segment's window ids, gathered in LDS
+        for (int i = tid; i < nids; i += BLOCK) count_id(s.ids[i]);
+    else                                              // a longer window: the whole window again, from memory
         for (int64_t i = rc.b + tid; i < rc.len; i += BLOCK) {
             const int id = hist_at(a, rc, i);
             if (id >= 0 && id < a.V) count_id(id);

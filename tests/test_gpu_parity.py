@@ -230,6 +230,38 @@ def test_penalty_windows_and_out_of_range_ids():
     assert nb == 0
 
 
+def test_count_penalties_by_wave_and_by_table():
+    """Frequency / presence counts (sampler.cpp:11-18 plus the extension) on 8-tile segments (B=64 x V=262144), where
+    each segment buckets its window ids by tile and every wave counts its own logits, next to the per-tile table
+    that a segment with more than 2048 window ids keeps: Zipf windows, a 6000-id window inside segment 0, one id
+    repeated 300 times, ids on every wave's logits of one tile, a one-id window and an empty one; greedy, k <= 64
+    and k > 64 rows, and whole-row (top_k = 0, k > 2048) rows with the 6000-id window. (A window with more than
+    2048 ids in a segment was once counted twice: the gathered ids and then the whole window again.)"""
+    V, B = 262144, 64
+    rng = np.random.default_rng(64)
+    rows = list(W.mixture_logits(rng, B, V))
+    hists = [W.zipf_ids(rng, V, 1024) for _ in range(B)]
+    for b in range(0, B, 8):
+        hists[b] = rng.integers(0, 8 * 4096, 6000).astype(np.int32)           # > 2048 ids in segment 0
+    for b in range(1, B, 8):
+        top = int(np.argmax(rows[b]))
+        hists[b] = np.concatenate([np.full(300, top, np.int32), W.zipf_ids(rng, V, 200)])   # a count of 300
+    for b in range(2, B, 8):
+        t = int(rng.integers(0, V // 4096)) * 4096                            # one tile, every wave's logits
+        hists[b] = (t + np.arange(0, 4096, 7)).astype(np.int32)
+    hists[3] = np.array([int(np.argmax(rows[3]))], np.int32)
+    hists[4] = np.zeros(0, np.int32)
+    p = W.make_params(B, temperature=0.9, top_k=40, top_p=0.95, repetition_penalty=1.1,
+                      frequency_penalty=0.6, presence_penalty=0.4)
+    p["top_k"][::3] = 700
+    p["temperature"][::5] = 0.0
+    p["repetition_penalty"][::4] = 1.0
+    p["presence_penalty"][1::4] = 0.0
+    p["top_k"][48], p["top_k"][56] = 0, 3000                                 # whole-row path, long windows
+    g, o, nb = check(_case(rows, p, hists, rng.random(B), "count_penalties"), kcap=700)
+    assert nb <= 1
+
+
 def test_large_k_full_vocab():
     """k > 2048 (top_k = 0 is ferro's k = n, sampler.cpp:26): the whole-row path, with every candidate's
     probability compared (kcap = V) and the draw at the extremes of u."""
