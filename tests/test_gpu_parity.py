@@ -262,6 +262,27 @@ def test_count_penalties_by_wave_and_by_table():
     assert nb <= 1
 
 
+@pytest.mark.parametrize("B,V", [(203, 65536), (130, 262144)])
+def test_balanced_layouts(B, V):
+    """Batches with 16 to 64 rows per XCD, where each XCD apportions its segment workgroups over its rows by their
+    sampling settings (XCDs holding one row more or less when B is not a multiple of 8): greedy, small and large
+    k, k > 2048 and top_k = 0 (whole-row rows whose segments meet at row barriers), penalties and softcap mixed."""
+    rng = np.random.default_rng(B)
+    x = W.mixture_logits(rng, B, V)
+    p = W.make_params(B, temperature=0.9)
+    p["temperature"] = rng.choice([0.0, 0.5, 0.9, 1.4], B)
+    p["top_k"] = rng.choice([1, 8, 64, 200, 1000, 2048, 3000, 0], B)
+    p["top_p"] = rng.choice([1.0, 0.9], B)
+    p["min_p"] = rng.choice([0.0, 0.0, 0.05], B)
+    p["repetition_penalty"] = rng.choice([1.0, 1.2], B)
+    p["frequency_penalty"] = rng.choice([0.0, 0.5], B)
+    p["presence_penalty"] = rng.choice([0.0, 0.3], B)
+    p["softcap"][::7] = 30.0
+    hists = [W.zipf_ids(rng, V, int(rng.integers(0, 600))) for _ in range(B)]
+    g, o, nb = check(_case(list(x), p, hists, rng.random(B), f"balanced_B{B}_V{V}"), kcap=256)
+    assert nb <= 2
+
+
 def test_large_k_full_vocab():
     """k > 2048 (top_k = 0 is ferro's k = n, sampler.cpp:26): the whole-row path, with every candidate's
     probability compared (kcap = V) and the draw at the extremes of u."""

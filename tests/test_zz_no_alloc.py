@@ -1,8 +1,8 @@
 """GPU: fs_sample_batch_static (the entry point that allocates nothing) against fs_sample_batch.
 
 Both entry points run the same kernels; the static one binds the device's file-scope workspace instead of the
-context's allocated one. Every output (tokens, candidate ids, probabilities, kept counts) must be identical, on two
-calls in a row, the second with a smaller batch and a shorter vocabulary (the workspace keeps the first call's
+context's allocated one. Every output (tokens, candidate ids, probabilities, kept counts) must be identical, on
+three calls in a row, each with a smaller batch than the one before (the workspace keeps the previous call's
 contents), and the device error bits must stay clear. A batch past the static limits is refused with FS_E_LIMIT.
 """
 import ctypes
@@ -80,7 +80,8 @@ def mixed(seed, B, V):
 def test_static_entry_matches_allocating_entry():
     L = lib()
     ctx_a, ctx_s = Context(), Context()
-    for w, kcap in ((W.config3(), 64), (mixed(7, 5, 70001), 96)):
+    # cfg5 (balanced layout, every (row, segment) slot of the static workspace), then cfg3, then a small ragged batch
+    for w, kcap in ((W.config5(), 2048), (W.config3(), 64), (mixed(7, 5, 70001), 96)):
         say(f"case {w.name}: B={w.B} V={w.V} kcap={kcap}, fs_sample_batch_static then fs_sample_batch")
         got = run(L.fs_sample_batch_static, ctx_s, w, kcap)
         ref = run(L.fs_sample_batch, ctx_a, w, kcap)
