@@ -1054,10 +1054,7 @@ __device__ __forceinline__ void gather_window(const Args& a, const RowCtx& rc, i
     const int tid = threadIdx.x;
     if (tid == 0) s.nids = 0u;
     __syncthreads();
-    for (int64_t i0 = rc.b; i0 < rc.len; i0 += BLOCK) {
-        const int64_t i = i0 + tid;
-        int id = -1;
-        if (i < rc.len) id = hist_at(a, rc, i);
+    auto take = [&](int id) {
         const bool in = id >= seg_lo && id < seg_hi;
         const uint64_t m = __ballot(in);
         if (m != 0ull) {
@@ -1067,6 +1064,20 @@ __device__ __forceinline__ void gather_window(const Args& a, const RowCtx& rc, i
             const uint32_t pos = base + mbcnt(m);
             if (in && pos < (uint32_t)WIDS) s.ids[pos] = id;
         }
+    };
+    // the first GW * BLOCK ids requested together (one round trip), the rest round by round
+    constexpr int GW = 4;
+    int idq[GW];
+#pragma unroll
+    for (int q = 0; q < GW; ++q) {
+        const int64_t i = rc.b + q * BLOCK + tid;
+        idq[q] = i < rc.len ? hist_at(a, rc, i) : -1;
+    }
+#pragma unroll
+    for (int q = 0; q < GW; ++q) take(idq[q]);
+    for (int64_t i0 = rc.b + GW * BLOCK; i0 < rc.len; i0 += BLOCK) {
+        const int64_t i = i0 + tid;
+        take(i < rc.len ? hist_at(a, rc, i) : -1);
     }
     __syncthreads();
 }
