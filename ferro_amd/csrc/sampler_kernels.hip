@@ -2972,7 +2972,8 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
             }
             if (topk) {
                 lastn = 0;
-                const int n = check(1, safe);
+                // with tile 0's appends deferred the buffer is still empty: no check (two barriers) is needed
+                const int n = defer0 ? 0 : check(1, safe);
                 overflow = n > CAP;
                 if (!safe && ntiles >= 3) snap1 = row_snap(rsr, tkey);
                 const int per_tile = n > 32 ? n : 32;
