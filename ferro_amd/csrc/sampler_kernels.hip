@@ -2849,10 +2849,11 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
     // the headroom short (or more than KMAX entries) it keeps exactly the segment's k largest.
     int lastn = 0;
     const bool dyncount = topk && k > WAVE;      // k > 64: the buffered entries are counted at checks
-    auto check = [&](int tiles, bool strict) -> int {
+    // last: the segment's final check, after which nothing is appended (its count needs no second barrier)
+    auto check = [&](int tiles, bool strict, bool last = false) -> int {
         __syncthreads();
         int n = (int)s.count;
-        __syncthreads();                               // every wave holds the same count before any appends again
+        if (!last) __syncthreads();                    // every wave holds the same count before any appends again
         int rate = (n - lastn) / (tiles > 0 ? tiles : 1);
         rate = rate > 341 ? rate : 341;
         auto short_room = [&](int m) {
@@ -3069,7 +3070,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
         }
 
         if (!topk) break;
-        if (!overflow) overflow = check(since, true) > CAP;
+        if (!overflow) overflow = check(since, true, true) > CAP;
         if (!overflow) break;
         // overflow: the buffer lost candidates. tkey is still a valid bound; stream the segment again in safe mode
         // (its logits are already counted in the row histogram).
