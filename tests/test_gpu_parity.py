@@ -18,7 +18,7 @@ torch = pytest.importorskip("torch")
 from oracle import oracle as O  # noqa: E402
 from ferro_amd import workloads as W  # noqa: E402
 import ferro_amd as F  # noqa: E402
-from parity_util import compare, oracle_decode_loop  # noqa: E402
+from parity_util import boundary_row, compare, oracle_decode_loop  # noqa: E402
 
 NT = min(16, os.cpu_count() or 1)
 
@@ -281,6 +281,33 @@ def test_balanced_layouts(B, V):
     hists = [W.zipf_ids(rng, V, int(rng.integers(0, 600))) for _ in range(B)]
     g, o, nb = check(_case(list(x), p, hists, rng.random(B), f"balanced_B{B}_V{V}"), kcap=256)
     assert nb <= 2
+
+
+@pytest.mark.parametrize("which", ["cfg3", "cfg5", "topk0"])
+def test_token_only_calls(which):
+    """Calls without candidate outputs (kcap = 0, as the server and bench.py call): tokens and kept counts equal
+    the oracle's, except where the draw lies within 1e-6 of a cumulative boundary (counted)."""
+    w = {"cfg3": W.config3, "cfg5": W.config5, "topk0": W.config3_all_tokens}[which]()
+    kk = np.where((w.params["top_k"] > 0) & (w.params["top_k"] < w.V), w.params["top_k"], w.V)
+    kcap = int(min(max(kk.max(), 1), w.V))
+    say(f"case {w.name}: B={w.B} V={w.V}, GPU kcap=0, oracle kcap={kcap}")
+    g = run_gpu(w, 0)
+    o = run_oracle(w, kcap)
+    assert F.device_error() == 0
+    near = differ = 0
+    for b in range(w.B):
+        p = w.params[b]
+        if p["temperature"] <= 0 or p["top_k"] == 1:
+            assert g["tok"][b] == o["tok"][b], f"row {b} greedy token"
+            continue
+        m = int(o["ncand"][b])
+        edge = boundary_row(o["cand_probs"][b, :m], int(o["keep"][b]), w.u[b], float(p["top_p"]), float(p["min_p"]))
+        near += int(edge)
+        if g["tok"][b] != o["tok"][b] or g["keep"][b] != o["keep"][b]:
+            assert edge, f"row {b}: tok {g['tok'][b]} vs {o['tok'][b]}, keep {g['keep'][b]} vs {o['keep'][b]}"
+            differ += 1
+    say(f"  {w.name}: {near} rows near a boundary, {differ} of them differ")
+    assert near <= 2
 
 
 def test_large_k_full_vocab():
