@@ -106,7 +106,7 @@ struct Args {
 // keeps the constant 100 MHz clock (s_memrealtime) of phase i in LDS (no memory store, so no wait on the memory
 // counter in the middle of the kernel) and writes them to trace[blockIdx * TRACE_W + i] at its end; slots 13-15 hold
 // the role (1 segment, 2 merge), the row and the segment.
-constexpr int TRACE_W = 16;
+[[maybe_unused]] constexpr int TRACE_W = 16;
 #ifdef FS_TRACE
 #define FS_MARK(i)                                                                                        \
     do {                                                                                                  \
@@ -1002,8 +1002,7 @@ __device__ __forceinline__ void bucket_window(int seg_lo, int ntiles, Shared& s)
 // (e / (4 * BLOCK)) * 4 * WAVE + e % (4 * WAVE) of its table (lane l's four logits of float4 j sit at
 // j * 4 * WAVE + 4 * l). A wave's LDS accesses complete in order, so no barrier is needed; tiles holding no window
 // id skip the pass. Same arithmetic as apply_penalties.
-__device__ __forceinline__ void wave_penalties(float (&x)[TPT], const Args& a, const RowCtx& rc, int lo, int tt,
-                                               Shared& s) {
+__device__ __forceinline__ void wave_penalties(float (&x)[TPT], const RowCtx& rc, int lo, int tt, Shared& s) {
     static_assert(NV * 4 * WAVE * NWAVES == TILE, "a tile is the waves' float4 columns");
     static_assert(WIDS < 0xFFFF, "16-bit counts");
     const int b0 = tt > 0 ? (int)s.off[tt - 1] : 0, b1 = (int)s.off[tt];
@@ -2913,7 +2912,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
             }
             if (rc.capped) softcap_vals_unrolled(x, rc.p.softcap);
             if (tablepen) apply_penalties(x, a, rc, lo, s);
-            if (wavepen) wave_penalties(x, a, rc, lo, 0, s);
+            if (wavepen) wave_penalties(x, rc, lo, 0, s);
             if (fastpen) bitmap_pen(x, lo);
             if (rc.greedy) {
                 greedy_update(x, 0);
@@ -3015,7 +3014,7 @@ __device__ __forceinline__ void process_segment(const Args& a, const RowCtx& rc,
                     const int lo = seg_lo + tt * TILE;
                     if (rc.capped) softcap_vals_unrolled(x, rc.p.softcap);
                     if (tablepen) apply_penalties(x, a, rc, lo, s);
-                    if (wavepen) wave_penalties(x, a, rc, lo, tt, s);
+                    if (wavepen) wave_penalties(x, rc, lo, tt, s);
                     if (fastpen) bitmap_pen(x, lo);
                     if (p == 0 && take1) raise_key(row_bound(snap1, k));
                     if (p == 0 && dpend) raise_key(row_bound(snapd, k));
