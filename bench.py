@@ -6,8 +6,9 @@ headline rows with top_k = 0 (every token a candidate); --workload all prints on
 
 A step is one fs_sample_batch (fs_verify for cfg4) call over the whole batch (penalty -> top-k -> softmax/top-p ->
 draw, one kernel) with inputs already resident in HBM. The logits rotate over enough copies (> 256 MB MALL) that
-every step streams its rows from HBM. Each line carries rows/s, the kernel's HBM roofline fraction (HIP events on
-the launch stream), the HBM traffic of the committed rocprofv3 PMC summary for that workload, and the CPU baseline
+every step streams its rows from HBM. The K timed calls are captured once into a HIP graph and replayed back to
+back, as a serving loop issues them (the same calls launched one by one from Python are reported beside). Each line
+carries rows/s, the kernel's HBM roofline fraction (HIP events on the replay stream), the HBM traffic of the committed rocprofv3 PMC summary for that workload, and the CPU baseline
 (ferro's own sampler.cpp compiled by oracle/Makefile where it supports the workload's parameters, else the oracle
 restatement) timed on this host's cores on a bounded sample of the same rows. The CPU leg also checks the GPU's
 tokens: rows whose token differs from the reference are counted, and so are the rows whose draw lies within 1e-6 of
@@ -183,6 +184,51 @@ def cpu_all_cores(w, hist, hoff, params, budget_s, nth):
                 sample=f"{rows_done} rows (the B={w.B} batch repeated), rows spread over {nth} threads ({t_used:.1f} s)")
 
 
+def graph_wall(torch, call, what, ctx, bufs, nrot, V, fixed, K, tok, want, L):
+    """K calls captured into one HIP graph (torch.cuda.CUDAGraph over the capture stream) and replayed: returns the
+    replay's wall-clock seconds and its HIP-event time per call (ms; an event pair on the replay stream around the
+    whole replay, so back-to-back launches with no host work between them). The calls launch kernels only (no
+    allocation, copy or memset once warm), so they capture as they run eagerly. Replays are checked against the
+    eager tokens, with eager calls between them."""
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            cs = ctypes.c_void_p(side.cuda_stream)
+            for i in range(K):
+                rc = call(ctx.h, P(bufs[i % nrot]), V, *fixed[:-1], cs)
+                if rc != 0:
+                    raise RuntimeError(f"{what} returned {rc} under capture")
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    walls, evms = [], []
+    stream = torch.cuda.current_stream()
+    for rep in range(3):
+        tok.fill_(-1)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        walls.append(time.perf_counter() - t0)
+        evms.append(e0.elapsed_time(e1) / K)
+        if not np.array_equal(tok.cpu().numpy(), want):
+            raise RuntimeError(f"graph replay {rep} changed the tokens")
+        rc = call(ctx.h, P(bufs[0]), V, *fixed)          # eager work between the replays
+        if rc != 0:
+            raise RuntimeError(f"{what} returned {rc}")
+        torch.cuda.synchronize()
+    if F_device_error(L, ctx, fixed[-1]) != 0:
+        raise RuntimeError("device error bits set after the graph replays")
+    del g
+    best = 1 + int(np.argmin(walls[1:]))
+    return walls[best], evms[best]
+
+
 def run_workload(name, args, torch):
     from ferro_amd import workloads as W
     from ferro_amd import _lib
@@ -245,29 +291,34 @@ def run_workload(name, args, torch):
         raise RuntimeError("tokens changed between steps on identical inputs")
     if F_device_error(L, ctx, sh) != 0:
         raise RuntimeError("device error bits set after the timed steps")
+    wall_graph, graph_ms = graph_wall(torch, call, what, ctx, bufs, nrot, w.V, fixed, K, tok, gpu_tok, L)
 
     alg_bytes = w.algorithmic_bytes()
-    achieved = alg_bytes / (kern_ms * 1e-3) / 1e9
+    achieved = alg_bytes / (graph_ms * 1e-3) / 1e9
     out = {
         "metric": METRIC,
-        "value": w.B * K / wall,
+        "value": w.B * K / wall_graph,
         "unit": "rows/s",
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
-        "ms_per_step": wall / K * 1e3,
+        "ms_per_step": wall_graph / K * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded; BASELINE.json's logit, history and parameter distributions for this config)",
         "config": {"workload": desc, "B": w.B, "V": w.V, "entry_point": what, "logit_copies_rotated": nrot},
-        "value_note": ("rows/s over the wall clock of K back-to-back calls from Python (ctypes launch included); "
-                       "roofline.kernel_ms is the HIP-event time of one call on its stream"),
+        "value_note": ("rows/s over the wall clock of the K calls captured once into a HIP graph and replayed "
+                       "(as a serving loop issues them); roofline.kernel_ms is the HIP-event time per call over "
+                       "that replay, on its stream"),
+        "python_launch": {"value": w.B * K / wall, "ms_per_step": wall / K * 1e3,
+                          "note": "the same K calls launched one by one from Python through ctypes, an event pair "
+                                  "around each"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(name),
                      "kernel": f"{what}: {KERNEL} (segments, then a merging workgroup per row, one grid)",
-                     "kernel_ms": kern_ms, "algorithmic_bytes": alg_bytes,
+                     "kernel_ms": graph_ms, "kernel_ms_python_launch": kern_ms, "algorithmic_bytes": alg_bytes,
                      "algorithmic_bytes_note": "4*V per row (one read of the fp32 row) + 4 per history id"},
     }
     if args.copy_calib:
