@@ -229,6 +229,45 @@ def graph_wall(torch, call, what, ctx, bufs, nrot, V, fixed, K, tok, want, L):
     return walls[best], evms[best]
 
 
+def host_rows_rate(torch, w, dst, step_on, steps):
+    """The PCIe-inclusive rate: each step first copies the batch's fp32 rows from pinned host memory to the device
+    (as a caller holding host rows must; ferro's own call sites copy every row back from the GPU before sampling,
+    model_lfm2_lm.cpp:477-480), then samples them. Also times the copies alone."""
+    host = torch.from_numpy(w.logits).pin_memory()
+    view = dst[:, :w.V] if dst.dim() == 2 else dst
+    stream = torch.cuda.current_stream()
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, e0.elapsed_time(e1) / steps
+
+    def copy_only():
+        view.copy_(host, non_blocking=True)
+
+    def copy_and_sample():
+        view.copy_(host, non_blocking=True)
+        rc = step_on(dst)
+        if rc != 0:
+            raise RuntimeError(f"call returned {rc}")
+
+    wall_c, ms_c = timed(copy_only)
+    wall_s, ms_s = timed(copy_and_sample)
+    nbytes = w.logits.nbytes
+    return {"value": w.B * steps / wall_s, "unit": "rows/s", "ms_per_step": ms_s,
+            "copy_ms": ms_c, "copy_GBps": nbytes / (ms_c * 1e-3) / 1e9, "bytes_copied": nbytes,
+            "note": "each step copies the batch's rows host -> device (pinned, one async copy) and then samples "
+                    "them; ms from HIP events on the stream"}
+
+
 def run_workload(name, args, torch):
     from ferro_amd import workloads as W
     from ferro_amd import _lib
@@ -321,6 +360,9 @@ def run_workload(name, args, torch):
                      "kernel_ms": graph_ms, "kernel_ms_python_launch": kern_ms, "algorithmic_bytes": alg_bytes,
                      "algorithmic_bytes_note": "4*V per row (one read of the fp32 row) + 4 per history id"},
     }
+    if args.host_rows:
+        out["host_rows"] = host_rows_rate(torch, w, bufs[0], step_on=lambda dst: call(ctx.h, P(dst), w.V, *fixed),
+                                          steps=K)
     if args.copy_calib:
         src = torch.empty(64 << 20, dtype=torch.float32, device=dev)   # 256 MiB
         dst = torch.empty_like(src)
@@ -415,6 +457,8 @@ def main():
                          "top_k = 0; all: one line per workload")
     ap.add_argument("--breakdown", action="store_true",
                     help="instead of the bench line: per-stage ablation timings of the workload (one JSON line)")
+    ap.add_argument("--host-rows", action="store_true",
+                    help="also report the PCIe-inclusive rate: the rows copied from pinned host memory every step")
     ap.add_argument("--copy-calib", action="store_true",
                     help="after the timed steps, run plain 256 MiB device copies (counter calibration for rocprofv3)")
     args = ap.parse_args()
