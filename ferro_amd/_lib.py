@@ -7,6 +7,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+import warnings
 
 import numpy as np
 
@@ -19,6 +20,8 @@ FS_E_HIP = -2
 FS_E_NOMEM = -3
 FS_E_DEVICE = -4
 FS_E_LIMIT = -5
+FS_W_RECOVERED = 1          # success; an earlier call's give-up was cleared (FS_DEVERR_INTERNAL stays set)
+FS_WAIT_GIVE_UP = 0xFFFFFFFF
 FS_DEVERR_COUNT_OVERFLOW = 1
 FS_DEVERR_INTERNAL = 2
 
@@ -45,6 +48,7 @@ SIGNATURES = {
     "fs_softcap_batch": (ctypes.c_int, [_P, _P, _I64, ctypes.c_float, _P]),
     "fs_device_error": (ctypes.c_int, [_P, _P, _P]),
     "fs_set_wait_limit": (ctypes.c_int, [_P, ctypes.c_uint32]),
+    "fs_plan_layout": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32, _P, _P, _P]),
     "fs_rng_create": (ctypes.c_int, [ctypes.c_uint64, _P]),
     "fs_rng_destroy": (ctypes.c_int, [_P]),
     "fs_rng_next_u": (ctypes.c_int, [_P, _P, _I32]),
@@ -83,7 +87,25 @@ def lib():
     return _lib
 
 
-def check(rc: int, what: str) -> None:
-    if rc != FS_OK:
+class RecoveredWarning(UserWarning):
+    """A call returned FS_W_RECOVERED: it succeeded after clearing the workspace an earlier call's give-up left."""
+
+
+def check(rc: int, what: str) -> int:
+    """Raise on a negative status; warn (RecoveredWarning) on FS_W_RECOVERED. Returns rc."""
+    if rc < 0:
         msg = lib().fs_strerror(rc).decode()
         raise SamplerError(f"{what} failed: {msg} ({rc})")
+    if rc == FS_W_RECOVERED:
+        warnings.warn(f"{what}: {lib().fs_strerror(rc).decode()}", RecoveredWarning, stacklevel=3)
+    elif rc != FS_OK:
+        raise SamplerError(f"{what}: unexpected status {rc}")
+    return rc
+
+
+def plan_layout(cus: int, xccs: int, B: int, V: int, static_ws: bool = False):
+    """fs_plan_layout: (nseg, seg_tiles, slots) the sampling call would launch on such a device (host only)."""
+    n, t, sl = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+    rc = lib().fs_plan_layout(cus, xccs, B, V, 1 if static_ws else 0, ctypes.byref(n), ctypes.byref(t),
+                              ctypes.byref(sl))
+    return rc, n.value, t.value, sl.value

@@ -41,7 +41,7 @@ def _run(cmd, what, verbose):
         raise RuntimeError(f"{cmd[0]} failed ({r.returncode}) building {what}")
 
 
-def build(verbose: bool = False, trace: bool = True) -> str:
+def build(verbose: bool = False, trace: bool = False) -> str:
     jobs = [([HIPCC, *FLAGS, "-o", LIB, SRC], LIB)]
     if trace:
         jobs.append(([HIPCC, *FLAGS, "-DFS_TRACE", "-o", TRACE_LIB, SRC], TRACE_LIB))
@@ -64,4 +64,5 @@ def build(verbose: bool = False, trace: bool = True) -> str:
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    # `python ferro_amd/build.py --trace` also builds the phase-timestamp library that ferro_amd/trace_phases.py loads
+    print(build(verbose=True, trace="--trace" in sys.argv[1:]))

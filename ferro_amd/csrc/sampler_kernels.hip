@@ -30,6 +30,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+#include <cstring>
 #include <mutex>
 #include <new>
 #include <random>
@@ -98,7 +100,7 @@ struct Args {
     uint32_t* stream_cnt;          // [n_streams] verify completion counters, left at 0
     int32_t* err;                  // device error bits
     int32_t* dirty;                // nonzero: a merge gave up waiting; the row histograms and counters may be stale
-    uint32_t merge_spins;          // bounded wait of the merge role (polls)
+    uint32_t merge_spins;          // bounded wait of the merge role (polls); 0: give up without waiting
     uint64_t* trace;               // FS_TRACE builds: per-workgroup phase timestamps (NULL: none)
 };
 
@@ -3146,7 +3148,7 @@ __device__ __forceinline__ bool row_sync(const Args& a, int row, uint32_t target
         for (;;) {
             const uint32_t v = __hip_atomic_fetch_add(c, 0x10000u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             if (v & ROW_ABANDONED) { ok = 0u; break; }
-            if ((v & 0x7FFFu) >= target) break;
+            if ((v & 0x7FFFu) >= target && a.merge_spins != 0u) break;
             if (++spins >= a.merge_spins) {
                 __hip_atomic_fetch_or(c, ROW_ABANDONED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 ok = 0u;
@@ -3717,12 +3719,15 @@ __device__ __forceinline__ void merge_role(const Args& a, int mi, Shared& s) {
         // still adds to this row's counter and histogram) and this row, too, is computed alone.
         uint32_t alone = ld_agent(a.dirty) != 0 ? 1u : 0u;
         uint32_t spins = 0u;
-        while (!alone &&
-               (__hip_atomic_fetch_add(ctr, 0x10000u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & 0xFFFFu) <
-                   (uint32_t)rc.nseg) {
+        while (!alone && (a.merge_spins == 0u ||
+                          (__hip_atomic_fetch_add(ctr, 0x10000u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) &
+                           0xFFFFu) < (uint32_t)rc.nseg)) {
             if (++spins >= a.merge_spins) {
                 atomicOr(a.err, FS_DEVERR_INTERNAL);
                 __hip_atomic_store(a.dirty, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                // err[2..3]: the address of a host-mapped flag that the next call reads on the host (or 0)
+                int32_t* hf = (int32_t*)ld_agent(reinterpret_cast<const uint64_t*>(a.err + 2));
+                if (hf) __hip_atomic_store(hf, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 alone = 1u;
                 break;
             }
@@ -3816,18 +3821,19 @@ __global__ __launch_bounds__(BLOCK, 4) void segment_kernel(const float* logits, 
     FS_FLUSH();
 }
 
-// Merge kernel: one workgroup per row, after the segment kernel. The segment lists are requested first, so their
-// latency overlaps the row's parameter loads.
+// Merge kernel: one workgroup per row, for rows shorter than one tile (no segments; the segment lists are requested
+// first, so their latency overlaps the row's parameter loads), or, with `alone`, every row sampled from its logits by
+// one workgroup (a device whose XCD layout the segment grid's hand-off cannot rely on).
 __global__ __launch_bounds__(BLOCK) void merge_kernel(int nseg, uint64_t* cand, uint32_t* meta, uint32_t* rhist,
-                                                      const fs_row_params* params, Args a) {
+                                                      const fs_row_params* params, int alone, Args a) {
     static_assert(2 * SMALL * 8 <= NBINS * 4, "rank-sort buffers alias the histogram");
     __shared__ __align__(16) Shared s;
     a.nseg = nseg; a.cand = cand; a.meta = meta; a.rhist = rhist; a.params = params;
     const int row = __builtin_amdgcn_readfirstlane((int)blockIdx.x);
-    Pre pre;
+    Pre pre = {};
     const RowCtx rc = row_ctx(a, row);
-    prefetch_lists(a, rc, pre);
-    merge_row(a, rc, s, pre);
+    if (!alone) prefetch_lists(a, rc, pre);
+    merge_row(a, rc, s, pre, alone != 0);
 }
 
 // fs_softcap_batch: the sampler's fused final-logit cap as a standalone elementwise pass.
@@ -4082,6 +4088,12 @@ struct fs_context {
     std::mutex mu;
     int device = -1;
     int cus = 0;               // compute units of the device
+    int xccs = 0;              // XCDs of the device (hipDeviceAttributeNumberOfXccs)
+    bool seg_layout = true;    // the segment grid's hand-off holds on this device (XCDS % xccs == 0)
+    int32_t* hflag = nullptr;  // host-mapped: a merge of an earlier call gave up (set by the kernel, read here)
+    int32_t* hflag_dev = nullptr;
+    bool captured = false;     // a call was recorded into a graph: workspaces are retired, never freed, on growth
+    std::vector<void*> retired;
     uint64_t* cand = nullptr;
     size_t cand_slots = 0;     // chunk slots of CAP entries
     uint32_t* meta = nullptr;
@@ -4090,27 +4102,48 @@ struct fs_context {
     size_t row_cap = 0;
     uint32_t* stream_cnt = nullptr;
     size_t stream_cap = 0;
-    int32_t* err = nullptr;        // [0]: error bits; [1]: dirty (a merge gave up; see fs_device_error)
+    int32_t* err = nullptr;        // [0]: error bits; [1]: dirty (a merge gave up; see fs_device_error); [2..3]: hflag_dev
     uint32_t merge_spins = fs::MERGE_SPINS;
     int static_dev = -1;       // device whose static workspace fs_sample_batch_static used with this context
     uint64_t* trace = nullptr; // FS_TRACE builds: phase timestamps, trace_cap entries (fs_trace_set)
     int64_t trace_cap = 0;
 };
 
+namespace fs {
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0u;
+}
+}  // namespace fs
+
 namespace {
+
+// Zero n words on st with a fill kernel (no hipMemsetAsync: the call may be recorded into a graph).
+void clear_words(hipStream_t st, void* p, int64_t n) {
+    if (!p || n <= 0) return;
+    const int64_t blocks = std::min<int64_t>(1024, (n + 255) / 256);
+    hipLaunchKernelGGL(fs::zero_words_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (uint32_t*)p, n);
+}
+
+// A workspace buffer that is replaced: freed, or, once a call of the context has been recorded into a HIP graph
+// (whose replays keep using the old addresses), kept until fs_destroy.
+void release(fs_context* c, void* p) {
+    if (!p) return;
+    if (c->captured) c->retired.push_back(p);
+    else (void)hipFree(p);
+}
 
 int grow(fs_context* c, size_t slots, size_t rows, size_t streams) {
     if (slots > c->cand_slots) {
-        if (c->cand) (void)hipFree(c->cand);
-        if (c->meta) (void)hipFree(c->meta);
+        release(c, c->cand);
+        release(c, c->meta);
         c->cand = nullptr; c->meta = nullptr; c->cand_slots = 0;
         if (hipMalloc(&c->cand, slots * fs::CAP * sizeof(uint64_t)) != hipSuccess) return FS_E_NOMEM;
         if (hipMalloc(&c->meta, slots * 2 * sizeof(uint32_t)) != hipSuccess) return FS_E_NOMEM;
         c->cand_slots = slots;
     }
     if (rows > c->row_cap) {
-        if (c->rhist) (void)hipFree(c->rhist);
-        if (c->rmass) (void)hipFree(c->rmass);
+        release(c, c->rhist);
+        release(c, c->rmass);
         c->rhist = nullptr; c->rmass = nullptr; c->row_cap = 0;
         if (hipMalloc(&c->rhist, rows * fs::RBINS * sizeof(uint32_t)) != hipSuccess) return FS_E_NOMEM;
         if (hipMemset(c->rhist, 0, rows * fs::RBINS * sizeof(uint32_t)) != hipSuccess) return FS_E_HIP;
@@ -4119,15 +4152,24 @@ int grow(fs_context* c, size_t slots, size_t rows, size_t streams) {
         c->row_cap = rows;
     }
     if (streams > c->stream_cap) {
-        if (c->stream_cnt) (void)hipFree(c->stream_cnt);
+        release(c, c->stream_cnt);
         c->stream_cnt = nullptr; c->stream_cap = 0;
         if (hipMalloc(&c->stream_cnt, streams * sizeof(uint32_t)) != hipSuccess) return FS_E_NOMEM;
         if (hipMemset(c->stream_cnt, 0, streams * sizeof(uint32_t)) != hipSuccess) return FS_E_HIP;
         c->stream_cap = streams;
     }
+    if (!c->hflag) {
+        if (hipHostMalloc((void**)&c->hflag, sizeof(int32_t), hipHostMallocMapped) != hipSuccess) return FS_E_NOMEM;
+        *(volatile int32_t*)c->hflag = 0;
+        if (hipHostGetDevicePointer((void**)&c->hflag_dev, c->hflag, 0) != hipSuccess) return FS_E_HIP;
+    }
     if (!c->err) {
-        if (hipMalloc(&c->err, 2 * sizeof(int32_t)) != hipSuccess) return FS_E_NOMEM;
-        if (hipMemset(c->err, 0, 2 * sizeof(int32_t)) != hipSuccess) return FS_E_HIP;
+        // error bits, dirty flag, then the device address of the host-mapped give-up flag (read by a give-up only)
+        int32_t h[4] = {0, 0, 0, 0};
+        const uint64_t fa = (uint64_t)(uintptr_t)c->hflag_dev;
+        memcpy(h + 2, &fa, sizeof(fa));
+        if (hipMalloc(&c->err, sizeof(h)) != hipSuccess) return FS_E_NOMEM;
+        if (hipMemcpy(c->err, h, sizeof(h), hipMemcpyHostToDevice) != hipSuccess) return FS_E_HIP;
     }
     return FS_OK;
 }
@@ -4136,8 +4178,11 @@ int grow(fs_context* c, size_t slots, size_t rows, size_t streams) {
 // would double the time), at least one per row; a segment streams >= 1 full tile of 4096 logits. The merge
 // handles each row's partial last tile (all of a row shorter than one tile). Sets a.nseg / a.seg_tiles and the
 // workspace the call needs (items = (row, segment) slots).
-int plan(int cus, fs::Args& a, int64_t rows, int64_t& items, int64_t& seg_grid) {
+// max_slots > 0 caps the workspace slots (XCDS * nseg * ceil(rows / XCDS)) by taking fewer segments per row; one
+// segment per row always fits rows <= max_slots.
+int plan(int cus, fs::Args& a, int64_t rows, int64_t& items, int64_t& seg_grid, int64_t max_slots = 0) {
     const int64_t tiles_row = a.V / fs::TILE;
+    const int64_t per_slot = (rows + fs::XCDS - 1) / fs::XCDS;
     a.nseg = 0;
     a.seg_tiles = 1;
     if (tiles_row > 0) {
@@ -4145,8 +4190,12 @@ int plan(int cus, fs::Args& a, int64_t rows, int64_t& items, int64_t& seg_grid) 
         if (want < 1) want = 1;
         if (want > tiles_row) want = tiles_row;
         if (want > fs::BLOCK - 1) want = fs::BLOCK - 1;   // the merge gives each list (segments + tail) a thread
-        a.seg_tiles = (int)((tiles_row + want - 1) / want);
-        a.nseg = (int)((tiles_row + a.seg_tiles - 1) / a.seg_tiles);
+        for (;;) {
+            a.seg_tiles = (int)((tiles_row + want - 1) / want);
+            a.nseg = (int)((tiles_row + a.seg_tiles - 1) / a.seg_tiles);
+            if (max_slots <= 0 || want <= 1 || (int64_t)fs::XCDS * a.nseg * per_slot <= max_slots) break;
+            --want;
+        }
     }
     if (a.nseg > fs::MAX_SEGS) return FS_E_INVALID;
     items = rows * a.nseg;
@@ -4175,17 +4224,53 @@ int launch_planned(const fs::Args& a, int64_t rows, int64_t seg_grid, hipStream_
         return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
     }
     hipLaunchKernelGGL(fs::merge_kernel, dim3((unsigned)rows), dim3(fs::BLOCK), 0, st, a.nseg, a.cand, a.meta, a.rhist,
-                       a.params, a);
+                       a.params, 0, a);
     return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
 }
 
+// Every row sampled alone by one workgroup from its logits (a device whose XCD layout the segment grid's hand-off
+// does not fit).
+int launch_alone(fs::Args a, int64_t rows, hipStream_t st) {
+    a.nseg = 0;
+    a.balance = 0;
+    hipLaunchKernelGGL(fs::merge_kernel, dim3((unsigned)rows), dim3(fs::BLOCK), 0, st, 0, a.cand, a.meta, a.rhist,
+                       a.params, 1, a);
+    return hipGetLastError() == hipSuccess ? FS_OK : FS_E_HIP;
+}
+
+// The segment grid places a row's segments and its merging workgroup on workgroups of one index class mod XCDS, so
+// that they share an XCD (and its L2) under round-robin dispatch over the device's XCDs: that holds when the XCD
+// count divides XCDS (8, 4, 2 or 1: every MI355X partition mode). On other devices every row is sampled alone.
+bool layout_fits(int xccs) { return xccs >= 1 && fs::XCDS % xccs == 0; }
+
 int device_of(fs_context* ctx) {
     if (ctx->device < 0) {
-        if (hipGetDevice(&ctx->device) != hipSuccess) return FS_E_HIP;
-        if (hipDeviceGetAttribute(&ctx->cus, hipDeviceAttributeMultiprocessorCount, ctx->device) != hipSuccess)
+        int dev = -1;
+        if (hipGetDevice(&dev) != hipSuccess) return FS_E_HIP;
+        if (hipDeviceGetAttribute(&ctx->cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return FS_E_HIP;
+        int x = 0;
+        if (hipDeviceGetAttribute(&x, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess) return FS_E_HIP;
+        ctx->xccs = x;
+        ctx->seg_layout = layout_fits(x);
+        ctx->device = dev;
     }
     return FS_OK;
+}
+
+// Whether an earlier call's merge gave up waiting for its segments (the kernel sets the host-mapped flag). The
+// caller then enqueues, ahead of its own launch, fill kernels that clear what the late segments may have left (they
+// have finished once the stream reaches the fills), so the call runs normally instead of computing every row alone;
+// it returns FS_W_RECOVERED. The error bits stay for fs_device_error.
+bool gave_up(int32_t* flag) {
+    if (!flag || *(volatile int32_t*)flag == 0) return false;
+    *(volatile int32_t*)flag = 0;
+    return true;
+}
+
+bool capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
 }
 
 int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream_t st) {
@@ -4197,16 +4282,31 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
     if (rc != FS_OK) return rc;
     rc = grow(ctx, (size_t)(items > 0 ? items : 1), (size_t)rows, (size_t)(streams > 0 ? streams : 1));
     if (rc != FS_OK) return rc;
+    if (capturing(st)) ctx->captured = true;
     a.cand = ctx->cand; a.meta = ctx->meta; a.rhist = ctx->rhist; a.rmass = ctx->rmass;
     a.stream_cnt = ctx->stream_cnt; a.err = ctx->err; a.dirty = ctx->err + 1; a.merge_spins = ctx->merge_spins;
     a.trace = nullptr;
+    int done = FS_OK;
+    if (gave_up(ctx->hflag)) {
+        clear_words(st, ctx->rhist, (int64_t)(ctx->row_cap * fs::RBINS));
+        clear_words(st, ctx->rmass, (int64_t)(ctx->row_cap * fs::LB * 2));
+        clear_words(st, ctx->stream_cnt, (int64_t)ctx->stream_cap);
+        clear_words(st, ctx->err + 1, 1);
+        if (hipGetLastError() != hipSuccess) return FS_E_HIP;
+        done = FS_W_RECOVERED;
+    }
+    if (!ctx->seg_layout) {
+        rc = launch_alone(a, rows, st);
+        return rc != FS_OK ? rc : done;
+    }
 #ifdef FS_TRACE
     {
         const int64_t grid = seg_grid > 0 ? seg_grid + (int64_t)fs::XCDS * ((rows + fs::XCDS - 1) / fs::XCDS) : rows;
         if (ctx->trace && grid * fs::TRACE_W <= ctx->trace_cap) a.trace = ctx->trace;   // else: untraced
     }
 #endif
-    return launch_planned(a, rows, seg_grid, st);
+    rc = launch_planned(a, rows, seg_grid, st);
+    return rc != FS_OK ? rc : done;
 }
 
 }  // namespace
@@ -4224,21 +4324,19 @@ constexpr size_t ST_META_OFF = 256;
 constexpr size_t ST_RHIST_OFF = ST_META_OFF + ((ST_SLOTS * 2 * sizeof(uint32_t) + 255) / 256) * 256;
 constexpr size_t ST_RMASS_OFF = ST_RHIST_OFF + (size_t)ST_ROWS * fs::RBINS * sizeof(uint32_t);
 constexpr size_t ST_CAND_OFF = ST_RMASS_OFF + (size_t)ST_ROWS * fs::LB * sizeof(uint64_t);
-constexpr size_t ST_BYTES = ST_CAND_OFF + (size_t)ST_SLOTS * fs::CAP * sizeof(uint64_t);   // 50.6 MB
+constexpr size_t ST_BYTES = ST_CAND_OFF + (size_t)ST_SLOTS * fs::CAP * sizeof(uint64_t);   // 50,336,000 B
 
 static __device__ __align__(256) unsigned char scratch[ST_BYTES];
 
-namespace fs {
-__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0u;
-}
-}  // namespace fs
 
 namespace {
 
 constexpr int ST_MAX_DEVICES = 64;
 std::mutex g_static_mu;
 unsigned char* g_static_ptr[ST_MAX_DEVICES] = {};   // the device address of `scratch` on each device
+int32_t* g_static_flag[ST_MAX_DEVICES] = {};        // host-mapped give-up flag of each device's static workspace
+
+__global__ void store_u64_kernel(uint64_t* p, uint64_t v) { *p = v; }
 
 // The static workspace of the current device: its address from hipGetSymbolAddress (the array's name is not a
 // device address in host code), once per device; the first call also zeroes the error words and row histograms
@@ -4250,8 +4348,17 @@ int static_workspace(int dev, hipStream_t st, unsigned char** out) {
         void* ptr = nullptr;
         if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return FS_E_HIP;
         unsigned char* base = (unsigned char*)ptr;
+        int32_t* flag = nullptr;
+        int32_t* flag_dev = nullptr;
+        if (hipHostMalloc((void**)&flag, sizeof(int32_t), hipHostMallocMapped) != hipSuccess) return FS_E_NOMEM;
+        *(volatile int32_t*)flag = 0;
+        if (hipHostGetDevicePointer((void**)&flag_dev, flag, 0) != hipSuccess) return FS_E_HIP;
         hipLaunchKernelGGL(fs::zero_words_kernel, dim3(1), dim3(256), 0, st, (uint32_t*)(base + ST_ERR_OFF),
                            (int64_t)(ST_META_OFF / 4));
+        // error word 2..3: the give-up flag's device address (a kernel store: the call may be under graph capture)
+        hipLaunchKernelGGL(store_u64_kernel, dim3(1), dim3(1), 0, st, (uint64_t*)(base + ST_ERR_OFF + 8),
+                           (uint64_t)(uintptr_t)flag_dev);
+        g_static_flag[dev] = flag;
         hipLaunchKernelGGL(fs::zero_words_kernel, dim3(1024), dim3(256), 0, st, (uint32_t*)(base + ST_RHIST_OFF),
                            (int64_t)((ST_CAND_OFF - ST_RHIST_OFF) / 4));   // row and mass histograms
         if (hipGetLastError() != hipSuccess) return FS_E_HIP;
@@ -4291,6 +4398,8 @@ int fs_destroy(fs_context* c) {
     (void)hipFree(c->rmass);
     (void)hipFree(c->stream_cnt);
     (void)hipFree(c->err);
+    for (void* p : c->retired) (void)hipFree(p);
+    if (c->hflag) (void)hipHostFree(c->hflag);
     delete c;
     return FS_OK;
 }
@@ -4330,7 +4439,7 @@ int fs_sample_batch_static(fs_context* ctx, const float* d_logits, int64_t ld, i
     if (hipGetDevice(&dev) != hipSuccess) return FS_E_HIP;
     if (ctx->static_dev >= 0 && ctx->static_dev != dev) return FS_E_INVALID;   // a context stays on one device
     int64_t items = 0, seg_grid = 0;
-    rc = plan(ctx->cus, a, B, items, seg_grid);
+    rc = plan(ctx->cus, a, B, items, seg_grid, ST_SLOTS);        // fewer segments per row where the slots run out
     if (rc != FS_OK) return rc;
     if (items > ST_SLOTS) return FS_E_LIMIT;
     unsigned char* base = nullptr;
@@ -4344,7 +4453,20 @@ int fs_sample_batch_static(fs_context* ctx, const float* d_logits, int64_t ld, i
     a.cand = (uint64_t*)(base + ST_CAND_OFF);
     a.stream_cnt = nullptr;                          // sampling mode has no verify streams
     a.merge_spins = ctx->merge_spins;
-    return launch_planned(a, B, seg_grid, st);
+    int done = FS_OK;
+    int32_t* sflag = nullptr;
+    {
+        std::lock_guard<std::mutex> gs(g_static_mu);
+        sflag = g_static_flag[dev];
+    }
+    if (gave_up(sflag)) {                            // an earlier call on the device gave up: clear what it left
+        clear_words(st, base + ST_RHIST_OFF, (int64_t)((ST_CAND_OFF - ST_RHIST_OFF) / 4));
+        clear_words(st, a.dirty, 1);
+        if (hipGetLastError() != hipSuccess) return FS_E_HIP;
+        done = FS_W_RECOVERED;
+    }
+    rc = ctx->seg_layout ? launch_planned(a, B, seg_grid, st) : launch_alone(a, B, st);
+    return rc != FS_OK ? rc : done;
 }
 
 int fs_argmax_batch(fs_context* ctx, const float* d_logits, int64_t ld, int32_t B, int32_t V, const int32_t* d_hist,
@@ -4476,10 +4598,26 @@ int fs_device_error(fs_context* ctx, void* stream, int32_t* bits) {
     return FS_OK;
 }
 
+int fs_plan_layout(int32_t cus, int32_t xccs, int32_t B, int32_t V, int32_t static_ws, int32_t* nseg,
+                   int32_t* seg_tiles, int64_t* slots) {
+    if (cus < 1 || xccs < 0 || B < 1 || V < 1 || V > FS_MAX_VOCAB || !nseg || !seg_tiles || !slots) return FS_E_INVALID;
+    if (static_ws && B > ST_ROWS) return FS_E_LIMIT;
+    *nseg = 0; *seg_tiles = 0; *slots = 0;
+    if (!layout_fits(xccs)) return FS_OK;                 // every row sampled alone by one workgroup
+    fs::Args a = {};
+    a.B = B; a.V = V; a.mode = fs::MODE_SAMPLE;
+    int64_t items = 0, seg_grid = 0;
+    const int rc = plan(cus, a, B, items, seg_grid, static_ws ? ST_SLOTS : 0);
+    if (rc != FS_OK) return rc;
+    if (static_ws && items > ST_SLOTS) return FS_E_LIMIT;
+    *nseg = a.nseg; *seg_tiles = a.seg_tiles; *slots = items;
+    return FS_OK;
+}
+
 int fs_set_wait_limit(fs_context* ctx, uint32_t polls) {
     if (!ctx) return FS_E_INVALID;
     std::lock_guard<std::mutex> g(ctx->mu);
-    ctx->merge_spins = polls ? polls : fs::MERGE_SPINS;
+    ctx->merge_spins = polls == FS_WAIT_GIVE_UP ? 0u : (polls ? polls : fs::MERGE_SPINS);
     return FS_OK;
 }
 
@@ -4609,6 +4747,7 @@ const char* fs_strerror(int code) {
         case FS_E_NOMEM: return "device allocation failed";
         case FS_E_DEVICE: return "device-side error";
         case FS_E_LIMIT: return "batch exceeds the static workspace of fs_sample_batch_static";
+        case FS_W_RECOVERED: return "ok; an earlier call's merge gave up waiting and this call cleared its workspace";
         default: return "unknown error";
     }
 }

@@ -71,6 +71,13 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
+def _lptr(t):
+    """Device pointer of a logits matrix: rows may be strided (the C ABI takes the row stride ld), elements packed."""
+    if t.dim() == 2 and t.shape[1] > 1 and t.stride(1) != 1:
+        raise SamplerError("logits rows must be packed (stride 1 along the vocabulary)")
+    return ctypes.c_void_p(t.data_ptr())
+
+
 def _dev(x, dtype, device):
     """An input array or tensor as a packed device tensor of `dtype` (a strided view is copied, not misread)."""
     return torch.as_tensor(x, dtype=dtype, device=device).contiguous()
@@ -249,7 +256,7 @@ def sample_batch(logits, params, u, hist=None, hist_off=None, V=None, kcap=0, ct
     probs = torch.empty((B, kcap), dtype=torch.float64, device=dev) if kcap else None
     ctx = ctx or Context.default(dev)
     with ctx.lock:
-        check(lib().fs_sample_batch(ctx.h, _ptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p), _ptr(u),
+        check(lib().fs_sample_batch(ctx.h, _lptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p), _ptr(u),
                                     _ptr(tok), kcap, _ptr(ids), _ptr(probs), _ptr(keep), _stream(stream)),
               "fs_sample_batch")
     return dict(tok=tok, keep=keep, cand_ids=ids, cand_probs=probs, _keepalive=(p, u, hist, hist_off))
@@ -265,7 +272,7 @@ def argmax_batch(logits, hist=None, hist_off=None, params=None, V=None, ctx=None
     tok = torch.empty(B, dtype=torch.int32, device=dev)
     ctx = ctx or Context.default(dev)
     with ctx.lock:
-        check(lib().fs_argmax_batch(ctx.h, _ptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p), _ptr(tok),
+        check(lib().fs_argmax_batch(ctx.h, _lptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p), _ptr(tok),
                                     _stream(stream)), "fs_argmax_batch")
     return tok
 
@@ -288,7 +295,7 @@ def verify(logits, rows, row_off, params, u=None, hist=None, hist_off=None, eos_
     acc = torch.empty(S, dtype=torch.int32, device=dev)
     ctx = ctx or Context.default(dev)
     with ctx.lock:
-        check(lib().fs_verify(ctx.h, _ptr(logits), ld, S, R, n, _ptr(rows), _ptr(row_off), _ptr(hist),
+        check(lib().fs_verify(ctx.h, _lptr(logits), ld, S, R, n, _ptr(rows), _ptr(row_off), _ptr(hist),
                               _ptr(hist_off), _ptr(p), _ptr(u), int(eos_id), _ptr(tok), _ptr(acc), _stream(stream)),
               "fs_verify")
     return tok, acc
@@ -307,7 +314,7 @@ def penalize_batch(logits, params, hist=None, hist_off=None, V=None, ctx=None, s
     hist, hist_off = _hist_tensors(hist, hist_off, B, dev)
     ctx = ctx or Context.default(dev)
     with ctx.lock:
-        check(lib().fs_penalize_batch(ctx.h, _ptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p),
+        check(lib().fs_penalize_batch(ctx.h, _lptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p),
                                       _stream(stream)), "fs_penalize_batch")
     t2 = target if target.dim() == 2 else target.unsqueeze(0)
     if logits.data_ptr() != t2.data_ptr():            # repacked into an aligned copy: write the rows back

@@ -35,7 +35,7 @@ TICK_US = 0.01                                    # s_memrealtime: 100 MHz
 def load():
     from ferro_amd._lib import SIGNATURES
     if not os.path.exists(TRACE_LIB):
-        raise RuntimeError(f"{TRACE_LIB} is missing: build it with `python ferro_amd/build.py`")
+        raise RuntimeError(f"{TRACE_LIB} is missing: build it with `python ferro_amd/build.py --trace`")
     L = ctypes.CDLL(TRACE_LIB)
     for name, (res, args) in SIGNATURES.items():
         f = getattr(L, name)

@@ -31,14 +31,17 @@ extern "C" {
 #define FS_E_NOMEM (-3)     /* workspace allocation failed */
 #define FS_E_DEVICE (-4)    /* a kernel reported a row it could not process (see fs_device_error) */
 #define FS_E_LIMIT (-5)     /* fs_sample_batch_static: the batch exceeds its static workspace */
+#define FS_W_RECOVERED 1    /* success; an earlier call's merge had given up waiting for its segments
+                               (FS_DEVERR_INTERNAL, kept for fs_device_error) and this call cleared the workspace
+                               that call left, so the context does not stay in its compute-alone mode */
 
 /* Device-side error bits (fs_device_error). */
 #define FS_DEVERR_COUNT_OVERFLOW 1   /* one token occurs > 65535 times in a penalty window */
 #define FS_DEVERR_INTERNAL 2         /* an internal invariant failed, or a row's merge gave up waiting for its
                                         segments (workgroups not dispatched round-robin over the XCDs by index, or
                                         a wait limit below the segments' time). The row was then computed alone from
-                                        its logits (the token is exact); the context stays in that slower mode until
-                                        fs_device_error, which clears its workspace */
+                                        its logits (the token is exact). The next sampling call on the context (or
+                                        fs_device_error) clears the workspace; that call returns FS_W_RECOVERED */
 #define FS_DEVERR_HIST_APPEND 4      /* fs_hist_append: the new histories exceed out_cap (ids past it are not
                                         written), or a count lies outside [0, its stream's rows] (clamped) */
 
@@ -87,10 +90,12 @@ int fs_sample_batch(fs_context* ctx, const float* d_logits, int64_t ld, int32_t 
  * device memory during a call - code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
  * Same arguments, semantics and outputs as fs_sample_batch; ctx only carries settings (fs_set_wait_limit) and
  * error reporting (fs_device_error reads and clears this workspace's error bits too). The workspace is one static
- * device array per GPU (50.3 MB, held until the process ends), shared by every context on that GPU: calls that
- * overlap in time on one GPU race (serialise them on one stream). Limits: B <= 512 rows and at most 512
- * (row, segment) slots, i.e. 2 per compute unit on MI355X; beyond them the call returns FS_E_LIMIT and launches
- * nothing. The first call on a device also enqueues a clear of the workspace on `stream`. */
+ * device array per GPU (50.3 MB; it is part of the library's code object, so it is reserved on every device where
+ * the library's module is loaded, held until the process ends, whether or not this entry point is ever called),
+ * shared by every context on that GPU: calls that
+ * overlap in time on one GPU race (serialise them on one stream). Limits: B <= 512 rows (beyond: FS_E_LIMIT, nothing
+ * launched); every B <= 512 fits its 512 (row, segment) slots, taking fewer segments per row than fs_sample_batch
+ * where the slots would run out (B = 17..23 at V = 262144, for example). The first call on a device also enqueues a clear of the workspace on `stream`. */
 int fs_sample_batch_static(fs_context* ctx, const float* d_logits, int64_t ld, int32_t B, int32_t V,
                            const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params,
                            const double* d_u, int32_t* d_tok, int32_t kcap, int32_t* d_cand_ids, double* d_cand_probs,
@@ -185,8 +190,18 @@ int fs_softcap_batch(const float* d_in, float* d_out, int64_t n, float cap, void
 int fs_device_error(fs_context* ctx, void* stream, int32_t* bits);
 
 /* The merge's bounded wait for a row's segments, in polls (0 = the default, 2^20: far above any segment's time).
- * A smaller limit makes merges give up (FS_DEVERR_INTERNAL) and compute their rows alone: a test of that path. */
+ * A smaller limit makes merges give up (FS_DEVERR_INTERNAL) and compute their rows alone; FS_WAIT_GIVE_UP makes
+ * every merge give up without polling: tests of that path. */
+#define FS_WAIT_GIVE_UP 0xFFFFFFFFu
 int fs_set_wait_limit(fs_context* ctx, uint32_t polls);
+
+/* Host-only: the layout fs_sample_batch (static_ws = 0) or fs_sample_batch_static (static_ws != 0) launches for B
+ * rows of V logits on a device with `cus` compute units and `xccs` XCDs: *nseg segments of *seg_tiles 4096-logit
+ * tiles per row and *slots workspace slots. *nseg = 0 with V >= 4096: every row is sampled alone by one workgroup
+ * (an XCD count that does not divide 8, where the segment grid's hand-off would not hold). Returns FS_E_LIMIT where
+ * fs_sample_batch_static would. No counterpart in the reference; it lets tests check the planner without a GPU. */
+int fs_plan_layout(int32_t cus, int32_t xccs, int32_t B, int32_t V, int32_t static_ws, int32_t* nseg,
+                   int32_t* seg_tiles, int64_t* slots);
 
 /* Static description of the error code. */
 const char* fs_strerror(int code);

@@ -89,3 +89,42 @@ def test_rng_is_libstdcxx_stream(seed):
     # copy continues the same stream independently
     c = r.copy()
     np.testing.assert_array_equal(c.next_u(5), r.next_u(5))
+
+
+def test_planner_layouts_on_mocked_devices():
+    """fs_plan_layout: the segment grid on MI355X (256 CUs, 8 XCDs), and its XCD-count guard on mocked devices."""
+    rc, nseg, st, slots = _lib.plan_layout(256, 8, 64, 262144)      # the headline batch: 8 segments of 8 tiles
+    assert (rc, nseg, st, slots) == (_lib.FS_OK, 8, 8, 512)
+    rc, nseg, st, slots = _lib.plan_layout(256, 8, 272, 65536)      # cfg4: one segment per row
+    assert (rc, nseg, st) == (_lib.FS_OK, 1, 16)
+    for x in (1, 2, 4, 8):                                           # every partition mode keeps the hand-off
+        rc, nseg, _, _ = _lib.plan_layout(32 * x, x, 64, 262144)
+        assert rc == _lib.FS_OK and nseg >= 1, x
+    for x in (0, 3, 5, 6, 7, 12, 16):                                # counts that do not divide 8: every row alone
+        rc, nseg, st, slots = _lib.plan_layout(256, x, 64, 262144)
+        assert (rc, nseg, slots) == (_lib.FS_OK, 0, 0), x
+    rc, nseg, _, _ = _lib.plan_layout(256, 8, 4, 1000)              # rows shorter than a tile: no segments
+    assert (rc, nseg) == (_lib.FS_OK, 0)
+
+
+@pytest.mark.parametrize("V", [262144, 151936, 65536, 4096 * 600])
+def test_static_planner_fits_every_batch(V):
+    """fs_sample_batch_static takes every B <= 512 (fewer segments where its 512 slots would run out)."""
+    for B in range(1, 513):
+        rc, nseg, st, slots = _lib.plan_layout(256, 8, B, V, static_ws=True)
+        assert rc == _lib.FS_OK, (B, rc)
+        assert 1 <= nseg and slots <= 512 and slots == 8 * nseg * ((B + 7) // 8), (B, nseg, slots)
+        assert nseg * st >= V // 4096 and (nseg - 1) * st < V // 4096, (B, nseg, st)
+        d = _lib.plan_layout(256, 8, B, V)
+        assert nseg <= d[1], B                                      # never more segments than fs_sample_batch
+    assert _lib.plan_layout(256, 8, 513, V, static_ws=True)[0] == _lib.FS_E_LIMIT
+
+
+def test_status_codes():
+    L = _lib.lib()
+    assert L.fs_strerror(_lib.FS_W_RECOVERED).startswith(b"ok")
+    assert _lib.check(_lib.FS_OK, "x") == _lib.FS_OK
+    with pytest.warns(_lib.RecoveredWarning):
+        assert _lib.check(_lib.FS_W_RECOVERED, "x") == _lib.FS_W_RECOVERED
+    with pytest.raises(_lib.SamplerError):
+        _lib.check(_lib.FS_E_INVALID, "x")

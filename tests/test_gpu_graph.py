@@ -134,3 +134,39 @@ def test_graph_replays_match_eager(B, V, static):
         torch.cuda.synchronize()
         check_clean(ctx)
     del g
+
+
+def test_replay_after_the_context_grew():
+    """A captured call keeps the workspace addresses it was recorded with. An eager call on the same context that
+    needs a larger workspace then replaces the buffers: they are retired (kept until the context is destroyed), not
+    freed, so the replay still runs on valid memory and matches its eager outputs."""
+    say("graph replay after growth: capture B=24, eager B=300, replay")
+    L = lib()
+    ctx = Context()
+    small = Call(mixed(301, 24, 65536), kcap=16)
+    big = Call(mixed(302, 300, 65536), kcap=16)
+    cur = torch.cuda.current_stream()
+    small.poison()
+    small.launch(L.fs_sample_batch, ctx, cur)
+    torch.cuda.synchronize()
+    want = small.out()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(cur)
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            small.launch(L.fs_sample_batch, ctx, side)
+    cur.wait_stream(side)
+    torch.cuda.synchronize()
+    big.launch(L.fs_sample_batch, ctx, cur)            # grows every workspace buffer of the context
+    torch.cuda.synchronize()
+    check_clean(ctx)
+    for rep in range(2):
+        small.poison()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = small.out()
+        for k in want:
+            np.testing.assert_array_equal(got[k], want[k], err_msg=f"replay {rep} {k}")
+    del g

@@ -161,6 +161,38 @@ def test_known_answer_through_gpu():
     assert list(g["tok"]) == list(want.values())
 
 
+def test_combined_penalties_hand_computed_on_device():
+    """Repetition + frequency + presence over windows cut by repeat_last_n and penalty_from, on the device: the
+    in-place penalty pass reproduces the hand-computed rows bit for bit, and the sampler's fused penalties give the
+    same candidate order and probabilities (k = V, so every penalised logit is a candidate)."""
+    row = np.array([4.0, -1.5, 3.0, 0.5, -2.0, 6.0, 1.0, -0.25, 2.5, 8.0], np.float32)
+    h = [5, 5, 2, 9, 5, 1, 3, 9, 9, 7, 2, 12, -1, 5]
+    cases = [(9, 2, [4.0, -3.75, 0.75, -0.5, -2.0, 2.25, 1.0, -1.25, 2.5, 2.75]),
+             (9, 8, [4.0, -1.5, 0.75, 0.5, -2.0, 2.25, 1.0, -1.25, 2.5, 3.25]),
+             (-1, 0, [4.0, -3.75, 0.25, -0.5, -2.0, 0.75, 1.0, -1.25, 2.5, 2.25])]
+    B = len(cases)
+    p = W.make_params(B, temperature=1.0, top_k=0, repetition_penalty=2.0, frequency_penalty=0.5,
+                      presence_penalty=0.25)
+    for i, (ln, fr, _) in enumerate(cases):
+        p["repeat_last_n"][i] = ln
+        p["penalty_from"][i] = fr
+    hist = np.array(h * B, np.int32)
+    hoff = np.arange(B + 1, dtype=np.int64) * len(h)
+    x = torch.from_numpy(np.stack([row] * B)).cuda()
+    y = F.sampler.penalize_batch(x.clone(), p, hist=hist, hist_off=hoff)
+    torch.cuda.synchronize()
+    want = np.array([c[2] for c in cases], np.float32)
+    np.testing.assert_array_equal(y.cpu().numpy(), want)
+    res = F.sample_batch(x, p, np.full(B, 0.5), hist=hist, hist_off=hoff, kcap=10)
+    torch.cuda.synchronize()
+    for i in range(B):
+        order = sorted(range(10), key=lambda j: (-want[i][j], j))
+        assert list(res["cand_ids"][i].cpu().numpy()) == order, i
+        e = np.exp((want[i][order] - want[i][order[0]]).astype(np.float64))
+        np.testing.assert_allclose(res["cand_probs"][i].cpu().numpy(), e / e.sum(), rtol=1e-12)
+    assert F.device_error() == 0
+
+
 @pytest.mark.parametrize("V", [1, 2, 6, 17, 1000, 4097, 8193, 65537, 100003])
 def test_odd_vocab_sizes(V):
     rng = np.random.default_rng(V)
@@ -479,8 +511,26 @@ def test_device_logits_handoff_in_place():
     torch.cuda.synchronize()
     g = {k: v.cpu().numpy() for k, v in res.items() if v is not None and not k.startswith("_")}
     w = _case(list(out[:, :V].cpu().numpy()), p, hists, u, "handoff")
-    nb = compare(g, run_oracle(w, 64), p, u, 64)
+    ref = run_oracle(w, 64)
+    nb = compare(g, ref, p, u, 64)
     assert nb <= 1
+    # the same buffer passed as the view out[:, :V] (B > 1: not contiguous, row stride ld): read in place too
+    view = out[:, :V]
+    assert not view.is_contiguous()
+    fed, fed_ld, _ = F.sampler._check_logits(view, None)
+    assert fed.data_ptr() == out.data_ptr() and fed_ld == ld
+    res2 = F.sample_batch(view, p, u, hist=hist, hist_off=hoff, kcap=64)
+    torch.cuda.synchronize()
+    g2 = {k: v.cpu().numpy() for k, v in res2.items() if v is not None and not k.startswith("_")}
+    for k in ("tok", "keep"):
+        np.testing.assert_array_equal(g2[k], g[k], err_msg=f"view {k}")
+    for b in range(B):                                  # the candidates each row defines (greedy rows: one)
+        m = min(int(ref["ncand"][b]), 64)
+        np.testing.assert_array_equal(g2["cand_ids"][b, :m], g["cand_ids"][b, :m], err_msg=f"view ids row {b}")
+        np.testing.assert_array_equal(g2["cand_probs"][b, :m], g["cand_probs"][b, :m], err_msg=f"view probs row {b}")
+    pg = W.make_params(B, temperature=0.0, repetition_penalty=1.1)
+    np.testing.assert_array_equal(F.argmax_batch(view, hist=hist, hist_off=hoff, params=pg).cpu().numpy(),
+                                  F.argmax_batch(out, hist=hist, hist_off=hoff, params=pg, V=V).cpu().numpy())
     assert F.device_error() == 0
 
 

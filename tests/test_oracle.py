@@ -160,6 +160,36 @@ def test_frequency_presence_extension():
                                                  f32(3.0) - (f32(2) * f32(0.5) + f32(0.25))], np.float32))
 
 
+def test_combined_penalties_hand_computed():
+    """Repetition, frequency and presence penalties together, over a window that repeat_last_n and penalty_from cut
+    through repeated ids (sampler.cpp:11-18 plus the llama.cpp-convention extension after it). Every value is exact
+    in fp32 (rep 2, freq 0.5, pres 0.25), so the expected rows are written out by hand."""
+    row = np.array([4.0, -1.5, 3.0, 0.5, -2.0, 6.0, 1.0, -0.25, 2.5, 8.0], np.float32)
+    h = [5, 5, 2, 9, 5, 1, 3, 9, 9, 7, 2, 12, -1, 5]        # 12 and -1 lie outside [0, V): never penalised
+    # window h[14-9 .. 14) = [1, 3, 9, 9, 7, 2, 12, -1, 5]: the 5s at positions 0, 1, 4 fall before it
+    #   id 1: -1.5 * 2 = -3.0, then - (1*0.5 + 0.25) = -3.75        id 3: 0.5 / 2 = 0.25, - 0.75 = -0.5
+    #   id 9:  8.0 / 2 =  4.0, then - (2*0.5 + 0.25) =  2.75        id 7: -0.25 * 2 = -0.5, - 0.75 = -1.25
+    #   id 2:  3.0 / 2 =  1.5, - 0.75 = 0.75                        id 5: 6.0 / 2 = 3.0, - 0.75 = 2.25
+    p = O.make_params(repetition_penalty=2.0, frequency_penalty=0.5, presence_penalty=0.25, repeat_last_n=9,
+                      penalty_from=2)
+    want = np.array([4.0, -3.75, 0.75, -0.5, -2.0, 2.25, 1.0, -1.25, 2.5, 2.75], np.float32)
+    np.testing.assert_array_equal(O.penalize(row, h, p), want)
+    # penalty_from 8 moves the window start past repeat_last_n's: h[8 .. 14) = [9, 7, 2, 12, -1, 5]
+    p = O.make_params(repetition_penalty=2.0, frequency_penalty=0.5, presence_penalty=0.25, repeat_last_n=9,
+                      penalty_from=8)
+    want2 = np.array([4.0, -1.5, 0.75, 0.5, -2.0, 2.25, 1.0, -1.25, 2.5, 3.25], np.float32)
+    np.testing.assert_array_equal(O.penalize(row, h, p), want2)
+    # whole history (repeat_last_n -1, penalty_from 0): ids 5 x4, 9 x3, 2 x2, 1, 3, 7 x1
+    #   id 5: 3.0 - (4*0.5 + 0.25) = 0.75     id 9: 4.0 - 1.75 = 2.25     id 2: 1.5 - 1.25 = 0.25
+    p = O.make_params(repetition_penalty=2.0, frequency_penalty=0.5, presence_penalty=0.25, repeat_last_n=-1)
+    want3 = np.array([4.0, -3.75, 0.25, -0.5, -2.0, 0.75, 1.0, -1.25, 2.5, 2.25], np.float32)
+    np.testing.assert_array_equal(O.penalize(row, h, p), want3)
+    # the greedy token of the penalised row
+    p = O.make_params(temperature=0.0, repetition_penalty=2.0, frequency_penalty=0.5, presence_penalty=0.25,
+                      repeat_last_n=9, penalty_from=2)
+    assert O.sample(row, h, p)[0] == 0
+
+
 def test_verify_rule_hand_built():
     V = 8
     # stream 0: rows predict 5, 6, 7; drafts fed are [x, 5, 6] -> both drafts accepted -> acc 3

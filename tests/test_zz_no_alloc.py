@@ -90,6 +90,39 @@ def test_static_entry_matches_allocating_entry():
         assert (got["tok"] >= 0).all() and (got["tok"] < w.V).all()
 
 
+def test_static_entry_takes_every_batch_up_to_its_limit():
+    """Every B = 1..512 at V = 262144 fits the static workspace (fewer segments per row where its 512 (row, segment)
+    slots would run out) and gives fs_sample_batch's tokens."""
+    L = lib()
+    ctx_a, ctx_s = Context(), Context()
+    dev = torch.device("cuda", 0)
+    Bmax, V = 512, 262144
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    x = torch.randn((Bmax, V), generator=g, device=dev, dtype=torch.float32) * 1.5
+    p = W.make_params(Bmax, temperature=0.8, top_k=64, top_p=0.95, repetition_penalty=1.0)
+    p["temperature"][::7] = 0.0
+    params = torch.from_numpy(p.view(np.uint8).copy()).to(dev)
+    u = torch.rand(Bmax, generator=g, device=dev, dtype=torch.float64)
+    ta = torch.empty(Bmax, dtype=torch.int32, device=dev)
+    ts = torch.empty(Bmax, dtype=torch.int32, device=dev)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    say(f"case sweep: B = 1..{Bmax}, V={V}")
+    for B in range(1, Bmax + 1):
+        ts.fill_(-7)
+        rs = L.fs_sample_batch_static(ctx_s.h, P(x), V, B, V, None, None, P(params), P(u), P(ts), 0, None, None, None,
+                                      st)
+        ra = L.fs_sample_batch(ctx_a.h, P(x), V, B, V, None, None, P(params), P(u), P(ta), 0, None, None, None, st)
+        assert rs == 0 and ra == 0, f"B={B}: rc static {rs}, allocating {ra}"
+        if B % 32 == 1 or B in (17, 23, 33, 46, 73, 97, 511, 512):
+            torch.cuda.synchronize()
+            assert torch.equal(ts[:B], ta[:B]), f"B={B}: tokens differ between the entry points"
+    torch.cuda.synchronize()
+    for c in (ctx_a, ctx_s):
+        bits = ctypes.c_int32(-1)
+        assert lib().fs_device_error(c.h, st, ctypes.byref(bits)) == 0 and bits.value == 0
+
+
 def test_static_entry_refuses_batches_past_its_limit():
     L = lib()
     ctx = Context()
