@@ -31,6 +31,26 @@ METRIC = "sampled rows/s + logits HBM GB/s (% of peak), top-k/top-p, B=64, V=262
 HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 << 20
 KERNEL = "fs::segment_kernel"
+SMALL_K = 64                                       # fs_sample_batch_hp's small-k kernel: k <= 64 or greedy rows
+
+
+def kernel_of(w, route, cus=256):
+    """The kernel a sampling call of this workload launches: fs_sample_batch_hp (route "host") runs the small-k kernel
+    when every row is greedy or has k <= 64 and no frequency / presence penalty; otherwise the fused kernel."""
+    if route != "host":
+        return KERNEL, "segments, then a merging workgroup per row, one grid"
+    p = w.params
+    greedy = (p["temperature"] <= 0) | (p["top_k"] == 1)
+    k = np.where((p["top_k"] > 0) & (p["top_k"] < w.V), p["top_k"], w.V)
+    fits = bool(((greedy | (k <= SMALL_K)) & (p["frequency_penalty"] == 0) & (p["presence_penalty"] == 0)).all())
+    if not fits:
+        return KERNEL, "segments, then a merging workgroup per row, one grid"
+    from ferro_amd import _lib
+    nl, ns = ctypes.c_int32(), ctypes.c_int32()
+    if _lib.lib().fs_small_k_plan(cus, w.B, w.V, ctypes.byref(nl), ctypes.byref(ns)) != 0:
+        return KERNEL, "segments, then a merging workgroup per row, one grid"
+    return (f"fs::small_k_kernel<{nl.value}>",
+            f"{ns.value} segments of {1024 * nl.value} logits per row, the last segment of a row merges it, one grid")
 
 # workload -> (constructor name in ferro_amd.workloads, entry point, description)
 WORKLOADS = {
@@ -299,10 +319,17 @@ def run_workload(name, args, torch):
         acc = torch.empty(S, dtype=torch.int32, device=dev)
         fixed = (S, w.B, w.V, P(rows), P(roff), P(hist), P(hoff), P(params), P(u), -1, P(tok), P(acc), sh)
         call, what = L.fs_verify, "fs_verify"
+    elif args.route == "host":
+        acc = None
+        hp = np.ascontiguousarray(w.params)             # the host copy of the parameters (picks the kernel)
+        fixed = (w.B, w.V, P(hist), P(hoff), P(params), hp.ctypes.data_as(ctypes.c_void_p), P(u), P(tok), 0, None,
+                 None, P(keep), sh)
+        call, what = L.fs_sample_batch_hp, "fs_sample_batch_hp"
     else:
         acc = None
         fixed = (w.B, w.V, P(hist), P(hoff), P(params), P(u), P(tok), 0, None, None, P(keep), sh)
         call, what = L.fs_sample_batch, "fs_sample_batch"
+    kname, kdesc = kernel_of(w, args.route if entry == "sample" else "device", ctx_cus(torch))
 
     def step(i):
         rc = call(ctx.h, P(bufs[i % nrot]), w.V, *fixed)
@@ -356,7 +383,7 @@ def run_workload(name, args, torch):
                                   "around each"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(name),
-                     "kernel": f"{what}: {KERNEL} (segments, then a merging workgroup per row, one grid)",
+                     "kernel": f"{what}: {kname} ({kdesc})",
                      "kernel_ms": graph_ms, "kernel_ms_python_launch": kern_ms, "algorithmic_bytes": alg_bytes,
                      "algorithmic_bytes_note": "4*V per row (one read of the fp32 row) + 4 per history id"},
     }
@@ -392,6 +419,11 @@ BREAKDOWN = [
 ]
 
 
+def _with(w, prm):
+    from dataclasses import replace
+    return replace(w, params=prm)
+
+
 def run_breakdown(name, args, torch):
     """One JSON line: the HIP-event time per call of each ablation variant of the workload."""
     from ferro_amd import workloads as W
@@ -422,21 +454,31 @@ def run_breakdown(name, args, torch):
             prm[f] = v
         params = torch.from_numpy(prm.view(np.uint8).copy()).to(dev)
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        hp = np.ascontiguousarray(prm)
         for i in range(args.warmup + args.steps):
             if i >= args.warmup:
                 ev[i - args.warmup][0].record(stream)
-            rc = L.fs_sample_batch(ctx.h, P(bufs[i % nrot]), w.V, w.B, w.V, P(hist), P(hoff), P(params), P(u), P(tok),
-                                   0, None, None, None, sh)
+            if args.route == "host":
+                rc = L.fs_sample_batch_hp(ctx.h, P(bufs[i % nrot]), w.V, w.B, w.V, P(hist), P(hoff), P(params),
+                                          hp.ctypes.data_as(ctypes.c_void_p), P(u), P(tok), 0, None, None, None, sh)
+            else:
+                rc = L.fs_sample_batch(ctx.h, P(bufs[i % nrot]), w.V, w.B, w.V, P(hist), P(hoff), P(params), P(u),
+                                       P(tok), 0, None, None, None, sh)
             if rc != 0:
                 raise RuntimeError(f"fs_sample_batch returned {rc}")
             if i >= args.warmup:
                 ev[i - args.warmup][1].record(stream)
         torch.cuda.synchronize()
         ms = float(np.median([a.elapsed_time(b) for a, b in ev]))
-        out.append({"variant": label, "us_per_call": ms * 1e3,
+        out.append({"variant": label, "kernel": kernel_of(w if not over else _with(w, prm), args.route)[0],
+                    "us_per_call": ms * 1e3,
                     "GB_per_s": w.algorithmic_bytes() / (ms * 1e-3) / 1e9})
     return {"breakdown": desc, "B": w.B, "V": w.V, "steps": args.steps, "timing": "median HIP-event time per call",
             "variants": out}
+
+
+def ctx_cus(torch):
+    return torch.cuda.get_device_properties(0).multi_processor_count
 
 
 def F_device_error(L, ctx, sh):
@@ -459,6 +501,10 @@ def main():
                     help="instead of the bench line: per-stage ablation timings of the workload (one JSON line)")
     ap.add_argument("--host-rows", action="store_true",
                     help="also report the PCIe-inclusive rate: the rows copied from pinned host memory every step")
+    ap.add_argument("--route", choices=["host", "device"], default="host",
+                    help="host (default): sampling calls pass the host copy of the parameters too "
+                         "(fs_sample_batch_hp, which picks the small-k kernel for batches it fits, as a serving loop "
+                         "holding its requests' parameters does); device: fs_sample_batch (the fused kernel)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="after the timed steps, run plain 256 MiB device copies (counter calibration for rocprofv3)")
     args = ap.parse_args()

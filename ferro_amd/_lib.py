@@ -42,6 +42,8 @@ SIGNATURES = {
     "fs_destroy": (ctypes.c_int, [_P]),
     "fs_sample_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P]),
     "fs_sample_batch_static": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P]),
+    "fs_sample_batch_hp": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P]),
+    "fs_small_k_plan": (ctypes.c_int, [_I32, _I32, _I32, _P, _P]),
     "fs_argmax_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P]),
     "fs_verify": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P]),
     "fs_penalize_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P]),

@@ -4081,6 +4081,587 @@ __global__ __launch_bounds__(64) void drng_skip_kernel(uint64_t* mts, int32_t* i
     idxs[sidx] = idx;
 }
 
+// ------------------------------------------------------------------------------------------------ small-k kernel
+// A separate kernel for batches whose every row is greedy or samples from k <= SK_K candidates with at most a
+// repetition penalty (no frequency / presence counts) - the serving batches of ferro's decode loop (server.cpp:603-606:
+// top-k 40-64 on every row). The host picks it from a host copy of the parameters (fs_sample_batch_hp). It has its own
+// register budget (it shares no code path with the fused kernel above), which lets it stream a row differently:
+//   - one workgroup of SK_LT threads per (row, segment): every load of the segment (NL float4 per thread) is issued at
+//     once, so the whole batch is requested at the start. The memory system serves the requests roughly in dispatch
+//     order, so a row's segments (consecutive workgroups) receive their data together, and rows finish one after
+//     another: the merge of an early row overlaps the streaming of later rows;
+//   - per group of four logits only a maximum and, later, one compare: the bound is the ceil(k / waves)-th largest
+//     lane maximum of each wave, the smallest over the waves (each lane maximum is a distinct logit of the segment, so
+//     at least k logits of the segment reach it). Groups whose maximum reaches it are written to LDS, expanded to the
+//     candidates at or above it (about 1.5 k per segment on heavy-tailed rows), and sorted exactly into the segment's
+//     top k by a bitonic network in registers (DPP and permlane moves: no LDS round trips);
+//   - the last segment of a row to finish (an L2 ticket) merges the row's sorted lists by a tree of bitonic merges and
+//     finishes the row in one wave (softmax at temperature, min-p, top-p, draw: the merge path's wave_softmax).
+// A segment with more than SK_CAP candidates (ties at its bound) selects its exact top k by a radix select over the
+// composites held in registers instead (slow, exact).
+constexpr int SK_LT = 256;                 // threads per segment workgroup
+constexpr int SK_NW = SK_LT / WAVE;
+constexpr int SK_K = 64;                   // largest k (one candidate per lane of the finishing wave)
+constexpr int SK_GCAP = 128;               // groups of four a wave can hand to the expansion
+constexpr int SK_CAP = 512;                // candidates a segment ranks in LDS
+constexpr int SK_MAX_SEGS = 64;            // segments per row
+
+struct SkArgs {
+    const float* logits;
+    int64_t ld;
+    int B, V, nseg;
+    const int32_t* hist;
+    const int64_t* hist_off;
+    const fs_row_params* params;
+    const double* u;
+    int32_t* tok;
+    int kcap;
+    int32_t* cand_ids;
+    double* cand_probs;
+    int32_t* keep;
+    uint64_t* lists;                       // [B * nseg][SK_K]: each segment's top k, sorted, 0-padded
+    uint32_t* ticket;                      // [B]: segments finished (left at 0)
+    int32_t* err;
+    uint64_t* trace;                       // FS_TRACE builds: per-workgroup phase timestamps (NULL: none)
+};
+
+// lane ^ D over the wave, in the VALU: DPP for D < 16 (both shifts in full exec, then an arithmetic select: a branch
+// would run each DPP move on half the lanes), permlane swaps for 16 and 32 (gfx950)
+template <int D>
+__device__ __forceinline__ uint32_t xor_lane32(uint32_t v) {
+    if constexpr (D == 1) {
+        return dpp32<0xB1>(v);                                  // quad_perm [1,0,3,2]
+    } else if constexpr (D == 2) {
+        return dpp32<0x4E>(v);                                  // quad_perm [2,3,0,1]
+    } else if constexpr (D == 4 || D == 8) {
+        const uint32_t up = dpp32<0x100 + D>(v), dn = dpp32<0x110 + D>(v);   // row_shl: lane + D; row_shr: lane - D
+        const uint32_t m = 0u - (((uint32_t)lane_id() / D) & 1u);
+        return up ^ ((up ^ dn) & m);
+    } else if constexpr (D == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane_id() & 16) ? r[0] : r[1];
+    } else {
+        static_assert(D == 32, "xor distances 1..32");
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane_id() & 32) ? r[0] : r[1];
+    }
+}
+template <int D>
+__device__ __forceinline__ uint64_t xor_lane64(uint64_t v) {
+    return ((uint64_t)xor_lane32<D>((uint32_t)(v >> 32)) << 32) | (uint64_t)xor_lane32<D>((uint32_t)v);
+}
+// Bitonic compare-exchange at distance D: the lane keeps the larger of its pair iff (its bit D is clear) == up.
+template <int D>
+__device__ __forceinline__ uint64_t bcx(uint64_t v, bool up) {
+    const uint64_t o = xor_lane64<D>(v);
+    const bool keep_max = ((lane_id() & D) == 0) == up;
+    return keep_max ? (v > o ? v : o) : (v < o ? v : o);
+}
+// 32-bit compare-exchange and descending sort of the wave's 64 values (lane 0 the largest), VALU only.
+template <int D>
+__device__ __forceinline__ uint32_t bcx32(uint32_t v, bool up) {
+    const uint32_t o = xor_lane32<D>(v);
+    const bool keep_max = ((lane_id() & D) == 0) == up;
+    const uint32_t hi = v > o ? v : o, lo = v > o ? o : v;
+    return keep_max ? hi : lo;
+}
+__device__ __forceinline__ uint32_t sort64_desc_u32(uint32_t v) {
+    const int lane = lane_id();
+    { const bool up = (lane & 2) == 0; v = bcx32<1>(v, up); }
+    { const bool up = (lane & 4) == 0; v = bcx32<2>(v, up); v = bcx32<1>(v, up); }
+    { const bool up = (lane & 8) == 0; v = bcx32<4>(v, up); v = bcx32<2>(v, up); v = bcx32<1>(v, up); }
+    { const bool up = (lane & 16) == 0;
+      v = bcx32<8>(v, up); v = bcx32<4>(v, up); v = bcx32<2>(v, up); v = bcx32<1>(v, up); }
+    { const bool up = (lane & 32) == 0;
+      v = bcx32<16>(v, up); v = bcx32<8>(v, up); v = bcx32<4>(v, up); v = bcx32<2>(v, up); v = bcx32<1>(v, up); }
+    v = bcx32<32>(v, true); v = bcx32<16>(v, true); v = bcx32<8>(v, true); v = bcx32<4>(v, true);
+    v = bcx32<2>(v, true);
+    return bcx32<1>(v, true);
+}
+
+// The wave's 64 values sorted, descending (lane 0 the largest) or ascending.
+template <bool DESC>
+__device__ __forceinline__ uint64_t sort64(uint64_t v) {
+    const int lane = lane_id();
+    { const bool up = ((lane & 2) == 0) == DESC; v = bcx<1>(v, up); }
+    { const bool up = ((lane & 4) == 0) == DESC; v = bcx<2>(v, up); v = bcx<1>(v, up); }
+    { const bool up = ((lane & 8) == 0) == DESC; v = bcx<4>(v, up); v = bcx<2>(v, up); v = bcx<1>(v, up); }
+    { const bool up = ((lane & 16) == 0) == DESC;
+      v = bcx<8>(v, up); v = bcx<4>(v, up); v = bcx<2>(v, up); v = bcx<1>(v, up); }
+    { const bool up = ((lane & 32) == 0) == DESC;
+      v = bcx<16>(v, up); v = bcx<8>(v, up); v = bcx<4>(v, up); v = bcx<2>(v, up); v = bcx<1>(v, up); }
+    v = bcx<32>(v, DESC); v = bcx<16>(v, DESC); v = bcx<8>(v, DESC); v = bcx<4>(v, DESC); v = bcx<2>(v, DESC);
+    return bcx<1>(v, DESC);
+}
+// The top 64 of a (sorted descending) and b (sorted ascending), sorted descending (DESC) or ascending: the lane-wise
+// maximum is a bitonic sequence holding them, then a bitonic merge.
+template <bool DESC = true>
+__device__ __forceinline__ uint64_t merge_top64(uint64_t a_desc, uint64_t b_asc) {
+    uint64_t v = a_desc > b_asc ? a_desc : b_asc;
+    v = bcx<32>(v, DESC); v = bcx<16>(v, DESC); v = bcx<8>(v, DESC); v = bcx<4>(v, DESC); v = bcx<2>(v, DESC);
+    return bcx<1>(v, DESC);
+}
+
+struct SkShared {
+    float4 gval[SK_NW][SK_GCAP + 1];       // groups of four whose maximum reaches the bound (+ a dummy slot)
+    int32_t gidx[SK_NW][SK_GCAP + 1];      //   and the segment offset of their first logit
+    uint64_t cand[SK_CAP];                 // the segment's candidates (composites)
+    uint64_t wl[SK_NW][SK_K];              // per-wave sorted lists (segment sort, row merge)
+    uint32_t bmp[SK_LT * 16 * 4 / 32];     // repetition window ids in the segment (largest segment: NL = 16)
+    uint32_t hist[16];                     // radix select digits (exact fallback)
+    uint32_t wb[SK_NW];
+    uint32_t wcnt[SK_NW];
+    uint32_t tscan[SK_NW];
+    uint32_t misc[4];
+#ifdef FS_TRACE
+    uint64_t trace_t[16];
+#endif
+};
+// Phase timestamps of the small-k kernel (FS_TRACE builds only; thread 0, after the barrier that closes a phase):
+// 0 start, 1 window bitmap built, 2 bound (all of the segment's logits in), 3 groups handed over, 4 candidates
+// expanded, 5 list sorted and published, 6 ticket taken; merging workgroup: 7 lists folded, 8 row finished.
+// Slots 9-10: candidates and groups of the segment; 13-15: role (3 segment, 4 segment + merge), row, segment.
+#ifdef FS_TRACE
+#define SK_MARK(i) do { if (threadIdx.x == 0) s.trace_t[(i)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#define SK_TAG(i, v) do { if (threadIdx.x == 0) s.trace_t[(i)] = (uint64_t)(v); } while (0)
+#define SK_FLUSH() do { if (threadIdx.x == 0 && a.trace) \
+    for (int i_ = 0; i_ < TRACE_W; ++i_) a.trace[(int64_t)blockIdx.x * TRACE_W + i_] = s.trace_t[i_]; } while (0)
+#else
+#define SK_MARK(i) do {} while (0)
+#define SK_TAG(i, v) do {} while (0)
+#define SK_FLUSH() do {} while (0)
+#endif
+
+// The exact path, for segments whose candidates at the bound overflow SK_CAP (ties at the bound): the segment's
+// logits are re-read from memory (the L2 holds them by then) in batches of SK_EB per thread, sixteen loads in flight,
+// and transformed again (softcap, then the repetition penalty from the segment's bitmap; past n: NaN).
+constexpr int SK_EB = 16;
+template <bool CAP, class F>
+__device__ __forceinline__ void sk_each(const float* segp, int n, int nseg_elems, float cap, bool pen, float rep,
+                                        const uint32_t* bmp, F f) {
+    const int tid = threadIdx.x;
+#pragma unroll 1
+    for (int i0 = 0; i0 < nseg_elems; i0 += SK_LT * SK_EB) {
+        float x[SK_EB];
+#pragma unroll
+        for (int j = 0; j < SK_EB; ++j) {
+            const int i = i0 + j * SK_LT + tid;
+            x[j] = i < n ? segp[i] : 0.0f;
+        }
+        if (CAP && cap > 0.0f) softcap_vals(x, cap);
+#pragma unroll
+        for (int j = 0; j < SK_EB; ++j) {
+            const int i = i0 + j * SK_LT + tid;
+            float l = x[j];
+            if (pen && i < n && ((bmp[i >> 5] >> (i & 31)) & 1u)) l = l > 0.0f ? __fdiv_rn(l, rep) : __fmul_rn(l, rep);
+            f(i, i < n ? key_of(l) : 0u);
+        }
+    }
+}
+// The exact k-th largest composite of the segment (every composite is distinct: the id is part of it), by a radix
+// select over 4-bit digits. Slow, and rare.
+template <bool CAP>
+__device__ __forceinline__ uint64_t sk_kth_exact(const float* segp, int seg_lo, int n, int nseg_elems, float cap,
+                                                 bool pen, float rep, int k, SkShared& s) {
+    const int tid = threadIdx.x;
+    uint64_t prefix = 0ull;
+    int need = k;
+#pragma unroll 1
+    for (int sh = 60; sh >= 0; sh -= 4) {
+        if (tid < 16) s.hist[tid] = 0u;
+        __syncthreads();
+        const uint64_t hi_mask = sh + 4 >= 64 ? 0ull : (~0ull << (sh + 4));
+        sk_each<CAP>(segp, n, nseg_elems, cap, pen, rep, s.bmp, [&](int i, uint32_t key) {
+            const uint64_t cm = comp_of(key, (uint32_t)(seg_lo + i));
+            if (key != 0u && (cm & hi_mask) == prefix) atomicAdd(&s.hist[(uint32_t)(cm >> sh) & 15u], 1u);
+        });
+        __syncthreads();
+        if (tid == 0) {
+            int d = 15;
+            for (; d > 0; --d) {
+                const int c = (int)s.hist[d];
+                if (c >= need) break;
+                need -= c;
+            }
+            s.misc[2] = (uint32_t)d;
+            s.misc[3] = (uint32_t)need;
+        }
+        __syncthreads();
+        prefix |= (uint64_t)s.misc[2] << sh;
+        need = (int)s.misc[3];
+        __syncthreads();
+    }
+    return prefix;
+}
+
+// CAP: some row of the batch has a softcap (the cap's code is left out of batches without one).
+template <int NL, bool CAP>
+__global__ __launch_bounds__(SK_LT) void small_k_kernel(SkArgs a) {
+    constexpr int SEG = SK_LT * NL * 4;
+    static_assert(NL <= 16, "the repetition bitmap covers NL <= 16");
+    __shared__ __align__(16) SkShared s;
+    const int tid = threadIdx.x, lane = lane_id(), w = tid / WAVE;
+    // workgroup i: XCD slot i % XCDS takes rows x, x + XCDS, ...: a row's segments are consecutive workgroups of one
+    // index class mod XCDS, so they share an XCD and its L2 (the ticket and the lists)
+    const int x = (int)(blockIdx.x % (unsigned)XCDS);
+    const int j = (int)(blockIdx.x / (unsigned)XCDS);
+    const int q_row = __builtin_amdgcn_readfirstlane(j / a.nseg);
+    const int seg = j - q_row * a.nseg;
+    const int row = x + XCDS * q_row;
+    if (row >= a.B) return;
+    SK_MARK(0);
+    for (int i_ = 1; i_ < 13; ++i_) SK_TAG(i_, 0);
+    SK_TAG(13, 3); SK_TAG(14, row); SK_TAG(15, seg);
+    const int seg_lo = seg * SEG;
+    const int n_in = a.V - seg_lo < SEG ? a.V - seg_lo : SEG;         // logits of this segment (>= 1)
+
+    // the row's parameters (scalar loads) and its repetition window [b, len) over its history
+    const fs_row_params* pp = a.params + row;
+    const float temp = ld_const(&pp->temperature);
+    const int top_k = ld_const(&pp->top_k);
+    const float rep = ld_const(&pp->repetition_penalty);
+    const float cap = CAP ? ld_const(&pp->softcap) : 0.0f;
+    fs_row_params pw;
+    pw.repeat_last_n = ld_const(&pp->repeat_last_n);
+    pw.penalty_from = ld_const(&pp->penalty_from);
+    const bool greedy = temp <= 0.0f || top_k == 1;
+    const int k = greedy ? 1 : ((top_k > 0 && top_k < a.V) ? top_k : a.V);
+    int64_t h0 = 0, len = 0;
+    if (a.hist && a.hist_off) {
+        h0 = ld_const(a.hist_off + row);
+        len = ld_const(a.hist_off + row + 1) - h0;
+    }
+    bool pen = rep != 1.0f && pw.repeat_last_n != 0 && len > 0;
+    const int64_t wb0 = pen ? window_begin(len, pw) : len;
+    if (wb0 >= len) pen = false;
+    // the window's first ids, requested ahead of the logits (vector loads complete in order)
+    int wid[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int64_t i = wb0 + r * SK_LT + tid;
+        wid[r] = (pen && i < len) ? a.hist[h0 + i] : -1;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // every load of the segment at once; past the row's end (rounded up to four, inside ld) reads are zeros, masked
+    const float* rowp = a.logits + (int64_t)row * a.ld;
+    const int nrec = ((n_in + 3) & ~3) * 4;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(rowp + seg_lo), (short)0, nrec, 0x00020000);
+    float4 v[NL];
+#pragma unroll
+    for (int q = 0; q < NL; ++q) {
+        const f32x4 t = raw_buffer_load_f32x4(rs, (q * SK_LT + tid) * 16, 0, 2);    // nontemporal: read once
+        v[q] = make_float4(t.x, t.y, t.z, t.w);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // repetition penalty: an exact bitmap of the window's ids in this segment (each distinct id once: sampler.cpp:14-17)
+    uint64_t pm = 0ull;                        // 4 bits per group of this thread
+    if (pen) {
+        for (int i = tid; i < SEG / 32; i += SK_LT) s.bmp[i] = 0u;
+        __syncthreads();
+        auto mark = [&](int id) {
+            const uint32_t rel = (uint32_t)(id - seg_lo);
+            if (id >= 0 && id < a.V && rel < (uint32_t)SEG) atomicOr(&s.bmp[rel >> 5], 1u << (rel & 31u));
+        };
+        mark(wid[0]);
+        mark(wid[1]);
+        for (int64_t i = wb0 + 2 * SK_LT + tid; i < len; i += SK_LT) mark(a.hist[h0 + i]);
+        __syncthreads();
+        SK_MARK(1);
+#pragma unroll
+        for (int q = 0; q < NL; ++q) {
+            const uint32_t rel = (uint32_t)(q * SK_LT + tid) * 4u;
+            pm |= (uint64_t)((s.bmp[rel >> 5] >> (rel & 31u)) & 0xFu) << (4 * q);
+        }
+    }
+    const bool wpen = __ballot(pm != 0ull) != 0ull;
+    const bool tail = n_in < SEG;
+    // rep >= 1 never raises a logit (l > 0: l / rep <= l; l <= 0: l * rep <= l): penalised logits are then left out of
+    // the lane maxima (the bound counts unpenalised logits, which the penalty leaves as they are), a group is handed
+    // over when its raw maximum reaches the bound (a superset), and the penalty is applied to the few penalised logits
+    // of the handed-over groups only. rep < 1 penalises every flagged logit here.
+    const bool pen_late = rep >= 1.0f;
+
+    // the logits as ferro's sampler sees them (softcap, then the penalty; past the row's end: NaN, never a candidate),
+    // the group maxima and the lane maximum (NaN-free: fmaxf drops NaN; NaN when every logit of the lane is NaN)
+    float lm = __builtin_nanf("");
+#pragma unroll
+    for (int q = 0; q < NL; ++q) {
+        float e[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+        if (CAP && cap > 0.0f) softcap_vals(e, cap);       // a rolled loop: one copy of the cap per group
+        if (wpen && !pen_late) {
+            const uint32_t nib = (uint32_t)(pm >> (4 * q)) & 0xFu;
+            if (__ballot(nib != 0u)) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if ((nib >> c) & 1u) e[c] = e[c] > 0.0f ? __fdiv_rn(e[c], rep) : __fmul_rn(e[c], rep);
+            }
+        }
+        if (tail) {
+            const int e0 = (q * SK_LT + tid) * 4;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (e0 + c >= n_in) e[c] = __builtin_nanf("");
+        }
+        v[q] = make_float4(e[0], e[1], e[2], e[3]);
+        float gu = fmaxf(fmaxf(e[0], e[1]), fmaxf(e[2], e[3]));   // the maximum of the group's unpenalised logits
+        if (wpen && pen_late) {
+            const uint32_t nib = (uint32_t)(pm >> (4 * q)) & 0xFu;
+            if (__ballot(nib != 0u)) {
+                const float nan = __builtin_nanf("");
+                gu = fmaxf(fmaxf((nib & 1u) ? nan : e[0], (nib & 2u) ? nan : e[1]),
+                           fmaxf((nib & 4u) ? nan : e[2], (nib & 8u) ? nan : e[3]));
+            }
+        }
+        lm = fmaxf(lm, gu);
+    }
+    // the bound: each wave sorts its lane maxima in registers (no scalar round trips per step); lane kq - 1 holds its
+    // kq-th largest, and the smallest over the waves counts SK_NW kq >= k distinct logits
+    const uint32_t kq = (uint32_t)((k + SK_NW - 1) / SK_NW);
+    SK_MARK(11);
+    {
+        const uint32_t srt = sort64_desc_u32(key_of(lm));
+        if (lane == (int)kq - 1) s.wb[w] = srt;
+    }
+    SK_MARK(12);
+    __syncthreads();
+    SK_MARK(2);
+    uint32_t tau = s.wb[0];
+#pragma unroll
+    for (int q = 1; q < SK_NW; ++q) tau = s.wb[q] < tau ? s.wb[q] : tau;
+    if (tau == 0u) tau = 1u;                                   // NaN (key 0) is never a candidate
+    const float tf = tau > 0x007FFFFFu ? val_of(tau) : -__builtin_huge_valf();
+    // groups whose maximum reaches the bound: this wave's region of the group buffer, in lane order
+    uint32_t gmask = 0u;
+#pragma unroll
+    for (int q = 0; q < NL; ++q)                               // the group's raw maximum (recomputed: no register array)
+        gmask |= (fmaxf(fmaxf(v[q].x, v[q].y), fmaxf(v[q].z, v[q].w)) >= tf ? 1u : 0u) << q;
+    const uint32_t gn = (uint32_t)__popc(gmask);
+    const uint32_t gincl = wave_incl_scan_u32(gn);
+    const uint32_t wtot = (uint32_t)__builtin_amdgcn_readlane((int)gincl, WAVE - 1);
+    uint32_t go = gincl - gn;
+    // the groups any lane of the wave hands over (one scalar mask); per such group every lane writes, those without
+    // it into the region's dummy slot, so no per-lane branch waits on a compare
+    const uint32_t wmask = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)wave_allreduce(gmask, [](uint32_t x, uint32_t y) { return x | y; }));
+#pragma unroll
+    for (int q = 0; q < NL; ++q) {
+        if ((wmask >> q) & 1u) {
+            const bool mine = ((gmask >> q) & 1u) != 0u && go < (uint32_t)SK_GCAP;
+            const uint32_t slot = mine ? go : (uint32_t)SK_GCAP;
+            const uint32_t nib = pen_late ? (uint32_t)(pm >> (4 * q)) & 0xFu : 0u;   // still to be penalised
+            s.gval[w][slot] = v[q];
+            s.gidx[w][slot] = (int32_t)(((uint32_t)(q * SK_LT + tid) * 4u) | (nib << 28));
+            go += (gmask >> q) & 1u;
+        }
+    }
+    if (lane == 0) s.wcnt[w] = wtot;
+    __syncthreads();
+    SK_MARK(3);
+    // expansion: thread t takes group t of the concatenated regions, its logits at or above the bound become candidates
+    uint32_t goff[SK_NW + 1];
+    goff[0] = 0u;
+    bool gover = false;
+#pragma unroll
+    for (int q = 0; q < SK_NW; ++q) {
+        const uint32_t c = s.wcnt[q];
+        gover |= c > (uint32_t)SK_GCAP;
+        goff[q + 1] = goff[q] + (c < (uint32_t)SK_GCAP ? c : (uint32_t)SK_GCAP);
+    }
+    const uint32_t G = goff[SK_NW];
+    uint64_t cm[4] = {0ull, 0ull, 0ull, 0ull};
+    bool cp[4] = {false, false, false, false};
+    uint32_t nc = 0u;
+    if (!gover && (uint32_t)tid < G) {
+        int r = 0;
+        uint32_t gb = 0u;
+#pragma unroll
+        for (int q = 1; q < SK_NW; ++q) {
+            const bool past = (uint32_t)tid >= goff[q];
+            r += past ? 1 : 0;
+            gb = past ? goff[q] : gb;
+        }
+        const uint32_t gi = (uint32_t)tid - gb;
+        const float4 gv = s.gval[r][gi];
+        const uint32_t gw = (uint32_t)s.gidx[r][gi];
+        const int e0 = (int)(gw & 0x0FFFFFFFu);
+        const uint32_t nib = gw >> 28;
+        float e[4] = {gv.x, gv.y, gv.z, gv.w};
+        if (nib != 0u) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if ((nib >> c) & 1u) e[c] = e[c] > 0.0f ? __fdiv_rn(e[c], rep) : __fmul_rn(e[c], rep);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            cp[c] = e[c] >= tf;
+            cm[c] = comp_of(key_of(e[c]), (uint32_t)(seg_lo + e0 + c));
+            nc += cp[c] ? 1u : 0u;
+        }
+    }
+    if (G > (uint32_t)SK_LT) gover = true;                     // more groups than threads: the exact path
+    // block exclusive scan of the candidate counts
+    const uint32_t cincl = wave_incl_scan_u32(nc);
+    if (lane == WAVE - 1) s.tscan[w] = cincl;
+    __syncthreads();
+    SK_MARK(4);
+    uint32_t cbase = 0u, ntot = 0u;
+#pragma unroll
+    for (int q = 0; q < SK_NW; ++q) {
+        const uint32_t t = s.tscan[q];
+        cbase += q < w ? t : 0u;
+        ntot += t;
+    }
+    const bool exact = gover || ntot > (uint32_t)SK_CAP;       // uniform
+    if (!exact) {
+        uint32_t pos = cbase + cincl - nc;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (cp[c]) s.cand[pos++] = cm[c];
+    }
+    uint64_t* myl = a.lists + ((int64_t)row * a.nseg + seg) * SK_K;
+    if (exact) {
+        // ties at the bound: the exact k-th composite of the segment, then the (exactly k) composites at or above it
+        const float* segp = rowp + seg_lo;
+        const uint64_t kth = sk_kth_exact<CAP>(segp, seg_lo, n_in, SEG, cap, pen, rep, k, s);
+        if (tid == 0) s.misc[0] = 0u;
+        __syncthreads();
+        sk_each<CAP>(segp, n_in, SEG, cap, pen, rep, s.bmp, [&](int i, uint32_t key) {
+            const uint64_t c64 = comp_of(key, (uint32_t)(seg_lo + i));
+            if (key != 0u && c64 >= kth) {
+                const uint32_t p = atomicAdd(&s.misc[0], 1u);
+                if (p < (uint32_t)SK_K) s.cand[p] = c64;
+            }
+        });
+        __syncthreads();
+        ntot = s.misc[0] < (uint32_t)SK_K ? s.misc[0] : (uint32_t)SK_K;
+    }
+    __syncthreads();
+    // the segment's top k, sorted by rank: P threads per candidate each count the larger entries in 1/P of the list
+    // (LDS reads of one address per wave: broadcasts), the partial counts are summed and the first k placed by rank
+    uint64_t* sorted = &s.wl[0][0];
+    uint32_t* rk = reinterpret_cast<uint32_t*>(&s.wl[1][0]);    // [P][per] partial ranks (SK_LT words)
+    {
+        const int n = (int)ntot;
+        if (n <= SK_LT) {
+            const int P = n <= SK_LT / 4 ? 4 : (n <= SK_LT / 2 ? 2 : 1);
+            const int per = SK_LT / P;
+            const int c = tid % per, qq = tid / per;
+            const int span = (n + P - 1) / P;
+            if (c < n) {
+                const uint64_t me = s.cand[c];
+                const int j0 = qq * span, j1 = j0 + span < n ? j0 + span : n;
+                uint32_t r = 0u;
+                int jj = j0;
+                for (; jj + 4 <= j1; jj += 4) {                // four LDS reads in flight per step
+                    const uint64_t e0 = s.cand[jj], e1 = s.cand[jj + 1], e2 = s.cand[jj + 2], e3 = s.cand[jj + 3];
+                    r += (e0 > me ? 1u : 0u) + (e1 > me ? 1u : 0u) + (e2 > me ? 1u : 0u) + (e3 > me ? 1u : 0u);
+                }
+                for (; jj < j1; ++jj) r += s.cand[jj] > me ? 1u : 0u;
+                rk[qq * per + c] = r;
+            }
+            __syncthreads();
+            if (tid < n) {                                     // placed straight into the published list
+                uint32_t r = 0u;
+                for (int p2 = 0; p2 < P; ++p2) r += rk[p2 * per + tid];
+                if (r < (uint32_t)k) myl[r] = s.cand[tid];
+            }
+        } else {                                               // 256 < n <= SK_CAP: two candidates per thread
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int c = tid + h * SK_LT;
+                if (c < n) {
+                    const uint64_t me = s.cand[c];
+                    uint32_t r = 0u;
+                    int jj = 0;
+                    for (; jj + 4 <= n; jj += 4) {
+                        const uint64_t e0 = s.cand[jj], e1 = s.cand[jj + 1], e2 = s.cand[jj + 2], e3 = s.cand[jj + 3];
+                        r += (e0 > me ? 1u : 0u) + (e1 > me ? 1u : 0u) + (e2 > me ? 1u : 0u) + (e3 > me ? 1u : 0u);
+                    }
+                    for (; jj < n; ++jj) r += s.cand[jj] > me ? 1u : 0u;
+                    if (r < (uint32_t)k) myl[r] = me;
+                }
+            }
+        }
+        if (tid >= (n < k ? n : k) && tid < SK_K) myl[tid] = 0ull;   // slots past the segment's top k
+    }
+    (void)sorted;
+    vm_drain();                                                // the list is in the L2
+    __syncthreads();
+    SK_MARK(5);
+    SK_TAG(9, ntot);
+    SK_TAG(10, G);
+    if (tid == 0) {
+        const uint32_t t = __hip_atomic_fetch_add(a.ticket + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        s.misc[1] = t == (uint32_t)a.nseg - 1u ? 1u : 0u;
+    }
+    __syncthreads();
+    SK_MARK(6);
+    if (s.misc[1] == 0u) {
+        SK_FLUSH();
+        return;
+    }
+    SK_TAG(13, 4);
+    // ---- the row's merge (the last of its segments): wave w folds lists w, w + SK_NW, ... (the first as stored,
+    // the rest reversed: ascending), then wave 0 folds the waves' lists
+    const uint64_t* rl = a.lists + (int64_t)row * a.nseg * SK_K;
+    uint64_t acc = 0ull;
+    for (int L0 = w; L0 < a.nseg; L0 += 4 * SK_NW) {
+        // four lists per wave, requested together: lists 0 and 2 as stored (descending), 1 and 3 reversed
+        uint64_t b[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int L = L0 + r * SK_NW;
+            b[r] = L < a.nseg ? rl[L * SK_K + ((r & 1) ? WAVE - 1 - lane : lane)] : 0ull;
+        }
+        // two independent merges (their latencies overlap), then one
+        const uint64_t m01 = merge_top64<true>(b[0], b[1]);
+        const uint64_t m23 = merge_top64<false>(b[2], b[3]);
+        if (L0 == w) acc = merge_top64<true>(m01, m23);
+        else acc = merge_top64<true>(acc, merge_top64<false>(m01, m23));
+    }
+    // across the waves: waves 0 and 2 fold 1 and 3 (in parallel), then wave 0 folds wave 2's
+    s.wl[w][lane] = acc;
+    __syncthreads();
+    if (w == 0 || w == 2) acc = merge_top64(acc, s.wl[w + 1][WAVE - 1 - lane]);
+    if (w == 2) s.wl[2][lane] = acc;
+    __syncthreads();
+    if (w != 0) return;
+    SK_MARK(7);
+    if (tid == 0) a.ticket[row] = 0u;                         // every segment has counted itself: reset for the next call
+    acc = merge_top64(acc, s.wl[2][WAVE - 1 - lane]);
+    // the row's candidates: lane i holds the i-th in ferro's order (value desc, id asc); NaN never is one
+    const int kk = __popcll(__ballot(lane < k && acc != 0ull));
+    Args fa = {};
+    fa.mode = MODE_SAMPLE; fa.kcap = a.kcap; fa.cand_ids = a.cand_ids; fa.cand_probs = a.cand_probs;
+    RowCtx rc = {};
+    rc.row = row;
+    rc.p.temperature = temp; rc.p.top_k = top_k;
+    rc.p.top_p = ld_const(&pp->top_p); rc.p.min_p = ld_const(&pp->min_p);
+    int tok = 0, keep = 1;
+    if (greedy) {
+        // ferro's scan (sampler.cpp:19-23) keeps index 0 when its logit is NaN; otherwise the first maximum
+        float l0 = ld_const(rowp);
+        if (CAP && cap > 0.0f) l0 = softcap_one(l0, cap);
+        tok = (l0 != l0 || kk == 0) ? 0 : (int)comp_id(read_lane(acc, 0));
+        if (lane == 0 && a.kcap > 0) {
+            if (a.cand_ids) a.cand_ids[(int64_t)row * a.kcap] = tok;
+            if (a.cand_probs) a.cand_probs[(int64_t)row * a.kcap] = 1.0;
+        }
+    } else if (kk == 0) {
+        tok = 0; keep = 0;                                     // every logit NaN: token 0, nothing kept
+    } else {
+        wave_softmax(fa, rc, lane < kk ? acc : 0ull, kk, a.u ? ld_const(a.u + row) : 0.0, tok, keep);
+    }
+    if (lane == 0) {
+        a.tok[row] = tok;
+        if (a.keep) a.keep[row] = keep;
+    }
+    SK_MARK(8);
+    SK_FLUSH();
+}
+
 }  // namespace fs
 
 // ================================================================================================ host side
@@ -4094,6 +4675,10 @@ struct fs_context {
     int32_t* hflag_dev = nullptr;
     bool captured = false;     // a call was recorded into a graph: workspaces are retired, never freed, on growth
     std::vector<void*> retired;
+    uint64_t* sk_lists = nullptr;   // small-k kernel: [slots][SK_K] sorted segment lists
+    size_t sk_slots = 0;
+    uint32_t* sk_ticket = nullptr;  // small-k kernel: [rows] segment tickets, left at 0
+    size_t sk_rows = 0;
     uint64_t* cand = nullptr;
     size_t cand_slots = 0;     // chunk slots of CAP entries
     uint32_t* meta = nullptr;
@@ -4273,6 +4858,97 @@ bool capturing(hipStream_t st) {
     return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
 }
 
+// ---- small-k kernel (fs_sample_batch_hp)
+// Whether every row of the batch fits the small-k kernel: greedy, or k = min(top_k or V, V) <= SK_K, with no
+// frequency / presence penalty (h: the host copy of the parameters).
+bool small_k_batch(const fs_row_params* h, int64_t B, int32_t V) {
+    for (int64_t b = 0; b < B; ++b) {
+        const fs_row_params& p = h[b];
+        if (p.frequency_penalty != 0.0f || p.presence_penalty != 0.0f) return false;
+        const bool greedy = p.temperature <= 0.0f || p.top_k == 1;
+        const int64_t k = (p.top_k > 0 && p.top_k < V) ? p.top_k : V;
+        if (!greedy && k > fs::SK_K) return false;
+    }
+    return true;
+}
+
+// Logits per thread (NL float4 loads) and segments per row: the largest segments that still give every CU four
+// workgroups, else the smallest (most workgroups) whose row fits SK_MAX_SEGS lists; 0 when none does.
+int small_k_plan(int cus, int64_t B, int32_t V, int& nl, int& nseg) {
+    nl = 0;
+    nseg = 0;
+    const int nls[3] = {16, 8, 4};
+    for (int i = 0; i < 3; ++i) {
+        const int64_t seg = (int64_t)fs::SK_LT * nls[i] * 4;
+        const int64_t n = ((int64_t)V + seg - 1) / seg;
+        if (n > fs::SK_MAX_SEGS) break;
+        nl = nls[i];
+        nseg = (int)n;
+        if (B * n >= 4 * (int64_t)cus) break;
+    }
+    return nl > 0 ? FS_OK : FS_E_INVALID;
+}
+
+int grow_small(fs_context* c, size_t slots, size_t rows) {
+    if (slots > c->sk_slots) {
+        release(c, c->sk_lists);
+        c->sk_lists = nullptr; c->sk_slots = 0;
+        if (hipMalloc(&c->sk_lists, slots * fs::SK_K * sizeof(uint64_t)) != hipSuccess) return FS_E_NOMEM;
+        c->sk_slots = slots;
+    }
+    if (rows > c->sk_rows) {
+        release(c, c->sk_ticket);
+        c->sk_ticket = nullptr; c->sk_rows = 0;
+        if (hipMalloc(&c->sk_ticket, rows * sizeof(uint32_t)) != hipSuccess) return FS_E_NOMEM;
+        if (hipMemset(c->sk_ticket, 0, rows * sizeof(uint32_t)) != hipSuccess) return FS_E_HIP;
+        c->sk_rows = rows;
+    }
+    return FS_OK;
+}
+
+// Launches the small-k kernel when the batch fits it; *used = false (nothing launched) otherwise.
+int launch_small(fs_context* ctx, const fs::Args& a, const fs_row_params* h_params, hipStream_t st, bool& used) {
+    used = false;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    int rc = device_of(ctx);
+    if (rc != FS_OK) return rc;
+    if (!ctx->seg_layout || !small_k_batch(h_params, a.B, a.V)) return FS_OK;
+    int nl = 0, nseg = 0;
+    if (small_k_plan(ctx->cus, a.B, a.V, nl, nseg) != FS_OK) return FS_OK;
+    const int64_t per_x = ((int64_t)a.B + fs::XCDS - 1) / fs::XCDS;
+    const int64_t grid = (int64_t)fs::XCDS * nseg * per_x;
+    if (grid > 0x7fffffff) return FS_OK;
+    rc = grow(ctx, 0, 0, 0);                                    // the error word
+    if (rc != FS_OK) return rc;
+    rc = grow_small(ctx, (size_t)a.B * nseg, (size_t)a.B);
+    if (rc != FS_OK) return rc;
+    if (capturing(st)) ctx->captured = true;
+    fs::SkArgs k = {};
+    k.logits = a.logits; k.ld = a.ld; k.B = a.B; k.V = a.V; k.nseg = nseg;
+    k.hist = a.hist; k.hist_off = a.hist_off; k.params = a.params; k.u = a.u; k.tok = a.tok; k.kcap = a.kcap;
+    k.cand_ids = a.cand_ids; k.cand_probs = a.cand_probs; k.keep = a.keep;
+    k.lists = ctx->sk_lists; k.ticket = ctx->sk_ticket; k.err = ctx->err;
+    k.trace = nullptr;
+#ifdef FS_TRACE
+    if (ctx->trace && grid * fs::TRACE_W <= ctx->trace_cap) k.trace = ctx->trace;
+#endif
+    bool capped = false;
+    for (int64_t b = 0; b < a.B; ++b) capped |= h_params[b].softcap > 0.0f;
+    const dim3 gd((unsigned)grid), bd(fs::SK_LT);
+    if (capped) {
+        if (nl == 16) hipLaunchKernelGGL((fs::small_k_kernel<16, true>), gd, bd, 0, st, k);
+        else if (nl == 8) hipLaunchKernelGGL((fs::small_k_kernel<8, true>), gd, bd, 0, st, k);
+        else hipLaunchKernelGGL((fs::small_k_kernel<4, true>), gd, bd, 0, st, k);
+    } else {
+        if (nl == 16) hipLaunchKernelGGL((fs::small_k_kernel<16, false>), gd, bd, 0, st, k);
+        else if (nl == 8) hipLaunchKernelGGL((fs::small_k_kernel<8, false>), gd, bd, 0, st, k);
+        else hipLaunchKernelGGL((fs::small_k_kernel<4, false>), gd, bd, 0, st, k);
+    }
+    if (hipGetLastError() != hipSuccess) return FS_E_HIP;
+    used = true;
+    return FS_OK;
+}
+
 int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream_t st) {
     std::lock_guard<std::mutex> g(ctx->mu);
     int rc = device_of(ctx);
@@ -4392,6 +5068,8 @@ int fs_create(fs_context** out) {
 
 int fs_destroy(fs_context* c) {
     if (!c) return FS_E_INVALID;
+    (void)hipFree(c->sk_lists);
+    (void)hipFree(c->sk_ticket);
     (void)hipFree(c->cand);
     (void)hipFree(c->meta);
     (void)hipFree(c->rhist);
@@ -4416,6 +5094,35 @@ int fs_sample_batch(fs_context* ctx, const float* d_logits, int64_t ld, int32_t 
     a.u = d_u; a.tok = d_tok; a.kcap = kcap; a.cand_ids = d_cand_ids; a.cand_probs = d_cand_probs; a.keep = d_keep;
     a.mode = fs::MODE_SAMPLE; a.eos = -1;
     return launch(ctx, a, B, 0, (hipStream_t)stream);
+}
+
+int fs_sample_batch_hp(fs_context* ctx, const float* d_logits, int64_t ld, int32_t B, int32_t V,
+                       const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params,
+                       const fs_row_params* h_params, const double* d_u, int32_t* d_tok, int32_t kcap,
+                       int32_t* d_cand_ids, double* d_cand_probs, int32_t* d_keep, void* stream) {
+    if (!ctx || !d_params || !d_tok || kcap < 0 || ((d_cand_ids || d_cand_probs) && kcap == 0)) return FS_E_INVALID;
+    int rc = check_rows(d_logits, ld, B, V);
+    if (rc != FS_OK) return rc;
+    if (B == 0) return FS_OK;
+    fs::Args a = {};
+    a.logits = d_logits; a.ld = ld; a.B = B; a.V = V; a.hist = d_hist; a.hist_off = d_hist_off; a.params = d_params;
+    a.u = d_u; a.tok = d_tok; a.kcap = kcap; a.cand_ids = d_cand_ids; a.cand_probs = d_cand_probs; a.keep = d_keep;
+    a.mode = fs::MODE_SAMPLE; a.eos = -1;
+    if (h_params) {
+        bool used = false;
+        rc = launch_small(ctx, a, h_params, (hipStream_t)stream, used);
+        if (rc != FS_OK || used) return rc;
+    }
+    return launch(ctx, a, B, 0, (hipStream_t)stream);
+}
+
+int fs_small_k_plan(int32_t cus, int32_t B, int32_t V, int32_t* nl, int32_t* nseg) {
+    if (cus < 1 || B < 1 || V < 1 || V > FS_MAX_VOCAB || !nl || !nseg) return FS_E_INVALID;
+    int l = 0, n = 0;
+    const int rc = small_k_plan(cus, B, V, l, n);
+    *nl = l;
+    *nseg = n;
+    return rc == FS_OK ? FS_OK : FS_E_LIMIT;
 }
 
 int fs_sample_batch_static(fs_context* ctx, const float* d_logits, int64_t ld, int32_t B, int32_t V,

@@ -239,9 +239,16 @@ def _hist_tensors(hist, hist_off, B, device):
     return hist, hist_off
 
 
-def sample_batch(logits, params, u, hist=None, hist_off=None, V=None, kcap=0, ctx=None, stream=None):
-    """fs_sample_batch on device tensors: logits [B, ld] fp32 (rows 16-byte aligned), params (B records),
-    u [B] float64 draws, hist/hist_off CSR histories. Returns dict(tok, keep, cand_ids, cand_probs) (device)."""
+# How sample_batch passes the parameters: "host" also hands the library their host copy (fs_sample_batch_hp, which
+# picks the small-k kernel for batches it fits); "device" passes the device copy only (fs_sample_batch, the fused
+# kernel for every batch). Tests run both.
+ROUTE = "host"
+
+
+def sample_batch(logits, params, u, hist=None, hist_off=None, V=None, kcap=0, ctx=None, stream=None, route=None):
+    """fs_sample_batch(_hp) on device tensors: logits [B, ld] fp32 (rows 16-byte aligned), params (B records),
+    u [B] float64 draws, hist/hist_off CSR histories. Returns dict(tok, keep, cand_ids, cand_probs) (device).
+    route: "host" / "device" (default: the module's ROUTE); params given as a device tensor always go "device"."""
     logits, ld, n = _check_logits(logits, V)
     B = logits.shape[0]
     dev = logits.device
@@ -255,10 +262,18 @@ def sample_batch(logits, params, u, hist=None, hist_off=None, V=None, kcap=0, ct
     ids = torch.empty((B, kcap), dtype=torch.int32, device=dev) if kcap else None
     probs = torch.empty((B, kcap), dtype=torch.float64, device=dev) if kcap else None
     ctx = ctx or Context.default(dev)
+    hp = None                                             # the host copy of the parameters picks the kernel
+    if (route or ROUTE) == "host" and not isinstance(params, torch.Tensor):
+        hp = params_array(params)
     with ctx.lock:
-        check(lib().fs_sample_batch(ctx.h, _lptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p), _ptr(u),
-                                    _ptr(tok), kcap, _ptr(ids), _ptr(probs), _ptr(keep), _stream(stream)),
-              "fs_sample_batch")
+        if hp is not None:
+            check(lib().fs_sample_batch_hp(ctx.h, _lptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p),
+                                           hp.ctypes.data_as(ctypes.c_void_p), _ptr(u), _ptr(tok), kcap, _ptr(ids),
+                                           _ptr(probs), _ptr(keep), _stream(stream)), "fs_sample_batch_hp")
+        else:
+            check(lib().fs_sample_batch(ctx.h, _lptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p),
+                                        _ptr(u), _ptr(tok), kcap, _ptr(ids), _ptr(probs), _ptr(keep),
+                                        _stream(stream)), "fs_sample_batch")
     return dict(tok=tok, keep=keep, cand_ids=ids, cand_probs=probs, _keepalive=(p, u, hist, hist_off))
 
 

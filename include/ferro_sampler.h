@@ -86,6 +86,23 @@ int fs_sample_batch(fs_context* ctx, const float* d_logits, int64_t ld, int32_t 
                     const double* d_u, int32_t* d_tok, int32_t kcap, int32_t* d_cand_ids, double* d_cand_probs,
                     int32_t* d_keep, void* stream);
 
+/* fs_sample_batch with the parameters also in host memory: h_params holds the same B records as d_params (the
+ * caller fills both; ferro's call sites hold SamplerParams on the host, sampler.h:25, server.cpp:603-606). With the
+ * host copy the library picks the kernel for the batch without reading device memory: batches whose every row is
+ * greedy or samples from at most 64 candidates (k = top_k, or V when top_k is 0) with no frequency / presence
+ * penalty run on a kernel made for them (every segment's loads issued at once, bitonic sorts in registers); other
+ * batches, and h_params = NULL, run fs_sample_batch. Same outputs as fs_sample_batch. h_params is read before the
+ * call returns. */
+int fs_sample_batch_hp(fs_context* ctx, const float* d_logits, int64_t ld, int32_t B, int32_t V,
+                       const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params,
+                       const fs_row_params* h_params, const double* d_u, int32_t* d_tok, int32_t kcap,
+                       int32_t* d_cand_ids, double* d_cand_probs, int32_t* d_keep, void* stream);
+
+/* Host-only: the small-k kernel's layout for B rows of V logits on a device with `cus` compute units: *nl float4
+ * loads per thread (segments of 1024 * nl logits) and *nseg segments per row; FS_E_LIMIT when V needs more than 64
+ * segments (fs_sample_batch_hp then runs fs_sample_batch). No counterpart in the reference (a planner check). */
+int fs_small_k_plan(int32_t cus, int32_t B, int32_t V, int32_t* nl, int32_t* nseg);
+
 /* fs_sample_batch without any allocation. No counterpart in the reference: it is for callers that cannot allocate
  * device memory during a call - code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
  * Same arguments, semantics and outputs as fs_sample_batch; ctx only carries settings (fs_set_wait_limit) and

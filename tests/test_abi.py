@@ -128,3 +128,22 @@ def test_status_codes():
         assert _lib.check(_lib.FS_W_RECOVERED, "x") == _lib.FS_W_RECOVERED
     with pytest.raises(_lib.SamplerError):
         _lib.check(_lib.FS_E_INVALID, "x")
+
+
+def test_small_k_planner():
+    """fs_small_k_plan: the largest segments that give every CU four workgroups, else the most workgroups."""
+    def plan(cus, B, V):
+        nl, ns = ctypes.c_int32(), ctypes.c_int32()
+        rc = _lib.lib().fs_small_k_plan(cus, B, V, ctypes.byref(nl), ctypes.byref(ns))
+        return rc, nl.value, ns.value
+    assert plan(256, 64, 262144) == (_lib.FS_OK, 16, 16)           # the headline: 1024 workgroups of 64 KB
+    assert plan(256, 1, 65536) == (_lib.FS_OK, 4, 16)              # one row: 16 segments of 4096 logits
+    assert plan(256, 8, 65536) == (_lib.FS_OK, 4, 16)
+    assert plan(256, 256, 262144) == (_lib.FS_OK, 16, 16)
+    assert plan(256, 16, 262144) == (_lib.FS_OK, 4, 64)
+    assert plan(256, 3, 100) == (_lib.FS_OK, 4, 1)                 # one short segment of the smallest size
+    rc, nl, ns = plan(256, 2, 4 * 1024 * 16 * 64 + 1)              # more than 64 of the largest segments
+    assert rc == _lib.FS_E_LIMIT
+    for V in (1, 4095, 4096, 70001, 262144, 1 << 20):
+        rc, nl, ns = plan(256, 4, V)
+        assert rc == _lib.FS_OK and ns * 1024 * nl >= V and (ns - 1) * 1024 * nl < V and ns <= 64, V

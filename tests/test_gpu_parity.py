@@ -28,12 +28,17 @@ def say(*a):
     sys.stdout.flush()
 
 
-@pytest.fixture(scope="module", autouse=True)
-def gpu():
+@pytest.fixture(scope="module", autouse=True, params=["host", "device"])
+def gpu(request):
+    """Every test runs twice: with the host copy of the parameters (fs_sample_batch_hp: the small-k kernel for the
+    batches it fits) and with the device copy only (fs_sample_batch: the fused kernel for every batch)."""
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     F.sampler.Context.default()
+    F.sampler.ROUTE = request.param
+    say(f"== route {request.param}")
     yield
+    F.sampler.ROUTE = "host"
     torch.cuda.synchronize()
 
 
