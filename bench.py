@@ -477,6 +477,32 @@ def run_breakdown(name, args, torch):
             "variants": out}
 
 
+def run_dropin(args):
+    """The C++ drop-in ferro_amd::Sampler (include/ferro_sampler.hpp) one row per call, as ferro's single-row call
+    sites use ferro::Sampler (server.cpp:546, lm_cli.cpp:129,324): ferro_amd/dropin_bench, a separate process, on
+    config 1's row. Microseconds per call by the host's clock, the token back on the host each time."""
+    import subprocess
+    exe = os.path.join(ROOT, "ferro_amd", "dropin_bench")
+    if not os.path.exists(exe):
+        raise SystemExit(f"{exe} is missing: run __graft_entry__.build()")
+    r = subprocess.run([exe, str(max(200, args.steps * 10))], capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        raise RuntimeError(f"dropin_bench failed ({r.returncode}): {r.stderr[-500:]}")
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    return {"metric": "ferro_amd::Sampler per-call latency (C++ drop-in, one row per call)", "unit": "us/call",
+            "value": d["host_row_us"], "higher_is_better": False, "n_gpus": 1, "dtype": "f32",
+            "data": "synthetic (config 1's row: V=65536, N(0,2) + 8 spikes, repetition 1.1 over 64 ids, T 0.7, "
+                    "top-k 40, top-p 0.95)",
+            "config": {"workload": "dropin: ferro_amd::Sampler::sample (host row) / sample_device (device row)",
+                       "calls": d["calls"], "V": d["V"]},
+            "host_row_us": d["host_row_us"], "host_row_writeback_us": d["host_row_writeback_us"],
+            "device_row_us": d["device_row_us"],
+            "note": "host_row: the row copied host -> device each call (ferro's server call sites); "
+                    "host_row_writeback: also leaves the host row penalised in place like ferro's sample "
+                    "(lm_cli.cpp:353); device_row: the row already on the device. Each includes the draw, the "
+                    "history upload, the kernel, the token and error bits back, one stream synchronization."}
+
+
 def ctx_cus(torch):
     return torch.cuda.get_device_properties(0).multi_processor_count
 
@@ -494,9 +520,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=list(WORKLOADS) + ["all"], default="cfg3",
+    ap.add_argument("--workload", choices=list(WORKLOADS) + ["dropin", "all"], default="cfg3",
                     help="cfg3 (default): the headline; cfg1..cfg5: BASELINE.json's configurations; topk0: cfg3 with "
-                         "top_k = 0; all: one line per workload")
+                         "top_k = 0; dropin: the C++ drop-in's per-call latency on one row; all: one line each")
     ap.add_argument("--breakdown", action="store_true",
                     help="instead of the bench line: per-stage ablation timings of the workload (one JSON line)")
     ap.add_argument("--host-rows", action="store_true",
@@ -515,8 +541,12 @@ def main():
 
     import torch
     torch.cuda.set_device(torch.device("cuda", 0))
-    names = list(WORKLOADS) if args.workload == "all" else [args.workload]
+    names = list(WORKLOADS) + ["dropin"] if args.workload == "all" else [args.workload]
     for name in names:
+        if name == "dropin":
+            if not args.breakdown:
+                print(json.dumps(run_dropin(args)), flush=True)
+            continue
         if args.breakdown:
             if WORKLOADS[name][1] == "sample":
                 print(json.dumps(run_breakdown(name, args, torch)), flush=True)

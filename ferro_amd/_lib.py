@@ -51,6 +51,7 @@ SIGNATURES = {
     "fs_device_error": (ctypes.c_int, [_P, _P, _P]),
     "fs_set_wait_limit": (ctypes.c_int, [_P, ctypes.c_uint32]),
     "fs_plan_layout": (ctypes.c_int, [_I32, _I32, _I32, _I32, _I32, _P, _P, _P]),
+    "fs_error_word": (ctypes.c_int, [_P, _P]),
     "fs_rng_create": (ctypes.c_int, [ctypes.c_uint64, _P]),
     "fs_rng_destroy": (ctypes.c_int, [_P]),
     "fs_rng_next_u": (ctypes.c_int, [_P, _P, _I32]),

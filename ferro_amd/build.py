@@ -14,6 +14,9 @@ TRACE_LIB = os.path.join(PKG, "libferro_sampler_trace.so")
 # C++ drop-in test driver (tests/cpp): host code over include/ferro_sampler.hpp, linked against LIB
 SHIM_SRC = os.path.join(ROOT, "tests", "cpp", "shim_replay.cpp")
 SHIM_BIN = os.path.join(ROOT, "tests", "cpp", "shim_replay")
+# per-call timing of the C++ drop-in (bench.py --workload dropin)
+DROPIN_SRC = os.path.join(PKG, "csrc", "dropin_bench.cpp")
+DROPIN_BIN = os.path.join(PKG, "dropin_bench")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -55,11 +58,12 @@ def build(verbose: bool = False, trace: bool = False) -> str:
         if p.returncode != 0:
             sys.stderr.write(out)
             raise RuntimeError(f"{cmd[0]} failed ({p.returncode}) building {what}")
-    if os.path.exists(SHIM_SRC):
-        _run(["g++", "-O2", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROOT, "include"),
-              "-I" + os.path.join(ROCM, "include"), SHIM_SRC, "-o", SHIM_BIN, "-L" + PKG, "-lferro_sampler",
-              "-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,-rpath,$ORIGIN/../../ferro_amd",
-              "-Wl,-rpath," + os.path.join(ROCM, "lib")], SHIM_BIN, verbose)
+    for src, out, rpath in ((SHIM_SRC, SHIM_BIN, "$ORIGIN/../../ferro_amd"), (DROPIN_SRC, DROPIN_BIN, "$ORIGIN")):
+        if os.path.exists(src):
+            _run(["g++", "-O2", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I" + os.path.join(ROOT, "include"),
+                  "-I" + os.path.join(ROCM, "include"), src, "-o", out, "-L" + PKG, "-lferro_sampler",
+                  "-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,-rpath," + rpath,
+                  "-Wl,-rpath," + os.path.join(ROCM, "lib")], out, verbose)
     return LIB
 
 

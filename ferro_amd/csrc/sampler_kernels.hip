@@ -5321,6 +5321,15 @@ int fs_plan_layout(int32_t cus, int32_t xccs, int32_t B, int32_t V, int32_t stat
     return FS_OK;
 }
 
+int fs_error_word(fs_context* ctx, const int32_t** d_bits) {
+    if (!ctx || !d_bits) return FS_E_INVALID;
+    std::lock_guard<std::mutex> g(ctx->mu);
+    const int rc = grow(ctx, 0, 0, 0);
+    if (rc != FS_OK) return rc;
+    *d_bits = ctx->err;
+    return FS_OK;
+}
+
 int fs_set_wait_limit(fs_context* ctx, uint32_t polls) {
     if (!ctx) return FS_E_INVALID;
     std::lock_guard<std::mutex> g(ctx->mu);

@@ -206,6 +206,11 @@ int fs_softcap_batch(const float* d_in, float* d_out, int64_t n, float cap, void
  * called fs_sample_batch_static also reports and clears the bits of its device's static workspace. */
 int fs_device_error(fs_context* ctx, void* stream, int32_t* bits);
 
+/* The device address of the context's error bits (the word fs_device_error reads and clears). A caller that samples
+ * in a loop can copy it asynchronously on its stream together with its outputs, and call fs_device_error (which
+ * synchronizes, then clears) only when a bit is set. No counterpart in the reference (ferro's sample cannot fail). */
+int fs_error_word(fs_context* ctx, const int32_t** d_bits);
+
 /* The merge's bounded wait for a row's segments, in polls (0 = the default, 2^20: far above any segment's time).
  * A smaller limit makes merges give up (FS_DEVERR_INTERNAL) and compute their rows alone; FS_WAIT_GIVE_UP makes
  * every merge give up without polling: tests of that path. */

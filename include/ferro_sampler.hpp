@@ -10,16 +10,24 @@
 // (sampler.h:25), one generate_canonical draw per sampled (non-greedy) call and none for greedy calls
 // (sampler.cpp:19-23,45-46). Unlike ferro, failures of the device path throw std::runtime_error (ferro's
 // sample cannot fail). One instance per stream and caller thread, as ferro's.
+//
+// Per call (besides the row's own copy in sample()): the window offsets, the draw and the history are written to
+// pinned, device-mapped host memory that the kernel reads directly, and the kernel writes the token there too (no
+// copy commands for them); one kernel (fs_sample_batch_hp: the parameters are on the host, so the library picks its
+// kernel without reading them back); one device->host copy of the error bits; one stream synchronization.
 #pragma once
 
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstring>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
 #include "ferro_sampler.h"
+
+static_assert(sizeof(int) == sizeof(int32_t), "history ids are copied as int32");
 
 namespace ferro_amd {
 
@@ -58,13 +66,18 @@ public:
         rec_.repeat_last_n = p.repeat_last_n;
         rec_.penalty_from = p.penalty_from;
         rec_.softcap = p.softcap;
-        hip(hipMalloc(&d_small_, sizeof(Small)), "hipMalloc");
-        hip(hipMemcpy(&d_small_->rec, &rec_, sizeof(rec_), hipMemcpyHostToDevice), "hipMemcpy");
+        hip(hipMalloc(&d_rec_, sizeof(rec_)), "hipMalloc");
+        hip(hipMemcpy(d_rec_, &rec_, sizeof(rec_), hipMemcpyHostToDevice), "hipMemcpy");
+        hip(hipHostMalloc((void**)&h_out_, 2 * sizeof(int32_t), hipHostMallocMapped), "hipHostMalloc");
+        hip(hipHostGetDevicePointer((void**)&d_tok_, h_out_, 0), "hipHostGetDevicePointer");
+        check(fs_error_word(ctx_, &d_err_), "fs_error_word");
+        reserve(0);
     }
     ~Sampler() {
         (void)hipFree(d_row_);
-        (void)hipFree(d_hist_);
-        (void)hipFree(d_small_);
+        (void)hipFree(d_rec_);
+        (void)hipHostFree(h_io_);
+        (void)hipHostFree(h_out_);
         fs_rng_destroy(rng_);
         fs_destroy(ctx_);
     }
@@ -86,7 +99,7 @@ public:
             "hipMemcpyAsync");
         const int tok = run(d_row_, n_vocab, history);
         if (write_back_ && penalised_) {
-            check(fs_penalize_batch(ctx_, d_row_, ld, 1, n_vocab, d_hist_, &d_small_->off[0], &d_small_->rec, stream_),
+            check(fs_penalize_batch(ctx_, d_row_, ld, 1, n_vocab, hist_dev(), off_dev(), d_rec_, stream_),
                   "fs_penalize_batch");
             hip(hipMemcpyAsync(logits, d_row_, (size_t)n_vocab * sizeof(float), hipMemcpyDeviceToHost, stream_),
                 "hipMemcpyAsync");
@@ -103,12 +116,24 @@ public:
     const SamplerParams& params() const { return p_; }
 
 private:
-    struct Small {
-        fs_row_params rec;
-        int64_t off[2];
-        double u;
-        int32_t tok;
-    };
+    // the per-call upload, packed: the window offsets {0, h}, the draw, then the history ids
+    static constexpr size_t kHead = 2 * sizeof(int64_t) + sizeof(double);
+    int64_t* off_dev() const { return reinterpret_cast<int64_t*>(d_io_); }
+    double* u_dev() const { return reinterpret_cast<double*>(d_io_ + 2 * sizeof(int64_t)); }
+    int32_t* hist_dev() const { return reinterpret_cast<int32_t*>(d_io_ + kHead); }
+
+    void reserve(int64_t h) {
+        if (h <= hist_cap_ && d_io_) return;
+        const int64_t cap = h > 2 * hist_cap_ ? h : 2 * hist_cap_ + 64;
+        if (h_io_) hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");   // no kernel still reads it
+        (void)hipHostFree(h_io_);
+        d_io_ = nullptr;
+        h_io_ = nullptr;
+        hist_cap_ = 0;
+        hip(hipHostMalloc((void**)&h_io_, kHead + (size_t)cap * sizeof(int32_t), hipHostMallocMapped), "hipHostMalloc");
+        hip(hipHostGetDevicePointer((void**)&d_io_, h_io_, 0), "hipHostGetDevicePointer");
+        hist_cap_ = cap;
+    }
 
     static void check(int rc, const char* what) {
         if (rc != FS_OK) throw std::runtime_error(std::string("ferro_amd::Sampler: ") + what + ": " + fs_strerror(rc));
@@ -123,33 +148,28 @@ private:
         double u = 0.0;
         if (!greedy) check(fs_rng_next_u(rng_, &u, 1), "fs_rng_next_u");
         const int64_t h = (int64_t)history.size();
-        if (h > hist_cap_) {
-            (void)hipFree(d_hist_);
-            d_hist_ = nullptr;
-            hist_cap_ = 0;
-            hip(hipMalloc(&d_hist_, (size_t)h * sizeof(int32_t)), "hipMalloc");
-            hist_cap_ = h;
-        }
-        if (h) hip(hipMemcpyAsync(d_hist_, history.data(), (size_t)h * sizeof(int32_t), hipMemcpyHostToDevice, stream_),
-                   "hipMemcpyAsync");
-        host_.off[0] = 0;
-        host_.off[1] = h;
-        host_.u = u;
-        hip(hipMemcpyAsync(&d_small_->off[0], &host_.off[0], 2 * sizeof(int64_t) + sizeof(double),
-                           hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
+        reserve(h);
+        // {0, h}, u and the history in the mapped staging buffer, which the kernel reads over the bus (the previous
+        // call's kernel has finished with it: each call ends with a synchronization)
+        const int64_t off[2] = {0, h};
+        memcpy(h_io_, off, sizeof(off));
+        memcpy(h_io_ + 2 * sizeof(int64_t), &u, sizeof(u));
+        if (h) memcpy(h_io_ + kHead, history.data(), (size_t)h * sizeof(int32_t));   // int is int32_t here
         const int64_t ld = ((int64_t)n_vocab + 3) & ~(int64_t)3;
-        check(fs_sample_batch(ctx_, d_logits, ld, 1, n_vocab, h ? d_hist_ : nullptr, &d_small_->off[0], &d_small_->rec,
-                              &d_small_->u, &d_small_->tok, 0, nullptr, nullptr, nullptr, stream_),
-              "fs_sample_batch");
-        int32_t tok = -1;
-        hip(hipMemcpyAsync(&tok, &d_small_->tok, sizeof(tok), hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
+        const int rc = fs_sample_batch_hp(ctx_, d_logits, ld, 1, n_vocab, h ? hist_dev() : nullptr, off_dev(), d_rec_,
+                                          &rec_, u_dev(), d_tok_, 0, nullptr, nullptr, nullptr, stream_);
+        if (rc < 0) check(rc, "fs_sample_batch_hp");               // FS_W_RECOVERED: the call ran normally
+        // the token lands in h_out_[0] from the kernel; the error bits come back behind the same synchronization
+        hip(hipMemcpyAsync(&h_out_[1], d_err_, sizeof(int32_t), hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
         hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
-        int32_t bits = 0;
-        check(fs_device_error(ctx_, stream_, &bits), "fs_device_error");
-        if (bits) throw std::runtime_error("ferro_amd::Sampler: device error bits " + std::to_string(bits));
+        if (h_out_[1] != 0) {
+            int32_t bits = 0;
+            check(fs_device_error(ctx_, stream_, &bits), "fs_device_error");     // clears them
+            throw std::runtime_error("ferro_amd::Sampler: device error bits " + std::to_string(bits));
+        }
         penalised_ = h > 0 && p_.repeat_last_n != 0 &&
                      (p_.repetition_penalty != 1.0f || p_.frequency_penalty != 0.0f || p_.presence_penalty != 0.0f);
-        return tok;
+        return h_out_[0];
     }
 
     SamplerParams p_;
@@ -159,11 +179,14 @@ private:
     fs_context* ctx_ = nullptr;
     fs_rng* rng_ = nullptr;
     fs_row_params rec_{};
-    Small host_{};
-    Small* d_small_ = nullptr;
+    fs_row_params* d_rec_ = nullptr;
+    int32_t* d_tok_ = nullptr;
+    const int32_t* d_err_ = nullptr;
+    int32_t* h_out_ = nullptr;       // pinned, device-mapped: token (written by the kernel), error bits
+    unsigned char* h_io_ = nullptr;  // pinned, device-mapped: offsets, draw, history
+    unsigned char* d_io_ = nullptr;  // its device address
     float* d_row_ = nullptr;
     int64_t row_cap_ = 0;
-    int32_t* d_hist_ = nullptr;
     int64_t hist_cap_ = 0;
 };
 
