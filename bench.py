@@ -73,10 +73,12 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def read_traffic(name):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE, calibrated)."""
+def read_traffic(name, kernel):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary of this kernel on this workload
+    (profiles/<kernel>_<workload>_traffic.md: reads by request size + WRITE_SIZE, calibrated)."""
+    short = kernel.split("::")[-1].split("<")[0]
     try:
-        txt = open(os.path.join(ROOT, "profiles", f"sample_kernel_{name}_traffic.md")).read()
+        txt = open(os.path.join(ROOT, "profiles", f"{short}_{name}_traffic.md")).read()
     except OSError:
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", txt)
@@ -382,7 +384,7 @@ def run_workload(name, args, torch):
                           "note": "the same K calls launched one by one from Python through ctypes, an event pair "
                                   "around each"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(name),
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(name, kname),
                      "kernel": f"{what}: {kname} ({kdesc})",
                      "kernel_ms": graph_ms, "kernel_ms_python_launch": kern_ms, "algorithmic_bytes": alg_bytes,
                      "algorithmic_bytes_note": "4*V per row (one read of the fp32 row) + 4 per history id"},

@@ -14,6 +14,9 @@ TRACE_LIB = os.path.join(PKG, "libferro_sampler_trace.so")
 # C++ drop-in test driver (tests/cpp): host code over include/ferro_sampler.hpp, linked against LIB
 SHIM_SRC = os.path.join(ROOT, "tests", "cpp", "shim_replay.cpp")
 SHIM_BIN = os.path.join(ROOT, "tests", "cpp", "shim_replay")
+# launch and streaming-read floors for the rocprofv3 traces (profiles/launch_floor.md)
+FLOOR_SRC = os.path.join(PKG, "csrc", "launch_floor.hip")
+FLOOR_BIN = os.path.join(PKG, "launch_floor")
 # per-call timing of the C++ drop-in (bench.py --workload dropin)
 DROPIN_SRC = os.path.join(PKG, "csrc", "dropin_bench.cpp")
 DROPIN_BIN = os.path.join(PKG, "dropin_bench")
@@ -46,6 +49,9 @@ def _run(cmd, what, verbose):
 
 def build(verbose: bool = False, trace: bool = False) -> str:
     jobs = [([HIPCC, *FLAGS, "-o", LIB, SRC], LIB)]
+    if os.path.exists(FLOOR_SRC):
+        jobs.append(([HIPCC, *[f for f in FLAGS if f not in ("-shared", "-fPIC")], "-o", FLOOR_BIN, FLOOR_SRC],
+                     FLOOR_BIN))
     if trace:
         jobs.append(([HIPCC, *FLAGS, "-DFS_TRACE", "-o", TRACE_LIB, SRC], TRACE_LIB))
     procs = []
