@@ -34,15 +34,18 @@ KERNEL = "fs::segment_kernel"
 SMALL_K = 64                                       # fs_sample_batch_hp's small-k kernel: k <= 64 or greedy rows
 
 
-def kernel_of(w, route, cus=256):
-    """The kernel a sampling call of this workload launches: fs_sample_batch_hp (route "host") runs the small-k kernel
-    when every row is greedy or has k <= 64 and no frequency / presence penalty; otherwise the fused kernel."""
+def kernel_of(w, route, cus=256, verify=False):
+    """The kernel a call of this workload launches: fs_sample_batch_hp / fs_verify_hp (route "host") run the small-k
+    kernel when every row (stream) is greedy or has k <= 64 and no frequency / presence penalty (verification: no
+    active penalty at all); otherwise the fused kernel."""
     if route != "host":
         return KERNEL, "segments, then a merging workgroup per row, one grid"
     p = w.params
     greedy = (p["temperature"] <= 0) | (p["top_k"] == 1)
     k = np.where((p["top_k"] > 0) & (p["top_k"] < w.V), p["top_k"], w.V)
     fits = bool(((greedy | (k <= SMALL_K)) & (p["frequency_penalty"] == 0) & (p["presence_penalty"] == 0)).all())
+    if verify:
+        fits = fits and bool(((p["repetition_penalty"] == 1) | (p["repeat_last_n"] == 0)).all())
     if not fits:
         return KERNEL, "segments, then a merging workgroup per row, one grid"
     from ferro_amd import _lib
@@ -319,8 +322,14 @@ def run_workload(name, args, torch):
         roff = torch.from_numpy(w.row_off).to(dev)
         S = len(w.row_off) - 1
         acc = torch.empty(S, dtype=torch.int32, device=dev)
-        fixed = (S, w.B, w.V, P(rows), P(roff), P(hist), P(hoff), P(params), P(u), -1, P(tok), P(acc), sh)
-        call, what = L.fs_verify, "fs_verify"
+        if args.route == "host":
+            hp = np.ascontiguousarray(w.params)         # the host copy of the stream parameters
+            fixed = (S, w.B, w.V, P(rows), P(roff), P(hist), P(hoff), P(params), hp.ctypes.data_as(ctypes.c_void_p),
+                     P(u), -1, P(tok), P(acc), sh)
+            call, what = L.fs_verify_hp, "fs_verify_hp"
+        else:
+            fixed = (S, w.B, w.V, P(rows), P(roff), P(hist), P(hoff), P(params), P(u), -1, P(tok), P(acc), sh)
+            call, what = L.fs_verify, "fs_verify"
     elif args.route == "host":
         acc = None
         hp = np.ascontiguousarray(w.params)             # the host copy of the parameters (picks the kernel)
@@ -331,7 +340,7 @@ def run_workload(name, args, torch):
         acc = None
         fixed = (w.B, w.V, P(hist), P(hoff), P(params), P(u), P(tok), 0, None, None, P(keep), sh)
         call, what = L.fs_sample_batch, "fs_sample_batch"
-    kname, kdesc = kernel_of(w, args.route if entry == "sample" else "device", ctx_cus(torch))
+    kname, kdesc = kernel_of(w, args.route, ctx_cus(torch), verify=entry == "verify")
 
     def step(i):
         rc = call(ctx.h, P(bufs[i % nrot]), w.V, *fixed)

@@ -46,6 +46,7 @@ SIGNATURES = {
     "fs_small_k_plan": (ctypes.c_int, [_I32, _I32, _I32, _P, _P]),
     "fs_argmax_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P]),
     "fs_verify": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P]),
+    "fs_verify_hp": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P]),
     "fs_penalize_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P]),
     "fs_softcap_batch": (ctypes.c_int, [_P, _P, _I64, ctypes.c_float, _P]),
     "fs_device_error": (ctypes.c_int, [_P, _P, _P]),

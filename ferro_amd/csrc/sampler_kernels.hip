@@ -4123,6 +4123,13 @@ struct SkArgs {
     uint32_t* ticket;                      // [B]: segments finished (left at 0)
     int32_t* err;
     uint64_t* trace;                       // FS_TRACE builds: per-workgroup phase timestamps (NULL: none)
+    // verification windows (mode MODE_VERIFY; the host sends only windows without an active penalty here)
+    int mode;
+    const int32_t* rows;                   // token fed at each row
+    const int64_t* row_off;                // stream -> rows
+    int n_streams, eos;
+    int32_t* accepted;
+    uint32_t* stream_cnt;                  // [n_streams]: rows finished (left at 0)
 };
 
 // lane ^ D over the wave, in the VALU: DPP for D < 16 (both shifts in full exec, then an arithmetic select: a branch
@@ -4315,8 +4322,18 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(SkArgs a) {
     const int seg_lo = seg * SEG;
     const int n_in = a.V - seg_lo < SEG ? a.V - seg_lo : SEG;         // logits of this segment (>= 1)
 
+    // verification: the row's stream (its parameters); sampling: the row's own
+    int pidx = row;
+    if (a.mode == MODE_VERIFY) {
+        int s0 = 0, s1 = a.n_streams;                          // the largest s with row_off[s] <= row
+        while (s1 - s0 > 1) {
+            const int m = (s0 + s1) >> 1;
+            if (ld_const(a.row_off + m) <= row) s0 = m; else s1 = m;
+        }
+        pidx = s0;
+    }
     // the row's parameters (scalar loads) and its repetition window [b, len) over its history
-    const fs_row_params* pp = a.params + row;
+    const fs_row_params* pp = a.params + pidx;
     const float temp = ld_const(&pp->temperature);
     const int top_k = ld_const(&pp->top_k);
     const float rep = ld_const(&pp->repetition_penalty);
@@ -4327,7 +4344,7 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(SkArgs a) {
     const bool greedy = temp <= 0.0f || top_k == 1;
     const int k = greedy ? 1 : ((top_k > 0 && top_k < a.V) ? top_k : a.V);
     int64_t h0 = 0, len = 0;
-    if (a.hist && a.hist_off) {
+    if (a.hist && a.hist_off && a.mode != MODE_VERIFY) {
         h0 = ld_const(a.hist_off + row);
         len = ld_const(a.hist_off + row + 1) - h0;
     }
@@ -4654,9 +4671,31 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(SkArgs a) {
     } else {
         wave_softmax(fa, rc, lane < kk ? acc : 0ull, kk, a.u ? ld_const(a.u + row) : 0.0, tok, keep);
     }
-    if (lane == 0) {
-        a.tok[row] = tok;
-        if (a.keep) a.keep[row] = keep;
+    if (a.mode != MODE_VERIFY) {
+        if (lane == 0) {
+            a.tok[row] = tok;
+            if (a.keep) a.keep[row] = keep;
+        }
+    } else if (lane == 0) {
+        // the last row of a stream to finish computes its accepted prefix (server.cpp:627-637): the stream's rows
+        // run on several XCDs, so the tokens and the counter are agent-scope accesses
+        st_agent(&a.tok[row], (int32_t)tok);
+        vm_drain();
+        const int64_t r0 = ld_const(a.row_off + pidx);
+        const int m = (int)(ld_const(a.row_off + pidx + 1) - r0);
+        const uint32_t old = __hip_atomic_fetch_add(&a.stream_cnt[pidx], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == (uint32_t)m - 1u) {
+            st_agent(&a.stream_cnt[pidx], 0u);
+            int acc = 0;
+            for (int r = 0; r < m; ++r) {
+                const int t = ld_agent(&a.tok[r0 + r]);
+                acc = r + 1;
+                if (a.eos >= 0 && t == a.eos) break;
+                if (r + 1 < m && t == a.rows[r0 + r + 1]) continue;
+                break;
+            }
+            a.accepted[pidx] = acc;
+        }
     }
     SK_MARK(8);
     SK_FLUSH();
@@ -4906,19 +4945,31 @@ int grow_small(fs_context* c, size_t slots, size_t rows) {
     return FS_OK;
 }
 
-// Launches the small-k kernel when the batch fits it; *used = false (nothing launched) otherwise.
+// Verification windows fit the small-k kernel when every stream does and none has an active penalty (a row's
+// history would then include the drafts fed before it).
+bool small_k_windows(const fs_row_params* h, int64_t S, int32_t V) {
+    if (!small_k_batch(h, S, V)) return false;
+    for (int64_t s = 0; s < S; ++s)
+        if (h[s].repetition_penalty != 1.0f && h[s].repeat_last_n != 0) return false;
+    return true;
+}
+
+// Launches the small-k kernel when the batch fits it; *used = false (nothing launched) otherwise. a.mode selects
+// sampling (h_params: B records) or verification windows (h_params: n_streams records).
 int launch_small(fs_context* ctx, const fs::Args& a, const fs_row_params* h_params, hipStream_t st, bool& used) {
     used = false;
     std::lock_guard<std::mutex> g(ctx->mu);
     int rc = device_of(ctx);
     if (rc != FS_OK) return rc;
-    if (!ctx->seg_layout || !small_k_batch(h_params, a.B, a.V)) return FS_OK;
+    const bool verify = a.mode == fs::MODE_VERIFY;
+    if (!ctx->seg_layout) return FS_OK;
+    if (verify ? !small_k_windows(h_params, a.n_streams, a.V) : !small_k_batch(h_params, a.B, a.V)) return FS_OK;
     int nl = 0, nseg = 0;
     if (small_k_plan(ctx->cus, a.B, a.V, nl, nseg) != FS_OK) return FS_OK;
     const int64_t per_x = ((int64_t)a.B + fs::XCDS - 1) / fs::XCDS;
     const int64_t grid = (int64_t)fs::XCDS * nseg * per_x;
     if (grid > 0x7fffffff) return FS_OK;
-    rc = grow(ctx, 0, 0, 0);                                    // the error word
+    rc = grow(ctx, 0, 0, verify ? (size_t)a.n_streams : 0);  // the error word (and the verify stream counters)
     if (rc != FS_OK) return rc;
     rc = grow_small(ctx, (size_t)a.B * nseg, (size_t)a.B);
     if (rc != FS_OK) return rc;
@@ -4928,12 +4979,14 @@ int launch_small(fs_context* ctx, const fs::Args& a, const fs_row_params* h_para
     k.hist = a.hist; k.hist_off = a.hist_off; k.params = a.params; k.u = a.u; k.tok = a.tok; k.kcap = a.kcap;
     k.cand_ids = a.cand_ids; k.cand_probs = a.cand_probs; k.keep = a.keep;
     k.lists = ctx->sk_lists; k.ticket = ctx->sk_ticket; k.err = ctx->err;
+    k.mode = a.mode; k.rows = a.rows; k.row_off = a.row_off; k.n_streams = a.n_streams; k.eos = a.eos;
+    k.accepted = a.accepted; k.stream_cnt = ctx->stream_cnt;
     k.trace = nullptr;
 #ifdef FS_TRACE
     if (ctx->trace && grid * fs::TRACE_W <= ctx->trace_cap) k.trace = ctx->trace;
 #endif
     bool capped = false;
-    for (int64_t b = 0; b < a.B; ++b) capped |= h_params[b].softcap > 0.0f;
+    for (int64_t b = 0; b < (verify ? (int64_t)a.n_streams : (int64_t)a.B); ++b) capped |= h_params[b].softcap > 0.0f;
     const dim3 gd((unsigned)grid), bd(fs::SK_LT);
     if (capped) {
         if (nl == 16) hipLaunchKernelGGL((fs::small_k_kernel<16, true>), gd, bd, 0, st, k);
@@ -5114,6 +5167,27 @@ int fs_sample_batch_hp(fs_context* ctx, const float* d_logits, int64_t ld, int32
         if (rc != FS_OK || used) return rc;
     }
     return launch(ctx, a, B, 0, (hipStream_t)stream);
+}
+
+int fs_verify_hp(fs_context* ctx, const float* d_logits, int64_t ld, int32_t n_streams, int32_t total_rows, int32_t V,
+                 const int32_t* d_rows, const int64_t* d_row_off, const int32_t* d_hist, const int64_t* d_hist_off,
+                 const fs_row_params* d_params, const fs_row_params* h_params, const double* d_u, int32_t eos_id,
+                 int32_t* d_tok, int32_t* d_accepted, void* stream) {
+    if (!ctx || !d_rows || !d_row_off || !d_params || !d_tok || !d_accepted || n_streams < 0 || total_rows < 0)
+        return FS_E_INVALID;
+    int rc = check_rows(d_logits, ld, total_rows, V);
+    if (rc != FS_OK) return rc;
+    if (total_rows == 0 || n_streams == 0) return FS_OK;
+    fs::Args a = {};
+    a.logits = d_logits; a.ld = ld; a.B = total_rows; a.V = V; a.hist = d_hist; a.hist_off = d_hist_off;
+    a.params = d_params; a.u = d_u; a.tok = d_tok; a.rows = d_rows; a.row_off = d_row_off; a.n_streams = n_streams;
+    a.eos = eos_id; a.accepted = d_accepted; a.mode = fs::MODE_VERIFY;
+    if (h_params) {
+        bool used = false;
+        rc = launch_small(ctx, a, h_params, (hipStream_t)stream, used);
+        if (rc != FS_OK || used) return rc;
+    }
+    return launch(ctx, a, total_rows, n_streams, (hipStream_t)stream);
 }
 
 int fs_small_k_plan(int32_t cus, int32_t B, int32_t V, int32_t* nl, int32_t* nseg) {

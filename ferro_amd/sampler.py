@@ -293,8 +293,9 @@ def argmax_batch(logits, hist=None, hist_off=None, params=None, V=None, ctx=None
 
 
 def verify(logits, rows, row_off, params, u=None, hist=None, hist_off=None, eos_id=-1, V=None, ctx=None,
-           stream=None):
-    """fs_verify: per-row tokens and per-stream accepted prefix lengths of a speculative window."""
+           stream=None, route=None):
+    """fs_verify(_hp): per-row tokens and per-stream accepted prefix lengths of a speculative window. route as for
+    sample_batch ("host": the host copy of the stream parameters goes along, fs_verify_hp)."""
     logits, ld, n = _check_logits(logits, V)
     R = logits.shape[0]
     dev = logits.device
@@ -309,10 +310,18 @@ def verify(logits, rows, row_off, params, u=None, hist=None, hist_off=None, eos_
     tok = torch.empty(R, dtype=torch.int32, device=dev)
     acc = torch.empty(S, dtype=torch.int32, device=dev)
     ctx = ctx or Context.default(dev)
+    hp = None
+    if (route or ROUTE) == "host" and not isinstance(params, torch.Tensor):
+        hp = params_array(params)
     with ctx.lock:
-        check(lib().fs_verify(ctx.h, _lptr(logits), ld, S, R, n, _ptr(rows), _ptr(row_off), _ptr(hist),
-                              _ptr(hist_off), _ptr(p), _ptr(u), int(eos_id), _ptr(tok), _ptr(acc), _stream(stream)),
-              "fs_verify")
+        if hp is not None:
+            check(lib().fs_verify_hp(ctx.h, _lptr(logits), ld, S, R, n, _ptr(rows), _ptr(row_off), _ptr(hist),
+                                     _ptr(hist_off), _ptr(p), hp.ctypes.data_as(ctypes.c_void_p), _ptr(u),
+                                     int(eos_id), _ptr(tok), _ptr(acc), _stream(stream)), "fs_verify_hp")
+        else:
+            check(lib().fs_verify(ctx.h, _lptr(logits), ld, S, R, n, _ptr(rows), _ptr(row_off), _ptr(hist),
+                                  _ptr(hist_off), _ptr(p), _ptr(u), int(eos_id), _ptr(tok), _ptr(acc),
+                                  _stream(stream)), "fs_verify")
     return tok, acc
 
 

@@ -136,6 +136,15 @@ int fs_verify(fs_context* ctx, const float* d_logits, int64_t ld, int32_t n_stre
               const int64_t* d_hist_off, const fs_row_params* d_params, const double* d_u, int32_t eos_id,
               int32_t* d_tok, int32_t* d_accepted, void* stream);
 
+/* fs_verify with the stream parameters also in host memory (h_params: the same n_streams records as d_params). Windows
+ * whose every stream is greedy or samples from at most 64 candidates, with no active penalty (repetition 1, or
+ * repeat_last_n 0, and no frequency / presence penalty: a row's history then does not matter), run on the small-k
+ * kernel of fs_sample_batch_hp; other windows, and h_params = NULL, run fs_verify. Same outputs as fs_verify. */
+int fs_verify_hp(fs_context* ctx, const float* d_logits, int64_t ld, int32_t n_streams, int32_t total_rows,
+                 int32_t V, const int32_t* d_rows, const int64_t* d_row_off, const int32_t* d_hist,
+                 const int64_t* d_hist_off, const fs_row_params* d_params, const fs_row_params* h_params,
+                 const double* d_u, int32_t eos_id, int32_t* d_tok, int32_t* d_accepted, void* stream);
+
 /* Host draw source matching ferro::Sampler's std::mt19937_64 stream (src/sampler.h:25,32; sampler.cpp:45-46):
  * fs_rng_next_u returns generate_canonical<double,53> values, so u * tot is ferro's draw r. seed 0 = random.
  * A sampled (non-greedy) row consumes one u; greedy rows consume none (sampler.cpp:19-23). fs_rng_copy lets a

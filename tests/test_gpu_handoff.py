@@ -61,7 +61,7 @@ def mixed_batch(seed=11, B=12, V=65536):
 
 def run_and_check(w, ctx, kcap=64):
     x = torch.from_numpy(w.logits).cuda()
-    out = F.sample_batch(x, w.params, w.u, hist=w.hist, hist_off=w.hist_off, kcap=kcap, ctx=ctx)
+    out = F.sample_batch(x, w.params, w.u, hist=w.hist, hist_off=w.hist_off, kcap=kcap, ctx=ctx, route="device")
     torch.cuda.synchronize()
     g = {k: v.cpu().numpy() for k, v in out.items() if v is not None and not k.startswith("_")}
     o = O.sample_batch(w.logits, w.hist, w.hist_off, w.params, w.u, kcap=kcap, nthreads=NT)
@@ -99,18 +99,21 @@ def test_merge_give_up_is_exact_and_resets():
 
 
 def test_verify_give_up_is_exact():
+    """The fused kernel's verify path (the small-k kernel of fs_verify_hp never waits, so it never gives up)."""
     w = W.config4(S=6, M=9)
     ctx = F.sampler.Context()
     say(f"case verify give-up: rows={w.B} V={w.V}")
     ctx.set_wait_limit(FS_WAIT_GIVE_UP)
     x = torch.from_numpy(w.logits).cuda()
-    tok, acc = F.verify(x, w.rows, w.row_off, w.params, u=w.u, hist=w.hist, hist_off=w.hist_off, ctx=ctx)
+    tok, acc = F.verify(x, w.rows, w.row_off, w.params, u=w.u, hist=w.hist, hist_off=w.hist_off, ctx=ctx,
+                      route="device")
     otok, oacc = O.verify(w.logits, w.rows, w.row_off, w.hist, w.hist_off, w.params, w.u)
     np.testing.assert_array_equal(tok.cpu().numpy(), otok)
     np.testing.assert_array_equal(acc.cpu().numpy(), oacc)
     ctx.set_wait_limit(0)
     assert F.device_error(ctx) & FS_DEVERR_INTERNAL
-    tok, acc = F.verify(x, w.rows, w.row_off, w.params, u=w.u, hist=w.hist, hist_off=w.hist_off, ctx=ctx)
+    tok, acc = F.verify(x, w.rows, w.row_off, w.params, u=w.u, hist=w.hist, hist_off=w.hist_off, ctx=ctx,
+                      route="device")
     np.testing.assert_array_equal(tok.cpu().numpy(), otok)
     np.testing.assert_array_equal(acc.cpu().numpy(), oacc)
     assert F.device_error(ctx) == 0
