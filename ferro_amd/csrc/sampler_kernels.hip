@@ -4302,8 +4302,34 @@ __device__ __forceinline__ uint64_t sk_kth_exact(const float* segp, int seg_lo, 
 }
 
 // CAP: some row of the batch has a softcap (the cap's code is left out of batches without one).
+struct Ids16 {
+    int32_t v[16];
+};
+
+// small_k_kernel's argument list as a struct: the argument segment follows the same layout rules
+struct SkKernargs {
+    const float* logits;
+    int64_t ld;
+    int B, V, nseg, may_pen;
+    const fs_row_params* params;
+    const int64_t* hist_off;
+    const int32_t* hist;
+    SkArgs a;
+};
+constexpr size_t SK_ARGS_OFF = offsetof(SkKernargs, a);
+
+// Dynamic LDS a launch requests beyond SkShared (unused): with it a CU holds 4 workgroups (≈35 KB each of its 160 KB),
+// as the kernel's 95 VGPRs would otherwise allow 5. Measured on MI355X: a 272-row verification call (1088 workgroups)
+// 21.3 -> 20.6 us with the limit, the headline's 1024 workgroups unchanged.
+constexpr unsigned SK_PAD_LDS = 16384;
+
 template <int NL, bool CAP>
-__global__ __launch_bounds__(SK_LT) void small_k_kernel(SkArgs a) {
+__global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int64_t ld, int B, int V, int nseg,
+                                                        int may_pen, const fs_row_params* params,
+                                                        const int64_t* hist_off, const int32_t* hist, SkArgs a_) {
+    // The leading arguments arrive in SGPRs at wave launch (kernel-argument preloading), so the logits are requested
+    // before any scalar memory round trip. A call with a repetition window (may_pen, set by the host from its copy of
+    // the parameters) then reads the row's window bounds and requests its ids behind the logits.
     constexpr int SEG = SK_LT * NL * 4;
     static_assert(NL <= 16, "the repetition bitmap covers NL <= 16");
     __shared__ __align__(16) SkShared s;
@@ -4312,55 +4338,18 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(SkArgs a) {
     // index class mod XCDS, so they share an XCD and its L2 (the ticket and the lists)
     const int x = (int)(blockIdx.x % (unsigned)XCDS);
     const int j = (int)(blockIdx.x / (unsigned)XCDS);
-    const int q_row = __builtin_amdgcn_readfirstlane(j / a.nseg);
-    const int seg = j - q_row * a.nseg;
+    const int q_row = __builtin_amdgcn_readfirstlane(j / nseg);
+    const int seg = j - q_row * nseg;
     const int row = x + XCDS * q_row;
-    if (row >= a.B) return;
+    if (row >= B) return;
     SK_MARK(0);
     for (int i_ = 1; i_ < 13; ++i_) SK_TAG(i_, 0);
     SK_TAG(13, 3); SK_TAG(14, row); SK_TAG(15, seg);
     const int seg_lo = seg * SEG;
-    const int n_in = a.V - seg_lo < SEG ? a.V - seg_lo : SEG;         // logits of this segment (>= 1)
+    const int n_in = V - seg_lo < SEG ? V - seg_lo : SEG;             // logits of this segment (>= 1)
 
-    // verification: the row's stream (its parameters); sampling: the row's own
-    int pidx = row;
-    if (a.mode == MODE_VERIFY) {
-        int s0 = 0, s1 = a.n_streams;                          // the largest s with row_off[s] <= row
-        while (s1 - s0 > 1) {
-            const int m = (s0 + s1) >> 1;
-            if (ld_const(a.row_off + m) <= row) s0 = m; else s1 = m;
-        }
-        pidx = s0;
-    }
-    // the row's parameters (scalar loads) and its repetition window [b, len) over its history
-    const fs_row_params* pp = a.params + pidx;
-    const float temp = ld_const(&pp->temperature);
-    const int top_k = ld_const(&pp->top_k);
-    const float rep = ld_const(&pp->repetition_penalty);
-    const float cap = CAP ? ld_const(&pp->softcap) : 0.0f;
-    fs_row_params pw;
-    pw.repeat_last_n = ld_const(&pp->repeat_last_n);
-    pw.penalty_from = ld_const(&pp->penalty_from);
-    const bool greedy = temp <= 0.0f || top_k == 1;
-    const int k = greedy ? 1 : ((top_k > 0 && top_k < a.V) ? top_k : a.V);
-    int64_t h0 = 0, len = 0;
-    if (a.hist && a.hist_off && a.mode != MODE_VERIFY) {
-        h0 = ld_const(a.hist_off + row);
-        len = ld_const(a.hist_off + row + 1) - h0;
-    }
-    bool pen = rep != 1.0f && pw.repeat_last_n != 0 && len > 0;
-    const int64_t wb0 = pen ? window_begin(len, pw) : len;
-    if (wb0 >= len) pen = false;
-    // the window's first ids, requested ahead of the logits (vector loads complete in order)
-    int wid[2];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const int64_t i = wb0 + r * SK_LT + tid;
-        wid[r] = (pen && i < len) ? a.hist[h0 + i] : -1;
-    }
-    __builtin_amdgcn_sched_barrier(0);
     // every load of the segment at once; past the row's end (rounded up to four, inside ld) reads are zeros, masked
-    const float* rowp = a.logits + (int64_t)row * a.ld;
+    const float* rowp = logits + (int64_t)row * ld;
     const int nrec = ((n_in + 3) & ~3) * 4;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(rowp + seg_lo), (short)0, nrec, 0x00020000);
@@ -4372,20 +4361,83 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(SkArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // repetition penalty: an exact bitmap of the window's ids in this segment (each distinct id once: sampler.cpp:14-17)
-    uint64_t pm = 0ull;                        // 4 bits per group of this thread
+    // the repetition window [wb0, len) over the row's history (sampling rows only: verification windows reach this
+    // kernel only without an active penalty); its first 512 ids are requested behind the logits, two per thread
+    bool pen = false;
+    float rep = 1.0f;
+    int64_t h0 = 0, len = 0, wb0 = 0;
+    int wid[2] = {-1, -1};
+    if (may_pen) {
+        const fs_row_params* pr = params + row;
+        rep = ld_const(&pr->repetition_penalty);
+        fs_row_params pw;
+        pw.repeat_last_n = ld_const(&pr->repeat_last_n);
+        pw.penalty_from = ld_const(&pr->penalty_from);
+        h0 = ld_const(hist_off + row);
+        len = ld_const(hist_off + row + 1) - h0;
+        pen = rep != 1.0f && pw.repeat_last_n != 0 && len > 0;
+        wb0 = window_begin(len, pw);                           // unconditionally: all five loads in one round trip
+        if (!pen || wb0 >= len) { pen = false; wb0 = len; }
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int64_t i = wb0 + r * SK_LT + tid;
+            wid[r] = (pen && i < len) ? hist[h0 + i] : -1;
+        }
+    }
+    // The remaining arguments are read from here on, through a pointer the compiler cannot trace back to the argument
+    // segment: otherwise it loads some of them early and, short of scalar registers, spills them to vector lanes,
+    // which waits for those loads before the logits are requested.
+    const __attribute__((address_space(4))) char* kseg =
+        (const __attribute__((address_space(4))) char*)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(kseg) : : "memory");
+    const SkArgs& a = *(const SkArgs*)(kseg + SK_ARGS_OFF);
+    (void)a_;
+
+    // verification: the row's stream (its parameters); sampling: the row's own
+    int pidx = row;
+    if (a.mode == MODE_VERIFY) {
+        int s0 = 0, s1 = a.n_streams;                          // the largest s with row_off[s] <= row
+        while (s1 - s0 > 1) {
+            const int m = (s0 + s1) >> 1;
+            if (ld_const(a.row_off + m) <= row) s0 = m; else s1 = m;
+        }
+        pidx = s0;
+    }
+    const fs_row_params* pp = params + pidx;
+    const float temp = ld_const(&pp->temperature);
+    const int top_k = ld_const(&pp->top_k);
+    const float cap = CAP ? ld_const(&pp->softcap) : 0.0f;
+    const bool greedy = temp <= 0.0f || top_k == 1;
+    const int k = greedy ? 1 : ((top_k > 0 && top_k < V) ? top_k : V);
+
+    // repetition penalty: an exact bitmap of the window's ids in this segment (each distinct id once: sampler.cpp:14-17).
+    // rep >= 1 never raises a logit (l > 0: l / rep <= l; l <= 0: l * rep <= l), so the bound is taken over the raw
+    // logits, the bitmap is filled while the bound is sorted (the ids arrive right behind the logits), and the penalty
+    // is applied to the handed-over logits only; the bound then needs a check (below). rep < 1 raises the flagged
+    // logits: they are penalised before the bound (the bitmap first).
+    const bool pen_late = pen && rep >= 1.0f;
+    const bool pen_early = pen && !pen_late;
+    auto mark = [&](int id) {
+        const uint32_t rel = (uint32_t)(id - seg_lo);
+        if (id >= 0 && id < V && rel < (uint32_t)SEG) atomicOr(&s.bmp[rel >> 5], 1u << (rel & 31u));
+    };
+    auto mark_window = [&]() {
+        // the ids arrive behind the logits: an empty asm keeps the compiler from hoisting their first use (and the
+        // wait for every load it needs) above the branch that calls this
+        int i0 = wid[0], i1 = wid[1];
+        asm volatile("" : "+v"(i0), "+v"(i1));
+        mark(i0);
+        mark(i1);
+        for (int64_t i = wb0 + 2 * SK_LT + tid; i < len; i += SK_LT) mark(a.hist[h0 + i]);
+    };
     if (pen) {
         for (int i = tid; i < SEG / 32; i += SK_LT) s.bmp[i] = 0u;
         __syncthreads();
-        auto mark = [&](int id) {
-            const uint32_t rel = (uint32_t)(id - seg_lo);
-            if (id >= 0 && id < a.V && rel < (uint32_t)SEG) atomicOr(&s.bmp[rel >> 5], 1u << (rel & 31u));
-        };
-        mark(wid[0]);
-        mark(wid[1]);
-        for (int64_t i = wb0 + 2 * SK_LT + tid; i < len; i += SK_LT) mark(a.hist[h0 + i]);
+    }
+    uint64_t pm = 0ull;                        // rep < 1: 4 bits per group of this thread
+    if (pen_early) {
+        mark_window();
         __syncthreads();
-        SK_MARK(1);
 #pragma unroll
         for (int q = 0; q < NL; ++q) {
             const uint32_t rel = (uint32_t)(q * SK_LT + tid) * 4u;
@@ -4394,20 +4446,15 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(SkArgs a) {
     }
     const bool wpen = __ballot(pm != 0ull) != 0ull;
     const bool tail = n_in < SEG;
-    // rep >= 1 never raises a logit (l > 0: l / rep <= l; l <= 0: l * rep <= l): penalised logits are then left out of
-    // the lane maxima (the bound counts unpenalised logits, which the penalty leaves as they are), a group is handed
-    // over when its raw maximum reaches the bound (a superset), and the penalty is applied to the few penalised logits
-    // of the handed-over groups only. rep < 1 penalises every flagged logit here.
-    const bool pen_late = rep >= 1.0f;
 
-    // the logits as ferro's sampler sees them (softcap, then the penalty; past the row's end: NaN, never a candidate),
-    // the group maxima and the lane maximum (NaN-free: fmaxf drops NaN; NaN when every logit of the lane is NaN)
+    // the logits as ferro's sampler sees them (softcap; rep < 1: the penalty; past the row's end: NaN, never a
+    // candidate) and the lane maximum (NaN-free: fmaxf drops NaN; NaN when every logit of the lane is NaN)
     float lm = __builtin_nanf("");
 #pragma unroll
     for (int q = 0; q < NL; ++q) {
         float e[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
         if (CAP && cap > 0.0f) softcap_vals(e, cap);       // a rolled loop: one copy of the cap per group
-        if (wpen && !pen_late) {
+        if (wpen) {
             const uint32_t nib = (uint32_t)(pm >> (4 * q)) & 0xFu;
             if (__ballot(nib != 0u)) {
 #pragma unroll
@@ -4422,25 +4469,18 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(SkArgs a) {
                 if (e0 + c >= n_in) e[c] = __builtin_nanf("");
         }
         v[q] = make_float4(e[0], e[1], e[2], e[3]);
-        float gu = fmaxf(fmaxf(e[0], e[1]), fmaxf(e[2], e[3]));   // the maximum of the group's unpenalised logits
-        if (wpen && pen_late) {
-            const uint32_t nib = (uint32_t)(pm >> (4 * q)) & 0xFu;
-            if (__ballot(nib != 0u)) {
-                const float nan = __builtin_nanf("");
-                gu = fmaxf(fmaxf((nib & 1u) ? nan : e[0], (nib & 2u) ? nan : e[1]),
-                           fmaxf((nib & 4u) ? nan : e[2], (nib & 8u) ? nan : e[3]));
-            }
-        }
-        lm = fmaxf(lm, gu);
+        lm = fmaxf(lm, fmaxf(fmaxf(e[0], e[1]), fmaxf(e[2], e[3])));
     }
     // the bound: each wave sorts its lane maxima in registers (no scalar round trips per step); lane kq - 1 holds its
-    // kq-th largest, and the smallest over the waves counts SK_NW kq >= k distinct logits
-    const uint32_t kq = (uint32_t)((k + SK_NW - 1) / SK_NW);
+    // kq-th largest, and the smallest over the waves counts SK_NW kq >= k distinct logits (one lane more per wave when
+    // the penalty comes later: the raw logits counted may be among the penalised ones)
+    const uint32_t kq = (uint32_t)((k + SK_NW - 1) / SK_NW) + (pen_late ? 1u : 0u);
     SK_MARK(11);
     {
         const uint32_t srt = sort64_desc_u32(key_of(lm));
         if (lane == (int)kq - 1) s.wb[w] = srt;
     }
+    if (pen_late) mark_window();                               // completed by the barrier below
     SK_MARK(12);
     __syncthreads();
     SK_MARK(2);
@@ -4467,9 +4507,8 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(SkArgs a) {
         if ((wmask >> q) & 1u) {
             const bool mine = ((gmask >> q) & 1u) != 0u && go < (uint32_t)SK_GCAP;
             const uint32_t slot = mine ? go : (uint32_t)SK_GCAP;
-            const uint32_t nib = pen_late ? (uint32_t)(pm >> (4 * q)) & 0xFu : 0u;   // still to be penalised
             s.gval[w][slot] = v[q];
-            s.gidx[w][slot] = (int32_t)(((uint32_t)(q * SK_LT + tid) * 4u) | (nib << 28));
+            s.gidx[w][slot] = (int32_t)((uint32_t)(q * SK_LT + tid) * 4u);
             go += (gmask >> q) & 1u;
         }
     }
@@ -4502,10 +4541,11 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(SkArgs a) {
         const uint32_t gi = (uint32_t)tid - gb;
         const float4 gv = s.gval[r][gi];
         const uint32_t gw = (uint32_t)s.gidx[r][gi];
-        const int e0 = (int)(gw & 0x0FFFFFFFu);
-        const uint32_t nib = gw >> 28;
+        const int e0 = (int)gw;
+        // rep >= 1: the group's penalised logits, from the bitmap (its 4 bits share a word: e0 % 4 == 0)
         float e[4] = {gv.x, gv.y, gv.z, gv.w};
-        if (nib != 0u) {
+        if (pen_late) {
+            const uint32_t nib = (s.bmp[(uint32_t)e0 >> 5] >> ((uint32_t)e0 & 31u)) & 0xFu;
 #pragma unroll
             for (int c = 0; c < 4; ++c)
                 if ((nib >> c) & 1u) e[c] = e[c] > 0.0f ? __fdiv_rn(e[c], rep) : __fmul_rn(e[c], rep);
@@ -4530,7 +4570,10 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(SkArgs a) {
         cbase += q < w ? t : 0u;
         ntot += t;
     }
-    const bool exact = gover || ntot > (uint32_t)SK_CAP;       // uniform
+    // With the penalty applied after the bound, fewer than k logits may stay at or above it: the segment's top k may
+    // then hold a logit below the bound, which was not handed over (never expected with the spare lane per wave)
+    const bool short_k = pen_late && ntot < (uint32_t)k && tf > -__builtin_huge_valf();
+    const bool exact = gover || short_k || ntot > (uint32_t)SK_CAP;   // uniform
     if (!exact) {
         uint32_t pos = cbase + cincl - nc;
 #pragma unroll
@@ -4985,17 +5028,27 @@ int launch_small(fs_context* ctx, const fs::Args& a, const fs_row_params* h_para
 #ifdef FS_TRACE
     if (ctx->trace && grid * fs::TRACE_W <= ctx->trace_cap) k.trace = ctx->trace;
 #endif
-    bool capped = false;
-    for (int64_t b = 0; b < (verify ? (int64_t)a.n_streams : (int64_t)a.B); ++b) capped |= h_params[b].softcap > 0.0f;
+    bool capped = false, may_pen = false;
+    for (int64_t b = 0; b < (verify ? (int64_t)a.n_streams : (int64_t)a.B); ++b) {
+        const fs_row_params& p = h_params[b];
+        capped |= p.softcap > 0.0f;
+        may_pen |= p.repetition_penalty != 1.0f && p.repeat_last_n != 0;
+    }
+    // a verification window reaches this kernel only without an active penalty (small_k_windows)
+    may_pen = may_pen && !verify && a.hist && a.hist_off;
     const dim3 gd((unsigned)grid), bd(fs::SK_LT);
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, gd, bd, fs::SK_PAD_LDS, st, a.logits, a.ld, a.B, a.V, nseg, may_pen ? 1 : 0, a.params,
+                           a.hist_off, a.hist, k);
+    };
     if (capped) {
-        if (nl == 16) hipLaunchKernelGGL((fs::small_k_kernel<16, true>), gd, bd, 0, st, k);
-        else if (nl == 8) hipLaunchKernelGGL((fs::small_k_kernel<8, true>), gd, bd, 0, st, k);
-        else hipLaunchKernelGGL((fs::small_k_kernel<4, true>), gd, bd, 0, st, k);
+        if (nl == 16) go(fs::small_k_kernel<16, true>);
+        else if (nl == 8) go(fs::small_k_kernel<8, true>);
+        else go(fs::small_k_kernel<4, true>);
     } else {
-        if (nl == 16) hipLaunchKernelGGL((fs::small_k_kernel<16, false>), gd, bd, 0, st, k);
-        else if (nl == 8) hipLaunchKernelGGL((fs::small_k_kernel<8, false>), gd, bd, 0, st, k);
-        else hipLaunchKernelGGL((fs::small_k_kernel<4, false>), gd, bd, 0, st, k);
+        if (nl == 16) go(fs::small_k_kernel<16, false>);
+        else if (nl == 8) go(fs::small_k_kernel<8, false>);
+        else go(fs::small_k_kernel<4, false>);
     }
     if (hipGetLastError() != hipSuccess) return FS_E_HIP;
     used = true;

@@ -267,6 +267,29 @@ def test_penalty_windows_and_out_of_range_ids():
     assert nb == 0
 
 
+def test_penalised_top_of_a_segment_below_the_bound():
+    """rep >= 1 on the small-k kernel: the segment's bound is taken over the raw logits and the penalty applied to the
+    handed-over ones. Here the window holds most of a segment's largest logits and a strong penalty drops them below
+    that bound, so fewer than k candidates stay at or above it: the segment must take its exact path. Also rep < 1
+    (penalised before the bound) and greedy rows."""
+    rng = np.random.default_rng(17)
+    V, B = 65536, 8
+    rows, hists = [], []
+    for b in range(B):
+        r = (rng.standard_normal(V) * 1.5).astype(np.float32)
+        hot = rng.choice(16384, 200, replace=False) + 16384 * (b % 4)     # 200 large logits in one segment
+        r[hot] = rng.uniform(10.0, 20.0, 200).astype(np.float32)
+        order = hot[np.argsort(-r[hot])]
+        rows.append(r)
+        hists.append(order[:150].astype(np.int32))                          # its 150 largest are penalised
+    p = W.make_params(B, temperature=1.0, top_k=64, top_p=1.0, repetition_penalty=3.0)
+    p["top_k"] = [64, 64, 40, 8, 4, 2, 64, 1]
+    p["repetition_penalty"][6] = 0.5                                        # rep < 1 raises the penalised logits
+    p["temperature"][7] = 0.0
+    g, o, nb = check(_case(rows, p, hists, rng.random(B), "penalised_top_of_a_segment"))
+    assert nb == 0
+
+
 def test_count_penalties_by_wave_and_by_table():
     """Frequency / presence counts (sampler.cpp:11-18 plus the extension) on 8-tile segments (B=64 x V=262144), where
     each segment buckets its window ids by tile and every wave counts its own logits, next to the per-tile table
