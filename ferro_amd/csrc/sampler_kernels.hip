@@ -1392,6 +1392,11 @@ __device__ __forceinline__ void large_row_exact(const Args& a, const RowCtx& rc,
     double part = 0.0;
     row_elems(a, rc, s, [&](float x, uint32_t, uint64_t c) { if (c >= Xk) part += mass_of(x, mx, Td); });
     const double S = block_sum_f64(part, s.red);
+    if (S != S) {                             // an infinite maximum: every mass NaN, nothing cut, the draw falls
+        tok_out = (int)comp_id(Xk);           // through to the last candidate (sampler.cpp:43-49)
+        keep_out = keff;
+        return;
+    }
     // 4. min-p: the smallest key whose pr reaches pr[0] * min_p (pr[0] = 1 / S)
     uint64_t Xkeep = Xk;
     if (p.min_p > 0.0f) {
@@ -1659,6 +1664,12 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
         }
     });
     const double S = block_sum_f64(part, s.red);          // its barriers also complete the histogram
+    if (S != S) {                                         // an infinite maximum: every mass NaN, nothing cut, the
+        lo.valid = true; lo.keff = keff; lo.Xk = Xk; lo.kmax = kmax; lo.S = S;   // draw falls through to the last
+        tok_out = (int)comp_id(Xk);                       // candidate (sampler.cpp:43-49)
+        keep_out = keff;
+        return;
+    }
     uint64_t mv[LPT];
 #pragma unroll
     for (int j = 0; j < LPT; ++j) mv[j] = hm[LB - 1 - (LPT * tid + j)];
@@ -1874,9 +1885,9 @@ __device__ __forceinline__ void wave_finish(const Args& a, const RowCtx& rc, con
     const double pr = e / sum;
     const double cum = wave_scan_f64(pr);                 // ferro's running c (sampler.cpp:44,47)
     int keep_m = k;
-    if (p.min_p > 0.0f) {                                 // keep = 1 + the last index with pr >= pr[0]*min_p
+    if (p.min_p > 0.0f) {                                 // keep = 1 + the last index not below pr[0]*min_p (NaN masses stay)
         const double thr = lane_f64(pr, 0) * (double)p.min_p;
-        const uint64_t mm = __ballot(lane < k && pr >= thr);
+        const uint64_t mm = __ballot(lane < k && !(pr < thr));
         keep_m = mm ? 64 - __clzll((long long)mm) : 1;
     }
     int keep = keep_m;
@@ -1955,9 +1966,9 @@ __device__ __forceinline__ void wave_softmax(const Args& a, const RowCtx& rc, ui
     const double pr = e / sum;
     const double cum = wave_scan_f64(pr);                 // ferro's running c (sampler.cpp:44,47)
     int keep_m = k;
-    if (p.min_p > 0.0f) {                                 // keep = 1 + the last index with pr >= pr[0]*min_p
+    if (p.min_p > 0.0f) {                                 // keep = 1 + the last index not below pr[0]*min_p (NaN masses stay)
         const double thr = lane_f64(pr, 0) * (double)p.min_p;
-        const uint64_t mm = __ballot(lane < k && pr >= thr);
+        const uint64_t mm = __ballot(lane < k && !(pr < thr));
         keep_m = mm ? 64 - __clzll((long long)mm) : 1;
     }
     int keep = keep_m;
@@ -2487,14 +2498,14 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             double pr[KPT];
     #pragma unroll
             for (int q = 0; q < KPT; ++q) pr[q] = e[q] / sum;
-            // min-p: keep = 1 + the last index with pr >= pr[0]*min_p (at least 1)
+            // min-p: keep = 1 + the last index not below pr[0]*min_p (NaN masses stay) (at least 1)
             int keep_m = k;
             if (p.min_p > 0.0f) {
                 const double thr = (1.0 / sum) * (double)p.min_p;
                 int last = -1;
     #pragma unroll
                 for (int q = 0; q < KPT; ++q)
-                    if (i0 + q < k && pr[q] >= thr) last = i0 + q;
+                    if (i0 + q < k && !(pr[q] < thr)) last = i0 + q;
                 last = block_max_i32(last, s.red);
                 keep_m = last + 1 > 1 ? last + 1 : 1;
             }
@@ -3421,6 +3432,16 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
         fx_bk = t_;
     }
     FS_MARK(3);                                          // past the second barrier: S and Xk known
+    if (S != S) {                                        // an infinite maximum: every mass NaN, nothing cut, the
+        if (seg == 0 && tid == 0) {                      // draw falls through to the last candidate (sampler.cpp:43-49)
+            my[LS_TOK] = (uint64_t)comp_id(Xk) | ((uint64_t)(uint32_t)keff << 32);
+            my[LS_XK] = Xk;
+            my[LS_S] = (uint64_t)__double_as_longlong(S);
+            my[LS_KEFF] = (uint64_t)keff | ((uint64_t)kmax << 32);
+            my[LS_STATUS] = 1ull;
+        }
+        return;
+    }
     const uint32_t kk = comp_key(Xk);
     uint64_t mv[LPT];                                    // the candidates' mass histogram, descending positions
 #pragma unroll

@@ -665,6 +665,36 @@ def test_greedy_infinities_and_nan_rows():
     assert list(tok) == want == [0, 0, 0, V - 3, 5000]
 
 
+def test_sampled_rows_with_an_infinite_maximum():
+    """A sampled row whose maximum is -inf or +inf: exp((l - mx) / T) is NaN for every logit (inf - inf), so ferro's
+    sums are NaN, min-p and top-p cut nothing (their comparisons are false) and the walk ends on the last kept
+    candidate (sampler.cpp:37-49). Every candidate path: small k, k <= 2048, large k and every token; with and
+    without min-p / top-p."""
+    V = 3 * 4096 + 77
+    rng = np.random.default_rng(23)
+    rows, B = [], 0
+    for kind in ("neg", "pos"):
+        for k in (5, 100, 3000, 0):
+            for mp, tp in ((0.0, 1.0), (0.1, 0.9)):
+                if kind == "neg":
+                    r = np.full(V, -np.inf, np.float32)
+                else:
+                    r = (rng.standard_normal(V)).astype(np.float32)
+                    r[[17, V - 9]] = np.inf
+                rows.append((r, k, mp, tp))
+    B = len(rows)
+    p = W.make_params(B, temperature=0.9, top_k=0, repetition_penalty=1.0)
+    for b, (_, k, mp, tp) in enumerate(rows):
+        p["top_k"][b], p["min_p"][b], p["top_p"][b] = k, mp, tp
+    w = _case([r for r, *_ in rows], p, [[]] * B, rng.random(B), "infinite_max")
+    g = run_gpu(w, 0)
+    o = run_oracle(w, 0)
+    assert F.device_error() == 0
+    bad = [(b, rows[b][1:], (int(g["tok"][b]), int(g["keep"][b])), (int(o["tok"][b]), int(o["keep"][b])))
+           for b in range(B) if (g["tok"][b], g["keep"][b]) != (o["tok"][b], o["keep"][b])]
+    assert not bad, bad
+
+
 def test_penalize_in_place_matches_oracle():
     """fs_penalize_batch leaves each row exactly as ferro's sample() leaves its host row (sampler.cpp:11-18), with
     the frequency/presence extension, per-row windows and scopes (cfg5 rows: V=262144, H=1024)."""
