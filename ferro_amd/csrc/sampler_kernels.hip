@@ -615,6 +615,9 @@ struct Shared {
     uint32_t tmax;                     // segment kernel: the largest key of tile 0
     uint32_t rc64[WAVE];               // segment kernel: tile-0 counts in the 64 coarse bins up to tmax's
     uint32_t nids;
+    uint32_t nfast;                    // large-row segment: the cut's survivors written to the slot
+    uint32_t wcnt[NWAVES];             // large-row segment: each wave's part of the cut's LDS list
+    uint32_t tmx[2][NWAVES];           // large-row segment: the waves' tile maxima (keys), alternating tiles
     uint32_t misc_alone;               // merge role: the row is computed from its logits alone
 #ifdef FS_TRACE
     uint64_t trace_t[16];              // this workgroup's phase timestamps (written to a.trace at its end)
@@ -1809,6 +1812,8 @@ constexpr int LSC = 5 * LLINE;                 // scalar lines at the head of a 
 constexpr int LLR = ((CAP - LSC) / 3) / LLINE * LLINE;   // capacity of each of its three gather regions
 enum LargeSlot : int {
     LS_MAX = 0, LS_MIN, LS_NV,                                   // P1: largest / smallest composite, ordered count
+    LS_FN, LS_FC, LS_FT,                                         // P1, every token a candidate: the cut's list count,
+                                                                 // its fp64 mass and the rest's (both relative to LS_MAX)
     LS_SHI = LLINE, LS_NBK,                                      // P2: fp64 mass of the candidates above bk; bin bk's count
     LS_NBC = 2 * LLINE, LS_CA, LS_CNTM, LS_SUMM, LS_CLM,         // P3: bin bc's count, candidates above bc, min-p's
     LS_NBD = 3 * LLINE,                                          // P4: bin bd's count
@@ -2103,12 +2108,14 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
     lo.valid = false;
     bool whole = rc.large || alone;                   // sampled as a whole row: by the segments together or here
     bool from_segs = false;
+    bool cut_done = false;                            // sampled by large_cut: the histograms were never touched
     if (rc.large && !alone && nseg > 0) {
         // the row's segments sampled it together (large_segment): segment 0's slot holds the result unless the row
         // was abandoned (then it is sampled here alone, exactly)
         const uint64_t* s0 = a.cand + slot_of(rc, 0) * CAP;
         const uint32_t sc = *reinterpret_cast<volatile const uint32_t*>(row_sync_ctr(a, row));   // not read before
-        if (!(sc & ROW_ABANDONED) && s0[LS_STATUS] == 1ull) {
+        if (!(sc & ROW_ABANDONED) && s0[LS_STATUS] != 0ull) {
+            cut_done = s0[LS_STATUS] == 2ull;
             const uint64_t tk = s0[LS_TOK];
             tok = (int)(uint32_t)tk;
             keep = (int)(tk >> 32);
@@ -2560,8 +2567,9 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
     }
     if (!rc.greedy && nseg > 0 && !alone) {           // the segments' row histogram is spent: leave it at 0
         uint4* rz = reinterpret_cast<uint4*>(a.rhist + (int64_t)row * RBINS);
-        for (int i = tid; i < RBINS / 4; i += BLOCK) rz[i] = make_uint4(0u, 0u, 0u, 0u);
-        if (rc.large) {                                // and a large row's mass histogram
+        for (int i = cut_done ? RBINS / 4 - 1 + tid : tid; i < RBINS / 4; i += BLOCK)   // (large_cut: the counters)
+            rz[i] = make_uint4(0u, 0u, 0u, 0u);
+        if (rc.large && !cut_done) {                   // and a large row's mass histogram
             uint4* mz = reinterpret_cast<uint4*>(a.rmass + (int64_t)row * LB);
             for (int i = tid; i < LB / 2; i += BLOCK) mz[i] = make_uint4(0u, 0u, 0u, 0u);
         }
@@ -3179,8 +3187,9 @@ __device__ __forceinline__ bool row_sync(const Args& a, int row, uint32_t target
 // tiles in flight, softcap and penalties applied: f(x, key, composite) per ordered element. Ends with a barrier.
 // bmp: a repetition penalty alone, from a bitmap of the window's ids over the segment (bit i = id lo0 + i; a
 // thread's four consecutive logits share a word), else the per-tile count table (s.ids holds the window's ids).
-template <class F>
-__device__ __forceinline__ void seg_elems(const Args& a, const RowCtx& rc, Shared& s, int lo0, int hi, bool bmp, F f) {
+// g(x): a per-tile hook, called on each tile's (softcapped, penalised) logits before f sees them.
+template <class F, class G>
+__device__ __forceinline__ void seg_elems_g(const Args& a, const RowCtx& rc, Shared& s, int lo0, int hi, bool bmp, F f, G g) {
     const float* rowp = a.logits + (int64_t)rc.row * a.ld;
     const int nt = (hi - lo0 + TILE - 1) / TILE;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(rowp + lo0), (short)0,
@@ -3218,6 +3227,7 @@ __device__ __forceinline__ void seg_elems(const Args& a, const RowCtx& rc, Share
                     __syncthreads();                     // the previous tile's table reads are done
                     apply_penalties(x, a, rc, lo, s);
                 }
+                g(x, lo);
 #pragma unroll
                 for (int i = 0; i < TPT; ++i) {
                     const int e = elem_id(lo, i);
@@ -3229,6 +3239,11 @@ __device__ __forceinline__ void seg_elems(const Args& a, const RowCtx& rc, Share
         }
     }
     __syncthreads();
+}
+
+template <class F>
+__device__ __forceinline__ void seg_elems(const Args& a, const RowCtx& rc, Shared& s, int lo0, int hi, bool bmp, F f) {
+    seg_elems_g(a, rc, s, lo0, hi, bmp, f, [](const float (&)[TPT], int) {});
 }
 
 // The gathered lists of one region of every segment of the row, concatenated into s.cand[0, n) and sorted in
@@ -3281,6 +3296,259 @@ __device__ __forceinline__ uint64_t sum_slots_u64(const Args& a, const RowCtx& r
     return tot;
 }
 
+// Rows where every token is a candidate (k >= V) sampled from the logits within CUT_C * T of the row's maximum,
+// when the rest provably holds neither top-p's crossing, min-p's boundary nor the draw: after the first row barrier
+// every segment decides the same way from the published scalars (same inputs, same order); segment 0 then gathers the
+// lists (at most KMAX logits), sorts them, and runs sampler.cpp:37-49 over them in double precision, the rest's mass
+// (every element below e^-CUT_C of the maximum) added to S. Returns true when the row is done (or given to the merge:
+// a target that still lands in the rest abandons the row to the exact path); false: the segments go on with the
+// passes of the general large-row path.
+constexpr float CUT_C = 16.0f;
+constexpr double CFXS = 1125899906842624.0;      // 2^50: fixed-point scale of the lists' masses (each <= 1, <= CAP)
+
+template <bool DESC>
+__device__ __forceinline__ uint64_t sort64(uint64_t v);
+
+// large_cut's finish when the lists hold at most 64 logits and the row has at most 64 segments: one wave, the
+// logits in lanes (sampler.cpp:28-49 as in the block version below, with wave scans in candidate order).
+// Returns false when a target lands in the rest (the caller abandons the row).
+__device__ __forceinline__ bool wave_cut_finish(const Args& a, const RowCtx& rc, uint64_t* my, float mx, float cut,
+                                                double Td, double st, uint32_t ntot, int keff, uint32_t kmax,
+                                                uint64_t cmin, double u, bool min_in, double e_c) {
+    const int lane = lane_id(), nseg = rc.nseg;
+    const fs_row_params& p = rc.p;
+    // the lists' offsets (lane j: list j), then lane f takes flat entry f
+    const uint32_t cnt = lane < nseg ? (uint32_t)a.cand[slot_of(rc, lane) * CAP + LS_FN] : 0u;
+    const uint32_t inc = wave_incl_scan_u32(cnt);
+    const uint32_t off = inc - cnt;
+    const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+    int j = 0;
+    for (int q = 1; q < nseg; ++q)
+        if ((uint32_t)lane >= (uint32_t)__builtin_amdgcn_readlane((int)off, q)) j = q;
+    const uint32_t my_off = (uint32_t)__builtin_amdgcn_ds_bpermute(j << 2, (int)off);
+    uint64_t c = 0ull;
+    if ((uint32_t)lane < tot) c = a.cand[slot_of(rc, j) * CAP + LSC + ((uint32_t)lane - my_off)];
+    const float x = val_of(comp_key(c));
+    const bool in = (uint32_t)lane < tot && x >= mx - cut;
+    const uint64_t dm = ((uint32_t)lane < tot && !in) ? (uint64_t)(mass_of(x, mx, Td) * CFXS + 0.5) : 0ull;
+    const uint64_t dfx = wave_allreduce(dm, [](uint64_t p_, uint64_t q_) { return p_ + q_; });
+    const uint64_t v = sort64<true>(in ? c : 0ull);      // ferro's order; lanes >= n hold 0
+    const int n = __popcll(__ballot(in));
+    const double rest = st + (double)dfx / CFXS;
+    double e = 0.0;
+    if (lane < n) e = mass_of(val_of(comp_key(v)), mx, Td);
+    const double S = lane_f64(wave_scan_f64(e), WAVE - 1) + rest;
+    const double pr = e / S;
+    const double cum = wave_scan_f64(pr);
+    int keep_m = n;
+    bool m_beyond = (uint32_t)n < ntot;
+    if (p.min_p > 0.0f) {
+        const double thr = (1.0 / S) * (double)p.min_p;
+        const uint64_t mm = __ballot(lane < n && !(pr < thr));
+        keep_m = mm ? 64 - __clzll((long long)mm) : 1;
+        m_beyond = keep_m == n && (uint32_t)n < ntot && !min_in;
+    }
+    int keep = keep_m;
+    bool beyond = m_beyond;
+    if (p.top_p < 1.0f) {
+        const uint64_t mm = __ballot(lane < keep_m && cum >= (double)p.top_p);
+        if (mm) {
+            const int first = __ffsll((unsigned long long)mm) - 1;
+            keep = first + 1 < keep_m ? first + 1 : keep_m;
+            beyond = false;
+        } else if (m_beyond) {
+            return false;                                // top-p's crossing lies in the rest
+        }
+    } else if (m_beyond && p.min_p > 0.0f) {
+        return false;                                    // min-p's boundary lies in the rest
+    }
+    const double totk = beyond ? lane_f64(cum, n - 1) + rest / S : lane_f64(cum, keep - 1);
+    const double rr = u * totk + 0.0;
+    const int lim = beyond ? n : keep;
+    const uint64_t hm = __ballot(lane < lim && rr <= cum);
+    int at;
+    if (hm) at = __ffsll((unsigned long long)hm) - 1;
+    else if (beyond) return false;                       // the draw lies in the rest
+    else at = keep - 1;
+    const uint64_t pick = read_lane(v, at);
+    if (lane == 0) {
+        const uint32_t kp = beyond ? ntot : (uint32_t)keep;
+        my[LS_TOK] = (uint64_t)comp_id(pick) | ((uint64_t)kp << 32);
+        my[LS_XK] = cmin;
+        my[LS_S] = (uint64_t)__double_as_longlong(S);
+        my[LS_KEFF] = (uint64_t)(uint32_t)keff | ((uint64_t)kmax << 32);
+        my[LS_STATUS] = 2ull;
+    }
+    (void)e_c;
+    return true;
+}
+
+__device__ __forceinline__ bool large_cut(const Args& a, const RowCtx& rc, Shared& s, int seg, uint64_t* my, float mx,
+                                          uint32_t kmax, uint64_t cmin, uint32_t ntot, int keff) {
+    const int tid = threadIdx.x, nseg = rc.nseg, row = rc.row;
+    const fs_row_params& p = rc.p;
+    if (!(mx > -__builtin_huge_valf() && mx < __builtin_huge_valf())) return false;   // uniform
+    const double Td = (double)p.temperature;
+    const float cut = CUT_C * p.temperature;
+    // row-wide: the lists' total, their masses and the rest's, relative to mx
+    uint32_t nf = 0u, ovf = 0u;
+    double sc = 0.0, st = 0.0;
+    for (int j = tid; j < nseg; j += BLOCK) {
+        const uint64_t* sl = a.cand + slot_of(rc, j) * CAP;
+        const uint64_t n = sl[LS_FN];
+        if (n > (uint64_t)LLR) ovf = 1u; else nf += (uint32_t)n;
+        if (sl[LS_NV] != 0ull) {
+            const double F = exp(((double)val_of(comp_key(sl[LS_MAX])) - (double)mx) / Td);
+            sc += F * __longlong_as_double((long long)sl[LS_FC]);
+            st += F * __longlong_as_double((long long)sl[LS_FT]);
+        }
+    }
+    uint32_t nft;
+    (void)block_excl_scan<uint32_t>(nf, s.wsum, &nft);
+    ovf = block_max_u32(ovf, s.red);
+    sc = block_sum_f64(sc, s.red);
+    st = block_sum_f64(st, s.red);
+    const double S_est = sc + st;
+    const double e_c = exp(-(double)CUT_C);
+    const double sc_lo = sc - (double)nft * e_c;          // the row's cut moves at most e^-CUT_C per listed logit
+    const double mrg = 1.0 + 1e-5;
+    const double u = a.u ? a.u[row] : 0.0;
+    const bool min_in = p.min_p > 0.0f && (double)p.min_p >= e_c * 1.01;   // min-p keeps only listed logits
+    bool within = min_in;
+    if (p.top_p < 1.0f) within = within || (double)p.top_p * S_est * mrg < sc_lo;
+    if (!(p.top_p < 1.0f) && !(p.min_p > 0.0f)) within = u * S_est * mrg < sc_lo;
+    if (!(ovf == 0u && nft >= 1u && nft <= (uint32_t)KMAX && within)) return false;   // uniform
+    if (seg != 0) return true;
+    FS_MARK(6);                                          // decided
+    if (nseg <= WAVE && nft <= (uint32_t)WAVE) {          // one wave
+        if (tid < WAVE && !wave_cut_finish(a, rc, my, mx, cut, Td, st, ntot, keff, kmax, cmin, u, min_in, e_c))
+            row_abandon(a, row);
+        FS_MARK(8);
+        return true;
+    }
+    // ---- segment 0: the lists above mx - cut, sorted (sampler.cpp:28-35)
+    uint32_t mine = 0u;
+    if (tid < nseg) mine = (uint32_t)a.cand[slot_of(rc, tid) * CAP + LS_FN];
+    uint32_t tot;
+    const uint32_t off = block_excl_scan<uint32_t>(mine, s.wsum, &tot);
+    if (tid < nseg) s.off[tid] = off;
+    if (tid == 0) { s.off[nseg] = tot; s.count = 0u; }
+    __syncthreads();
+    uint64_t drop = 0ull;                                // fixed point: the lists' order is not fixed
+    for (uint32_t b0 = 0u; b0 < tot; b0 += BLOCK) {
+        const uint32_t f = b0 + (uint32_t)tid;
+        uint64_t c = 0ull;
+        if (f < tot) {
+            int c0 = 0, c1 = nseg;
+            while (c1 - c0 > 1) {
+                const int m = (c0 + c1) >> 1;
+                if (s.off[m] <= f) c0 = m; else c1 = m;
+            }
+            c = a.cand[slot_of(rc, c0) * CAP + LSC + (f - s.off[c0])];
+        }
+        const float x = val_of(comp_key(c));
+        const bool in = f < tot && x >= mx - cut;
+        if (f < tot && !in) drop += (uint64_t)(mass_of(x, mx, Td) * CFXS + 0.5);
+        wave_append(in, c, s.cand, &s.count, (uint32_t)CAP);
+    }
+    uint64_t dfx;
+    (void)block_excl_scan<uint64_t>(drop, s.red.u64b, &dfx);   // its barriers also complete the appends
+    const int n = (int)s.count;
+    FS_MARK(7);                                          // lists gathered
+    __syncthreads();
+    bin_sort_desc(n, s);
+    FS_MARK(2);                                          // sorted
+    // ---- softmax over the list plus the rest's mass, min-p, top-p, draw (sampler.cpp:37-49)
+    const int i0 = tid * KPT;
+    double e[KPT];
+    double part = 0.0;
+#pragma unroll
+    for (int q = 0; q < KPT; ++q) {
+        e[q] = i0 + q < n ? mass_of(val_of(comp_key(s.cand[i0 + q])), mx, Td) : 0.0;
+        part += e[q];
+    }
+    const double rest = st + (double)dfx / CFXS;
+    const double S = block_sum_f64(part, s.red) + rest;
+    FS_MARK(3);                                          // S
+    double pr[KPT];
+#pragma unroll
+    for (int q = 0; q < KPT; ++q) pr[q] = e[q] / S;
+    int keep_m = n;
+    bool m_beyond = (uint32_t)n < ntot;                  // every listed logit kept so far and the rest after them
+    if (p.min_p > 0.0f) {
+        const double thr = (1.0 / S) * (double)p.min_p;
+        int last = -1;
+#pragma unroll
+        for (int q = 0; q < KPT; ++q)
+            if (i0 + q < n && !(pr[q] < thr)) last = i0 + q;
+        last = block_max_i32(last, s.red);
+        keep_m = last + 1 > 1 ? last + 1 : 1;
+        m_beyond = keep_m == n && (uint32_t)n < ntot && !min_in;
+    }
+    double c[KPT];
+    double run = 0.0;
+#pragma unroll
+    for (int q = 0; q < KPT; ++q) { run += pr[q]; c[q] = run; }
+    double tot_all;
+    const double coff = block_excl_scan<double>(run, s.red.f64, &tot_all);
+#pragma unroll
+    for (int q = 0; q < KPT; ++q) c[q] += coff;
+    int keep = keep_m;
+    bool beyond = m_beyond;
+    bool fail = false;
+    if (p.top_p < 1.0f) {
+        int first = 0x7fffffff;
+#pragma unroll
+        for (int q = 0; q < KPT; ++q)
+            if (i0 + q < keep_m && c[q] >= (double)p.top_p && first == 0x7fffffff) first = i0 + q;
+        first = block_min_i32(first, s.red);
+        if (first != 0x7fffffff) {
+            keep = first + 1 < keep_m ? first + 1 : keep_m;
+            beyond = false;
+        } else if (m_beyond) {
+            fail = true;                                 // top-p's crossing lies in the rest
+        }
+    } else if (m_beyond && p.min_p > 0.0f) {
+        fail = true;                                     // min-p's boundary lies in the rest
+    }
+    // tot = the kept prefix's sum; r = u * tot; the first i with r <= c_i
+    double totk = 0.0;
+    if (!beyond) {
+#pragma unroll
+        for (int q = 0; q < KPT; ++q)
+            if (i0 + q == keep - 1) s.red.dmisc[0] = c[q];
+        __syncthreads();
+        totk = s.red.dmisc[0];
+    } else {
+        totk = tot_all + rest / S;
+    }
+    const double rr = u * totk + 0.0;
+    const int lim = beyond ? n : keep;
+    int hit = 0x7fffffff;
+#pragma unroll
+    for (int q = 0; q < KPT; ++q)
+        if (i0 + q < lim && rr <= c[q] && hit == 0x7fffffff) hit = i0 + q;
+    hit = block_min_i32(hit, s.red);
+    if (hit == 0x7fffffff) {
+        if (beyond) fail = true;                         // the draw lies in the rest
+        else hit = keep - 1;
+    }
+    FS_MARK(8);                                          // walked
+    if (fail) {
+        row_abandon(a, row);
+        return true;
+    }
+    if (tid == 0) {
+        const uint32_t kp = beyond ? ntot : (uint32_t)keep;
+        my[LS_TOK] = (uint64_t)comp_id(s.cand[hit]) | ((uint64_t)kp << 32);
+        my[LS_XK] = cmin;
+        my[LS_S] = (uint64_t)__double_as_longlong(S);
+        my[LS_KEFF] = (uint64_t)(uint32_t)keff | ((uint64_t)kmax << 32);
+        my[LS_STATUS] = 2ull;
+    }
+    return true;
+}
+
 // This segment's part of a large row (see above).
 __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, int seg, Shared& s, const SegStart& g) {
     const int tid = threadIdx.x;
@@ -3315,19 +3583,135 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
     }
     uint64_t cmax = 0ull, cmin = ~0ull;
     uint32_t nv = 0u;
-    seg_elems(a, rc, s, lo0, hi, bmpen, [&](bool ok, float, uint32_t kq, uint64_t c) {
-        if (ok) {
-            cmax = c > cmax ? c : cmax;
-            cmin = c < cmin ? c : cmin;
-            ++nv;
-            if (need_kth) atomicAdd(&hc[kq >> LB_SHIFT], 1u);
-        }
-    });
+    // Every token a candidate (k >= V): the logits within cut = CUT_C * T of the workgroup's running maximum (over its
+    // tiles so far, the current one included) go to an LDS list; the others (masses below e^-CUT_C of the row's, since
+    // the running maximum never exceeds the row's) are summed in single precision relative to that maximum, rescaled
+    // when it rises. Both depend only on the data (a barrier per tile), so the sums are deterministic.
+    const bool fastc = !need_kth;
+    const float cut = CUT_C * p.temperature;
+    const float inv_tl2 = 1.4426950408889634f / p.temperature;   // log2(e) / T: the rest's masses as powers of 2
+    float ref = -__builtin_huge_valf();
+    float tacc = 0.0f;
+    constexpr uint32_t WREG = CAP / NWAVES;              // each wave's own part of the LDS list: no atomics
+    uint64_t* const wl = s.cand + (tid / WAVE) * WREG;
+    uint32_t wcnt = 0u;                                  // wave-uniform
+    // (fastc: the extremes tracked as floats with their first / last index, as the composite order ranks ties)
+    float bmax = -__builtin_huge_valf(), bmin = __builtin_huge_valf();
+    int bmax_id = -1, bmin_id = -1;
+    if (!fastc) {
+        seg_elems(a, rc, s, lo0, hi, bmpen, [&](bool ok, float, uint32_t kq, uint64_t c) {
+            if (ok) {
+                cmax = c > cmax ? c : cmax;
+                cmin = c < cmin ? c : cmin;
+                ++nv;
+                if (need_kth) atomicAdd(&hc[kq >> LB_SHIFT], 1u);
+            }
+        });
+    } else {
+        seg_elems_g(a, rc, s, lo0, hi, bmpen, [](bool, float, uint32_t, uint64_t) {}, [&](const float (&x)[TPT], int lo) {
+            const bool full = lo + TILE <= hi;
+            bool valid[TPT];
+            float tm = -__builtin_huge_valf();
+#pragma unroll
+            for (int i = 0; i < TPT; ++i) {
+                valid[i] = (full || elem_id(lo, i) < hi) && x[i] == x[i];
+                tm = valid[i] && x[i] > tm ? x[i] : tm;
+                nv += valid[i] ? 1u : 0u;
+                if (valid[i] && x[i] <= bmin) { bmin = x[i]; bmin_id = elem_id(lo, i); }
+                if (valid[i] && (x[i] > bmax || bmax_id < 0)) { bmax = x[i]; bmax_id = elem_id(lo, i); }
+            }
+            // the running maximum of the workgroup's tiles so far (this one included), behind a barrier
+            uint32_t mk = wave_max(key_of(tm));
+            uint32_t* tmw = s.tmx[((lo - lo0) / TILE) & 1];
+            if (lane_id() == 0) tmw[tid / WAVE] = mk;
+            __syncthreads();
+#pragma unroll
+            for (int w = 0; w < NWAVES; ++w) mk = tmw[w] > mk ? tmw[w] : mk;
+            const float nr = mk > key_of(-__builtin_huge_valf()) ? val_of(mk) : -__builtin_huge_valf();
+            if (nr > ref) {
+                if (tacc != 0.0f) tacc *= __builtin_amdgcn_exp2f((ref - nr) * inv_tl2);
+                ref = nr;
+            }
+            const float thr = ref - cut;
+            uint32_t cm = 0u;
+#pragma unroll
+            for (int i = 0; i < TPT; ++i) {
+                const bool cand = valid[i] && x[i] >= thr;
+                cm |= cand ? 1u << i : 0u;
+                const float t = __builtin_amdgcn_exp2f((x[i] - ref) * inv_tl2);
+                tacc += (valid[i] && !cand) ? t : 0.0f;
+            }
+            if (__ballot(cm != 0u) != 0ull) {
+#pragma unroll
+                for (int i = 0; i < TPT; ++i) {
+                    const bool cand = (cm >> i) & 1u;
+                    const uint64_t m = __ballot(cand);
+                    if (m != 0ull) {
+                        const uint32_t pos = wcnt + mbcnt(m);
+                        if (cand && pos < WREG) wl[pos] = comp_of(key_of(x[i]), (uint32_t)elem_id(lo, i));
+                        wcnt += (uint32_t)__popcll(m);
+                    }
+                }
+            }
+        });
+    }
+    if (fastc) {
+        cmax = bmax_id >= 0 ? comp_of(key_of(bmax), (uint32_t)bmax_id) : 0ull;
+        cmin = bmin_id >= 0 ? comp_of(key_of(bmin), (uint32_t)bmin_id) : ~0ull;
+    }
     FS_MARK(1);                                          // P1 streamed
+    if (fastc && lane_id() == 0) s.wcnt[tid / WAVE] = wcnt;
     cmax = block_max_u64(cmax, s.red);
     cmin = block_min_u64(cmin, s.red);
     uint32_t nseg_v;
     (void)block_excl_scan<uint32_t>(nv, s.wsum, &nseg_v);
+    if (fastc) {
+        // the list cut again at this segment's maximum; its survivors to gather region 0 of the slot, their exact
+        // masses and the rest's summed relative to that maximum
+        // (the list's order depends on the waves' timing: its masses are summed in fixed point, order-free)
+        uint32_t n0 = 0u, wofs[NWAVES];                   // (the reductions above end with barriers)
+        bool wovf = false;
+#pragma unroll
+        for (int w = 0; w < NWAVES; ++w) {
+            wofs[w] = n0;
+            wovf |= s.wcnt[w] > WREG;
+            n0 += s.wcnt[w];
+        }
+        const float smax = nseg_v > 0u ? val_of(comp_key(cmax)) : -__builtin_huge_valf();
+        const double Td = (double)p.temperature;
+        double tsum = 0.0;
+        if (tacc != 0.0f) tsum = (double)tacc * exp((double)(ref - smax) / Td);
+        uint64_t cfx = 0ull, tfx = 0ull;
+        if (tid == 0) s.nfast = 0u;
+        __syncthreads();
+        if (!wovf && smax > -__builtin_huge_valf() && smax < __builtin_huge_valf()) {
+            for (uint32_t b0 = 0u; b0 < n0; b0 += BLOCK) {
+                const uint32_t i = b0 + (uint32_t)tid;
+                int w = 0;
+#pragma unroll
+                for (int v = 1; v < NWAVES; ++v) w = i >= wofs[v] ? v : w;
+                const uint64_t c = i < n0 ? s.cand[w * WREG + (i - wofs[w])] : 0ull;
+                const float x = val_of(comp_key(c));
+                const bool keep = i < n0 && x >= smax - cut;
+                if (i < n0) {
+                    const uint64_t m = (uint64_t)(mass_of(x, smax, Td) * CFXS + 0.5);
+                    if (keep) cfx += m; else tfx += m;
+                }
+                wave_append(keep, c, my + LSC, &s.nfast, (uint32_t)LLR);
+            }
+        }
+        uint64_t t_;
+        (void)block_excl_scan<uint64_t>(cfx, s.red.u64b, &t_);
+        const double csum = (double)t_ / CFXS;
+        (void)block_excl_scan<uint64_t>(tfx, s.red.u64b, &t_);
+        tsum = block_sum_f64(tsum, s.red) + (double)t_ / CFXS;
+        if (tid == 0) {
+            const bool ok = !wovf && s.nfast <= (uint32_t)LLR;
+            my[LS_FN] = ok ? s.nfast : 0xFFFFFFFFull;
+            my[LS_FC] = (uint64_t)__double_as_longlong(csum);
+            my[LS_FT] = (uint64_t)__double_as_longlong(tsum);
+        }
+    }
     uint32_t* rh = a.rhist + (int64_t)row * RBINS;
     if (need_kth)
         for (int i = tid; i < LB; i += BLOCK)
@@ -3359,6 +3743,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
     const float mx = val_of(kmax);
     const double Td = (double)p.temperature;
     const int keff = (uint32_t)rc.k < ntot ? rc.k : (int)ntot;
+    if (fastc && large_cut(a, rc, s, seg, my, mx, kmax, cmin, ntot, keff)) return;
     uint32_t bk = 0xFFFFFFFFu, abk = 0u;                 // the k-th's coarse bin (none: every element a candidate)
     if ((uint32_t)keff < ntot) {
         uint32_t cv[LPT];
