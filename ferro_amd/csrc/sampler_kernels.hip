@@ -3314,11 +3314,10 @@ __device__ __forceinline__ uint64_t sort64(uint64_t v);
 // Returns false when a target lands in the rest (the caller abandons the row).
 __device__ __forceinline__ bool wave_cut_finish(const Args& a, const RowCtx& rc, uint64_t* my, float mx, float cut,
                                                 double Td, double st, uint32_t ntot, int keff, uint32_t kmax,
-                                                uint64_t cmin, double u, bool min_in, double e_c) {
+                                                uint64_t cmin, double u, bool min_in, uint32_t cnt) {
     const int lane = lane_id(), nseg = rc.nseg;
     const fs_row_params& p = rc.p;
-    // the lists' offsets (lane j: list j), then lane f takes flat entry f
-    const uint32_t cnt = lane < nseg ? (uint32_t)a.cand[slot_of(rc, lane) * CAP + LS_FN] : 0u;
+    // the lists' offsets (lane j: list j's count cnt), then lane f takes flat entry f
     const uint32_t inc = wave_incl_scan_u32(cnt);
     const uint32_t off = inc - cnt;
     const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
@@ -3379,53 +3378,33 @@ __device__ __forceinline__ bool wave_cut_finish(const Args& a, const RowCtx& rc,
         my[LS_KEFF] = (uint64_t)(uint32_t)keff | ((uint64_t)kmax << 32);
         my[LS_STATUS] = 2ull;
     }
-    (void)e_c;
     return true;
 }
 
-__device__ __forceinline__ bool large_cut(const Args& a, const RowCtx& rc, Shared& s, int seg, uint64_t* my, float mx,
-                                          uint32_t kmax, uint64_t cmin, uint32_t ntot, int keff) {
-    const int tid = threadIdx.x, nseg = rc.nseg, row = rc.row;
-    const fs_row_params& p = rc.p;
-    if (!(mx > -__builtin_huge_valf() && mx < __builtin_huge_valf())) return false;   // uniform
-    const double Td = (double)p.temperature;
-    const float cut = CUT_C * p.temperature;
-    // row-wide: the lists' total, their masses and the rest's, relative to mx
-    uint32_t nf = 0u, ovf = 0u;
-    double sc = 0.0, st = 0.0;
-    for (int j = tid; j < nseg; j += BLOCK) {
-        const uint64_t* sl = a.cand + slot_of(rc, j) * CAP;
-        const uint64_t n = sl[LS_FN];
-        if (n > (uint64_t)LLR) ovf = 1u; else nf += (uint32_t)n;
-        if (sl[LS_NV] != 0ull) {
-            const double F = exp(((double)val_of(comp_key(sl[LS_MAX])) - (double)mx) / Td);
-            sc += F * __longlong_as_double((long long)sl[LS_FC]);
-            st += F * __longlong_as_double((long long)sl[LS_FT]);
-        }
-    }
-    uint32_t nft;
-    (void)block_excl_scan<uint32_t>(nf, s.wsum, &nft);
-    ovf = block_max_u32(ovf, s.red);
-    sc = block_sum_f64(sc, s.red);
-    st = block_sum_f64(st, s.red);
+// The cut's decision from the row's published sums: sc / st the listed logits' / the rest's mass relative to the
+// row's maximum, nft the lists' total. True when the rest provably holds neither top-p's crossing, min-p's boundary
+// nor the draw (estimates within 1e-5; the exact walk still checks).
+__device__ __forceinline__ bool cut_decide(const fs_row_params& p, double sc, double st, uint64_t nft, bool ovf,
+                                           double u, bool& min_in) {
     const double S_est = sc + st;
     const double e_c = exp(-(double)CUT_C);
     const double sc_lo = sc - (double)nft * e_c;          // the row's cut moves at most e^-CUT_C per listed logit
     const double mrg = 1.0 + 1e-5;
-    const double u = a.u ? a.u[row] : 0.0;
-    const bool min_in = p.min_p > 0.0f && (double)p.min_p >= e_c * 1.01;   // min-p keeps only listed logits
+    min_in = p.min_p > 0.0f && (double)p.min_p >= e_c * 1.01;   // min-p keeps only listed logits
     bool within = min_in;
     if (p.top_p < 1.0f) within = within || (double)p.top_p * S_est * mrg < sc_lo;
     if (!(p.top_p < 1.0f) && !(p.min_p > 0.0f)) within = u * S_est * mrg < sc_lo;
-    if (!(ovf == 0u && nft >= 1u && nft <= (uint32_t)KMAX && within)) return false;   // uniform
-    if (seg != 0) return true;
-    FS_MARK(6);                                          // decided
-    if (nseg <= WAVE && nft <= (uint32_t)WAVE) {          // one wave
-        if (tid < WAVE && !wave_cut_finish(a, rc, my, mx, cut, Td, st, ntot, keff, kmax, cmin, u, min_in, e_c))
-            row_abandon(a, row);
-        FS_MARK(8);
-        return true;
-    }
+    return !ovf && nft >= 1u && nft <= (uint64_t)KMAX && within;
+}
+
+// large_cut's finish by the whole block (the lists hold more than 64 logits, or the row more than 64 segments).
+__device__ __forceinline__ void cut_finish_block(const Args& a, const RowCtx& rc, Shared& s, uint64_t* my, float mx,
+                                                 uint32_t kmax, uint64_t cmin, uint32_t ntot, int keff, double st,
+                                                 double u, bool min_in) {
+    const int tid = threadIdx.x, nseg = rc.nseg, row = rc.row;
+    const fs_row_params& p = rc.p;
+    const double Td = (double)p.temperature;
+    const float cut = CUT_C * p.temperature;
     // ---- segment 0: the lists above mx - cut, sorted (sampler.cpp:28-35)
     uint32_t mine = 0u;
     if (tid < nseg) mine = (uint32_t)a.cand[slot_of(rc, tid) * CAP + LS_FN];
@@ -3536,7 +3515,7 @@ __device__ __forceinline__ bool large_cut(const Args& a, const RowCtx& rc, Share
     FS_MARK(8);                                          // walked
     if (fail) {
         row_abandon(a, row);
-        return true;
+        return;
     }
     if (tid == 0) {
         const uint32_t kp = beyond ? ntot : (uint32_t)keep;
@@ -3546,6 +3525,37 @@ __device__ __forceinline__ bool large_cut(const Args& a, const RowCtx& rc, Share
         my[LS_KEFF] = (uint64_t)(uint32_t)keff | ((uint64_t)kmax << 32);
         my[LS_STATUS] = 2ull;
     }
+}
+
+__device__ __forceinline__ bool large_cut(const Args& a, const RowCtx& rc, Shared& s, int seg, uint64_t* my, float mx,
+                                          uint32_t kmax, uint64_t cmin, uint32_t ntot, int keff) {
+    const int tid = threadIdx.x, nseg = rc.nseg, row = rc.row;
+    const fs_row_params& p = rc.p;
+    if (!(mx > -__builtin_huge_valf() && mx < __builtin_huge_valf())) return false;   // uniform
+    const double Td = (double)p.temperature;
+    // row-wide: the lists' total, their masses and the rest's, relative to mx
+    uint32_t nf = 0u, ovf = 0u;
+    double sc = 0.0, st = 0.0;
+    for (int j = tid; j < nseg; j += BLOCK) {
+        const uint64_t* sl = a.cand + slot_of(rc, j) * CAP;
+        const uint64_t n = sl[LS_FN];
+        if (n > (uint64_t)LLR) ovf = 1u; else nf += (uint32_t)n;
+        if (sl[LS_NV] != 0ull) {
+            const double F = exp(((double)val_of(comp_key(sl[LS_MAX])) - (double)mx) / Td);
+            sc += F * __longlong_as_double((long long)sl[LS_FC]);
+            st += F * __longlong_as_double((long long)sl[LS_FT]);
+        }
+    }
+    uint32_t nft;
+    (void)block_excl_scan<uint32_t>(nf, s.wsum, &nft);
+    ovf = block_max_u32(ovf, s.red);
+    sc = block_sum_f64(sc, s.red);
+    st = block_sum_f64(st, s.red);
+    const double u = a.u ? a.u[row] : 0.0;
+    bool min_in;
+    if (!cut_decide(p, sc, st, nft, ovf != 0u, u, min_in)) return false;   // uniform
+    if (seg != 0) return true;
+    cut_finish_block(a, rc, s, my, mx, kmax, cmin, ntot, keff, st, u, min_in);
     return true;
 }
 
@@ -3719,8 +3729,61 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
     if (tid == 0) { my[LS_MAX] = cmax; my[LS_MIN] = cmin; my[LS_NV] = nseg_v; }
     if (!row_sync(a, row, (uint32_t)nseg, s)) return;
     FS_MARK(5);                                          // past the first barrier
+    if (fastc && nseg <= WAVE) {
+        // wave 0 reads every segment's published line once: the row's extremes and count, and the cut's decision
+        // (large_cut below, in wave reductions); segment 0's wave 0 then samples a short list at once
+        if (tid < WAVE) {
+            const int lane = tid;
+            uint64_t smx = 0ull, smn = ~0ull, snv = 0ull, sfn = 0ull;
+            double sfc = 0.0, sft = 0.0;
+            if (lane < nseg) {
+                const uint64_t* sl = a.cand + slot_of(rc, lane) * CAP;
+                smx = sl[LS_MAX]; smn = sl[LS_MIN]; snv = sl[LS_NV]; sfn = sl[LS_FN];
+                sfc = __longlong_as_double((long long)sl[LS_FC]);
+                sft = __longlong_as_double((long long)sl[LS_FT]);
+            }
+            auto add_u = [](uint64_t x_, uint64_t y_) { return x_ + y_; };
+            auto add_d = [](double x_, double y_) { return x_ + y_; };
+            const uint64_t rmx = wave_max(smx), rmn = wave_min(smn), rnv = wave_allreduce(snv, add_u);
+            const float mxf = val_of(comp_key(rmx));
+            const bool fin = rnv != 0ull && mxf > -__builtin_huge_valf() && mxf < __builtin_huge_valf();
+            const double Td = (double)p.temperature;
+            const double F = fin && lane < nseg && snv != 0ull
+                                 ? exp(((double)val_of(comp_key(smx)) - (double)mxf) / Td) : 0.0;
+            const double sc = wave_allreduce(F * sfc, add_d), st = wave_allreduce(F * sft, add_d);
+            const bool ovf = wave_max(sfn > (uint64_t)LLR ? 1u : 0u) != 0u;
+            const uint64_t nft = wave_allreduce(sfn > (uint64_t)LLR ? 0ull : sfn, add_u);
+            const double u = a.u ? a.u[row] : 0.0;
+            bool min_in = false;
+            const bool fast = fin && cut_decide(p, sc, st, nft, ovf, u, min_in);
+            bool done = false;
+            if (fast && seg == 0 && nft <= (uint64_t)WAVE) {
+                FS_MARK(6);
+                if (!wave_cut_finish(a, rc, my, mxf, CUT_C * p.temperature, Td, st, (uint32_t)rnv, (int)rnv,
+                                     comp_key(rmx), rmn, u, min_in, (uint32_t)sfn))
+                    row_abandon(a, row);
+                FS_MARK(8);
+                done = true;
+            }
+            if (lane == 0) {
+                s.red.u64[0] = rmx; s.red.u64b[0] = rmn; s.red.misc[0] = (uint32_t)rnv;
+                s.red.misc[1] = (fast ? 1u : 0u) | (done ? 2u : 0u) | (min_in ? 4u : 0u);
+                s.red.dmisc[0] = st; s.red.dmisc[1] = u;
+            }
+        }
+        __syncthreads();
+        cmax = s.red.u64[0]; cmin = s.red.u64b[0]; nv = s.red.misc[0];
+        const uint32_t fl = s.red.misc[1];
+        const double st = s.red.dmisc[0], u = s.red.dmisc[1];
+        __syncthreads();                                 // Red is reused below
+        if (fl & 1u) {
+            if (seg == 0 && !(fl & 2u))
+                cut_finish_block(a, rc, s, my, val_of(comp_key(cmax)), comp_key(cmax), cmin, nv, (int)nv, st, u,
+                                 (fl & 4u) != 0u);
+            return;
+        }
+    } else {
     // row-wide: extremes, count; the k-th's coarse bin from the row histogram
-    {
         uint64_t mx_ = 0ull, mn_ = ~0ull, nv_ = 0ull;
         for (int j = tid; j < nseg; j += BLOCK) {
             const uint64_t* sl = a.cand + slot_of(rc, j) * CAP;
@@ -3743,7 +3806,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
     const float mx = val_of(kmax);
     const double Td = (double)p.temperature;
     const int keff = (uint32_t)rc.k < ntot ? rc.k : (int)ntot;
-    if (fastc && large_cut(a, rc, s, seg, my, mx, kmax, cmin, ntot, keff)) return;
+    if (fastc && nseg > WAVE && large_cut(a, rc, s, seg, my, mx, kmax, cmin, ntot, keff)) return;
     uint32_t bk = 0xFFFFFFFFu, abk = 0u;                 // the k-th's coarse bin (none: every element a candidate)
     if ((uint32_t)keff < ntot) {
         uint32_t cv[LPT];
