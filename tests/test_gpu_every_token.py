@@ -176,3 +176,59 @@ def test_randomized(seed):
     p["repetition_penalty"] = np.where(rng.random(B) < 0.5, 1.0, rng.uniform(0.8, 1.5, B))
     p["repeat_last_n"] = rng.choice([-1, 0, 16, 128], B)
     check(_case(rows, p, hists, rng.random(B), f"random_{seed}"))
+
+
+def _spiky(rng, V, B):
+    """Rows whose mass sits in a few spikes far above a N(0, 1.5) body: the case sampled from the logits within 16 T
+    of the maximum (the rest summed), with targets inside the short list."""
+    rows = []
+    for b in range(B):
+        r = (rng.standard_normal(V) * 1.5).astype(np.float32)
+        n = int(rng.integers(1, 40))
+        r[rng.choice(V, n, replace=False)] = rng.uniform(12, 40, n).astype(np.float32)
+        if b % 5 == 0:
+            r[rng.choice(V, 3, replace=False)] = r.max()      # ties at the maximum
+        rows.append(r)
+    return rows
+
+
+@pytest.mark.parametrize("V", [262144, 100003])
+def test_short_list_rows(V):
+    rng = np.random.default_rng(V + 1)
+    B = 24
+    rows = _spiky(rng, V, B)
+    p = W.make_params(B, temperature=1.0, top_k=0, repetition_penalty=1.0)
+    p["temperature"] = rng.choice([0.3, 0.8, 1.0, 2.0], B)
+    p["top_p"] = rng.choice([1.0, 0.95, 0.5, 0.99, 0.0], B)
+    p["min_p"] = rng.choice([0.0, 0.0, 0.05, 1e-9, 0.5], B)      # 1e-9: min-p's boundary below the list
+    p["top_k"][::7] = V + 3
+    us = rng.random(B)
+    us[::6] = 1.0 - 2 ** -53
+    us[1::6] = 0.0
+    hists = [np.argsort(-rows[b])[:3].astype(np.int32) if b % 3 == 0 else [] for b in range(B)]
+    p["repetition_penalty"][::3] = 1.3                         # the top tokens penalised
+    check(_case(rows, p, hists, us, f"short_list_{V}"))
+
+
+def test_short_list_outputs_and_repeat():
+    """Candidate outputs (kcap = 64) of short-list rows against the oracle (ids exact, probabilities to 1e-5
+    relative), and a second call bit-identical (the short list's sums do not depend on the waves' timing)."""
+    from parity_util import compare
+    rng = np.random.default_rng(77)
+    V, B, kcap = 262144, 12, 64
+    rows = _spiky(rng, V, B)
+    p = W.make_params(B, temperature=0.8, top_k=0, top_p=0.95, repetition_penalty=1.0)
+    p["top_p"][::4] = 1.0
+    p["min_p"][1::4] = 0.02
+    w = _case(rows, p, [[]] * B, rng.random(B), "short_list_outputs")
+    x = torch.from_numpy(w.logits).cuda()
+    outs = []
+    for _ in range(2):
+        o = F.sample_batch(x, w.params, w.u, kcap=kcap)
+        torch.cuda.synchronize()
+        outs.append({k: v.cpu().numpy() for k, v in o.items() if v is not None and not k.startswith("_")})
+    assert F.device_error() == 0
+    ora = O.sample_batch(w.logits, w.hist, w.hist_off, w.params, w.u, kcap=kcap, nthreads=NT)
+    compare(outs[0], ora, w.params, w.u, kcap)
+    for k in ("tok", "keep", "cand_ids", "cand_probs"):
+        assert np.array_equal(outs[0][k], outs[1][k]), k
