@@ -102,7 +102,49 @@ struct Args {
     int32_t* dirty;                // nonzero: a merge gave up waiting; the row histograms and counters may be stale
     uint32_t merge_spins;          // bounded wait of the merge role (polls); 0: give up without waiting
     uint64_t* trace;               // FS_TRACE builds: per-workgroup phase timestamps (NULL: none)
+    // one-launch decode step (fs_decode_step): the draws come from device streams (row r = stream r) instead of u,
+    // and each row's token is appended to its stream's history, out of place
+    uint64_t* dmt;                 // [B][312] mt19937_64 states (NULL: draws from u)
+    int32_t* didx;                 // [B] their next indices
+    int32_t* out_hist;             // the histories with the tokens appended (NULL: no append)
+    int64_t* out_hist_off;         // [B + 1]
+    int64_t out_cap;               // ids out_hist holds
 };
+
+constexpr int MT_N = 312, MT_M = 156;
+constexpr uint64_t MT_A = 0xB5026F5AA96619E9ull, MT_UPPER = 0xFFFFFFFF80000000ull, MT_LOWER = 0x7FFFFFFFull;
+
+__device__ __forceinline__ uint64_t mt_temper(uint64_t y) {
+    y ^= (y >> 29) & 0x5555555555555555ull;
+    y ^= (y << 17) & 0x71D67FFFEDA60000ull;
+    y ^= (y << 37) & 0xFFF7EEE000000000ull;
+    y ^= y >> 43;
+    return y;
+}
+__device__ __forceinline__ uint64_t mt_twist_one(uint64_t cur, uint64_t next, uint64_t far) {
+    const uint64_t x = (cur & MT_UPPER) | (next & MT_LOWER);
+    return far ^ (x >> 1) ^ ((x & 1ull) ? MT_A : 0ull);
+}
+__device__ void mt_twist(uint64_t* mt) {
+    for (int k = 0; k < MT_N; ++k) mt[k] = mt_twist_one(mt[k], mt[(k + 1) % MT_N], mt[(k + MT_M) % MT_N]);
+}
+__device__ __forceinline__ double mt_canonical(uint64_t x) {
+    const double r = __ull2double_rn(x) * 0x1p-64;
+    return r < 1.0 ? r : 0x1.fffffffffffffp-1;
+}
+__device__ __forceinline__ bool samples(const fs_row_params& p) { return p.temperature > 0.0f && p.top_k != 1; }
+
+// The draw of row `row` (sampler.cpp:45-46): u from the caller, or, in a decode step, the next value of the row's
+// device stream, read without advancing it (the row's merge commits it after every reader is done).
+__device__ __forceinline__ double row_u(const Args& a, int row) {
+    if (a.dmt) {
+        const uint64_t* mt = a.dmt + (int64_t)row * MT_N;
+        const int idx = a.didx[row];
+        const uint64_t y = idx < MT_N ? mt[idx] : mt_twist_one(mt[0], mt[1], mt[MT_M]);
+        return mt_canonical(mt_temper(y));
+    }
+    return a.u ? a.u[row] : 0.0;
+}
 
 // Phase timestamps (FS_TRACE builds only; the product library compiles these to nothing): thread 0 of a workgroup
 // keeps the constant 100 MHz clock (s_memrealtime) of phase i in LDS (no memory store, so no wait on the memory
@@ -1439,7 +1481,7 @@ __device__ __forceinline__ void large_row_exact(const Args& a, const RowCtx& rc,
     (void)block_excl_scan<uint32_t>(kc, s.wsum, &keep);
     clast = block_min_u64(clast, s.red);
     // 6. the draw r = u * tot (sampler.cpp:45-49), in mass units
-    const double u = a.u ? a.u[row] : 0.0;
+    const double u = row_u(a, row);
     uint64_t pick = large_mass_select(a, rc, s, u * tot + 0.0, Xkeep, comp_key(Xkeep), kmax, mx, Td);
     if (pick == 0ull) pick = clast;
     tok_out = (int)comp_id(pick);
@@ -1772,7 +1814,7 @@ __device__ __forceinline__ void large_row(const Args& a, const RowCtx& rc, Share
         clast = Xc;
     }
     // 5. the draw r = u * tot (sampler.cpp:45-49), in mass units
-    const double u = a.u ? a.u[row] : 0.0;
+    const double u = row_u(a, row);
     const double r = u * tot + 0.0;
     uint64_t abd = 0ull;
     int dd = desc_locate<uint64_t>(mv, (uint64_t)(r * FXS), &abd, s.red.u64b, s);
@@ -1940,7 +1982,7 @@ __device__ __forceinline__ void prefetch_lists(const Args& a, const RowCtx& rc, 
     pre.act = nseg > 0 && pre.r_me < pre.tps;
     const int64_t slot = slot_of(rc, pre.c_me);
     const uint64_t* lst = a.cand + slot * CAP;
-    pre.u = a.u ? ld_const(a.u + row) : 0.0;
+    pre.u = row_u(a, row);
     pre.l0 = ld_const(a.logits + (int64_t)row * a.ld);
     pre.t0m = 0u;
     pre.cnm = 0u;
@@ -2090,6 +2132,58 @@ __device__ __forceinline__ bool merge_fast(const Args& a, const RowCtx& rc, Shar
     FS_MARK(3);
     if (tid < WAVE) wave_softmax(a, rc, tid < k ? sorted[tid] : 0ull, k, pre.u, tok, keep);
     return true;
+}
+
+// ------------------------------------------------------------------------------------------------ decode step
+// fs_decode_step's two additions to a row's merge (server.cpp:603-606, then gen_token's hist.push_back,
+// server.cpp:342): its stream's history copied to the new histories (while the merge waits for its segments) and
+// the token appended after it; and the row's draw committed (its stream advanced) once every reader is done.
+// Stream s = row s; the new histories start at 0 and each stream gains one id (fs_hist_append's layout).
+__device__ __forceinline__ void decode_hist_copy(const Args& a, int row) {
+    if (!a.out_hist_off) return;
+    const int64_t h0 = a.hist_off ? a.hist_off[0] : 0, b = a.hist_off ? a.hist_off[row] : 0;
+    const int64_t e = a.hist_off ? a.hist_off[row + 1] : 0;
+    const int64_t nb = b - h0 + row;
+    for (int64_t i = threadIdx.x; i < e - b; i += BLOCK)
+        if (nb + i < a.out_cap) a.out_hist[nb + i] = a.hist[b + i];
+    if (threadIdx.x == 0) {
+        a.out_hist_off[row] = nb;
+        if (row == a.B - 1) a.out_hist_off[a.B] = e - h0 + a.B;
+        if (nb + (e - b) + 1 > a.out_cap) atomicOr(a.err, FS_DEVERR_HIST_APPEND);
+    }
+}
+__device__ __forceinline__ void decode_commit(const Args& a, const RowCtx& rc, Shared& s, int tok) {
+    const int row = rc.row, t = threadIdx.x;
+    if (a.out_hist_off && t == 0) {
+        const int64_t h0 = a.hist_off ? a.hist_off[0] : 0, b = a.hist_off ? a.hist_off[row] : 0;
+        const int64_t e = a.hist_off ? a.hist_off[row + 1] : 0;
+        const int64_t at = b - h0 + row + (e - b);
+        if (at < a.out_cap) a.out_hist[at] = tok;
+    }
+    if (!a.dmt || !samples(rc.p)) return;                // uniform; greedy rows draw nothing (sampler.cpp:19-23)
+    uint64_t* mt = a.dmt + (int64_t)row * MT_N;
+    const int idx = a.didx[row];
+    if (idx < MT_N) {
+        if (t == 0) a.didx[row] = idx + 1;
+        return;
+    }
+    // the state's twist (the draw was its first value), in LDS: entries k < N - M need old values only, the others
+    // the new ones below N - M and their own old neighbour (entry N - 1: the new entry 0)
+    uint64_t* w = s.cand;
+    __syncthreads();
+    if (t < MT_N) w[t] = mt[t];
+    __syncthreads();
+    uint64_t nv = 0ull;
+    if (t < MT_N - MT_M) nv = mt_twist_one(w[t], w[t + 1], w[t + MT_M]);
+    __syncthreads();
+    if (t < MT_N - MT_M) w[t] = nv;
+    __syncthreads();
+    if (t >= MT_N - MT_M && t < MT_N) nv = mt_twist_one(w[t], w[(t + 1) % MT_N], w[t - (MT_N - MT_M)]);
+    __syncthreads();
+    if (t >= MT_N - MT_M && t < MT_N) w[t] = nv;
+    __syncthreads();
+    if (t < MT_N) mt[t] = w[t];
+    if (t == 0) a.didx[row] = 1;
 }
 
 __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Shared& s, const Pre& pre, bool alone = false) {
@@ -2574,6 +2668,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             for (int i = tid; i < LB / 2; i += BLOCK) mz[i] = make_uint4(0u, 0u, 0u, 0u);
         }
     }
+    if (a.out_hist_off || a.dmt) decode_commit(a, rc, s, tok);   // uniform (a decode step)
     if (a.mode != MODE_VERIFY) {
         if (tid == 0) {
             a.tok[row] = tok;
@@ -3551,7 +3646,7 @@ __device__ __forceinline__ bool large_cut(const Args& a, const RowCtx& rc, Share
     ovf = block_max_u32(ovf, s.red);
     sc = block_sum_f64(sc, s.red);
     st = block_sum_f64(st, s.red);
-    const double u = a.u ? a.u[row] : 0.0;
+    const double u = row_u(a, row);
     bool min_in;
     if (!cut_decide(p, sc, st, nft, ovf != 0u, u, min_in)) return false;   // uniform
     if (seg != 0) return true;
@@ -3753,7 +3848,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
             const double sc = wave_allreduce(F * sfc, add_d), st = wave_allreduce(F * sft, add_d);
             const bool ovf = wave_max(sfn > (uint64_t)LLR ? 1u : 0u) != 0u;
             const uint64_t nft = wave_allreduce(sfn > (uint64_t)LLR ? 0ull : sfn, add_u);
-            const double u = a.u ? a.u[row] : 0.0;
+            const double u = row_u(a, row);
             bool min_in = false;
             const bool fast = fin && cut_decide(p, sc, st, nft, ovf, u, min_in);
             bool done = false;
@@ -3942,7 +4037,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
                                              ? ((bc << LB_SHIFT) | ((1u << LB_SHIFT) - 1u)) : kmax;
                 const double mhi = mass_of(val_of(top_key), mx, Td);
                 const double thi = tgt + mhi < S ? tgt + mhi : S;
-                const double u0 = a.u ? a.u[rc.row] : 0.0;
+                const double u0 = row_u(a, rc.row);
                 uint64_t ab_;
                 const int d0 = desc_locate<uint64_t>(mv, (uint64_t)(u0 * tgt * (1.0 - 1e-12) * FXS), &ab_, s.red.u64b, s);
                 const int d1 = desc_locate<uint64_t>(mv, (uint64_t)(u0 * thi * (1.0 + 1e-12) * FXS), &ab_, s.red.u64b, s);
@@ -4022,7 +4117,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
         clast = Xc;
     }
     // ---- P4: the draw r = u * tot (sampler.cpp:45-49) in its coarse bin
-    const double u = a.u ? a.u[rc.row] : 0.0;
+    const double u = row_u(a, rc.row);
     const double r = u * tot + 0.0;
     if (!(r > 0.0)) {                                    // r = 0: ferro's first candidate (r <= pr[0], sampler.cpp:48)
         if (seg == 0 && tid == 0) {
@@ -4180,6 +4275,7 @@ __device__ __forceinline__ void merge_role(const Args& a, int mi, Shared& s) {
     FS_TAG(13, 2); FS_TAG(14, row); FS_TAG(15, 0);
     RowCtx rc = row_ctx(a, row);                     // the row's inputs are read while the segments run
     row_layout(a, rc);
+    decode_hist_copy(a, row);                        // a decode step: while the segments run
     uint32_t* ctr = row_counter(a, row);
     if (threadIdx.x == 0) {
         // A context left dirty by an earlier give-up: its row histograms and counters may hold a late segment's
@@ -4302,6 +4398,7 @@ __global__ __launch_bounds__(BLOCK) void merge_kernel(int nseg, uint64_t* cand, 
     Pre pre = {};
     const RowCtx rc = row_ctx(a, row);
     if (!alone) prefetch_lists(a, rc, pre);
+    decode_hist_copy(a, row);
     merge_row(a, rc, s, pre, alone != 0);
 }
 
@@ -4477,28 +4574,6 @@ __global__ __launch_bounds__(LD_BLOCK) void lookup_draft_kernel(const int32_t* h
 // u = 29 / d = 0x5555555555555555, s = 17 / b = 0x71D67FFFEDA60000, t = 37 / c = 0xFFF7EEE000000000, l = 43) per
 // stream, and libstdc++'s generate_canonical<double, 53> of one 64-bit output: (double)x / 2^64, kept below 1.
 // This is ferro::Sampler's draw (sampler.h:25,32; sampler.cpp:45-46) moved next to the sampler.
-constexpr int MT_N = 312, MT_M = 156;
-constexpr uint64_t MT_A = 0xB5026F5AA96619E9ull, MT_UPPER = 0xFFFFFFFF80000000ull, MT_LOWER = 0x7FFFFFFFull;
-
-__device__ __forceinline__ uint64_t mt_temper(uint64_t y) {
-    y ^= (y >> 29) & 0x5555555555555555ull;
-    y ^= (y << 17) & 0x71D67FFFEDA60000ull;
-    y ^= (y << 37) & 0xFFF7EEE000000000ull;
-    y ^= y >> 43;
-    return y;
-}
-__device__ __forceinline__ uint64_t mt_twist_one(uint64_t cur, uint64_t next, uint64_t far) {
-    const uint64_t x = (cur & MT_UPPER) | (next & MT_LOWER);
-    return far ^ (x >> 1) ^ ((x & 1ull) ? MT_A : 0ull);
-}
-__device__ void mt_twist(uint64_t* mt) {
-    for (int k = 0; k < MT_N; ++k) mt[k] = mt_twist_one(mt[k], mt[(k + 1) % MT_N], mt[(k + MT_M) % MT_N]);
-}
-__device__ __forceinline__ double mt_canonical(uint64_t x) {
-    const double r = __ull2double_rn(x) * 0x1p-64;
-    return r < 1.0 ? r : 0x1.fffffffffffffp-1;
-}
-__device__ __forceinline__ bool samples(const fs_row_params& p) { return p.temperature > 0.0f && p.top_k != 1; }
 
 // One thread per stream. Stream s owns rows row_off[s] .. row_off[s+1]-1 (row_off NULL: row s alone); each row
 // whose stream samples takes one draw, in row order; greedy streams take none and get u = 0. peek != 0 leaves the
@@ -5975,6 +6050,28 @@ struct fs_drng {
     int32_t* idx = nullptr;     // [n]
     int32_t* err = nullptr;
 };
+
+// fs_decode_step: fs_sample_batch with the draws taken from the device streams r (row s = stream s) and each row's
+// token appended to its stream's history out of place, in the sampling grid itself (one launch).
+int fs_decode_step(fs_context* ctx, fs_drng* r, const float* d_logits, int64_t ld, int32_t B, int32_t V,
+                   const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params, int32_t* d_tok,
+                   int32_t* d_keep, int32_t* d_out_hist, int64_t* d_out_hist_off, int64_t out_cap, void* stream) {
+    if (!ctx || !r || !d_params || !d_tok || !d_out_hist_off || out_cap < 0 || (out_cap > 0 && !d_out_hist) ||
+        (d_hist == nullptr) != (d_hist_off == nullptr) || B > r->n)
+        return FS_E_INVALID;
+    int rc = check_rows(d_logits, ld, B, V);
+    if (rc != FS_OK) return rc;
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return FS_E_HIP;
+    if (dev != r->device) return FS_E_INVALID;
+    if (B == 0) return FS_OK;
+    fs::Args a = {};
+    a.logits = d_logits; a.ld = ld; a.B = B; a.V = V; a.hist = d_hist; a.hist_off = d_hist_off; a.params = d_params;
+    a.u = nullptr; a.tok = d_tok; a.kcap = 0; a.keep = d_keep;
+    a.mode = fs::MODE_SAMPLE; a.eos = -1;
+    a.dmt = r->mt; a.didx = r->idx; a.out_hist = d_out_hist; a.out_hist_off = d_out_hist_off; a.out_cap = out_cap;
+    return launch(ctx, a, B, 0, (hipStream_t)stream);
+}
 
 int fs_drng_create(int32_t n_streams, const uint64_t* seeds, void* stream, fs_drng** out) {
     if (!out || n_streams < 1 || !seeds) return FS_E_INVALID;

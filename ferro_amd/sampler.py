@@ -394,6 +394,34 @@ def hist_append(hist, hist_off, tok, row_off=None, count=None, out_cap=None, ctx
     return out, out_off
 
 
+def decode_step(logits, params, rng, hist=None, hist_off=None, out_cap=None, V=None, ctx=None, stream=None):
+    """fs_decode_step: one decode step in one launch - each row's draw from its DeviceRng stream (row s = stream s),
+    fs_sample_batch's token, and the token appended to the stream's history (server.cpp:603-606, then :342).
+    Returns (tok, keep, out_hist, out_off); out_hist holds out_cap ids (default: room for one more per stream), of
+    which out_off[-1] are used. Stays on the device."""
+    logits, ld, n = _check_logits(logits, V)
+    B = logits.shape[0]
+    dev = logits.device
+    p = _dev_params(params, dev)
+    if p.numel() != B * PARAMS_DTYPE.itemsize:
+        raise SamplerError("one params record per row")
+    if B > rng.n:
+        raise SamplerError(f"{B} rows for {rng.n} draw streams")
+    hist, hist_off = _hist_tensors(hist, hist_off, B, dev)
+    if out_cap is None:
+        out_cap = (hist.numel() if hist is not None else 0) + B
+    tok = torch.empty(B, dtype=torch.int32, device=dev)
+    keep = torch.empty(B, dtype=torch.int32, device=dev)
+    out = torch.empty(max(int(out_cap), 1), dtype=torch.int32, device=dev)
+    out_off = torch.empty(B + 1, dtype=torch.int64, device=dev)
+    ctx = ctx or Context.default(dev)
+    with ctx.lock:
+        check(lib().fs_decode_step(ctx.h, rng.h, _lptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p),
+                                   _ptr(tok), _ptr(keep), _ptr(out), _ptr(out_off), int(out_cap), _stream(stream)),
+              "fs_decode_step")
+    return tok, keep, out, out_off
+
+
 def device_error(ctx=None, stream=None) -> int:
     ctx = ctx or Context.default()
     bits = ctypes.c_int32(0)

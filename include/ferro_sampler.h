@@ -196,6 +196,19 @@ int fs_drng_skip(fs_drng* r, const int32_t* d_counts, const fs_row_params* d_par
 /* Waits for `stream`, then returns and clears the stream set's error bits. */
 int fs_drng_error(fs_drng* r, void* stream, int32_t* bits);
 
+/* One decode step in one launch: the loop body of server.cpp:603-606 (each stream's draw and sample()) followed by
+ * gen_token's hist.push_back (server.cpp:342), for B streams with one row each (row s = stream s of r, B <= its
+ * stream count). Equivalent to fs_drng_draw (d_row_off NULL) + fs_sample_batch (kcap 0) + fs_hist_append (one
+ * token per stream) on the same arguments, in the sampling grid: each row's merge copies its stream's history to
+ * the new histories while its segments run, reads its draw from the stream without advancing it, and after the
+ * row is sampled appends the token and advances the stream (greedy rows draw nothing). d_out_hist / d_out_hist_off
+ * are laid out as fs_hist_append's (offsets rebased to 0, out_cap ids; overflow sets FS_DEVERR_HIST_APPEND, read
+ * with fs_device_error) and must not alias the inputs. d_keep may be NULL. No counterpart call in the reference: it
+ * fuses three of its steps for a device-resident decode loop. */
+int fs_decode_step(fs_context* ctx, fs_drng* r, const float* d_logits, int64_t ld, int32_t B, int32_t V,
+                   const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params, int32_t* d_tok,
+                   int32_t* d_keep, int32_t* d_out_hist, int64_t* d_out_hist_off, int64_t out_cap, void* stream);
+
 /* The penalty stage alone, in place: row b of d_logits is left exactly as ferro's sample() leaves its host row
  * (sampler.cpp:11-18: each distinct window id in [0, V) once, l > 0 ? l/rep : l*rep, then the frequency/presence
  * extension). For callers that read the penalised row back (lm_cli.cpp:353); fs_sample_batch does not need it (it
