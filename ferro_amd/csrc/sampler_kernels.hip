@@ -3654,6 +3654,113 @@ __device__ __forceinline__ bool large_cut(const Args& a, const RowCtx& rc, Share
     return true;
 }
 
+// A crowded coarse bin (more candidates than the gather regions hold, e.g. the middle of a flat row): the element
+// at which the cumulative mass in ferro's order, from the row's top, reaches `target` inside bin b, through one
+// level of finer bins (the next FSB key bits). above_b is the mass of the candidates above bin b. All segments run
+// it together (uniform arguments, row barriers from nsync on):
+//   1. the row's fine histogram is cleared (rmass: fixed-point masses, rhist: counts; neither is read any more)
+//   2. each segment streams its tiles: masses and counts of its candidates in bin b by fine bin, added to the row's
+//   3. every segment locates the fine bin of the target (the same sums, the same decision) and gathers it
+//   4. the gathered lists, sorted, are walked in exact fp64 masses (large_walk)
+// Returns false (the row is then abandoned) when the fine bin still overflows or the walk leaves it; otherwise the
+// element, the cumulative mass through it and the number of candidates in bin b before it.
+constexpr int FSB = 11;                                    // fine bins: 2048 (row histogram bins below its counters)
+constexpr int FBN = 1 << FSB;
+constexpr int FSH = LB_SHIFT - FSB;
+static_assert(FBN <= RBINS - 2 && FBN <= LB && FSH >= 0, "fine bins fit the row histograms");
+__device__ __forceinline__ bool refine_bin(const Args& a, const RowCtx& rc, Shared& s, int seg_i, uint64_t* my, int lo0, int hi,
+                                        bool bmpen, uint32_t b, uint64_t Xlo, double above_b, double target, float mx,
+                                        double Td, uint32_t& nsync, uint64_t& pick, double& cum, uint32_t& before) {
+    const int tid = threadIdx.x, row = rc.row, nseg = rc.nseg;
+    uint64_t* rm = a.rmass + (int64_t)row * LB;
+    uint32_t* rh = a.rhist + (int64_t)row * RBINS;
+    // 1. clear this segment's slice of the row's fine histogram
+    const int per = (FBN + nseg - 1) / nseg;
+    for (int i = seg_i * per + tid; i < (seg_i + 1) * per && i < FBN; i += BLOCK) { rm[i] = 0ull; rh[i] = 0u; }
+    ++nsync;
+    if (!row_sync(a, row, nsync * (uint32_t)nseg, s)) return false;
+    // 2. this segment's candidates in bin b, by fine bin (LDS: masses in s.cand[0, FBN), counts after them)
+    uint64_t* fm = s.cand;
+    uint32_t* fc = reinterpret_cast<uint32_t*>(s.cand + FBN);
+    for (int i = tid; i < FBN; i += BLOCK) { fm[i] = 0ull; fc[i] = 0u; }
+    __syncthreads();
+    seg_elems(a, rc, s, lo0, hi, bmpen, [&](bool ok, float x, uint32_t kq, uint64_t c) {
+        if (ok && c >= Xlo && (kq >> LB_SHIFT) == b) {
+            const uint32_t f = (kq >> FSH) & (uint32_t)(FBN - 1);
+            atomicAdd(reinterpret_cast<unsigned long long*>(&fm[f]), (unsigned long long)(mass_of(x, mx, Td) * FXS + 0.5));
+            atomicAdd(&fc[f], 1u);
+        }
+    });
+    for (int i = tid; i < FBN; i += BLOCK) {
+        if (fm[i] != 0ull) __hip_atomic_fetch_add(rm + i, fm[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (fc[i] != 0u) __hip_atomic_fetch_add(rh + i, fc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    ++nsync;
+    if (!row_sync(a, row, nsync * (uint32_t)nseg, s)) return false;
+    l1_invalidate();                                     // lines this call read before may be stale in the L1
+    // 3. the fine bin holding the target (thread t: fine bins FBN-1-t*FPT .. descending), then its candidates
+    constexpr int FPT = FBN / BLOCK;
+    uint64_t v[LPT] = {};
+    uint32_t cnt_v[FPT];
+#pragma unroll
+    for (int j = 0; j < FPT; ++j) {
+        const int f = FBN - 1 - (FPT * tid + j);
+        v[j] = __hip_atomic_load(rm + f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        cnt_v[j] = __hip_atomic_load(rh + f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    const double rest = target - above_b;
+    uint64_t abf = 0ull;
+    const uint64_t tfx = rest > 0.0 ? (uint64_t)(rest * FXS) : 0ull;
+    // desc_locate over the FBN fine bins (LPT slots per thread, the first FPT used)
+    int d;
+    {
+        uint64_t sum = 0ull;
+#pragma unroll
+        for (int j = 0; j < FPT; ++j) sum += v[j];
+        uint64_t tot;
+        uint64_t run = block_excl_scan<uint64_t>(sum, s.red.u64b, &tot);
+        int hit = 0x7fffffff;
+        uint64_t ab = 0ull;
+#pragma unroll
+        for (int j = 0; j < FPT; ++j) {
+            if (hit == 0x7fffffff && v[j] != 0ull && run + v[j] >= tfx) { hit = FPT * tid + j; ab = run; }
+            run += v[j];
+        }
+        d = block_min_i32(hit, s.red);
+        if (d == 0x7fffffff) d = -1;
+        if (d >= 0 && hit == d) s.red.u64b[0] = ab;
+        __syncthreads();
+        abf = d >= 0 ? s.red.u64b[0] : 0ull;
+        __syncthreads();
+    }
+    if (d < 0) return false;                             // uniform
+    const uint32_t fb = (uint32_t)(FBN - 1 - d);
+    uint32_t cab = 0u;                                   // candidates in the fine bins above fb
+#pragma unroll
+    for (int j = 0; j < FPT; ++j) cab += (FPT * tid + j) < d ? cnt_v[j] : 0u;
+    uint32_t cabt;
+    (void)block_excl_scan<uint32_t>(cab, s.wsum, &cabt);
+    if (tid == 0) s.count = 0u;
+    __syncthreads();
+    uint64_t* regC = my + LSC + 2 * LLR;
+    seg_elems(a, rc, s, lo0, hi, bmpen, [&](bool ok, float, uint32_t kq, uint64_t c) {
+        const bool in = ok && c >= Xlo && (kq >> LB_SHIFT) == b && ((kq >> FSH) & (uint32_t)(FBN - 1)) == fb;
+        wave_append(in, c, regC, &s.count, (uint32_t)LLR);
+    });
+    if (tid == 0) my[LS_NBD] = s.count;
+    ++nsync;
+    if (!row_sync(a, row, nsync * (uint32_t)nseg, s)) return false;
+    l1_invalidate();                                     // lines this call read before may be stale in the L1
+    // 4. the walk inside the fine bin
+    const int n = load_lists(a, rc, 2, LS_NBD, s);
+    if (n < 0) return false;
+    const int ic = large_walk(s, n, Xlo, above_b + (double)abf / FXS, target, mx, Td, &cum);
+    if (ic < 0) return false;
+    pick = s.cand[ic];
+    before = cabt + (uint32_t)ic;
+    return true;
+}
+
 // This segment's part of a large row (see above).
 __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, int seg, Shared& s, const SegStart& g) {
     const int tid = threadIdx.x;
@@ -4019,6 +4126,7 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
     int nc = -1;
     uint32_t bc = 0xFFFFFFFFu;
     uint32_t bd_pred = 0xFFFFFFFFu;                      // the draw's bin, when P3 can gather it too
+    bool refined_c = false;                              // top-p's crossing bin was refined (gather region 2 in use)
     uint32_t nsync = 2u;
     if (p.top_p < 1.0f || need_m) {
         const double tgt = (double)p.top_p * S;
@@ -4092,13 +4200,29 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
         }
         if (p.top_p < 1.0f) {
             nc = load_lists(a, rc, 1, LS_NBC, s);
-            if (nc < 0) { row_abandon(a, row); return; }
-            double cum = 0.0;
-            const int ic = large_walk(s, nc, Xk, above_c, tgt, mx, Td, &cum);
-            if (ic < 0) { row_abandon(a, row); return; }   // outside the bin's exact masses: the exact path
-            Xc = s.cand[ic];
-            keep_c = ca_c + (uint32_t)ic + 1u;
-            tot_c = cum;
+            if (nc < 0) {
+                // a crowded crossing bin: one level of finer bins (its gather region is spent, and the draw's
+                // pre-gathered bin is overwritten)
+                uint64_t pk = 0ull;
+                double cm = 0.0;
+                uint32_t bf = 0u;
+                if (!refine_bin(a, rc, s, seg, my, lo0, hi, bmpen, bc, Xk, above_c, tgt, mx, Td, nsync, pk, cm, bf)) {
+                    row_abandon(a, row);
+                    return;
+                }
+                Xc = pk;
+                keep_c = ca_c + bf + 1u;
+                tot_c = cm;
+                bd_pred = 0xFFFFFFFFu;
+                refined_c = true;
+            } else {
+                double cum = 0.0;
+                const int ic = large_walk(s, nc, Xk, above_c, tgt, mx, Td, &cum);
+                if (ic < 0) { row_abandon(a, row); return; }   // outside the bin's exact masses: the exact path
+                Xc = s.cand[ic];
+                keep_c = ca_c + (uint32_t)ic + 1u;
+                tot_c = cum;
+            }
         }
     }
     // the kept prefix: the largest of the three thresholds (sampler.cpp:43-44)
@@ -4138,29 +4262,43 @@ __device__ __forceinline__ void large_segment(const Args& a, const RowCtx& rc, i
         nd = nc;                                         // the same bin is sorted in LDS already
     } else if (bd == bd_pred) {
         nd = load_lists(a, rc, 2, LS_NBD, s);           // gathered by P3
-        if (nd < 0) { row_abandon(a, row); return; }
     } else {
+        // after a refinement of top-p's bin the other segments may still read gather region 2: region 1 instead
+        // (its lists were never read), read through an invalidated L1 (its counts were)
+        const int rg = refined_c ? 1 : 2;
+        const int rs = refined_c ? LS_NBC : LS_NBD;
         if (tid == 0) s.count = 0u;
         __syncthreads();
-        uint64_t* regC = my + LSC + 2 * LLR;
+        uint64_t* regC = my + LSC + rg * LLR;
         seg_elems(a, rc, s, lo0, hi, bmpen, [&](bool ok, float, uint32_t kq, uint64_t c) {
             wave_append(ok && c >= Xkeep && (kq >> LB_SHIFT) == bd, c, regC, &s.count, (uint32_t)LLR);
         });
-        if (tid == 0) my[LS_NBD] = s.count;
+        if (tid == 0) my[rs] = s.count;
         FS_MARK(10);                                     // P4 streamed
-        if (!row_sync(a, row, (nsync + 1u) * (uint32_t)nseg, s)) return;
+        ++nsync;
+        if (!row_sync(a, row, nsync * (uint32_t)nseg, s)) return;
         FS_MARK(11);                                     // past the last barrier
-        nd = load_lists(a, rc, 2, LS_NBD, s);
-        if (nd < 0) { row_abandon(a, row); return; }
+        if (refined_c) l1_invalidate();
+        nd = load_lists(a, rc, rg, rs, s);
     }
-    double cum = 0.0;
-    const int id = large_walk(s, nd, Xkeep, (double)abd / FXS, r, mx, Td, &cum);
     uint64_t pick = 0ull;
-    if (id >= 0) {
-        pick = s.cand[id];
-    } else if (!(id == -2 && comp_key(Xkeep) >> LB_SHIFT == bd)) {
-        row_abandon(a, row);                             // a rounding step at the bin edge: the exact path
-        return;
+    if (nd < 0) {                                        // a crowded draw bin: one level of finer bins
+        double cm = 0.0;
+        uint32_t bf = 0u;
+        if (!refine_bin(a, rc, s, seg, my, lo0, hi, bmpen, bd, Xkeep, (double)abd / FXS, r, mx, Td, nsync, pick, cm,
+                        bf)) {
+            row_abandon(a, row);
+            return;
+        }
+    } else {
+        double cum = 0.0;
+        const int id = large_walk(s, nd, Xkeep, (double)abd / FXS, r, mx, Td, &cum);
+        if (id >= 0) {
+            pick = s.cand[id];
+        } else if (!(id == -2 && comp_key(Xkeep) >> LB_SHIFT == bd)) {
+            row_abandon(a, row);                         // a rounding step at the bin edge: the exact path
+            return;
+        }
     }
     if (pick == 0ull) pick = clast;                      // past the last kept candidate
     if (seg == 0 && tid == 0) {

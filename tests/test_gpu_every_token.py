@@ -232,3 +232,22 @@ def test_short_list_outputs_and_repeat():
     compare(outs[0], ora, w.params, w.u, kcap)
     for k in ("tok", "keep", "cand_ids", "cand_probs"):
         assert np.array_equal(outs[0][k], outs[1][k]), k
+
+
+@pytest.mark.parametrize("T", [1.0, 2.5])
+def test_flat_rows_crowded_bins(T):
+    """Flat rows (N(0, 1), or N(0, 2) at T 2.5): top-p's crossing and the draw fall in coarse bins holding thousands
+    of logits, which the segments narrow with one level of finer bins before the exact walk. Also 2048 < k < V."""
+    rng = np.random.default_rng(int(T * 10))
+    V, B = 262144, 10
+    rows = [(rng.standard_normal(V) * (1.0 if T < 2 else 2.0)).astype(np.float32) for _ in range(B)]
+    p = W.make_params(B, temperature=T, top_k=0, repetition_penalty=1.0)
+    p["top_p"] = [0.95, 0.5, 1.0, 0.9, 0.99, 0.7, 0.95, 0.8, 1.0, 0.6]
+    p["min_p"] = [0.0, 0.0, 0.0, 0.05, 0.0, 0.3, 0.0, 0.0, 0.01, 0.0]
+    p["top_k"][6] = 50000
+    p["top_k"][7] = 3000
+    hists = [rng.integers(0, V, 200).astype(np.int32) if b % 4 == 0 else [] for b in range(B)]
+    p["repetition_penalty"][::4] = 1.2
+    us = rng.random(B)
+    us[0] = 1.0 - 2 ** -53
+    check(_case(rows, p, hists, us, f"flat_T{T}"))
