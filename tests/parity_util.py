@@ -15,6 +15,15 @@ BOUNDARY = O.BOUNDARY
 boundary_row = O.near_boundary
 
 
+def bf16_valued(x):
+    """fp32 logits rounded to bfloat16 (round to nearest even) and widened back: what a model that emits bf16 logits
+    hands the sampler. A V=262144 row then holds only a few thousand distinct values, so equal logits meet at every
+    top-k boundary and top-p crossing (ties go to the lowest id)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
 class Parity(int):
     """Rows of a comparison whose draw lies near a cumulative boundary (the int value), with .diverged: the rows
     among them whose token or kept count actually differs from the oracle's."""

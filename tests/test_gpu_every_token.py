@@ -15,7 +15,7 @@ sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 from ferro_amd import workloads as W  # noqa: E402
 import ferro_amd as F  # noqa: E402
 from oracle import oracle as O  # noqa: E402
-from parity_util import boundary_row  # noqa: E402
+from parity_util import bf16_valued, boundary_row  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 NT = min(16, os.cpu_count() or 1)
@@ -73,6 +73,13 @@ def check(w, max_near=None):
 
 def test_cfg3_rows_every_token():
     check(W.config3_all_tokens())
+
+
+def test_bf16_valued_rows_every_token():
+    w = W.config3_all_tokens()
+    w.logits = bf16_valued(w.logits)
+    w.name += "_bf16"
+    check(w)
 
 
 @pytest.mark.parametrize("V", [1, 7, 4096, 16384, 16385, 100003])

@@ -18,7 +18,7 @@ torch = pytest.importorskip("torch")
 from oracle import oracle as O  # noqa: E402
 from ferro_amd import workloads as W  # noqa: E402
 import ferro_amd as F  # noqa: E402
-from parity_util import boundary_row, compare, oracle_decode_loop  # noqa: E402
+from parity_util import bf16_valued, boundary_row, compare, oracle_decode_loop  # noqa: E402
 
 NT = min(16, os.cpu_count() or 1)
 
@@ -142,6 +142,15 @@ def test_verify_sampled_with_penalties():
 def test_cfg5_heterogeneous_full():
     g, o, nb = check(W.config5())
     say(f"cfg5 boundary rows: {nb}")
+    assert nb <= 3
+
+
+@pytest.mark.parametrize("which", ["cfg3", "cfg5"])
+def test_bf16_valued_rows(which):
+    w = W.config3() if which == "cfg3" else W.config5(B=96)
+    w.logits = bf16_valued(w.logits)
+    w.name += "_bf16"
+    g, o, nb = check(w)
     assert nb <= 3
 
 

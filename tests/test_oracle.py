@@ -16,7 +16,7 @@ import pytest
 
 from oracle import oracle as O
 from ferro_amd import workloads as W
-from parity_util import oracle_decode_loop
+from parity_util import bf16_valued, oracle_decode_loop
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "sampler_golden.npz")
 
@@ -341,3 +341,16 @@ def test_nan_policy_numbers_only():
         e = np.array([np.exp(np.float64(np.float32(x[i] - mx)) / np.float64(np.float32(0.7))) for i in order[:kk]])
         np.testing.assert_allclose(probs, e / e.sum(), rtol=1e-13)
         assert x[tok] == x[tok]                        # a number is drawn
+
+
+def test_bf16_valued_matches_torch_rounding():
+    """The bf16-valued test rows (round to nearest even) agree with torch's float32 -> bfloat16 conversion, ties and
+    specials included."""
+    import torch
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal(1 << 16) * 3).astype(np.float32)
+    bits = x.view(np.uint32)
+    bits[:256] = (bits[:256] & 0xFFFF0000) | 0x8000         # exactly halfway: ties to even
+    x[256:260] = [np.inf, -np.inf, 0.0, -0.0]
+    want = torch.from_numpy(x.copy()).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(bf16_valued(x).view(np.uint32), want.view(np.uint32))
