@@ -2584,7 +2584,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             const double Td = (double)p.temperature;
             double e[KPT];
             double part = 0.0;
-    #pragma unroll
+#pragma unroll
             for (int q = 0; q < KPT; ++q) {
                 const int i = i0 + q;
                 e[q] = 0.0;
@@ -2597,14 +2597,14 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             const double sum = block_sum_f64(part, s.red);
             FS_MARK(8);                                 // exp and their sum
             double pr[KPT];
-    #pragma unroll
+#pragma unroll
             for (int q = 0; q < KPT; ++q) pr[q] = e[q] / sum;
             // min-p: keep = 1 + the last index not below pr[0]*min_p (NaN masses stay) (at least 1)
             int keep_m = k;
             if (p.min_p > 0.0f) {
                 const double thr = (1.0 / sum) * (double)p.min_p;
                 int last = -1;
-    #pragma unroll
+#pragma unroll
                 for (int q = 0; q < KPT; ++q)
                     if (i0 + q < k && !(pr[q] < thr)) last = i0 + q;
                 last = block_max_i32(last, s.red);
@@ -2613,16 +2613,16 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             // inclusive prefix of pr in candidate order
             double c[KPT];
             double run = 0.0;
-    #pragma unroll
+#pragma unroll
             for (int q = 0; q < KPT; ++q) { run += pr[q]; c[q] = run; }
             double tot_all;
             const double off = block_excl_scan<double>(run, s.red.f64, &tot_all);
-    #pragma unroll
+#pragma unroll
             for (int q = 0; q < KPT; ++q) c[q] += off;
             keep = keep_m;
             if (p.top_p < 1.0f) {
                 int first = 0x7fffffff;
-    #pragma unroll
+#pragma unroll
                 for (int q = 0; q < KPT; ++q)
                     if (i0 + q < keep_m && c[q] >= (double)p.top_p && first == 0x7fffffff) first = i0 + q;
                 first = block_min_i32(first, s.red);
@@ -2630,7 +2630,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 if (keep < 1) keep = 1;
             }
             // tot = sum of the kept prefix; r = u * tot; the first i with r <= c_i
-    #pragma unroll
+#pragma unroll
             for (int q = 0; q < KPT; ++q)
                 if (i0 + q == keep - 1) s.red.dmisc[0] = c[q];
             __syncthreads();
@@ -2638,7 +2638,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             const double u = pre.u;
             const double rr = u * tot + 0.0;
             int hit = 0x7fffffff;
-    #pragma unroll
+#pragma unroll
             for (int q = 0; q < KPT; ++q)
                 if (i0 + q < keep && rr <= c[q] && hit == 0x7fffffff) hit = i0 + q;
             hit = block_min_i32(hit, s.red);
@@ -2649,7 +2649,7 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
                 if (a.cand_ids)
                     for (int i = tid; i < m; i += BLOCK) a.cand_ids[(int64_t)row * a.kcap + i] = (int32_t)comp_id(top[i]);
                 if (a.cand_probs) {
-    #pragma unroll
+#pragma unroll
                     for (int q = 0; q < KPT; ++q)
                         if (i0 + q < m) a.cand_probs[(int64_t)row * a.kcap + i0 + q] = pr[q];
                 }
@@ -5153,187 +5153,215 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
         v[q] = make_float4(e[0], e[1], e[2], e[3]);
         lm = fmaxf(lm, fmaxf(fmaxf(e[0], e[1]), fmaxf(e[2], e[3])));
     }
-    // the bound: each wave sorts its lane maxima in registers (no scalar round trips per step); lane kq - 1 holds its
-    // kq-th largest, and the smallest over the waves counts SK_NW kq >= k distinct logits (one lane more per wave when
-    // the penalty comes later: the raw logits counted may be among the penalised ones)
-    const uint32_t kq = (uint32_t)((k + SK_NW - 1) / SK_NW) + (pen_late ? 1u : 0u);
-    SK_MARK(11);
-    {
-        const uint32_t srt = sort64_desc_u32(key_of(lm));
-        if (lane == (int)kq - 1) s.wb[w] = srt;
-    }
-    if (pen_late) mark_window();                               // completed by the barrier below
-    SK_MARK(12);
-    __syncthreads();
-    SK_MARK(2);
-    uint32_t tau = s.wb[0];
+    // Greedy rows without a penalty: the segment's list is its first maximum alone (ferro's scan, sampler.cpp:19-23,
+    // takes a larger logit only: the lowest index among equal maxima; NaN never), so the bound, the candidates and
+    // their ranks are skipped: a lane's first index holding its maximum, then the largest composite of the workgroup
+    // (value first, then the lower id). The rest of the list is zeros, which every merge reads as empty.
+    uint64_t* myl = a.lists + ((int64_t)row * a.nseg + seg) * SK_K;
+    const bool gfast = greedy && !pen;
+    if (gfast) {
+        uint64_t best = 0ull;
+        if (lm == lm) {                                        // NaN: every logit of the lane is NaN
+            uint32_t first = 0u;
 #pragma unroll
-    for (int q = 1; q < SK_NW; ++q) tau = s.wb[q] < tau ? s.wb[q] : tau;
-    if (tau == 0u) tau = 1u;                                   // NaN (key 0) is never a candidate
-    const float tf = tau > 0x007FFFFFu ? val_of(tau) : -__builtin_huge_valf();
-    // groups whose maximum reaches the bound: this wave's region of the group buffer, in lane order
-    uint32_t gmask = 0u;
-#pragma unroll
-    for (int q = 0; q < NL; ++q)                               // the group's raw maximum (recomputed: no register array)
-        gmask |= (fmaxf(fmaxf(v[q].x, v[q].y), fmaxf(v[q].z, v[q].w)) >= tf ? 1u : 0u) << q;
-    const uint32_t gn = (uint32_t)__popc(gmask);
-    const uint32_t gincl = wave_incl_scan_u32(gn);
-    const uint32_t wtot = (uint32_t)__builtin_amdgcn_readlane((int)gincl, WAVE - 1);
-    uint32_t go = gincl - gn;
-    // the groups any lane of the wave hands over (one scalar mask); per such group every lane writes, those without
-    // it into the region's dummy slot, so no per-lane branch waits on a compare
-    const uint32_t wmask = (uint32_t)__builtin_amdgcn_readfirstlane(
-        (int)wave_allreduce(gmask, [](uint32_t x, uint32_t y) { return x | y; }));
-#pragma unroll
-    for (int q = 0; q < NL; ++q) {
-        if ((wmask >> q) & 1u) {
-            const bool mine = ((gmask >> q) & 1u) != 0u && go < (uint32_t)SK_GCAP;
-            const uint32_t slot = mine ? go : (uint32_t)SK_GCAP;
-            s.gval[w][slot] = v[q];
-            s.gidx[w][slot] = (int32_t)((uint32_t)(q * SK_LT + tid) * 4u);
-            go += (gmask >> q) & 1u;
+            for (int q = NL - 1; q >= 0; --q) {
+                const uint32_t e0 = (uint32_t)(seg_lo + (q * SK_LT + tid) * 4);
+                first = v[q].w == lm ? e0 + 3u : first;
+                first = v[q].z == lm ? e0 + 2u : first;
+                first = v[q].y == lm ? e0 + 1u : first;
+                first = v[q].x == lm ? e0 : first;
+            }
+            best = comp_of(key_of(lm), first);
         }
-    }
-    if (lane == 0) s.wcnt[w] = wtot;
-    __syncthreads();
-    SK_MARK(3);
-    // expansion: thread t takes group t of the concatenated regions, its logits at or above the bound become candidates
-    uint32_t goff[SK_NW + 1];
-    goff[0] = 0u;
-    bool gover = false;
-#pragma unroll
-    for (int q = 0; q < SK_NW; ++q) {
-        const uint32_t c = s.wcnt[q];
-        gover |= c > (uint32_t)SK_GCAP;
-        goff[q + 1] = goff[q] + (c < (uint32_t)SK_GCAP ? c : (uint32_t)SK_GCAP);
-    }
-    const uint32_t G = goff[SK_NW];
-    uint64_t cm[4] = {0ull, 0ull, 0ull, 0ull};
-    bool cp[4] = {false, false, false, false};
-    uint32_t nc = 0u;
-    if (!gover && (uint32_t)tid < G) {
-        int r = 0;
-        uint32_t gb = 0u;
-#pragma unroll
-        for (int q = 1; q < SK_NW; ++q) {
-            const bool past = (uint32_t)tid >= goff[q];
-            r += past ? 1 : 0;
-            gb = past ? goff[q] : gb;
+        best = wave_max(best);
+        if (lane == 0) s.wl[w][0] = best;
+        __syncthreads();
+        if (w == 0) {
+            const uint64_t m = wave_max(lane < SK_NW ? s.wl[lane][0] : 0ull);
+            myl[lane] = lane == 0 ? m : 0ull;
         }
-        const uint32_t gi = (uint32_t)tid - gb;
-        const float4 gv = s.gval[r][gi];
-        const uint32_t gw = (uint32_t)s.gidx[r][gi];
-        const int e0 = (int)gw;
-        // rep >= 1: the group's penalised logits, from the bitmap (its 4 bits share a word: e0 % 4 == 0)
-        float e[4] = {gv.x, gv.y, gv.z, gv.w};
-        if (pen_late) {
-            const uint32_t nib = (s.bmp[(uint32_t)e0 >> 5] >> ((uint32_t)e0 & 31u)) & 0xFu;
+    } else {
+        // the bound: each wave sorts its lane maxima in registers (no scalar round trips per step); lane kq - 1 holds its
+        // kq-th largest, and the smallest over the waves counts SK_NW kq >= k distinct logits (one lane more per wave when
+        // the penalty comes later: the raw logits counted may be among the penalised ones)
+        const uint32_t kq = (uint32_t)((k + SK_NW - 1) / SK_NW) + (pen_late ? 1u : 0u);
+        SK_MARK(11);
+        {
+            const uint32_t srt = sort64_desc_u32(key_of(lm));
+            if (lane == (int)kq - 1) s.wb[w] = srt;
+        }
+        if (pen_late) mark_window();                               // completed by the barrier below
+        SK_MARK(12);
+        __syncthreads();
+        SK_MARK(2);
+        uint32_t tau = s.wb[0];
+#pragma unroll
+        for (int q = 1; q < SK_NW; ++q) tau = s.wb[q] < tau ? s.wb[q] : tau;
+        if (tau == 0u) tau = 1u;                                   // NaN (key 0) is never a candidate
+        const float tf = tau > 0x007FFFFFu ? val_of(tau) : -__builtin_huge_valf();
+        // groups whose maximum reaches the bound: this wave's region of the group buffer, in lane order
+        uint32_t gmask = 0u;
+#pragma unroll
+        for (int q = 0; q < NL; ++q)                               // the group's raw maximum (recomputed: no register array)
+            gmask |= (fmaxf(fmaxf(v[q].x, v[q].y), fmaxf(v[q].z, v[q].w)) >= tf ? 1u : 0u) << q;
+        const uint32_t gn = (uint32_t)__popc(gmask);
+        const uint32_t gincl = wave_incl_scan_u32(gn);
+        const uint32_t wtot = (uint32_t)__builtin_amdgcn_readlane((int)gincl, WAVE - 1);
+        uint32_t go = gincl - gn;
+        // the groups any lane of the wave hands over (one scalar mask); per such group every lane writes, those without
+        // it into the region's dummy slot, so no per-lane branch waits on a compare
+        const uint32_t wmask = (uint32_t)__builtin_amdgcn_readfirstlane(
+            (int)wave_allreduce(gmask, [](uint32_t x, uint32_t y) { return x | y; }));
+#pragma unroll
+        for (int q = 0; q < NL; ++q) {
+            if ((wmask >> q) & 1u) {
+                const bool mine = ((gmask >> q) & 1u) != 0u && go < (uint32_t)SK_GCAP;
+                const uint32_t slot = mine ? go : (uint32_t)SK_GCAP;
+                s.gval[w][slot] = v[q];
+                s.gidx[w][slot] = (int32_t)((uint32_t)(q * SK_LT + tid) * 4u);
+                go += (gmask >> q) & 1u;
+            }
+        }
+        if (lane == 0) s.wcnt[w] = wtot;
+        __syncthreads();
+        SK_MARK(3);
+        // expansion: thread t takes group t of the concatenated regions, its logits at or above the bound become candidates
+        uint32_t goff[SK_NW + 1];
+        goff[0] = 0u;
+        bool gover = false;
+#pragma unroll
+        for (int q = 0; q < SK_NW; ++q) {
+            const uint32_t c = s.wcnt[q];
+            gover |= c > (uint32_t)SK_GCAP;
+            goff[q + 1] = goff[q] + (c < (uint32_t)SK_GCAP ? c : (uint32_t)SK_GCAP);
+        }
+        const uint32_t G = goff[SK_NW];
+        uint64_t cm[4] = {0ull, 0ull, 0ull, 0ull};
+        bool cp[4] = {false, false, false, false};
+        uint32_t nc = 0u;
+        if (!gover && (uint32_t)tid < G) {
+            int r = 0;
+            uint32_t gb = 0u;
+#pragma unroll
+            for (int q = 1; q < SK_NW; ++q) {
+                const bool past = (uint32_t)tid >= goff[q];
+                r += past ? 1 : 0;
+                gb = past ? goff[q] : gb;
+            }
+            const uint32_t gi = (uint32_t)tid - gb;
+            const float4 gv = s.gval[r][gi];
+            const uint32_t gw = (uint32_t)s.gidx[r][gi];
+            const int e0 = (int)gw;
+            // rep >= 1: the group's penalised logits, from the bitmap (its 4 bits share a word: e0 % 4 == 0)
+            float e[4] = {gv.x, gv.y, gv.z, gv.w};
+            if (pen_late) {
+                const uint32_t nib = (s.bmp[(uint32_t)e0 >> 5] >> ((uint32_t)e0 & 31u)) & 0xFu;
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if ((nib >> c) & 1u) e[c] = e[c] > 0.0f ? __fdiv_rn(e[c], rep) : __fmul_rn(e[c], rep);
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                cp[c] = e[c] >= tf;
+                cm[c] = comp_of(key_of(e[c]), (uint32_t)(seg_lo + e0 + c));
+                nc += cp[c] ? 1u : 0u;
+            }
+        }
+        if (G > (uint32_t)SK_LT) gover = true;                     // more groups than threads: the exact path
+        // block exclusive scan of the candidate counts
+        const uint32_t cincl = wave_incl_scan_u32(nc);
+        if (lane == WAVE - 1) s.tscan[w] = cincl;
+        __syncthreads();
+        SK_MARK(4);
+        uint32_t cbase = 0u, ntot = 0u;
+#pragma unroll
+        for (int q = 0; q < SK_NW; ++q) {
+            const uint32_t t = s.tscan[q];
+            cbase += q < w ? t : 0u;
+            ntot += t;
+        }
+        // With the penalty applied after the bound, fewer than k logits may stay at or above it: the segment's top k may
+        // then hold a logit below the bound, which was not handed over (never expected with the spare lane per wave)
+        const bool short_k = pen_late && ntot < (uint32_t)k && tf > -__builtin_huge_valf();
+        const bool exact = gover || short_k || ntot > (uint32_t)SK_CAP;   // uniform
+        if (!exact) {
+            uint32_t pos = cbase + cincl - nc;
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-                if ((nib >> c) & 1u) e[c] = e[c] > 0.0f ? __fdiv_rn(e[c], rep) : __fmul_rn(e[c], rep);
+                if (cp[c]) s.cand[pos++] = cm[c];
         }
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            cp[c] = e[c] >= tf;
-            cm[c] = comp_of(key_of(e[c]), (uint32_t)(seg_lo + e0 + c));
-            nc += cp[c] ? 1u : 0u;
-        }
-    }
-    if (G > (uint32_t)SK_LT) gover = true;                     // more groups than threads: the exact path
-    // block exclusive scan of the candidate counts
-    const uint32_t cincl = wave_incl_scan_u32(nc);
-    if (lane == WAVE - 1) s.tscan[w] = cincl;
-    __syncthreads();
-    SK_MARK(4);
-    uint32_t cbase = 0u, ntot = 0u;
-#pragma unroll
-    for (int q = 0; q < SK_NW; ++q) {
-        const uint32_t t = s.tscan[q];
-        cbase += q < w ? t : 0u;
-        ntot += t;
-    }
-    // With the penalty applied after the bound, fewer than k logits may stay at or above it: the segment's top k may
-    // then hold a logit below the bound, which was not handed over (never expected with the spare lane per wave)
-    const bool short_k = pen_late && ntot < (uint32_t)k && tf > -__builtin_huge_valf();
-    const bool exact = gover || short_k || ntot > (uint32_t)SK_CAP;   // uniform
-    if (!exact) {
-        uint32_t pos = cbase + cincl - nc;
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-            if (cp[c]) s.cand[pos++] = cm[c];
-    }
-    uint64_t* myl = a.lists + ((int64_t)row * a.nseg + seg) * SK_K;
-    if (exact) {
-        // ties at the bound: the exact k-th composite of the segment, then the (exactly k) composites at or above it
-        const float* segp = rowp + seg_lo;
-        const uint64_t kth = sk_kth_exact<CAP>(segp, seg_lo, n_in, SEG, cap, pen, rep, k, s);
-        if (tid == 0) s.misc[0] = 0u;
-        __syncthreads();
-        sk_each<CAP>(segp, n_in, SEG, cap, pen, rep, s.bmp, [&](int i, uint32_t key) {
-            const uint64_t c64 = comp_of(key, (uint32_t)(seg_lo + i));
-            if (key != 0u && c64 >= kth) {
-                const uint32_t p = atomicAdd(&s.misc[0], 1u);
-                if (p < (uint32_t)SK_K) s.cand[p] = c64;
-            }
-        });
-        __syncthreads();
-        ntot = s.misc[0] < (uint32_t)SK_K ? s.misc[0] : (uint32_t)SK_K;
-    }
-    __syncthreads();
-    // the segment's top k, sorted by rank: P threads per candidate each count the larger entries in 1/P of the list
-    // (LDS reads of one address per wave: broadcasts), the partial counts are summed and the first k placed by rank
-    uint64_t* sorted = &s.wl[0][0];
-    uint32_t* rk = reinterpret_cast<uint32_t*>(&s.wl[1][0]);    // [P][per] partial ranks (SK_LT words)
-    {
-        const int n = (int)ntot;
-        if (n <= SK_LT) {
-            const int P = n <= SK_LT / 4 ? 4 : (n <= SK_LT / 2 ? 2 : 1);
-            const int per = SK_LT / P;
-            const int c = tid % per, qq = tid / per;
-            const int span = (n + P - 1) / P;
-            if (c < n) {
-                const uint64_t me = s.cand[c];
-                const int j0 = qq * span, j1 = j0 + span < n ? j0 + span : n;
-                uint32_t r = 0u;
-                int jj = j0;
-                for (; jj + 4 <= j1; jj += 4) {                // four LDS reads in flight per step
-                    const uint64_t e0 = s.cand[jj], e1 = s.cand[jj + 1], e2 = s.cand[jj + 2], e3 = s.cand[jj + 3];
-                    r += (e0 > me ? 1u : 0u) + (e1 > me ? 1u : 0u) + (e2 > me ? 1u : 0u) + (e3 > me ? 1u : 0u);
-                }
-                for (; jj < j1; ++jj) r += s.cand[jj] > me ? 1u : 0u;
-                rk[qq * per + c] = r;
-            }
+        if (exact) {
+            // ties at the bound: the exact k-th composite of the segment, then the (exactly k) composites at or above it
+            const float* segp = rowp + seg_lo;
+            const uint64_t kth = sk_kth_exact<CAP>(segp, seg_lo, n_in, SEG, cap, pen, rep, k, s);
+            if (tid == 0) s.misc[0] = 0u;
             __syncthreads();
-            if (tid < n) {                                     // placed straight into the published list
-                uint32_t r = 0u;
-                for (int p2 = 0; p2 < P; ++p2) r += rk[p2 * per + tid];
-                if (r < (uint32_t)k) myl[r] = s.cand[tid];
-            }
-        } else {                                               // 256 < n <= SK_CAP: two candidates per thread
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int c = tid + h * SK_LT;
+            sk_each<CAP>(segp, n_in, SEG, cap, pen, rep, s.bmp, [&](int i, uint32_t key) {
+                const uint64_t c64 = comp_of(key, (uint32_t)(seg_lo + i));
+                if (key != 0u && c64 >= kth) {
+                    const uint32_t p = atomicAdd(&s.misc[0], 1u);
+                    if (p < (uint32_t)SK_K) s.cand[p] = c64;
+                }
+            });
+            __syncthreads();
+            ntot = s.misc[0] < (uint32_t)SK_K ? s.misc[0] : (uint32_t)SK_K;
+        }
+        __syncthreads();
+        // the segment's top k, sorted by rank: P threads per candidate each count the larger entries in 1/P of the list
+        // (LDS reads of one address per wave: broadcasts), the partial counts are summed and the first k placed by rank
+        uint64_t* sorted = &s.wl[0][0];
+        uint32_t* rk = reinterpret_cast<uint32_t*>(&s.wl[1][0]);    // [P][per] partial ranks (SK_LT words)
+        {
+            const int n = (int)ntot;
+            if (n <= SK_LT) {
+                const int P = n <= SK_LT / 4 ? 4 : (n <= SK_LT / 2 ? 2 : 1);
+                const int per = SK_LT / P;
+                const int c = tid % per, qq = tid / per;
+                const int span = (n + P - 1) / P;
                 if (c < n) {
                     const uint64_t me = s.cand[c];
+                    const int j0 = qq * span, j1 = j0 + span < n ? j0 + span : n;
                     uint32_t r = 0u;
-                    int jj = 0;
-                    for (; jj + 4 <= n; jj += 4) {
+                    int jj = j0;
+                    for (; jj + 4 <= j1; jj += 4) {                // four LDS reads in flight per step
                         const uint64_t e0 = s.cand[jj], e1 = s.cand[jj + 1], e2 = s.cand[jj + 2], e3 = s.cand[jj + 3];
                         r += (e0 > me ? 1u : 0u) + (e1 > me ? 1u : 0u) + (e2 > me ? 1u : 0u) + (e3 > me ? 1u : 0u);
                     }
-                    for (; jj < n; ++jj) r += s.cand[jj] > me ? 1u : 0u;
-                    if (r < (uint32_t)k) myl[r] = me;
+                    for (; jj < j1; ++jj) r += s.cand[jj] > me ? 1u : 0u;
+                    rk[qq * per + c] = r;
+                }
+                __syncthreads();
+                if (tid < n) {                                     // placed straight into the published list
+                    uint32_t r = 0u;
+                    for (int p2 = 0; p2 < P; ++p2) r += rk[p2 * per + tid];
+                    if (r < (uint32_t)k) myl[r] = s.cand[tid];
+                }
+            } else {                                               // 256 < n <= SK_CAP: two candidates per thread
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int c = tid + h * SK_LT;
+                    if (c < n) {
+                        const uint64_t me = s.cand[c];
+                        uint32_t r = 0u;
+                        int jj = 0;
+                        for (; jj + 4 <= n; jj += 4) {
+                            const uint64_t e0 = s.cand[jj], e1 = s.cand[jj + 1], e2 = s.cand[jj + 2], e3 = s.cand[jj + 3];
+                            r += (e0 > me ? 1u : 0u) + (e1 > me ? 1u : 0u) + (e2 > me ? 1u : 0u) + (e3 > me ? 1u : 0u);
+                        }
+                        for (; jj < n; ++jj) r += s.cand[jj] > me ? 1u : 0u;
+                        if (r < (uint32_t)k) myl[r] = me;
+                    }
                 }
             }
+            if (tid >= (n < k ? n : k) && tid < SK_K) myl[tid] = 0ull;   // slots past the segment's top k
         }
-        if (tid >= (n < k ? n : k) && tid < SK_K) myl[tid] = 0ull;   // slots past the segment's top k
+        (void)sorted;
+        SK_TAG(9, ntot);
+        SK_TAG(10, G);
     }
-    (void)sorted;
     vm_drain();                                                // the list is in the L2
     __syncthreads();
     SK_MARK(5);
-    SK_TAG(9, ntot);
-    SK_TAG(10, G);
     if (tid == 0) {
         const uint32_t t = __hip_atomic_fetch_add(a.ticket + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         s.misc[1] = t == (uint32_t)a.nseg - 1u ? 1u : 0u;
@@ -5349,30 +5377,38 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
     // the rest reversed: ascending), then wave 0 folds the waves' lists
     const uint64_t* rl = a.lists + (int64_t)row * a.nseg * SK_K;
     uint64_t acc = 0ull;
-    for (int L0 = w; L0 < a.nseg; L0 += 4 * SK_NW) {
-        // four lists per wave, requested together: lists 0 and 2 as stored (descending), 1 and 3 reversed
-        uint64_t b[4];
+    if (greedy) {
+        // k = 1: every list holds its segment's top composite first; wave 0 takes the largest of the nseg heads
+        if (w != 0) return;
+        SK_MARK(7);
+        if (tid == 0) a.ticket[row] = 0u;                     // every segment has counted itself: reset for the next call
+        acc = wave_max(lane < a.nseg ? rl[lane * SK_K] : 0ull);
+    } else {
+        for (int L0 = w; L0 < a.nseg; L0 += 4 * SK_NW) {
+            // four lists per wave, requested together: lists 0 and 2 as stored (descending), 1 and 3 reversed
+            uint64_t b[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int L = L0 + r * SK_NW;
-            b[r] = L < a.nseg ? rl[L * SK_K + ((r & 1) ? WAVE - 1 - lane : lane)] : 0ull;
+            for (int r = 0; r < 4; ++r) {
+                const int L = L0 + r * SK_NW;
+                b[r] = L < a.nseg ? rl[L * SK_K + ((r & 1) ? WAVE - 1 - lane : lane)] : 0ull;
+            }
+            // two independent merges (their latencies overlap), then one
+            const uint64_t m01 = merge_top64<true>(b[0], b[1]);
+            const uint64_t m23 = merge_top64<false>(b[2], b[3]);
+            if (L0 == w) acc = merge_top64<true>(m01, m23);
+            else acc = merge_top64<true>(acc, merge_top64<false>(m01, m23));
         }
-        // two independent merges (their latencies overlap), then one
-        const uint64_t m01 = merge_top64<true>(b[0], b[1]);
-        const uint64_t m23 = merge_top64<false>(b[2], b[3]);
-        if (L0 == w) acc = merge_top64<true>(m01, m23);
-        else acc = merge_top64<true>(acc, merge_top64<false>(m01, m23));
+        // across the waves: waves 0 and 2 fold 1 and 3 (in parallel), then wave 0 folds wave 2's
+        s.wl[w][lane] = acc;
+        __syncthreads();
+        if (w == 0 || w == 2) acc = merge_top64(acc, s.wl[w + 1][WAVE - 1 - lane]);
+        if (w == 2) s.wl[2][lane] = acc;
+        __syncthreads();
+        if (w != 0) return;
+        SK_MARK(7);
+        if (tid == 0) a.ticket[row] = 0u;                         // every segment has counted itself: reset for the next call
+        acc = merge_top64(acc, s.wl[2][WAVE - 1 - lane]);
     }
-    // across the waves: waves 0 and 2 fold 1 and 3 (in parallel), then wave 0 folds wave 2's
-    s.wl[w][lane] = acc;
-    __syncthreads();
-    if (w == 0 || w == 2) acc = merge_top64(acc, s.wl[w + 1][WAVE - 1 - lane]);
-    if (w == 2) s.wl[2][lane] = acc;
-    __syncthreads();
-    if (w != 0) return;
-    SK_MARK(7);
-    if (tid == 0) a.ticket[row] = 0u;                         // every segment has counted itself: reset for the next call
-    acc = merge_top64(acc, s.wl[2][WAVE - 1 - lane]);
     // the row's candidates: lane i holds the i-th in ferro's order (value desc, id asc); NaN never is one
     const int kk = __popcll(__ballot(lane < k && acc != 0ull));
     Args fa = {};

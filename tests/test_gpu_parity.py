@@ -672,6 +672,60 @@ def test_greedy_infinities_and_nan_rows():
     tok = F.argmax_batch(torch.from_numpy(x).cuda()).cpu().numpy()
     want = [O.sample(row, [], O.make_params(temperature=0.0, repetition_penalty=1.0))[0] for row in rows]
     assert list(tok) == want == [0, 0, 0, V - 3, 5000]
+    # the same rows as greedy sampling rows (host route: the small-k kernel's greedy lists)
+    p = W.make_params(len(rows), temperature=0.0, repetition_penalty=1.0)
+    out = F.sample_batch(torch.from_numpy(x).cuda(), p, np.zeros(len(rows)))
+    assert list(out["tok"].cpu().numpy()) == want
+
+
+def _first_max(row):
+    """ferro's greedy scan (sampler.cpp:19-23) restated with numpy: index 0 unless a later logit is strictly larger
+    than every earlier one; NaN never compares larger."""
+    if np.isnan(row[0]):
+        return 0
+    r = np.where(np.isnan(row), -np.inf, row)
+    return int(np.argmax(r))            # np.argmax: the first index of the maximum
+
+
+def test_greedy_batch_ties_across_segments():
+    """A full-size greedy batch (B=64 x V=262144): maxima tied across segment boundaries, inside one lane's four
+    logits, at the row's ends, +-0 and infinities; tokens must be the first maximum of each row."""
+    rng = np.random.default_rng(21)
+    B, V = 64, 262144
+    x = rng.standard_normal((B, V)).astype(np.float32)
+    seg = 16384
+    for b in range(B):
+        kind = b % 8
+        if kind == 0:                                   # a tie in two segments: the lower one wins
+            i, j = sorted(rng.choice(V, 2, replace=False))
+            x[b, i] = x[b, j] = 7.5
+        elif kind == 1:                                 # a tie at both sides of a segment boundary
+            s = int(rng.integers(1, V // seg)) * seg
+            x[b, s - 1] = x[b, s] = 9.0
+        elif kind == 2:                                 # a tie inside one group of four
+            g = int(rng.integers(0, V // 4)) * 4
+            x[b, g + 1] = x[b, g + 3] = 8.0
+        elif kind == 3:                                 # the maximum at the very end
+            x[b, V - 1] = 10.0
+        elif kind == 4:                                 # +0 and -0 as the maximum
+            x[b] = -np.abs(x[b]) - 1.0
+            x[b, 777] = -0.0
+            x[b, 100000] = 0.0
+        elif kind == 5:                                 # +inf twice
+            x[b, 5000] = np.inf
+            x[b, 200000] = np.inf
+        elif kind == 6:                                 # NaN on the maximum's left and at index 0's right
+            x[b, 1] = np.nan
+            x[b, 3000] = 6.0
+            x[b, 2999] = np.nan
+        else:                                           # many equal maxima spread over every segment
+            x[b, rng.choice(V, 300, replace=False)] = 5.0
+    want = [_first_max(r) for r in x]
+    p = W.make_params(B, temperature=0.0, repetition_penalty=1.0)
+    out = F.sample_batch(torch.from_numpy(x).cuda(), p, np.zeros(B))
+    assert list(out["tok"].cpu().numpy()) == want
+    tok = F.argmax_batch(torch.from_numpy(x).cuda()).cpu().numpy()
+    assert list(tok) == want
 
 
 def test_sampled_rows_with_an_infinite_maximum():
