@@ -276,6 +276,22 @@ template <class T>
 __device__ __forceinline__ T wave_min(T v) {
     return wave_allreduce(v, [](T x, T y) { return y < x ? y : x; });
 }
+// The verification rule (server.cpp:627-637) over a stream's m >= 1 tokens, read by the whole wave at once (agent
+// scope: the stream's rows ran on several XCDs): 1 + the leading rows whose token equals the next row's draft, the
+// walk ending after an eos token. Uniform over the wave.
+__device__ __forceinline__ int accepted_prefix(const int32_t* tok, const int32_t* rows, int64_t r0, int m, int eos) {
+    for (int c0 = 0; c0 < m; c0 += WAVE) {
+        const int r = c0 + lane_id();
+        bool stop = false;
+        if (r < m) {
+            const int t = ld_agent(&tok[r0 + r]);
+            stop = (eos >= 0 && t == eos) || r + 1 >= m || t != rows[r0 + r + 1];
+        }
+        const uint64_t b = __ballot(stop);
+        if (b) return c0 + __ffsll((unsigned long long)b);    // 1-based: the row that ends the walk, plus one
+    }
+    return m;
+}
 // inclusive sum over lanes 0..lane (32-bit integers): row shifts 1, 2, 4, 8, then row broadcasts 15 and 31
 __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t x) {
     x += dpp32<0x111>(x);
@@ -2674,25 +2690,21 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             a.tok[row] = tok;
             if (a.keep) a.keep[row] = keep;
         }
-    } else if (tid == 0) {
-        // verify: the last row of a stream to finish computes the accepted prefix (server.cpp:627-637)
-        st_agent(&a.tok[row], (int32_t)tok);
-        vm_drain();
+    } else if (tid < WAVE) {
+        // verify: the last row of a stream to finish computes the accepted prefix (server.cpp:627-637), wave 0
         const int st = rc.pidx;
         const int64_t r0 = a.row_off[st];
         const int m = (int)(a.row_off[st + 1] - r0);
-        const uint32_t old = __hip_atomic_fetch_add(&a.stream_cnt[st], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == (uint32_t)m - 1u) {
-            st_agent(&a.stream_cnt[st], 0u);
-            int acc = 0;
-            for (int r = 0; r < m; ++r) {
-                const int t = ld_agent(&a.tok[r0 + r]);
-                acc = r + 1;
-                if (a.eos >= 0 && t == a.eos) break;
-                if (r + 1 < m && t == a.rows[r0 + r + 1]) continue;
-                break;
-            }
-            a.accepted[st] = acc;
+        uint32_t old = 0u;
+        if (tid == 0) {
+            st_agent(&a.tok[row], (int32_t)tok);
+            vm_drain();
+            old = __hip_atomic_fetch_add(&a.stream_cnt[st], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (read_lane(old, 0) == (uint32_t)m - 1u) {
+            if (tid == 0) st_agent(&a.stream_cnt[st], 0u);
+            const int acc = accepted_prefix(a.tok, a.rows, r0, m, a.eos);
+            if (tid == 0) a.accepted[st] = acc;
         }
     }
     __syncthreads();                                   // LDS is reused by the caller's next chunk
@@ -5437,25 +5449,21 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
             a.tok[row] = tok;
             if (a.keep) a.keep[row] = keep;
         }
-    } else if (lane == 0) {
+    } else {
         // the last row of a stream to finish computes its accepted prefix (server.cpp:627-637): the stream's rows
         // run on several XCDs, so the tokens and the counter are agent-scope accesses
-        st_agent(&a.tok[row], (int32_t)tok);
-        vm_drain();
         const int64_t r0 = ld_const(a.row_off + pidx);
         const int m = (int)(ld_const(a.row_off + pidx + 1) - r0);
-        const uint32_t old = __hip_atomic_fetch_add(&a.stream_cnt[pidx], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == (uint32_t)m - 1u) {
-            st_agent(&a.stream_cnt[pidx], 0u);
-            int acc = 0;
-            for (int r = 0; r < m; ++r) {
-                const int t = ld_agent(&a.tok[r0 + r]);
-                acc = r + 1;
-                if (a.eos >= 0 && t == a.eos) break;
-                if (r + 1 < m && t == a.rows[r0 + r + 1]) continue;
-                break;
-            }
-            a.accepted[pidx] = acc;
+        uint32_t old = 0u;
+        if (lane == 0) {
+            st_agent(&a.tok[row], (int32_t)tok);
+            vm_drain();
+            old = __hip_atomic_fetch_add(&a.stream_cnt[pidx], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (read_lane(old, 0) == (uint32_t)m - 1u) {
+            if (lane == 0) st_agent(&a.stream_cnt[pidx], 0u);
+            const int acc = accepted_prefix(a.tok, a.rows, r0, m, a.eos);
+            if (lane == 0) a.accepted[pidx] = acc;
         }
     }
     SK_MARK(8);
