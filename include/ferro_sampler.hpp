@@ -14,11 +14,14 @@
 // Per call (besides the row's own copy in sample()): the window offsets, the draw and the history are written to
 // pinned, device-mapped host memory that the kernel reads directly, and the kernel writes the token there too (no
 // copy commands for them); one kernel (fs_sample_batch_hp: the parameters are on the host, so the library picks its
-// kernel without reading them back); one device->host copy of the error bits; one stream synchronization.
+// kernel without reading them back); one device->host copy of the error bits into mapped memory, whose arrival the
+// host polls for (it follows the kernel on the stream) instead of synchronizing the stream.
 #pragma once
 
 #include <hip/hip_runtime.h>
 
+#include <chrono>
+#include <climits>
 #include <cstdint>
 #include <cstring>
 #include <stdexcept>
@@ -135,6 +138,25 @@ private:
         hist_cap_ = cap;
     }
 
+    // The call's last command is the copy of the error bits into h_out_[1]: both mapped words leave kPending only
+    // after the kernel (which wrote the token) has finished. Polling them returns about 5 us sooner than a stream
+    // synchronization; a call still pending after kSpinUs falls back to the synchronization.
+    static constexpr int32_t kPending = INT32_MIN;
+    static constexpr double kSpinUs = 100000.0;
+    void wait_done() {
+        volatile const int32_t* out = h_out_;
+        const auto t0 = std::chrono::steady_clock::now();
+        for (unsigned i = 1;; ++i) {
+            if (out[1] != kPending && out[0] != kPending) return;
+            if ((i & 1023u) == 0u &&
+                std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count() > kSpinUs)
+                break;
+        }
+        hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+        if (out[1] == kPending || out[0] == kPending)
+            throw std::runtime_error("ferro_amd::Sampler: the call finished without writing its token");
+    }
+
     static void check(int rc, const char* what) {
         if (rc != FS_OK) throw std::runtime_error(std::string("ferro_amd::Sampler: ") + what + ": " + fs_strerror(rc));
     }
@@ -156,12 +178,15 @@ private:
         memcpy(h_io_ + 2 * sizeof(int64_t), &u, sizeof(u));
         if (h) memcpy(h_io_ + kHead, history.data(), (size_t)h * sizeof(int32_t));   // int is int32_t here
         const int64_t ld = ((int64_t)n_vocab + 3) & ~(int64_t)3;
+        volatile int32_t* out = h_out_;
+        out[0] = kPending;
+        out[1] = kPending;
         const int rc = fs_sample_batch_hp(ctx_, d_logits, ld, 1, n_vocab, h ? hist_dev() : nullptr, off_dev(), d_rec_,
                                           &rec_, u_dev(), d_tok_, 0, nullptr, nullptr, nullptr, stream_);
         if (rc < 0) check(rc, "fs_sample_batch_hp");               // FS_W_RECOVERED: the call ran normally
-        // the token lands in h_out_[0] from the kernel; the error bits come back behind the same synchronization
+        // the token lands in h_out_[0] from the kernel; the error bits are copied into h_out_[1] behind it
         hip(hipMemcpyAsync(&h_out_[1], d_err_, sizeof(int32_t), hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
-        hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+        wait_done();
         if (h_out_[1] != 0) {
             int32_t bits = 0;
             check(fs_device_error(ctx_, stream_, &bits), "fs_device_error");     // clears them
