@@ -36,22 +36,27 @@ SMALL_K = 64                                       # fs_sample_batch_hp's small-
 
 def kernel_of(w, route, cus=256, verify=False):
     """The kernel a call of this workload launches: fs_sample_batch_hp / fs_verify_hp (route "host") run the small-k
-    kernel when every row (stream) is greedy or has k <= 64 and no frequency / presence penalty (verification: no
-    active penalty at all); otherwise the fused kernel."""
+    kernel when every row (stream) is greedy or has k <= 64 and no frequency / presence penalty, greedy rows with
+    frequency / presence penalties only on segments of 4096 logits (verification: no active penalty at all);
+    otherwise the fused kernel."""
+    fused = (KERNEL, "segments, then a merging workgroup per row, one grid")
     if route != "host":
-        return KERNEL, "segments, then a merging workgroup per row, one grid"
+        return fused
     p = w.params
     greedy = (p["temperature"] <= 0) | (p["top_k"] == 1)
     k = np.where((p["top_k"] > 0) & (p["top_k"] < w.V), p["top_k"], w.V)
-    fits = bool(((greedy | (k <= SMALL_K)) & (p["frequency_penalty"] == 0) & (p["presence_penalty"] == 0)).all())
+    fp = (p["frequency_penalty"] != 0) | (p["presence_penalty"] != 0)
+    fits = bool((greedy | ((k <= SMALL_K) & ~fp)).all())
     if verify:
-        fits = fits and bool(((p["repetition_penalty"] == 1) | (p["repeat_last_n"] == 0)).all())
+        fits = fits and bool((((p["repetition_penalty"] == 1) & ~fp) | (p["repeat_last_n"] == 0)).all())
     if not fits:
-        return KERNEL, "segments, then a merging workgroup per row, one grid"
+        return fused
     from ferro_amd import _lib
     nl, ns = ctypes.c_int32(), ctypes.c_int32()
     if _lib.lib().fs_small_k_plan(cus, w.B, w.V, ctypes.byref(nl), ctypes.byref(ns)) != 0:
-        return KERNEL, "segments, then a merging workgroup per row, one grid"
+        return fused
+    if bool((fp & (p["repeat_last_n"] != 0)).any()) and nl.value != 4:
+        return fused
     return (f"fs::small_k_kernel<{nl.value}>",
             f"{ns.value} segments of {1024 * nl.value} logits per row, the last segment of a row merges it, one grid")
 

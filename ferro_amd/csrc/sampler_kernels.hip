@@ -5057,19 +5057,24 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
 
     // the repetition window [wb0, len) over the row's history (sampling rows only: verification windows reach this
     // kernel only without an active penalty); its first 512 ids are requested behind the logits, two per thread
-    bool pen = false;
-    float rep = 1.0f;
+    bool pen = false, cnt_on = false;
+    float rep = 1.0f, fq = 0.0f, pres = 0.0f;
     int64_t h0 = 0, len = 0, wb0 = 0;
     int wid[2] = {-1, -1};
     if (may_pen) {
         const fs_row_params* pr = params + row;
         rep = ld_const(&pr->repetition_penalty);
+        fq = ld_const(&pr->frequency_penalty);
+        pres = ld_const(&pr->presence_penalty);
         fs_row_params pw;
         pw.repeat_last_n = ld_const(&pr->repeat_last_n);
         pw.penalty_from = ld_const(&pr->penalty_from);
         h0 = ld_const(hist_off + row);
         len = ld_const(hist_off + row + 1) - h0;
-        pen = rep != 1.0f && pw.repeat_last_n != 0 && len > 0;
+        // frequency / presence penalties (greedy rows only, segments of 4096 logits: the host checks both) need
+        // each window id's count in the segment
+        cnt_on = NL == 4 && (fq != 0.0f || pres != 0.0f);
+        pen = (rep != 1.0f || cnt_on) && pw.repeat_last_n != 0 && len > 0;
         wb0 = window_begin(len, pw);                           // unconditionally: all five loads in one round trip
         if (!pen || wb0 >= len) { pen = false; wb0 = len; }
 #pragma unroll
@@ -5109,11 +5114,24 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
     // logits, the bitmap is filled while the bound is sorted (the ids arrive right behind the logits), and the penalty
     // is applied to the handed-over logits only; the bound then needs a check (below). rep < 1 raises the flagged
     // logits: they are penalised before the bound (the bitmap first).
-    const bool pen_late = pen && rep >= 1.0f;
+    // greedy rows take the penalty before their maximum (no bound to protect), with its counts when cnt_on
+    const bool pen_late = pen && rep >= 1.0f && !greedy;
     const bool pen_early = pen && !pen_late;
+    cnt_on = cnt_on && pen;
+    // cnt_on: 16-bit counts of the window's ids per logit of the segment, in the group buffer (unused on this path)
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(&s.gval[0][0]);
+    static_assert(sizeof(SkShared::gval) >= SK_LT * 4 * 4 / 2, "a 4096-logit segment's counts fit the group buffer");
+    bool ovf = false;
     auto mark = [&](int id) {
         const uint32_t rel = (uint32_t)(id - seg_lo);
-        if (id >= 0 && id < V && rel < (uint32_t)SEG) atomicOr(&s.bmp[rel >> 5], 1u << (rel & 31u));
+        if (id >= 0 && id < V && rel < (uint32_t)SEG) {
+            atomicOr(&s.bmp[rel >> 5], 1u << (rel & 31u));
+            if (cnt_on) {
+                const uint32_t sh = (rel & 1u) * 16u;
+                const uint32_t old = atomicAdd(&cnt[rel >> 1], 1u << sh);
+                ovf |= ((old >> sh) & 0xFFFFu) == 0xFFFFu;
+            }
+        }
     };
     auto mark_window = [&]() {
         // the ids arrive behind the logits: an empty asm keeps the compiler from hoisting their first use (and the
@@ -5126,11 +5144,14 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
     };
     if (pen) {
         for (int i = tid; i < SEG / 32; i += SK_LT) s.bmp[i] = 0u;
+        if (cnt_on)
+            for (int i = tid; i < SEG / 2; i += SK_LT) cnt[i] = 0u;
         __syncthreads();
     }
-    uint64_t pm = 0ull;                        // rep < 1: 4 bits per group of this thread
+    uint64_t pm = 0ull;                        // rep < 1 or greedy: 4 bits per group of this thread
     if (pen_early) {
         mark_window();
+        if (ovf) atomicOr(a.err, FS_DEVERR_COUNT_OVERFLOW);
         __syncthreads();
 #pragma unroll
         for (int q = 0; q < NL; ++q) {
@@ -5153,7 +5174,15 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
             if (__ballot(nib != 0u)) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
-                    if ((nib >> c) & 1u) e[c] = e[c] > 0.0f ? __fdiv_rn(e[c], rep) : __fmul_rn(e[c], rep);
+                    if ((nib >> c) & 1u) {
+                        float l = e[c] > 0.0f ? __fdiv_rn(e[c], rep) : __fmul_rn(e[c], rep);
+                        if (cnt_on) {                      // l - (count * frequency + presence), as the fused kernel
+                            const uint32_t rel = (uint32_t)(q * SK_LT + tid) * 4u + (uint32_t)c;
+                            const float cc = (float)((cnt[rel >> 1] >> ((rel & 1u) * 16u)) & 0xFFFFu);
+                            l = __fsub_rn(l, __fadd_rn(__fmul_rn(cc, fq), pres));
+                        }
+                        e[c] = l;
+                    }
             }
         }
         if (tail) {
@@ -5165,12 +5194,13 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
         v[q] = make_float4(e[0], e[1], e[2], e[3]);
         lm = fmaxf(lm, fmaxf(fmaxf(e[0], e[1]), fmaxf(e[2], e[3])));
     }
-    // Greedy rows without a penalty: the segment's list is its first maximum alone (ferro's scan, sampler.cpp:19-23,
-    // takes a larger logit only: the lowest index among equal maxima; NaN never), so the bound, the candidates and
-    // their ranks are skipped: a lane's first index holding its maximum, then the largest composite of the workgroup
-    // (value first, then the lower id). The rest of the list is zeros, which every merge reads as empty.
+    // Greedy rows (their penalties already applied above): the segment's list is its first maximum alone (ferro's
+    // scan, sampler.cpp:19-23, takes a larger logit only: the lowest index among equal maxima; NaN never), so the
+    // bound, the candidates and their ranks are skipped: a lane's first index holding its maximum, then the largest
+    // composite of the workgroup (value first, then the lower id). The rest of the list is zeros, which every merge
+    // reads as empty.
     uint64_t* myl = a.lists + ((int64_t)row * a.nseg + seg) * SK_K;
-    const bool gfast = greedy && !pen;
+    const bool gfast = greedy;
     if (gfast) {
         uint64_t best = 0ull;
         if (lm == lm) {                                        // NaN: every logit of the lane is NaN
@@ -5672,8 +5702,8 @@ bool capturing(hipStream_t st) {
 bool small_k_batch(const fs_row_params* h, int64_t B, int32_t V) {
     for (int64_t b = 0; b < B; ++b) {
         const fs_row_params& p = h[b];
-        if (p.frequency_penalty != 0.0f || p.presence_penalty != 0.0f) return false;
         const bool greedy = p.temperature <= 0.0f || p.top_k == 1;
+        if (!greedy && (p.frequency_penalty != 0.0f || p.presence_penalty != 0.0f)) return false;
         const int64_t k = (p.top_k > 0 && p.top_k < V) ? p.top_k : V;
         if (!greedy && k > fs::SK_K) return false;
     }
@@ -5719,7 +5749,9 @@ int grow_small(fs_context* c, size_t slots, size_t rows) {
 bool small_k_windows(const fs_row_params* h, int64_t S, int32_t V) {
     if (!small_k_batch(h, S, V)) return false;
     for (int64_t s = 0; s < S; ++s)
-        if (h[s].repetition_penalty != 1.0f && h[s].repeat_last_n != 0) return false;
+        if ((h[s].repetition_penalty != 1.0f || h[s].frequency_penalty != 0.0f || h[s].presence_penalty != 0.0f) &&
+            h[s].repeat_last_n != 0)
+            return false;
     return true;
 }
 
@@ -5754,12 +5786,15 @@ int launch_small(fs_context* ctx, const fs::Args& a, const fs_row_params* h_para
 #ifdef FS_TRACE
     if (ctx->trace && grid * fs::TRACE_W <= ctx->trace_cap) k.trace = ctx->trace;
 #endif
-    bool capped = false, may_pen = false;
+    bool capped = false, may_pen = false, counts = false;
     for (int64_t b = 0; b < (verify ? (int64_t)a.n_streams : (int64_t)a.B); ++b) {
         const fs_row_params& p = h_params[b];
+        const bool fp = p.frequency_penalty != 0.0f || p.presence_penalty != 0.0f;
         capped |= p.softcap > 0.0f;
-        may_pen |= p.repetition_penalty != 1.0f && p.repeat_last_n != 0;
+        may_pen |= (p.repetition_penalty != 1.0f || fp) && p.repeat_last_n != 0;
+        counts |= fp && p.repeat_last_n != 0;
     }
+    if (counts && nl != 4) return FS_OK;         // count tables fit segments of 4096 logits only: the fused kernel
     // a verification window reaches this kernel only without an active penalty (small_k_windows)
     may_pen = may_pen && !verify && a.hist && a.hist_off;
     const dim3 gd((unsigned)grid), bd(fs::SK_LT);

@@ -331,6 +331,47 @@ def test_count_penalties_by_wave_and_by_table():
     assert nb <= 1
 
 
+@pytest.mark.parametrize("B,V", [(8, 65536), (40, 65536), (64, 262144)])
+def test_greedy_rows_with_every_penalty(B, V):
+    """Greedy rows with repetition (above and below 1), frequency and presence penalties, windows cut by
+    repeat_last_n / penalty_from, the row's maximum repeated 300 times, ids past V and negative ids, an id on every
+    logit of a 4096-logit segment, and penalties that lower the maximum below its runner-up in another segment. On the
+    host route the small-k kernel takes them (greedy rows apply the penalties before their maximum; frequency /
+    presence counts on 4096-logit segments: B=8 and B=40 at V=65536); at B=64 x V=262144 the fused kernel does."""
+    rng = np.random.default_rng(B + 7)
+    rows = [rng.standard_normal(V).astype(np.float32) * 2 for _ in range(B)]
+    hists = []
+    for b in range(B):
+        top = int(np.argmax(rows[b]))
+        second = int(np.argsort(rows[b])[-2])
+        kind = b % 8
+        if kind == 0:
+            h = np.concatenate([np.full(300, top, np.int32), W.zipf_ids(rng, V, 200)])
+        elif kind == 1:
+            h = np.array([top, top, second, V + 5, -3, top], np.int32)
+        elif kind == 2:
+            t = int(rng.integers(0, V // 4096)) * 4096
+            h = (t + np.arange(4096)).astype(np.int32)                   # every logit of one segment
+        elif kind == 3:
+            h = np.zeros(0, np.int32)
+        elif kind == 4:
+            h = np.concatenate([W.zipf_ids(rng, V, 700), np.full(5, top, np.int32)])
+        else:
+            h = W.zipf_ids(rng, V, 256)
+        hists.append(h)
+    p = W.make_params(B, temperature=0.0, repetition_penalty=1.1, frequency_penalty=0.5, presence_penalty=0.3)
+    p["repetition_penalty"][2::8] = 0.8                                      # rep < 1 raises the flagged logits
+    p["frequency_penalty"][3::8] = 0.0
+    p["presence_penalty"][5::8] = 0.0
+    p["frequency_penalty"][6::8] = -0.5                                      # negative: the counted logits rise
+    p["repeat_last_n"][4::8] = 3                                             # only the last three ids
+    p["penalty_from"][5::8] = 100
+    p["top_k"][7::8] = 1                                                     # greedy through top_k = 1 (T > 0)
+    p["temperature"][7::8] = 0.9
+    g, o, nb = check(_case(rows, p, hists, rng.random(B), "greedy_penalties"), kcap=1)
+    assert nb == 0
+
+
 @pytest.mark.parametrize("B,V", [(203, 65536), (130, 262144)])
 def test_balanced_layouts(B, V):
     """Batches with 16 to 64 rows per XCD, where each XCD apportions its segment workgroups over its rows by their
