@@ -5603,13 +5603,14 @@ int grow(fs_context* c, size_t slots, size_t rows, size_t streams) {
 // workspace the call needs (items = (row, segment) slots).
 // max_slots > 0 caps the workspace slots (XCDS * nseg * ceil(rows / XCDS)) by taking fewer segments per row; one
 // segment per row always fits rows <= max_slots.
-int plan(int cus, fs::Args& a, int64_t rows, int64_t& items, int64_t& seg_grid, int64_t max_slots = 0) {
+int plan(int cus, fs::Args& a, int64_t rows, int64_t& items, int64_t& seg_grid, int64_t max_slots = 0,
+         int per_cu = 2) {
     const int64_t tiles_row = a.V / fs::TILE;
     const int64_t per_slot = (rows + fs::XCDS - 1) / fs::XCDS;
     a.nseg = 0;
     a.seg_tiles = 1;
     if (tiles_row > 0) {
-        int64_t want = (2 * (int64_t)cus) / rows;
+        int64_t want = ((int64_t)per_cu * (int64_t)cus) / rows;
         if (want < 1) want = 1;
         if (want > tiles_row) want = tiles_row;
         if (want > fs::BLOCK - 1) want = fs::BLOCK - 1;   // the merge gives each list (segments + tail) a thread
@@ -5699,6 +5700,26 @@ bool capturing(hipStream_t st) {
 // ---- small-k kernel (fs_sample_batch_hp)
 // Whether every row of the batch fits the small-k kernel: greedy, or k = min(top_k or V, V) <= SK_K, with no
 // frequency / presence penalty (h: the host copy of the parameters).
+// A batch whose rows cost very differently: rows sampled with 64 < k <= KMAX beside greedy or k <= 64 rows, none on
+// the whole-row path (k > KMAX), 16 to 64 rows per XCD (the balanced layout). The host copy of the parameters shows
+// the mix, and such batches take about four segments per CU instead of two, which gives the balanced layout finer
+// shares to apportion (B=256 x V=262144 with k from 1 to 2048: 119.7 -> 116.6-117.4 us). Uniform batches lose with
+// more segments (more lists to merge, a second round of workgroups).
+bool mixed_merges(const fs_row_params* h, int64_t B, int32_t V) {
+    const int64_t per_x = (B + fs::XCDS - 1) / fs::XCDS;
+    if (per_x < 16 || per_x > fs::WAVE) return false;
+    bool heavy = false, light = false;
+    for (int64_t b = 0; b < B; ++b) {
+        const fs_row_params& p = h[b];
+        const bool greedy = !(p.temperature > 0.0f && p.top_k != 1);
+        const int64_t k = greedy ? 1 : ((p.top_k > 0 && p.top_k < V) ? p.top_k : V);
+        if (k > fs::KMAX) return false;
+        if (k > 64) heavy = true;
+        else light = true;
+    }
+    return heavy && light;
+}
+
 bool small_k_batch(const fs_row_params* h, int64_t B, int32_t V) {
     for (int64_t b = 0; b < B; ++b) {
         const fs_row_params& p = h[b];
@@ -5816,12 +5837,12 @@ int launch_small(fs_context* ctx, const fs::Args& a, const fs_row_params* h_para
     return FS_OK;
 }
 
-int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream_t st) {
+int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream_t st, int per_cu = 2) {
     std::lock_guard<std::mutex> g(ctx->mu);
     int rc = device_of(ctx);
     if (rc != FS_OK) return rc;
     int64_t items = 0, seg_grid = 0;
-    rc = plan(ctx->cus, a, rows, items, seg_grid);
+    rc = plan(ctx->cus, a, rows, items, seg_grid, 0, per_cu);
     if (rc != FS_OK) return rc;
     rc = grow(ctx, (size_t)(items > 0 ? items : 1), (size_t)rows, (size_t)(streams > 0 ? streams : 1));
     if (rc != FS_OK) return rc;
@@ -5979,6 +6000,7 @@ int fs_sample_batch_hp(fs_context* ctx, const float* d_logits, int64_t ld, int32
         bool used = false;
         rc = launch_small(ctx, a, h_params, (hipStream_t)stream, used);
         if (rc != FS_OK || used) return rc;
+        if (mixed_merges(h_params, B, V)) return launch(ctx, a, B, 0, (hipStream_t)stream, 4);
     }
     return launch(ctx, a, B, 0, (hipStream_t)stream);
 }
