@@ -5530,11 +5530,24 @@ struct fs_context {
     int static_dev = -1;       // device whose static workspace fs_sample_batch_static used with this context
     uint64_t* trace = nullptr; // FS_TRACE builds: phase timestamps, trace_cap entries (fs_trace_set)
     int64_t trace_cap = 0;
+    fs_row_params* greedy = nullptr;      // fs_argmax_batch without parameters: [greedy_cap] greedy records
+    size_t greedy_cap = 0;
+    std::vector<fs_row_params> h_greedy;  //   and their host copy (the small-k kernel's greedy path)
 };
 
 namespace fs {
 __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int64_t n) {
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0u;
+}
+// n parameter records of a greedy row without penalties (fs_argmax_batch without parameters)
+__global__ __launch_bounds__(256) void greedy_params_kernel(fs_row_params* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+        fs_row_params r;
+        r.temperature = 0.0f; r.top_k = 1; r.top_p = 1.0f; r.min_p = 0.0f; r.repetition_penalty = 1.0f;
+        r.frequency_penalty = 0.0f; r.presence_penalty = 0.0f; r.repeat_last_n = 0; r.penalty_from = 0;
+        r.softcap = 0.0f;
+        p[i] = r;
+    }
 }
 }  // namespace fs
 
@@ -5776,6 +5789,28 @@ bool small_k_windows(const fs_row_params* h, int64_t S, int32_t V) {
     return true;
 }
 
+// B greedy parameter records without penalties on the device (filled by a kernel on st, no memset: the call may be
+// captured) and on the host.
+int greedy_params(fs_context* ctx, int64_t B, hipStream_t st) {
+    std::lock_guard<std::mutex> g(ctx->mu);
+    int rc = device_of(ctx);
+    if (rc != FS_OK) return rc;
+    if ((size_t)B <= ctx->greedy_cap) return FS_OK;
+    const size_t cap = std::max<size_t>((size_t)B, 2 * ctx->greedy_cap);
+    release(ctx, ctx->greedy);
+    ctx->greedy = nullptr;
+    ctx->greedy_cap = 0;
+    if (hipMalloc(&ctx->greedy, cap * sizeof(fs_row_params)) != hipSuccess) return FS_E_NOMEM;
+    const int64_t blocks = std::min<int64_t>(1024, ((int64_t)cap + 255) / 256);
+    hipLaunchKernelGGL(fs::greedy_params_kernel, dim3((unsigned)blocks), dim3(256), 0, st, ctx->greedy, (int64_t)cap);
+    if (hipGetLastError() != hipSuccess) return FS_E_HIP;
+    fs_row_params r = {};
+    r.temperature = 0.0f; r.top_k = 1; r.top_p = 1.0f; r.repetition_penalty = 1.0f;
+    ctx->h_greedy.assign(cap, r);
+    ctx->greedy_cap = cap;
+    return FS_OK;
+}
+
 // Launches the small-k kernel when the batch fits it; *used = false (nothing launched) otherwise. a.mode selects
 // sampling (h_params: B records) or verification windows (h_params: n_streams records).
 int launch_small(fs_context* ctx, const fs::Args& a, const fs_row_params* h_params, hipStream_t st, bool& used) {
@@ -5964,6 +5999,7 @@ int fs_destroy(fs_context* c) {
     (void)hipFree(c->rmass);
     (void)hipFree(c->stream_cnt);
     (void)hipFree(c->err);
+    (void)hipFree(c->greedy);
     for (void* p : c->retired) (void)hipFree(p);
     if (c->hflag) (void)hipHostFree(c->hflag);
     delete c;
@@ -6095,6 +6131,19 @@ int fs_argmax_batch(fs_context* ctx, const float* d_logits, int64_t ld, int32_t 
     fs::Args a = {};
     a.logits = d_logits; a.ld = ld; a.B = B; a.V = V; a.hist = d_hist; a.hist_off = d_params ? d_hist_off : nullptr;
     a.params = d_params; a.tok = d_tok; a.mode = fs::MODE_ARGMAX; a.eos = -1;
+    if (!d_params) {
+        // no penalties: every row greedy, so the small-k kernel's greedy path takes the batch (its parameters are
+        // greedy records the context keeps on the device and the host)
+        rc = greedy_params(ctx, B, (hipStream_t)stream);
+        if (rc != FS_OK) return rc;
+        fs::Args g = a;
+        g.mode = fs::MODE_SAMPLE;
+        g.hist = nullptr;
+        g.params = ctx->greedy;
+        bool used = false;
+        rc = launch_small(ctx, g, ctx->h_greedy.data(), (hipStream_t)stream, used);
+        if (rc != FS_OK || used) return rc;
+    }
     return launch(ctx, a, B, 0, (hipStream_t)stream);
 }
 

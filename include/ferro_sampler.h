@@ -119,7 +119,8 @@ int fs_sample_batch_static(fs_context* ctx, const float* d_logits, int64_t ld, i
                            int32_t* d_keep, void* stream);
 
 /* Greedy batch: argmax after penalties, lowest index on ties (sampler.cpp:19-23). d_params may be NULL (no
- * penalties); otherwise only the penalty fields are read and every row is treated as greedy. */
+ * penalties: the context keeps greedy parameter records of its own, on the device and the host, for the small-k
+ * kernel); otherwise only the penalty fields are read and every row is treated as greedy. */
 int fs_argmax_batch(fs_context* ctx, const float* d_logits, int64_t ld, int32_t B, int32_t V,
                     const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params,
                     int32_t* d_tok, void* stream);

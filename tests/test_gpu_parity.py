@@ -728,6 +728,23 @@ def _first_max(row):
     return int(np.argmax(r))            # np.argmax: the first index of the maximum
 
 
+@pytest.mark.parametrize("V", [1, 3, 5, 4095, 4097, 65537])
+def test_argmax_without_parameters_odd_vocab(V):
+    """fs_argmax_batch without parameters (the small-k kernel's greedy path) on vocabularies that end inside a group
+    of four, inside a segment or just past one; rows with NaN at 0, ties and -inf."""
+    rng = np.random.default_rng(V)
+    x = rng.standard_normal((6, V)).astype(np.float32)
+    x[0, 0] = np.nan
+    x[1, :] = -np.inf
+    x[2, V - 1] = 50.0
+    x[3, rng.integers(0, V, 3)] = 20.0
+    if V > 2:
+        x[4, 1] = np.nan
+    want = [_first_max(r) for r in x]
+    tok = F.argmax_batch(torch.from_numpy(x).cuda()).cpu().numpy()
+    assert list(tok) == want
+
+
 def test_greedy_batch_ties_across_segments():
     """A full-size greedy batch (B=64 x V=262144): maxima tied across segment boundaries, inside one lane's four
     logits, at the row's ends, +-0 and infinities; tokens must be the first maximum of each row."""
