@@ -4918,6 +4918,7 @@ struct SkShared {
     uint64_t trace_t[16];
 #endif
 };
+static_assert(offsetof(SkShared, cand) % 16 == 0, "the rank loops read the candidates in 16-byte pairs");
 // Phase timestamps of the small-k kernel (FS_TRACE builds only; thread 0, after the barrier that closes a phase):
 // 0 start, 1 window bitmap built, 2 bound (all of the segment's logits in), 3 groups handed over, 4 candidates
 // expanded, 5 list sorted and published, 6 ticket taken; merging workgroup: 7 lists folded, 8 row finished.
@@ -5359,15 +5360,19 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
                 const int P = n <= SK_LT / 4 ? 4 : (n <= SK_LT / 2 ? 2 : 1);
                 const int per = SK_LT / P;
                 const int c = tid % per, qq = tid / per;
-                const int span = (n + P - 1) / P;
+                const int span = (((n + P - 1) / P) + 1) & ~1;     // even: every part starts on a 16-byte pair
                 if (c < n) {
                     const uint64_t me = s.cand[c];
                     const int j0 = qq * span, j1 = j0 + span < n ? j0 + span : n;
                     uint32_t r = 0u;
                     int jj = j0;
-                    for (; jj + 4 <= j1; jj += 4) {                // four LDS reads in flight per step
-                        const uint64_t e0 = s.cand[jj], e1 = s.cand[jj + 1], e2 = s.cand[jj + 2], e3 = s.cand[jj + 3];
-                        r += (e0 > me ? 1u : 0u) + (e1 > me ? 1u : 0u) + (e2 > me ? 1u : 0u) + (e3 > me ? 1u : 0u);
+                    const ulonglong2* c2 = reinterpret_cast<const ulonglong2*>(s.cand);
+                    for (; jj + 8 <= j1; jj += 8) {                // eight entries per step: four 16-byte LDS reads
+                        const ulonglong2 e0 = c2[jj >> 1], e1 = c2[(jj >> 1) + 1], e2 = c2[(jj >> 1) + 2],
+                                         e3 = c2[(jj >> 1) + 3];
+                        r += (e0.x > me ? 1u : 0u) + (e0.y > me ? 1u : 0u) + (e1.x > me ? 1u : 0u) +
+                             (e1.y > me ? 1u : 0u) + (e2.x > me ? 1u : 0u) + (e2.y > me ? 1u : 0u) +
+                             (e3.x > me ? 1u : 0u) + (e3.y > me ? 1u : 0u);
                     }
                     for (; jj < j1; ++jj) r += s.cand[jj] > me ? 1u : 0u;
                     rk[qq * per + c] = r;
@@ -5386,9 +5391,13 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
                         const uint64_t me = s.cand[c];
                         uint32_t r = 0u;
                         int jj = 0;
-                        for (; jj + 4 <= n; jj += 4) {
-                            const uint64_t e0 = s.cand[jj], e1 = s.cand[jj + 1], e2 = s.cand[jj + 2], e3 = s.cand[jj + 3];
-                            r += (e0 > me ? 1u : 0u) + (e1 > me ? 1u : 0u) + (e2 > me ? 1u : 0u) + (e3 > me ? 1u : 0u);
+                        const ulonglong2* c2 = reinterpret_cast<const ulonglong2*>(s.cand);
+                        for (; jj + 8 <= n; jj += 8) {
+                            const ulonglong2 e0 = c2[jj >> 1], e1 = c2[(jj >> 1) + 1], e2 = c2[(jj >> 1) + 2],
+                                             e3 = c2[(jj >> 1) + 3];
+                            r += (e0.x > me ? 1u : 0u) + (e0.y > me ? 1u : 0u) + (e1.x > me ? 1u : 0u) +
+                                 (e1.y > me ? 1u : 0u) + (e2.x > me ? 1u : 0u) + (e2.y > me ? 1u : 0u) +
+                                 (e3.x > me ? 1u : 0u) + (e3.y > me ? 1u : 0u);
                         }
                         for (; jj < n; ++jj) r += s.cand[jj] > me ? 1u : 0u;
                         if (r < (uint32_t)k) myl[r] = me;
