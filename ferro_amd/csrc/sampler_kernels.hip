@@ -5121,7 +5121,8 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
     cnt_on = cnt_on && pen;
     // cnt_on: 16-bit counts of the window's ids per logit of the segment, in the group buffer (unused on this path)
     uint32_t* cnt = reinterpret_cast<uint32_t*>(&s.gval[0][0]);
-    static_assert(sizeof(SkShared::gval) >= SK_LT * 4 * 4 / 2, "a 4096-logit segment's counts fit the group buffer");
+    static_assert(sizeof(SkShared::gval) >= SK_LT * 4 * 4 / 2 * sizeof(uint32_t),
+                  "a 4096-logit segment's 16-bit counts fit the group buffer");
     bool ovf = false;
     auto mark = [&](int id) {
         const uint32_t rel = (uint32_t)(id - seg_lo);
@@ -5224,9 +5225,9 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
             myl[lane] = lane == 0 ? m : 0ull;
         }
     } else {
-        // the bound: each wave sorts its lane maxima in registers (no scalar round trips per step); lane kq - 1 holds its
-        // kq-th largest, and the smallest over the waves counts SK_NW kq >= k distinct logits (one lane more per wave when
-        // the penalty comes later: the raw logits counted may be among the penalised ones)
+        // the bound: each wave sorts its lane maxima in registers (no scalar round trips per step); lane kq - 1 holds
+        // its kq-th largest, and the smallest over the waves counts SK_NW kq >= k distinct logits (one lane more per
+        // wave when the penalty comes later: the raw logits counted may be among the penalised ones)
         const uint32_t kq = (uint32_t)((k + SK_NW - 1) / SK_NW) + (pen_late ? 1u : 0u);
         SK_MARK(11);
         {
@@ -5245,7 +5246,7 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
         // groups whose maximum reaches the bound: this wave's region of the group buffer, in lane order
         uint32_t gmask = 0u;
 #pragma unroll
-        for (int q = 0; q < NL; ++q)                               // the group's raw maximum (recomputed: no register array)
+        for (int q = 0; q < NL; ++q)                     // the group's raw maximum (recomputed: no register array)
             gmask |= (fmaxf(fmaxf(v[q].x, v[q].y), fmaxf(v[q].z, v[q].w)) >= tf ? 1u : 0u) << q;
         const uint32_t gn = (uint32_t)__popc(gmask);
         const uint32_t gincl = wave_incl_scan_u32(gn);
@@ -5268,7 +5269,8 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
         if (lane == 0) s.wcnt[w] = wtot;
         __syncthreads();
         SK_MARK(3);
-        // expansion: thread t takes group t of the concatenated regions, its logits at or above the bound become candidates
+        // expansion: thread t takes group t of the concatenated regions, its logits at or above the bound become
+        // candidates
         uint32_t goff[SK_NW + 1];
         goff[0] = 0u;
         bool gover = false;
@@ -5323,8 +5325,9 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
             cbase += q < w ? t : 0u;
             ntot += t;
         }
-        // With the penalty applied after the bound, fewer than k logits may stay at or above it: the segment's top k may
-        // then hold a logit below the bound, which was not handed over (never expected with the spare lane per wave)
+        // With the penalty applied after the bound, fewer than k logits may stay at or above it: the segment's top k
+        // may then hold a logit below the bound, which was not handed over (never expected with the spare lane per
+        // wave)
         const bool short_k = pen_late && ntot < (uint32_t)k && tf > -__builtin_huge_valf();
         const bool exact = gover || short_k || ntot > (uint32_t)SK_CAP;   // uniform
         if (!exact) {
@@ -5334,7 +5337,8 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
                 if (cp[c]) s.cand[pos++] = cm[c];
         }
         if (exact) {
-            // ties at the bound: the exact k-th composite of the segment, then the (exactly k) composites at or above it
+            // ties at the bound: the exact k-th composite of the segment, then the (exactly k) composites at or above
+            // it
             const float* segp = rowp + seg_lo;
             const uint64_t kth = sk_kth_exact<CAP>(segp, seg_lo, n_in, SEG, cap, pen, rep, k, s);
             if (tid == 0) s.misc[0] = 0u;
@@ -5432,7 +5436,7 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
         // k = 1: every list holds its segment's top composite first; wave 0 takes the largest of the nseg heads
         if (w != 0) return;
         SK_MARK(7);
-        if (tid == 0) a.ticket[row] = 0u;                     // every segment has counted itself: reset for the next call
+        if (tid == 0) a.ticket[row] = 0u;                     // all segments have counted: reset for the next call
         acc = wave_max(lane < a.nseg ? rl[lane * SK_K] : 0ull);
     } else {
         for (int L0 = w; L0 < a.nseg; L0 += 4 * SK_NW) {
@@ -5457,7 +5461,7 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
         __syncthreads();
         if (w != 0) return;
         SK_MARK(7);
-        if (tid == 0) a.ticket[row] = 0u;                         // every segment has counted itself: reset for the next call
+        if (tid == 0) a.ticket[row] = 0u;                     // all segments have counted: reset for the next call
         acc = merge_top64(acc, s.wl[2][WAVE - 1 - lane]);
     }
     // the row's candidates: lane i holds the i-th in ferro's order (value desc, id asc); NaN never is one
