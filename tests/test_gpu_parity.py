@@ -331,6 +331,26 @@ def test_count_penalties_by_wave_and_by_table():
     assert nb <= 1
 
 
+@pytest.mark.parametrize("V", [65536, 262144])
+def test_count_overflow_is_reported(V):
+    """A window holding one id 70000 times overflows the 16-bit penalty counts: the call reports
+    FS_DEVERR_COUNT_OVERFLOW (small-k kernel at V=65536 on the host route, fused kernel otherwise), and the next
+    clean call reports nothing."""
+    from ferro_amd._lib import FS_DEVERR_COUNT_OVERFLOW
+    rng = np.random.default_rng(V)
+    x = torch.from_numpy(rng.standard_normal((2, V)).astype(np.float32)).cuda()
+    hist = np.concatenate([np.full(70000, 123, np.int32), np.arange(10, dtype=np.int32)])
+    hist_off = np.array([0, 70000, 70010], np.int64)
+    p = W.make_params(2, temperature=0.0, repetition_penalty=1.0, frequency_penalty=0.5)
+    F.sample_batch(x, p, np.zeros(2), hist=hist, hist_off=hist_off)
+    torch.cuda.synchronize()
+    assert F.device_error() & FS_DEVERR_COUNT_OVERFLOW
+    hist2 = np.arange(20, dtype=np.int32)
+    F.sample_batch(x, p, np.zeros(2), hist=hist2, hist_off=np.array([0, 10, 20], np.int64))
+    torch.cuda.synchronize()
+    assert F.device_error() == 0
+
+
 @pytest.mark.parametrize("B,V", [(8, 65536), (40, 65536), (64, 262144)])
 def test_greedy_rows_with_every_penalty(B, V):
     """Greedy rows with repetition (above and below 1), frequency and presence penalties, windows cut by
