@@ -4920,9 +4920,10 @@ struct SkShared {
 };
 static_assert(offsetof(SkShared, cand) % 16 == 0, "the rank loops read the candidates in 16-byte pairs");
 // Phase timestamps of the small-k kernel (FS_TRACE builds only; thread 0, after the barrier that closes a phase):
-// 0 start, 1 window bitmap built, 2 bound (all of the segment's logits in), 3 groups handed over, 4 candidates
-// expanded, 5 list sorted and published, 6 ticket taken; merging workgroup: 7 lists folded, 8 row finished.
-// Slots 9-10: candidates and groups of the segment; 13-15: role (3 segment, 4 segment + merge), row, segment.
+// 0 start, 11 the segment's logits in and transformed, 12 lane maxima sorted, 2 bound, 3 groups handed over,
+// 4 candidates expanded, 5 list ranked and published, 6 ticket taken; merging workgroup: 7 lists folded, 8 row
+// finished (greedy rows set only 0, 5-8). Slots 9-10: candidates and groups of the segment; 13-15: role (3 segment,
+// 4 segment + merge), row, segment. ferro_amd/trace_phases.py --route host reads them.
 #ifdef FS_TRACE
 #define SK_MARK(i) do { if (threadIdx.x == 0) s.trace_t[(i)] = __builtin_amdgcn_s_memrealtime(); } while (0)
 #define SK_TAG(i, v) do { if (threadIdx.x == 0) s.trace_t[(i)] = (uint64_t)(v); } while (0)

@@ -9,7 +9,14 @@ row's segments seen done, 2 candidates gathered (short merge), 3 candidates rank
 Slots 5-12 of a segment workgroup: on the fused path, when the slowest of its waves finished tiles 0-7; on the
 large-k path, the row passes (see sampler_kernels.hip). Slots 13-15 tag role, row, segment.
 
-Usage (on a GPU):  python ferro_amd/trace_phases.py --workload cfg3 [--calls 5]
+With --route host the call goes through fs_sample_batch_hp / fs_verify_hp, which run the small-k kernel for batches it
+fits. Its slots (thread 0 of every (row, segment) workgroup): 0 start, 11 the segment's logits in and transformed,
+12 lane maxima sorted, 2 bound (after the barrier), 3 groups handed over, 4 candidates expanded, 5 list ranked and
+published, 6 ticket taken; the row's last segment: 7 lists folded, 8 row finished. Slots 9-10: candidates and
+groups; 13: role (3 segment, 4 segment that merged its row); 14-15: row, segment. Greedy rows leave 11-4 unset
+(their "published" step is then counted from the start).
+
+Usage (on a GPU):  python ferro_amd/trace_phases.py --workload cfg3 [--calls 5] [--route host]
 Prints a markdown table: when each phase happens (µs from the first workgroup's start; min / median / max over the
 workgroups, median over the traced calls) and how long it takes per workgroup.
 """
@@ -46,11 +53,21 @@ def load():
     return L
 
 
-def one_call(L, ctx, w, entry, bufs, dev_in, trace, i, torch):
+def one_call(L, ctx, w, entry, bufs, dev_in, trace, i, torch, hp=None):
     P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     x = bufs[i % len(bufs)]
-    if entry == "verify":
+    if hp is not None:
+        h = hp.ctypes.data_as(ctypes.c_void_p)
+        if entry == "verify":
+            rc = L.fs_verify_hp(ctx, P(x), w.V, len(w.row_off) - 1, w.B, w.V, P(dev_in["rows"]), P(dev_in["roff"]),
+                                P(dev_in["hist"]), P(dev_in["hoff"]), P(dev_in["params"]), h, P(dev_in["u"]), -1,
+                                P(dev_in["tok"]), P(dev_in["acc"]), st)
+        else:
+            rc = L.fs_sample_batch_hp(ctx, P(x), w.V, w.B, w.V, P(dev_in["hist"]), P(dev_in["hoff"]),
+                                      P(dev_in["params"]), h, P(dev_in["u"]), P(dev_in["tok"]), 0, None, None,
+                                      P(dev_in["keep"]), st)
+    elif entry == "verify":
         rc = L.fs_verify(ctx, P(x), w.V, len(w.row_off) - 1, w.B, w.V, P(dev_in["rows"]), P(dev_in["roff"]),
                          P(dev_in["hist"]), P(dev_in["hoff"]), P(dev_in["params"]), P(dev_in["u"]), -1,
                          P(dev_in["tok"]), P(dev_in["acc"]), st)
@@ -118,11 +135,49 @@ def summarize(calls, seg_tiles):
     return rows, span
 
 
+SK_PHASES = [(11, "logits in (transformed)"), (12, "lane maxima sorted"), (2, "bound (barrier)"),
+             (3, "groups handed over"), (4, "candidates expanded"), (5, "list ranked and published"),
+             (6, "ticket taken")]
+
+
+def summarize_small_k(trs):
+    """trs: list over calls of [grid, TRACE_W] uint64 (small-k kernel) -> (rows (name, min, median, max, per
+    workgroup), span, median candidates per top-k segment)."""
+    per = {}
+    cands, spans = [], []
+    for tr in trs:
+        tr = tr[tr[:, 13] >= 3]
+        t0 = np.int64(tr[:, 0].min())
+        rel = lambda j: (tr[:, j].astype(np.int64) - t0) * TICK_US  # noqa: E731
+        topk = tr[:, 11] != 0                          # greedy rows leave the selection slots unset
+        mer = tr[:, 13] == 4
+        per.setdefault("segment start", []).append((rel(0), None))
+        prev = 0
+        for j, name in SK_PHASES:
+            sel = topk if j not in (5, 6) else np.ones_like(topk)     # greedy rows: start -> published -> ticket
+            step = rel(j) - np.where(topk | (j == 6), rel(prev), rel(0))
+            per.setdefault(name, []).append((rel(j)[sel], step[sel]))
+            prev = j
+        per.setdefault("lists folded (the row's last segment)", []).append((rel(7)[mer], (rel(7) - rel(6))[mer]))
+        per.setdefault("row finished (softmax, top-p, draw)", []).append((rel(8)[mer], (rel(8) - rel(7))[mer]))
+        cands.append(np.median(tr[topk, 9]) if topk.any() else np.nan)
+        spans.append(rel(8)[mer].max())
+    rows = []
+    for name, vals in per.items():
+        t = [np.percentile(v, [0, 50, 100]) for v, _ in vals if v.size]
+        t = np.median(np.array(t), axis=0) if t else (np.nan,) * 3
+        d = [np.median(x) for _, x in vals if x is not None and x.size]
+        rows.append((name, *t, np.median(d) if d else np.nan))
+    return rows, float(np.median(spans)), float(np.median(cands))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--workload", default="cfg3")
     ap.add_argument("--calls", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--route", choices=["device", "host"], default="device",
+                    help="host: the host copy of the parameters goes along (the small-k kernel where it fits)")
     args = ap.parse_args()
 
     import torch
@@ -149,15 +204,16 @@ def main():
                       acc=torch.empty(len(w.row_off) - 1, dtype=torch.int32, device=dev))
     cap = 1 << 20
     trace = torch.zeros(cap, dtype=torch.int64, device=dev)
+    hp = np.ascontiguousarray(w.params) if args.route == "host" else None
     for i in range(args.warmup):
-        one_call(L, ctx, w, entry, bufs, dev_in, trace, i, torch)
-    calls = []
+        one_call(L, ctx, w, entry, bufs, dev_in, trace, i, torch, hp)
+    calls, raws = [], []
     for c in range(args.calls):
         trace.zero_()
         torch.cuda.synchronize()
         if L.fs_trace_set(ctx, ctypes.c_void_p(trace.data_ptr()), cap) != 0:
             raise RuntimeError("fs_trace_set failed")
-        one_call(L, ctx, w, entry, bufs, dev_in, trace, args.warmup + c, torch)
+        one_call(L, ctx, w, entry, bufs, dev_in, trace, args.warmup + c, torch, hp)
         torch.cuda.synchronize()
         L.fs_trace_set(ctx, None, 0)
         tr = trace.cpu().numpy().view(np.uint64).reshape(-1, TRACE_W)
@@ -165,8 +221,24 @@ def main():
         n = int(np.nonzero(used)[0].max()) + 1 if used.any() else 0
         if n == 0:
             raise RuntimeError("nothing traced (grid larger than the trace buffer?)")
-        calls.append(phases(tr[:n]))
-        one_call(L, ctx, w, entry, bufs, dev_in, trace, args.warmup + c + 1, torch)   # untraced spacer
+        if int(tr[used, 13].max()) >= 3:
+            raws.append(tr[:n].copy())
+        else:
+            calls.append(phases(tr[:n]))
+        one_call(L, ctx, w, entry, bufs, dev_in, trace, args.warmup + c + 1, torch, hp)   # untraced spacer
+    f = lambda v: "" if np.isnan(v) else f"{v:.2f}"  # noqa: E731
+    if raws:
+        rows, span, cand = summarize_small_k(raws)
+        print(f"Phase timeline of one call of the small-k kernel, {desc} ({len(raws[0][raws[0][:, 13] >= 3])} "
+              f"segment workgroups); µs from the first workgroup's start, median over {len(raws)} traced calls; "
+              f"the per-workgroup column is the step from the previous phase:\n")
+        print("| phase | first | median | last | per workgroup (median) |")
+        print("|---|---|---|---|---|")
+        for name, lo, med, hi, d in rows:
+            print(f"| {name} | {f(lo)} | {f(med)} | {f(hi)} | {f(d)} |")
+        print(f"\nFirst workgroup start to the last row finished: {span:.2f} µs; candidates per top-k segment "
+              f"(median): {cand:.0f}")
+        return
     tiles_row = w.V // 4096
     segs = int(np.median([len(c["seg"]) for c in calls]) / max(w.B, 1))
     seg_tiles = -(-tiles_row // max(segs, 1))
@@ -177,7 +249,6 @@ def main():
     print("| phase | first | median | last | per workgroup (median) |")
     print("|---|---|---|---|---|")
     for name, lo, med, hi, d in rows:
-        f = lambda v: "" if np.isnan(v) else f"{v:.2f}"  # noqa: E731
         print(f"| {name} | {f(lo)} | {f(med)} | {f(hi)} | {f(d)} |")
     print(f"\nFirst workgroup start to last workgroup end: {span:.2f} µs")
 
