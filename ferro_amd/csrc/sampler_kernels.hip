@@ -5019,7 +5019,8 @@ constexpr size_t SK_ARGS_OFF = offsetof(SkKernargs, a);
 // 21.3 -> 20.6 us with the limit, the headline's 1024 workgroups unchanged.
 constexpr unsigned SK_PAD_LDS = 16384;
 
-template <int NL, bool CAP>
+// GREEDY: every row of the batch is greedy (the selection code is left out: fewer registers, more workgroups per CU).
+template <int NL, bool CAP, bool GREEDY>
 __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int64_t ld, int B, int V, int nseg,
                                                         int may_pen, const fs_row_params* params,
                                                         const int64_t* hist_off, const int32_t* hist, SkArgs a_) {
@@ -5108,7 +5109,7 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
     const float temp = ld_const(&pp->temperature);
     const int top_k = ld_const(&pp->top_k);
     const float cap = CAP ? ld_const(&pp->softcap) : 0.0f;
-    const bool greedy = temp <= 0.0f || top_k == 1;
+    const bool greedy = GREEDY || temp <= 0.0f || top_k == 1;
     const int k = greedy ? 1 : ((top_k > 0 && top_k < V) ? top_k : V);
 
     // repetition penalty: an exact bitmap of the window's ids in this segment (each distinct id once: sampler.cpp:14-17).
@@ -5856,10 +5857,11 @@ int launch_small(fs_context* ctx, const fs::Args& a, const fs_row_params* h_para
 #ifdef FS_TRACE
     if (ctx->trace && grid * fs::TRACE_W <= ctx->trace_cap) k.trace = ctx->trace;
 #endif
-    bool capped = false, may_pen = false, counts = false;
+    bool capped = false, may_pen = false, counts = false, all_greedy = true;
     for (int64_t b = 0; b < (verify ? (int64_t)a.n_streams : (int64_t)a.B); ++b) {
         const fs_row_params& p = h_params[b];
         const bool fp = p.frequency_penalty != 0.0f || p.presence_penalty != 0.0f;
+        all_greedy = all_greedy && !(p.temperature > 0.0f && p.top_k != 1);
         capped |= p.softcap > 0.0f;
         may_pen |= (p.repetition_penalty != 1.0f || fp) && p.repeat_last_n != 0;
         counts |= fp && p.repeat_last_n != 0;
@@ -5868,18 +5870,30 @@ int launch_small(fs_context* ctx, const fs::Args& a, const fs_row_params* h_para
     // a verification window reaches this kernel only without an active penalty (small_k_windows)
     may_pen = may_pen && !verify && a.hist && a.hist_off;
     const dim3 gd((unsigned)grid), bd(fs::SK_LT);
-    auto go = [&](auto kern) {
-        hipLaunchKernelGGL(kern, gd, bd, fs::SK_PAD_LDS, st, a.logits, a.ld, a.B, a.V, nseg, may_pen ? 1 : 0, a.params,
+    // all-greedy batches: the greedy-only kernel, without the LDS pad (its registers allow more workgroups per CU)
+    auto go = [&](auto kern, unsigned pad) {
+        hipLaunchKernelGGL(kern, gd, bd, pad, st, a.logits, a.ld, a.B, a.V, nseg, may_pen ? 1 : 0, a.params,
                            a.hist_off, a.hist, k);
     };
-    if (capped) {
-        if (nl == 16) go(fs::small_k_kernel<16, true>);
-        else if (nl == 8) go(fs::small_k_kernel<8, true>);
-        else go(fs::small_k_kernel<4, true>);
+    const unsigned pad = fs::SK_PAD_LDS;
+    if (all_greedy) {
+        if (capped) {
+            if (nl == 16) go(fs::small_k_kernel<16, true, true>, 0u);
+            else if (nl == 8) go(fs::small_k_kernel<8, true, true>, 0u);
+            else go(fs::small_k_kernel<4, true, true>, 0u);
+        } else {
+            if (nl == 16) go(fs::small_k_kernel<16, false, true>, 0u);
+            else if (nl == 8) go(fs::small_k_kernel<8, false, true>, 0u);
+            else go(fs::small_k_kernel<4, false, true>, 0u);
+        }
+    } else if (capped) {
+        if (nl == 16) go(fs::small_k_kernel<16, true, false>, pad);
+        else if (nl == 8) go(fs::small_k_kernel<8, true, false>, pad);
+        else go(fs::small_k_kernel<4, true, false>, pad);
     } else {
-        if (nl == 16) go(fs::small_k_kernel<16, false>);
-        else if (nl == 8) go(fs::small_k_kernel<8, false>);
-        else go(fs::small_k_kernel<4, false>);
+        if (nl == 16) go(fs::small_k_kernel<16, false, false>, pad);
+        else if (nl == 8) go(fs::small_k_kernel<8, false, false>, pad);
+        else go(fs::small_k_kernel<4, false, false>, pad);
     }
     if (hipGetLastError() != hipSuccess) return FS_E_HIP;
     used = true;
