@@ -5015,7 +5015,7 @@ struct SkKernargs {
 constexpr size_t SK_ARGS_OFF = offsetof(SkKernargs, a);
 
 // Dynamic LDS a launch requests beyond SkShared (unused): with it a CU holds 4 workgroups (≈35 KB each of its 160 KB),
-// as the kernel's 95 VGPRs would otherwise allow 5. Measured on MI355X: a 272-row verification call (1088 workgroups)
+// as the kernel's 96 VGPRs would otherwise allow 5. Measured on MI355X: a 272-row verification call (1088 workgroups)
 // 21.3 -> 20.6 us with the limit, the headline's 1024 workgroups unchanged.
 constexpr unsigned SK_PAD_LDS = 16384;
 
