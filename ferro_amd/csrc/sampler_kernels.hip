@@ -5015,8 +5015,9 @@ struct SkKernargs {
 constexpr size_t SK_ARGS_OFF = offsetof(SkKernargs, a);
 
 // Dynamic LDS a launch requests beyond SkShared (unused): with it a CU holds 4 workgroups (≈35 KB each of its 160 KB),
-// as the kernel's 96 VGPRs would otherwise allow 5. Measured on MI355X: a 272-row verification call (1088 workgroups)
-// 21.3 -> 20.6 us with the limit, the headline's 1024 workgroups unchanged.
+// as the kernel's 96 VGPRs would otherwise allow 5. Measured on MI355X with this instantiation: a 272-row call of 1088
+// workgroups 21.3 -> 20.6 us with the limit, the headline's 1024 workgroups unchanged. (All-greedy batches run the
+// greedy-only instantiation without it.)
 constexpr unsigned SK_PAD_LDS = 16384;
 
 // GREEDY: every row of the batch is greedy (the selection code is left out: fewer registers, more workgroups per CU).
