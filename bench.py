@@ -31,34 +31,22 @@ METRIC = "sampled rows/s + logits HBM GB/s (% of peak), top-k/top-p, B=64, V=262
 HBM_PEAK_GBS = 8000.0
 MALL_BYTES = 256 << 20
 KERNEL = "fs::segment_kernel"
-SMALL_K = 64                                       # fs_sample_batch_hp's small-k kernel: k <= 64 or greedy rows
 
 
 def kernel_of(w, route, cus=256, verify=False):
-    """The kernel a call of this workload launches: fs_sample_batch_hp / fs_verify_hp (route "host") run the small-k
-    kernel when every row (stream) is greedy or has k <= 64 and no frequency / presence penalty, greedy rows with
-    frequency / presence penalties only on segments of 4096 logits (verification: no active penalty at all);
-    otherwise the fused kernel."""
+    """The kernel a call of this workload launches, as the library routes it (fs_route_plan): fs_sample_batch_hp /
+    fs_verify_hp (route "host") pick the small-k kernel (its greedy-only form for all-greedy batches) where the batch
+    fits it, else the fused kernel; fs_sample_batch / fs_verify (route "device") always run the fused kernel."""
     fused = (KERNEL, "segments, then a merging workgroup per row, one grid")
     if route != "host":
         return fused
-    p = w.params
-    greedy = (p["temperature"] <= 0) | (p["top_k"] == 1)
-    k = np.where((p["top_k"] > 0) & (p["top_k"] < w.V), p["top_k"], w.V)
-    fp = (p["frequency_penalty"] != 0) | (p["presence_penalty"] != 0)
-    fits = bool((greedy | ((k <= SMALL_K) & ~fp)).all())
-    if verify:
-        fits = fits and bool((((p["repetition_penalty"] == 1) & ~fp) | (p["repeat_last_n"] == 0)).all())
-    if not fits:
-        return fused
     from ferro_amd import _lib
-    nl, ns = ctypes.c_int32(), ctypes.c_int32()
-    if _lib.lib().fs_small_k_plan(cus, w.B, w.V, ctypes.byref(nl), ctypes.byref(ns)) != 0:
-        return fused
-    if bool((fp & (p["repeat_last_n"] != 0)).any()) and nl.value != 4:
-        return fused
-    return (f"fs::small_k_kernel<{nl.value}>",
-            f"{ns.value} segments of {1024 * nl.value} logits per row, the last segment of a row merges it, one grid")
+    kind, nl, ns, per_cu = _lib.route_plan(cus, w.params, w.V, total_rows=w.B, verify=verify)
+    if kind == 0:
+        return (KERNEL, f"segments ({per_cu} per CU), then a merging workgroup per row, one grid")
+    return (f"fs::small_k_kernel<{nl}>",
+            f"{ns} segments of {1024 * nl} logits per row, the last segment of a row merges it, one grid"
+            + (" (greedy-only form)" if kind == 2 else ""))
 
 # workload -> (constructor name in ferro_amd.workloads, entry point, description)
 WORKLOADS = {

@@ -44,6 +44,7 @@ SIGNATURES = {
     "fs_sample_batch_static": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P]),
     "fs_sample_batch_hp": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P]),
     "fs_small_k_plan": (ctypes.c_int, [_I32, _I32, _I32, _P, _P]),
+    "fs_route_plan": (ctypes.c_int, [_I32, _P, _I32, _I32, _I32, _I32, _P, _P, _P, _P]),
     "fs_argmax_batch": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _P, _P, _P, _P, _P]),
     "fs_verify": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P]),
     "fs_verify_hp": (ctypes.c_int, [_P, _P, _I64, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _P]),
@@ -115,3 +116,16 @@ def plan_layout(cus: int, xccs: int, B: int, V: int, static_ws: bool = False):
     rc = lib().fs_plan_layout(cus, xccs, B, V, 1 if static_ws else 0, ctypes.byref(n), ctypes.byref(t),
                               ctypes.byref(sl))
     return rc, n.value, t.value, sl.value
+
+
+def route_plan(cus: int, params, V: int, total_rows: int = None, verify: bool = False):
+    """fs_route_plan: (kernel, nl, nseg, per_cu) fs_sample_batch_hp / fs_verify_hp would launch for these host
+    parameter records (numpy structured array of fs_row_params); kernel 0 fused, 1 small-k, 2 greedy-only small-k."""
+    import numpy as np
+    p = np.ascontiguousarray(params)
+    n = len(p)
+    k, nl, ns, pc = (ctypes.c_int32() for _ in range(4))
+    rc = lib().fs_route_plan(cus, p.ctypes.data_as(ctypes.c_void_p), n, total_rows if total_rows else n, V,
+                             1 if verify else 0, ctypes.byref(k), ctypes.byref(nl), ctypes.byref(ns), ctypes.byref(pc))
+    check(rc, "fs_route_plan")
+    return k.value, nl.value, ns.value, pc.value

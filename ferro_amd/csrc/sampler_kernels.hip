@@ -5827,6 +5827,29 @@ int greedy_params(fs_context* ctx, int64_t B, hipStream_t st) {
     return FS_OK;
 }
 
+// The small-k kernel's plan for n host parameter records (B rows, or n_streams windows with `verify`): false when
+// the batch does not fit it (the fused kernel runs). nl / nseg: its segments; all_greedy: the greedy-only form;
+// capped: some row has a softcap; may_pen: some row has an active penalty window.
+struct SmallKChoice {
+    int nl = 0, nseg = 0;
+    bool all_greedy = true, capped = false, may_pen = false;
+};
+bool small_k_choice(int cus, const fs_row_params* h, int64_t n, int64_t B, int32_t V, bool verify, SmallKChoice& c) {
+    if (verify ? !small_k_windows(h, n, V) : !small_k_batch(h, n, V)) return false;
+    if (small_k_plan(cus, B, V, c.nl, c.nseg) != FS_OK) return false;
+    if ((int64_t)fs::XCDS * c.nseg * ((B + fs::XCDS - 1) / fs::XCDS) > 0x7fffffff) return false;
+    bool counts = false;
+    for (int64_t b = 0; b < n; ++b) {
+        const fs_row_params& p = h[b];
+        const bool fp = p.frequency_penalty != 0.0f || p.presence_penalty != 0.0f;
+        c.all_greedy = c.all_greedy && !(p.temperature > 0.0f && p.top_k != 1);
+        c.capped |= p.softcap > 0.0f;
+        c.may_pen |= (p.repetition_penalty != 1.0f || fp) && p.repeat_last_n != 0;
+        counts |= fp && p.repeat_last_n != 0;
+    }
+    return !(counts && c.nl != 4);               // count tables fit segments of 4096 logits only: the fused kernel
+}
+
 // Launches the small-k kernel when the batch fits it; *used = false (nothing launched) otherwise. a.mode selects
 // sampling (h_params: B records) or verification windows (h_params: n_streams records).
 int launch_small(fs_context* ctx, const fs::Args& a, const fs_row_params* h_params, hipStream_t st, bool& used) {
@@ -5836,12 +5859,12 @@ int launch_small(fs_context* ctx, const fs::Args& a, const fs_row_params* h_para
     if (rc != FS_OK) return rc;
     const bool verify = a.mode == fs::MODE_VERIFY;
     if (!ctx->seg_layout) return FS_OK;
-    if (verify ? !small_k_windows(h_params, a.n_streams, a.V) : !small_k_batch(h_params, a.B, a.V)) return FS_OK;
-    int nl = 0, nseg = 0;
-    if (small_k_plan(ctx->cus, a.B, a.V, nl, nseg) != FS_OK) return FS_OK;
+    SmallKChoice ch;
+    if (!small_k_choice(ctx->cus, h_params, verify ? (int64_t)a.n_streams : (int64_t)a.B, a.B, a.V, verify, ch))
+        return FS_OK;
+    const int nl = ch.nl, nseg = ch.nseg;
     const int64_t per_x = ((int64_t)a.B + fs::XCDS - 1) / fs::XCDS;
     const int64_t grid = (int64_t)fs::XCDS * nseg * per_x;
-    if (grid > 0x7fffffff) return FS_OK;
     rc = grow(ctx, 0, 0, verify ? (size_t)a.n_streams : 0);  // the error word (and the verify stream counters)
     if (rc != FS_OK) return rc;
     rc = grow_small(ctx, (size_t)a.B * nseg, (size_t)a.B);
@@ -5858,16 +5881,8 @@ int launch_small(fs_context* ctx, const fs::Args& a, const fs_row_params* h_para
 #ifdef FS_TRACE
     if (ctx->trace && grid * fs::TRACE_W <= ctx->trace_cap) k.trace = ctx->trace;
 #endif
-    bool capped = false, may_pen = false, counts = false, all_greedy = true;
-    for (int64_t b = 0; b < (verify ? (int64_t)a.n_streams : (int64_t)a.B); ++b) {
-        const fs_row_params& p = h_params[b];
-        const bool fp = p.frequency_penalty != 0.0f || p.presence_penalty != 0.0f;
-        all_greedy = all_greedy && !(p.temperature > 0.0f && p.top_k != 1);
-        capped |= p.softcap > 0.0f;
-        may_pen |= (p.repetition_penalty != 1.0f || fp) && p.repeat_last_n != 0;
-        counts |= fp && p.repeat_last_n != 0;
-    }
-    if (counts && nl != 4) return FS_OK;         // count tables fit segments of 4096 logits only: the fused kernel
+    const bool capped = ch.capped, all_greedy = ch.all_greedy;
+    bool may_pen = ch.may_pen;
     // a verification window reaches this kernel only without an active penalty (small_k_windows)
     may_pen = may_pen && !verify && a.hist && a.hist_off;
     const dim3 gd((unsigned)grid), bd(fs::SK_LT);
@@ -6098,6 +6113,33 @@ int fs_small_k_plan(int32_t cus, int32_t B, int32_t V, int32_t* nl, int32_t* nse
     *nl = l;
     *nseg = n;
     return rc == FS_OK ? FS_OK : FS_E_LIMIT;
+}
+
+int fs_route_plan(int32_t cus, const fs_row_params* h_params, int32_t n, int32_t total_rows, int32_t V,
+                  int32_t verify, int32_t* kernel, int32_t* nl, int32_t* nseg, int32_t* per_cu) {
+    if (cus < 1 || !h_params || n < 1 || total_rows < 1 || V < 1 || V > FS_MAX_VOCAB || !kernel || !nl || !nseg ||
+        !per_cu)
+        return FS_E_INVALID;
+    if (!verify && total_rows != n) return FS_E_INVALID;
+    SmallKChoice ch;
+    *nl = 0;
+    if (small_k_choice(cus, h_params, n, total_rows, V, verify != 0, ch)) {
+        *kernel = ch.all_greedy ? 2 : 1;
+        *nl = ch.nl;
+        *nseg = ch.nseg;
+        *per_cu = 0;
+        return FS_OK;
+    }
+    fs::Args a = {};
+    a.V = V;
+    a.mode = verify ? fs::MODE_VERIFY : fs::MODE_SAMPLE;
+    *per_cu = (!verify && mixed_merges(h_params, n, V)) ? 4 : 2;
+    int64_t items = 0, seg_grid = 0;
+    const int rc = plan(cus, a, total_rows, items, seg_grid, 0, *per_cu);
+    if (rc != FS_OK) return rc;
+    *kernel = 0;
+    *nseg = a.nseg;
+    return FS_OK;
 }
 
 int fs_sample_batch_static(fs_context* ctx, const float* d_logits, int64_t ld, int32_t B, int32_t V,

@@ -103,6 +103,14 @@ int fs_sample_batch_hp(fs_context* ctx, const float* d_logits, int64_t ld, int32
  * segments (fs_sample_batch_hp then runs fs_sample_batch). No counterpart in the reference (a planner check). */
 int fs_small_k_plan(int32_t cus, int32_t B, int32_t V, int32_t* nl, int32_t* nseg);
 
+/* Host-only: the kernel fs_sample_batch_hp (verify = 0: n = total_rows = B row records) or fs_verify_hp (verify != 0:
+ * n stream records over total_rows rows) launches for these host parameters, on a device with `cus` compute units
+ * whose XCD count divides 8: *kernel 0 the fused kernel (*nseg segments per row, *per_cu segments per CU of its
+ * layout), 1 the small-k kernel, 2 its greedy-only form (*nl float4 loads per thread, *nseg segments per row). No
+ * counterpart in the reference (a routing check for callers and tests). */
+int fs_route_plan(int32_t cus, const fs_row_params* h_params, int32_t n, int32_t total_rows, int32_t V,
+                  int32_t verify, int32_t* kernel, int32_t* nl, int32_t* nseg, int32_t* per_cu);
+
 /* fs_sample_batch without any allocation. No counterpart in the reference: it is for callers that cannot allocate
  * device memory during a call - code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
  * Same arguments, semantics and outputs as fs_sample_batch; ctx only carries settings (fs_set_wait_limit) and

@@ -147,3 +147,32 @@ def test_small_k_planner():
     for V in (1, 4095, 4096, 70001, 262144, 1 << 20):
         rc, nl, ns = plan(256, 4, V)
         assert rc == _lib.FS_OK and ns * 1024 * nl >= V and (ns - 1) * 1024 * nl < V and ns <= 64, V
+
+
+def test_route_plan_of_the_benchmark_configurations():
+    """fs_route_plan, the host parameters' kernel choice of fs_sample_batch_hp / fs_verify_hp, on every configuration
+    (host only): the small-k kernel for k <= 64 batches and for greedy ones (its greedy-only form, frequency /
+    presence counts only on 4096-logit segments), the fused kernel with four segments per CU for mixed k batches."""
+    from ferro_amd import workloads as W
+    rp = _lib.route_plan
+    assert rp(256, W.config1().params, 65536) == (1, 4, 16, 0)
+    assert rp(256, W.config2().params, 65536) == (2, 4, 16, 0)        # greedy, counts, NL = 4
+    assert rp(256, W.config3().params, 262144) == (1, 16, 16, 0)
+    w4 = W.config4()
+    assert rp(256, w4.params, w4.V, total_rows=w4.B, verify=True) == (2, 16, 4, 0)
+    w5 = W.config5()
+    k, nl, ns, pc = rp(256, w5.params, w5.V)
+    assert (k, pc, ns) == (0, 4, 4)
+    k, nl, ns, pc = rp(256, W.config3_all_tokens().params, 262144)
+    assert (k, pc) == (0, 2)
+    g = W.make_params(64, temperature=0.0, frequency_penalty=0.5)      # counts on 16384-logit segments: fused
+    assert rp(256, g, 262144)[0] == 0
+    g["frequency_penalty"] = 0.0
+    g["repetition_penalty"] = 1.3
+    assert rp(256, g, 262144)[:2] == (2, 16)                        # greedy with a repetition penalty
+    p = W.make_params(64, temperature=0.8, top_k=65)                    # k > 64: fused, uniform layout
+    assert rp(256, p, 262144)[0] == 0 and rp(256, p, 262144)[3] == 2
+    v = W.make_params(16, temperature=0.0, repetition_penalty=1.2)     # a window with a penalty: fused
+    assert rp(256, v, 65536, total_rows=272, verify=True)[0] == 0
+    with pytest.raises(_lib.SamplerError):
+        rp(256, W.config3().params, 262144, total_rows=65)              # sampling: one record per row
