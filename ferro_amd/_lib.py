@@ -65,6 +65,8 @@ SIGNATURES = {
     "fs_drng_draw": (ctypes.c_int, [_P, _P, _P, _P, _I32, _P]),
     "fs_decode_step": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P,
                                       ctypes.c_int64, _P]),
+    "fs_decode_step_hp": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _P,
+                                         ctypes.c_int64, _P]),
     "fs_drng_skip": (ctypes.c_int, [_P, _P, _P, _P]),
     "fs_drng_error": (ctypes.c_int, [_P, _P, _P]),
     "fs_strerror": (ctypes.c_char_p, [ctypes.c_int]),

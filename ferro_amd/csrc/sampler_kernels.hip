@@ -4824,6 +4824,12 @@ struct SkArgs {
     int n_streams, eos;
     int32_t* accepted;
     uint32_t* stream_cnt;                  // [n_streams]: rows finished (left at 0)
+    // a decode step (fs_decode_step_hp; NULL otherwise): draw streams and the histories with the tokens appended
+    uint64_t* dmt;
+    int32_t* didx;
+    int32_t* out_hist;
+    int64_t* out_hist_off;
+    int64_t out_cap;
 };
 
 // lane ^ D over the wave, in the VALU: DPP for D < 16 (both shifts in full exec, then an arithmetic select: a branch
@@ -4901,6 +4907,82 @@ __device__ __forceinline__ uint64_t merge_top64(uint64_t a_desc, uint64_t b_asc)
     uint64_t v = a_desc > b_asc ? a_desc : b_asc;
     v = bcx<32>(v, DESC); v = bcx<16>(v, DESC); v = bcx<8>(v, DESC); v = bcx<4>(v, DESC); v = bcx<2>(v, DESC);
     return bcx<1>(v, DESC);
+}
+
+// fs_decode_step_hp on the small-k kernel (the fused kernel's decode_hist_copy / row_u / decode_commit for this
+// kernel's merging workgroup): the stream's history copied to the new histories by the whole workgroup before the
+// merge; the draw read from the stream without advancing it; after the token, wave 0 appends it and advances the
+// stream (greedy rows draw nothing).
+__device__ __forceinline__ void sk_hist_copy(const SkArgs& a, int row) {
+    const int64_t h0 = a.hist_off ? a.hist_off[0] : 0, b = a.hist_off ? a.hist_off[row] : 0;
+    const int64_t e = a.hist_off ? a.hist_off[row + 1] : 0;
+    const int64_t nb = b - h0 + row;
+    for (int64_t i = threadIdx.x; i < e - b; i += SK_LT)
+        if (nb + i < a.out_cap) a.out_hist[nb + i] = a.hist[b + i];
+    if (threadIdx.x == 0) {
+        a.out_hist_off[row] = nb;
+        if (row == a.B - 1) a.out_hist_off[a.B] = e - h0 + a.B;
+        if (nb + (e - b) + 1 > a.out_cap) atomicOr(a.err, FS_DEVERR_HIST_APPEND);
+    }
+}
+__device__ __forceinline__ double sk_row_u(const SkArgs& a, int row) {
+    if (a.dmt) {
+        const uint64_t* mt = a.dmt + (int64_t)row * MT_N;
+        const int idx = a.didx[row];
+        const uint64_t y = idx < MT_N ? mt[idx] : mt_twist_one(mt[0], mt[1], mt[MT_M]);
+        return mt_canonical(mt_temper(y));
+    }
+    return a.u ? ld_const(a.u + row) : 0.0;
+}
+// Wave 0 alone: w is LDS scratch of MT_N entries. The twist in three passes, each reading every value it needs
+// before it writes: entries below N - M from old values only (all computed, then written); the rest in ascending
+// chunks of one wave (each reads its own and the next old entry and a new one below N - M; entry N - 1 the new
+// entry 0), so no entry is overwritten before it is read.
+__device__ __forceinline__ void sk_decode_commit(const SkArgs& a, int row, bool sampled, int tok, uint64_t* w) {
+    const int lane = lane_id();
+    if (a.out_hist_off && lane == 0) {
+        const int64_t h0 = a.hist_off ? a.hist_off[0] : 0, b = a.hist_off ? a.hist_off[row] : 0;
+        const int64_t e = a.hist_off ? a.hist_off[row + 1] : 0;
+        const int64_t at = b - h0 + row + (e - b);
+        if (at < a.out_cap) a.out_hist[at] = tok;
+    }
+    if (!a.dmt || !sampled) return;
+    uint64_t* mt = a.dmt + (int64_t)row * MT_N;
+    const int idx = a.didx[row];
+    if (idx < MT_N) {
+        if (lane == 0) a.didx[row] = idx + 1;
+        return;
+    }
+    auto wave_sync = []() {
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+    };
+    for (int t = lane; t < MT_N; t += WAVE) w[t] = mt[t];
+    wave_sync();
+    constexpr int LO = MT_N - MT_M, NLO = (LO + WAVE - 1) / WAVE;
+    uint64_t nv[NLO];
+#pragma unroll
+    for (int c = 0; c < NLO; ++c) {
+        const int t = c * WAVE + lane;
+        nv[c] = t < LO ? mt_twist_one(w[t], w[t + 1], w[t + MT_M]) : 0ull;
+    }
+    wave_sync();
+#pragma unroll
+    for (int c = 0; c < NLO; ++c) {
+        const int t = c * WAVE + lane;
+        if (t < LO) w[t] = nv[c];
+    }
+    wave_sync();
+    for (int t0 = LO; t0 < MT_N; t0 += WAVE) {
+        const int t = t0 + lane;
+        uint64_t v = 0ull;
+        if (t < MT_N) v = mt_twist_one(w[t], w[(t + 1) % MT_N], w[t - LO]);
+        wave_sync();
+        if (t < MT_N) w[t] = v;
+        wave_sync();
+    }
+    for (int t = lane; t < MT_N; t += WAVE) mt[t] = w[t];
+    if (lane == 0) a.didx[row] = 1;
 }
 
 struct SkShared {
@@ -5431,6 +5513,7 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
         return;
     }
     SK_TAG(13, 4);
+    if (a.out_hist_off) sk_hist_copy(a, row);                  // a decode step: every thread, before the merge
     // ---- the row's merge (the last of its segments): wave w folds lists w, w + SK_NW, ... (the first as stored,
     // the rest reversed: ascending), then wave 0 folds the waves' lists
     const uint64_t* rl = a.lists + (int64_t)row * a.nseg * SK_K;
@@ -5488,13 +5571,14 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
     } else if (kk == 0) {
         tok = 0; keep = 0;                                     // every logit NaN: token 0, nothing kept
     } else {
-        wave_softmax(fa, rc, lane < kk ? acc : 0ull, kk, a.u ? ld_const(a.u + row) : 0.0, tok, keep);
+        wave_softmax(fa, rc, lane < kk ? acc : 0ull, kk, sk_row_u(a, row), tok, keep);
     }
     if (a.mode != MODE_VERIFY) {
         if (lane == 0) {
             a.tok[row] = tok;
             if (a.keep) a.keep[row] = keep;
         }
+        if (a.out_hist_off || a.dmt) sk_decode_commit(a, row, !greedy, tok, &s.cand[0]);
     } else {
         // the last row of a stream to finish computes its accepted prefix (server.cpp:627-637): the stream's rows
         // run on several XCDs, so the tokens and the counter are agent-scope accesses
@@ -5877,6 +5961,7 @@ int launch_small(fs_context* ctx, const fs::Args& a, const fs_row_params* h_para
     k.lists = ctx->sk_lists; k.ticket = ctx->sk_ticket; k.err = ctx->err;
     k.mode = a.mode; k.rows = a.rows; k.row_off = a.row_off; k.n_streams = a.n_streams; k.eos = a.eos;
     k.accepted = a.accepted; k.stream_cnt = ctx->stream_cnt;
+    k.dmt = a.dmt; k.didx = a.didx; k.out_hist = a.out_hist; k.out_hist_off = a.out_hist_off; k.out_cap = a.out_cap;
     k.trace = nullptr;
 #ifdef FS_TRACE
     if (ctx->trace && grid * fs::TRACE_W <= ctx->trace_cap) k.trace = ctx->trace;
@@ -6412,9 +6497,10 @@ struct fs_drng {
 
 // fs_decode_step: fs_sample_batch with the draws taken from the device streams r (row s = stream s) and each row's
 // token appended to its stream's history out of place, in the sampling grid itself (one launch).
-int fs_decode_step(fs_context* ctx, fs_drng* r, const float* d_logits, int64_t ld, int32_t B, int32_t V,
-                   const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params, int32_t* d_tok,
-                   int32_t* d_keep, int32_t* d_out_hist, int64_t* d_out_hist_off, int64_t out_cap, void* stream) {
+int fs_decode_step_hp(fs_context* ctx, fs_drng* r, const float* d_logits, int64_t ld, int32_t B, int32_t V,
+                      const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params,
+                      const fs_row_params* h_params, int32_t* d_tok, int32_t* d_keep, int32_t* d_out_hist,
+                      int64_t* d_out_hist_off, int64_t out_cap, void* stream) {
     if (!ctx || !r || !d_params || !d_tok || !d_out_hist_off || out_cap < 0 || (out_cap > 0 && !d_out_hist) ||
         (d_hist == nullptr) != (d_hist_off == nullptr) || B > r->n)
         return FS_E_INVALID;
@@ -6429,7 +6515,19 @@ int fs_decode_step(fs_context* ctx, fs_drng* r, const float* d_logits, int64_t l
     a.u = nullptr; a.tok = d_tok; a.kcap = 0; a.keep = d_keep;
     a.mode = fs::MODE_SAMPLE; a.eos = -1;
     a.dmt = r->mt; a.didx = r->idx; a.out_hist = d_out_hist; a.out_hist_off = d_out_hist_off; a.out_cap = out_cap;
+    if (h_params) {
+        bool used = false;
+        rc = launch_small(ctx, a, h_params, (hipStream_t)stream, used);
+        if (rc != FS_OK || used) return rc;
+    }
     return launch(ctx, a, B, 0, (hipStream_t)stream);
+}
+
+int fs_decode_step(fs_context* ctx, fs_drng* r, const float* d_logits, int64_t ld, int32_t B, int32_t V,
+                   const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params, int32_t* d_tok,
+                   int32_t* d_keep, int32_t* d_out_hist, int64_t* d_out_hist_off, int64_t out_cap, void* stream) {
+    return fs_decode_step_hp(ctx, r, d_logits, ld, B, V, d_hist, d_hist_off, d_params, nullptr, d_tok, d_keep,
+                             d_out_hist, d_out_hist_off, out_cap, stream);
 }
 
 int fs_drng_create(int32_t n_streams, const uint64_t* seeds, void* stream, fs_drng** out) {

@@ -394,11 +394,13 @@ def hist_append(hist, hist_off, tok, row_off=None, count=None, out_cap=None, ctx
     return out, out_off
 
 
-def decode_step(logits, params, rng, hist=None, hist_off=None, out_cap=None, V=None, ctx=None, stream=None):
-    """fs_decode_step: one decode step in one launch - each row's draw from its DeviceRng stream (row s = stream s),
-    fs_sample_batch's token, and the token appended to the stream's history (server.cpp:603-606, then :342).
+def decode_step(logits, params, rng, hist=None, hist_off=None, out_cap=None, V=None, ctx=None, stream=None,
+                route=None):
+    """fs_decode_step(_hp): one decode step in one launch - each row's draw from its DeviceRng stream (row s = stream
+    s), fs_sample_batch's token, and the token appended to the stream's history (server.cpp:603-606, then :342).
     Returns (tok, keep, out_hist, out_off); out_hist holds out_cap ids (default: room for one more per stream), of
-    which out_off[-1] are used. Stays on the device."""
+    which out_off[-1] are used. Stays on the device. route as for sample_batch ("host": the host copy of the
+    parameters goes along, fs_decode_step_hp)."""
     logits, ld, n = _check_logits(logits, V)
     B = logits.shape[0]
     dev = logits.device
@@ -415,10 +417,16 @@ def decode_step(logits, params, rng, hist=None, hist_off=None, out_cap=None, V=N
     out = torch.empty(max(int(out_cap), 1), dtype=torch.int32, device=dev)
     out_off = torch.empty(B + 1, dtype=torch.int64, device=dev)
     ctx = ctx or Context.default(dev)
+    hp = params_array(params) if (route or ROUTE) == "host" and not isinstance(params, torch.Tensor) else None
     with ctx.lock:
-        check(lib().fs_decode_step(ctx.h, rng.h, _lptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p),
-                                   _ptr(tok), _ptr(keep), _ptr(out), _ptr(out_off), int(out_cap), _stream(stream)),
-              "fs_decode_step")
+        if hp is not None:
+            check(lib().fs_decode_step_hp(ctx.h, rng.h, _lptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p),
+                                          hp.ctypes.data_as(ctypes.c_void_p), _ptr(tok), _ptr(keep), _ptr(out),
+                                          _ptr(out_off), int(out_cap), _stream(stream)), "fs_decode_step_hp")
+        else:
+            check(lib().fs_decode_step(ctx.h, rng.h, _lptr(logits), ld, B, n, _ptr(hist), _ptr(hist_off), _ptr(p),
+                                       _ptr(tok), _ptr(keep), _ptr(out), _ptr(out_off), int(out_cap),
+                                       _stream(stream)), "fs_decode_step")
     return tok, keep, out, out_off
 
 

@@ -218,6 +218,15 @@ int fs_decode_step(fs_context* ctx, fs_drng* r, const float* d_logits, int64_t l
                    const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params, int32_t* d_tok,
                    int32_t* d_keep, int32_t* d_out_hist, int64_t* d_out_hist_off, int64_t out_cap, void* stream);
 
+/* fs_decode_step with a host copy of the parameters too (h_params: B records, as fs_sample_batch_hp): batches the
+ * small-k kernel fits run on it, with the same three additions in each row's merge; others run fs_decode_step.
+ * Same outputs and stream semantics. No counterpart call in the reference (the server holds its SamplerParams on
+ * the host, server.cpp:603-606). */
+int fs_decode_step_hp(fs_context* ctx, fs_drng* r, const float* d_logits, int64_t ld, int32_t B, int32_t V,
+                      const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params,
+                      const fs_row_params* h_params, int32_t* d_tok, int32_t* d_keep, int32_t* d_out_hist,
+                      int64_t* d_out_hist_off, int64_t out_cap, void* stream);
+
 /* The penalty stage alone, in place: row b of d_logits is left exactly as ferro's sample() leaves its host row
  * (sampler.cpp:11-18: each distinct window id in [0, V) once, l > 0 ? l/rep : l*rep, then the frequency/presence
  * extension). For callers that read the penalised row back (lm_cli.cpp:353); fs_sample_batch does not need it (it

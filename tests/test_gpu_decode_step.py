@@ -1,4 +1,4 @@
-"""fs_decode_step: one decode step in one launch - each stream's draw from its device mt19937_64 stream, the sampled
+"""fs_decode_step(_hp): one decode step in one launch - each stream's draw from its device mt19937_64 stream, the sampled
 token, and the token appended to the stream's history (server.cpp:603-606, then gen_token's push_back at :342) -
 against the oracle's decode loop (sample each stream with its own std::mt19937_64 draws, then append), which is
 pinned against ferro's Sampler objects. Includes steps across the engine's twists (every 312 draws), large rows
@@ -25,12 +25,17 @@ def say(*a):
     print(*a, flush=True)
 
 
-@pytest.fixture(scope="module", autouse=True)
-def gpu():
+@pytest.fixture(scope="module", autouse=True, params=["host", "device"])
+def gpu(request):
+    """Every test runs twice: with the host copy of the parameters (fs_decode_step_hp: the small-k kernel for the
+    batches it fits) and with the device copy only (fs_decode_step: the fused kernel)."""
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     F.sampler.Context.default()
+    F.sampler.ROUTE = request.param
+    say(f"== route {request.param}")
     yield
+    F.sampler.ROUTE = "host"
     torch.cuda.synchronize()
 
 
@@ -121,3 +126,23 @@ def test_decode_step_capacity():
     assert bits & 4, bits                               # FS_DEVERR_HIST_APPEND
     np.testing.assert_array_equal(oo.cpu().numpy(), [0, 3, 5, 6, 10])
     assert F.device_error() == 0
+
+
+def test_decode_steps_small_k_serving_rows():
+    """Serving rows that the small-k kernel takes on the host route: top-k 40-64 with top-p and repetition windows,
+    greedy rows among them (one with frequency / presence counts), then an all-greedy batch (the greedy-only kernel:
+    no draw consumed, tokens appended)."""
+    rng = np.random.default_rng(64)
+    S, V, steps = 12, 65536, 5
+    p = W.make_params(S, temperature=0.8, top_k=64, top_p=0.95, repetition_penalty=1.1)
+    p["top_k"][3::4] = 40
+    p["temperature"][1] = 0.0
+    p["temperature"][5] = 0.0
+    p["frequency_penalty"][5], p["presence_penalty"][5] = 0.4, 0.2
+    p["repeat_last_n"][7] = 8
+    seeds = list(range(500, 500 + S))
+    hist0 = [list(W.zipf_ids(rng, V, int(rng.integers(0, 300)))) for _ in range(S)]
+    rows = [W.mixture_logits(rng, S, V) for _ in range(steps)]
+    _check(rows, p, seeds, hist0)
+    g = W.make_params(4, temperature=0.0, repetition_penalty=1.2)
+    _check([W.mixture_logits(rng, 4, V) for _ in range(3)], g, [1, 2, 3, 4], [[5, 6], [], [7], [8, 8, 8]])
