@@ -517,6 +517,48 @@ def F_device_error(L, ctx, sh):
     return bits.value if rc == 0 else -1
 
 
+def run_decode(args, torch):
+    """The one-launch decode step on cfg3's batch (fs_decode_step_hp: the small-k kernel; fs_decode_step: the fused
+    kernel): each step samples every stream from its device draw stream and appends the token to its history, whose
+    output becomes the next step's input. The same logits every step (a model's output would differ); µs per step
+    from HIP events on the stream, launched one by one. Tokens of the two routes are compared step by step."""
+    import ferro_amd as F
+    from ferro_amd import workloads as W
+    w = W.config3()
+    x = torch.from_numpy(w.logits).cuda()
+    out = {"metric": "one-launch decode step (sample + draw + history append), cfg3's batch", "unit": "us/step",
+           "note": "HIP events around each Python call (its tensor allocations and launch included); the kernel "
+                   "time alone comes from rocprofv3 (profiles/decode_step_cfg3_kernel_trace.md)",
+           "higher_is_better": False, "n_gpus": 1, "dtype": "f32", "steps": args.steps, "warmup": args.warmup,
+           "data": "synthetic (cfg3's rows every step)", "config": {"workload": "decode: cfg3 B=64 x V=262144"}}
+    toks = {}
+    for route, entry in (("host", "fs_decode_step_hp"), ("device", "fs_decode_step")):
+        d = F.DeviceRng(np.arange(1, w.B + 1, dtype=np.uint64))
+        hist = torch.from_numpy(w.hist).cuda()
+        off = torch.from_numpy(w.hist_off).cuda()
+        cap = int(w.hist.size + w.B * (args.warmup + args.steps + 1))
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        seq = []
+        for i in range(args.warmup + args.steps):
+            if i >= args.warmup:
+                ev[i - args.warmup][0].record()
+            tok, _, hist, off = F.decode_step(x, w.params, d, hist=hist, hist_off=off, out_cap=cap, route=route)
+            if i >= args.warmup:
+                ev[i - args.warmup][1].record()
+            seq.append(tok)
+        torch.cuda.synchronize()
+        if F.device_error() != 0:
+            raise RuntimeError(f"{entry}: device error bits set")
+        toks[route] = torch.stack(seq).cpu().numpy()
+        out[f"{route}_us_per_step"] = float(np.median([a.elapsed_time(b) for a, b in ev]) * 1000.0)
+        out[f"{route}_entry"] = entry
+    out["tokens_equal_across_routes"] = bool(np.array_equal(toks["host"], toks["device"]))
+    if not out["tokens_equal_across_routes"]:
+        raise RuntimeError("the two decode routes disagree")
+    out["value"] = out["host_us_per_step"]
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -524,9 +566,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=list(WORKLOADS) + ["dropin", "all"], default="cfg3",
+    ap.add_argument("--workload", choices=list(WORKLOADS) + ["dropin", "decode", "all"], default="cfg3",
                     help="cfg3 (default): the headline; cfg1..cfg5: BASELINE.json's configurations; topk0: cfg3 with "
-                         "top_k = 0; dropin: the C++ drop-in's per-call latency on one row; all: one line each")
+                         "top_k = 0; dropin: the C++ drop-in's per-call latency on one row; decode: the one-launch "
+                         "decode step on cfg3's batch, both entry points; all: one line each")
     ap.add_argument("--breakdown", action="store_true",
                     help="instead of the bench line: per-stage ablation timings of the workload (one JSON line)")
     ap.add_argument("--host-rows", action="store_true",
@@ -550,6 +593,10 @@ def main():
         if name == "dropin":
             if not args.breakdown:
                 print(json.dumps(run_dropin(args)), flush=True)
+            continue
+        if name == "decode":
+            if not args.breakdown:
+                print(json.dumps(run_decode(args, torch)), flush=True)
             continue
         if args.breakdown:
             if WORKLOADS[name][1] == "sample":
