@@ -5890,11 +5890,8 @@ bool small_k_windows(const fs_row_params* h, int64_t S, int32_t V) {
 }
 
 // B greedy parameter records without penalties on the device (filled by a kernel on st, no memset: the call may be
-// captured) and on the host.
+// captured) and on the host. The caller holds ctx->mu.
 int greedy_params(fs_context* ctx, int64_t B, hipStream_t st) {
-    std::lock_guard<std::mutex> g(ctx->mu);
-    int rc = device_of(ctx);
-    if (rc != FS_OK) return rc;
     if ((size_t)B <= ctx->greedy_cap) return FS_OK;
     const size_t cap = std::max<size_t>((size_t)B, 2 * ctx->greedy_cap);
     release(ctx, ctx->greedy);
@@ -5936,11 +5933,20 @@ bool small_k_choice(int cus, const fs_row_params* h, int64_t n, int64_t B, int32
 
 // Launches the small-k kernel when the batch fits it; *used = false (nothing launched) otherwise. a.mode selects
 // sampling (h_params: B records) or verification windows (h_params: n_streams records).
-int launch_small(fs_context* ctx, const fs::Args& a, const fs_row_params* h_params, hipStream_t st, bool& used) {
+// h_params NULL: every row greedy without penalties (fs_argmax_batch without parameters): the context's greedy
+// records stand for the parameters, on the device and the host.
+int launch_small(fs_context* ctx, const fs::Args& a_in, const fs_row_params* h_params, hipStream_t st, bool& used) {
     used = false;
     std::lock_guard<std::mutex> g(ctx->mu);
     int rc = device_of(ctx);
     if (rc != FS_OK) return rc;
+    fs::Args a = a_in;
+    if (!h_params) {
+        rc = greedy_params(ctx, a.B, st);
+        if (rc != FS_OK) return rc;
+        h_params = ctx->h_greedy.data();
+        a.params = ctx->greedy;
+    }
     const bool verify = a.mode == fs::MODE_VERIFY;
     if (!ctx->seg_layout) return FS_OK;
     SmallKChoice ch;
@@ -6290,14 +6296,11 @@ int fs_argmax_batch(fs_context* ctx, const float* d_logits, int64_t ld, int32_t 
     if (!d_params) {
         // no penalties: every row greedy, so the small-k kernel's greedy path takes the batch (its parameters are
         // greedy records the context keeps on the device and the host)
-        rc = greedy_params(ctx, B, (hipStream_t)stream);
-        if (rc != FS_OK) return rc;
         fs::Args g = a;
         g.mode = fs::MODE_SAMPLE;
         g.hist = nullptr;
-        g.params = ctx->greedy;
         bool used = false;
-        rc = launch_small(ctx, g, ctx->h_greedy.data(), (hipStream_t)stream, used);
+        rc = launch_small(ctx, g, nullptr, (hipStream_t)stream, used);
         if (rc != FS_OK || used) return rc;
     }
     return launch(ctx, a, B, 0, (hipStream_t)stream);
