@@ -89,10 +89,12 @@ int fs_sample_batch(fs_context* ctx, const float* d_logits, int64_t ld, int32_t 
 /* fs_sample_batch with the parameters also in host memory: h_params holds the same B records as d_params (the
  * caller fills both; ferro's call sites hold SamplerParams on the host, sampler.h:25, server.cpp:603-606). With the
  * host copy the library picks the kernel for the batch without reading device memory: batches whose every row is
- * greedy or samples from at most 64 candidates (k = top_k, or V when top_k is 0) with no frequency / presence
- * penalty run on a kernel made for them (every segment's loads issued at once, bitonic sorts in registers); other
- * batches, and h_params = NULL, run fs_sample_batch. Same outputs as fs_sample_batch. h_params is read before the
- * call returns. */
+ * greedy (frequency / presence penalties only where rows split into segments of 4096 logits) or samples from at
+ * most 64 candidates (k = top_k, or V when top_k is 0) with no frequency / presence penalty run on a kernel made for
+ * them (every segment's loads issued at once, bitonic sorts in registers; all-greedy batches a greedy-only form);
+ * batches mixing rows of 64 < k <= 2048 with cheaper rows run fs_sample_batch's kernel with about twice its segments;
+ * other batches, and h_params = NULL, run fs_sample_batch. fs_route_plan reports the choice. Same outputs as
+ * fs_sample_batch. h_params is read before the call returns. */
 int fs_sample_batch_hp(fs_context* ctx, const float* d_logits, int64_t ld, int32_t B, int32_t V,
                        const int32_t* d_hist, const int64_t* d_hist_off, const fs_row_params* d_params,
                        const fs_row_params* h_params, const double* d_u, int32_t* d_tok, int32_t kcap,
