@@ -4823,7 +4823,7 @@ struct SkArgs {
     const int64_t* row_off;                // stream -> rows
     int n_streams, eos;
     int32_t* accepted;
-    uint32_t* stream_cnt;                  // [n_streams]: rows finished (left at 0)
+    uint32_t* stream_cnt;                  // [3 n_streams]: 64-bit counts + stop bits, 32-bit counts (left at 0)
     // a decode step (fs_decode_step_hp; NULL otherwise): draw streams and the histories with the tokens appended
     uint64_t* dmt;
     int32_t* didx;
@@ -5581,17 +5581,41 @@ __global__ __launch_bounds__(SK_LT) void small_k_kernel(const float* logits, int
         if (a.out_hist_off || a.dmt) sk_decode_commit(a, row, !greedy, tok, &s.cand[0]);
     } else {
         // the last row of a stream to finish computes its accepted prefix (server.cpp:627-637): the stream's rows
-        // run on several XCDs, so the tokens and the counter are agent-scope accesses
+        // run on several XCDs, so the exchange is agent-scope.
         const int64_t r0 = ld_const(a.row_off + pidx);
         const int m = (int)(ld_const(a.row_off + pidx + 1) - r0);
+        if (m <= 32) {
+            // Streams of up to 32 rows: one 64-bit atomic per row carries everything - the count of rows done in its
+            // high word, in its low word a bit for each row that ends the walk (an eos token, the last row, or a
+            // token other than the next row's draft). The last row's fetched value holds every other row's bit, so
+            // its accepted prefix is the lowest set bit + 1, with no token exchanged and no wait for stores.
+            if (lane == 0) {
+                a.tok[row] = tok;
+                const int rr = row - (int)r0;
+                const bool stop = (a.eos >= 0 && tok == a.eos) || rr + 1 >= m || tok != ld_const(a.rows + row + 1);
+                const uint64_t mine = stop ? (1ull << rr) : 0ull;
+                uint64_t* cnt = reinterpret_cast<uint64_t*>(a.stream_cnt) + pidx;
+                const uint64_t old = __hip_atomic_fetch_add(cnt, (1ull << 32) | mine, __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_AGENT);
+                if ((uint32_t)(old >> 32) == (uint32_t)m - 1u) {
+                    __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    a.accepted[pidx] = __ffs((int)((uint32_t)old | (uint32_t)mine));
+                }
+            }
+            SK_MARK(8);
+            SK_FLUSH();
+            return;
+        }
+        // longer streams: the token at agent scope, a row counter (after the 64-bit words), the last row walks
+        uint32_t* cnt32 = a.stream_cnt + 2 * (int64_t)a.n_streams + pidx;
         uint32_t old = 0u;
         if (lane == 0) {
             st_agent(&a.tok[row], (int32_t)tok);
             vm_drain();
-            old = __hip_atomic_fetch_add(&a.stream_cnt[pidx], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            old = __hip_atomic_fetch_add(cnt32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         if (read_lane(old, 0) == (uint32_t)m - 1u) {
-            if (lane == 0) st_agent(&a.stream_cnt[pidx], 0u);
+            if (lane == 0) st_agent(cnt32, 0u);
             const int acc = accepted_prefix(a.tok, a.rows, r0, m, a.eos);
             if (lane == 0) a.accepted[pidx] = acc;
         }
@@ -5955,7 +5979,9 @@ int launch_small(fs_context* ctx, const fs::Args& a_in, const fs_row_params* h_p
     const int nl = ch.nl, nseg = ch.nseg;
     const int64_t per_x = ((int64_t)a.B + fs::XCDS - 1) / fs::XCDS;
     const int64_t grid = (int64_t)fs::XCDS * nseg * per_x;
-    rc = grow(ctx, 0, 0, verify ? (size_t)a.n_streams : 0);  // the error word (and the verify stream counters)
+    // the error word and the verify stream counters: a 64-bit word per stream, then the 32-bit counters of streams
+    // longer than 32 rows
+    rc = grow(ctx, 0, 0, verify ? 3 * (size_t)a.n_streams : 0);
     if (rc != FS_OK) return rc;
     rc = grow_small(ctx, (size_t)a.B * nseg, (size_t)a.B);
     if (rc != FS_OK) return rc;

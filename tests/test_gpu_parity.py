@@ -120,6 +120,39 @@ def test_cfg4_verify_full():
     assert (oacc > 1).any() and (oacc < 17).any()
 
 
+@pytest.mark.parametrize("seed", [0, 1])
+def test_verify_windows_lengths_and_eos(seed):
+    """Verification windows without a penalty (the small-k kernel on the host route): streams of 1 to 40 rows (the
+    one-atomic exchange takes windows of up to 32 rows, longer ones the token walk), drafts that match the row's
+    argmax for a while and then stop, an eos token inside a window, greedy and sampled streams."""
+    rng = np.random.default_rng(seed + 40)
+    V = 8192
+    lens = [1, 2, 5, 17, 31, 32, 33, 40]
+    S = len(lens)
+    row_off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    R = int(row_off[-1])
+    x = (rng.standard_normal((R, V)) * 2).astype(np.float32)
+    am = np.argmax(x, axis=1)
+    rows = rng.integers(0, V, R).astype(np.int32)
+    for st in range(S):
+        r0, m = int(row_off[st]), lens[st]
+        good = int(rng.integers(0, m + 1))                     # drafts equal to the previous row's argmax
+        for r in range(1, min(good, m)):
+            rows[r0 + r] = am[r0 + r - 1]
+    eos = int(am[int(row_off[3]) + 2])                          # stream 3's third row yields eos
+    p = W.make_params(S, temperature=0.0, repetition_penalty=1.0)
+    p["temperature"][1::3] = 0.9
+    p["top_k"][1::3] = 40
+    u = rng.random(R)
+    hist = np.zeros(0, np.int32)
+    hist_off = np.zeros(S + 1, np.int64)
+    tok, acc = F.verify(torch.from_numpy(x).cuda(), rows, row_off, p, u=u, hist=hist, hist_off=hist_off, eos_id=eos)
+    otok, oacc = O.verify(x, rows, row_off, hist, hist_off, p, u, eos_id=eos)
+    np.testing.assert_array_equal(tok.cpu().numpy(), otok)
+    np.testing.assert_array_equal(acc.cpu().numpy(), oacc)
+    assert F.device_error() == 0
+
+
 def test_verify_sampled_with_penalties():
     rng = np.random.default_rng(7)
     S, M, V = 6, 5, 3000
