@@ -2691,20 +2691,40 @@ __device__ __forceinline__ void merge_row(const Args& a, const RowCtx& rc, Share
             if (a.keep) a.keep[row] = keep;
         }
     } else if (tid < WAVE) {
-        // verify: the last row of a stream to finish computes the accepted prefix (server.cpp:627-637), wave 0
+        // verify: the last row of a stream to finish computes the accepted prefix (server.cpp:627-637), wave 0.
+        // Streams of up to 32 rows: one 64-bit atomic per row (the count of rows done, and a bit for each row that
+        // ends the walk), the last row's fetched value gives the prefix; longer ones: tokens at agent scope, a row
+        // counter after the 64-bit words, and the walk.
         const int st = rc.pidx;
         const int64_t r0 = a.row_off[st];
         const int m = (int)(a.row_off[st + 1] - r0);
-        uint32_t old = 0u;
-        if (tid == 0) {
-            st_agent(&a.tok[row], (int32_t)tok);
-            vm_drain();
-            old = __hip_atomic_fetch_add(&a.stream_cnt[st], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        if (read_lane(old, 0) == (uint32_t)m - 1u) {
-            if (tid == 0) st_agent(&a.stream_cnt[st], 0u);
-            const int acc = accepted_prefix(a.tok, a.rows, r0, m, a.eos);
-            if (tid == 0) a.accepted[st] = acc;
+        if (m <= 32) {
+            if (tid == 0) {
+                a.tok[row] = tok;
+                const int rr = row - (int)r0;
+                const bool stop = (a.eos >= 0 && tok == a.eos) || rr + 1 >= m || tok != a.rows[row + 1];
+                const uint64_t mine = stop ? (1ull << rr) : 0ull;
+                uint64_t* cnt = reinterpret_cast<uint64_t*>(a.stream_cnt) + st;
+                const uint64_t old = __hip_atomic_fetch_add(cnt, (1ull << 32) | mine, __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_AGENT);
+                if ((uint32_t)(old >> 32) == (uint32_t)m - 1u) {
+                    __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    a.accepted[st] = __ffs((int)((uint32_t)old | (uint32_t)mine));
+                }
+            }
+        } else {
+            uint32_t* cnt32 = a.stream_cnt + 2 * (int64_t)a.n_streams + st;
+            uint32_t old = 0u;
+            if (tid == 0) {
+                st_agent(&a.tok[row], (int32_t)tok);
+                vm_drain();
+                old = __hip_atomic_fetch_add(cnt32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            if (read_lane(old, 0) == (uint32_t)m - 1u) {
+                if (tid == 0) st_agent(cnt32, 0u);
+                const int acc = accepted_prefix(a.tok, a.rows, r0, m, a.eos);
+                if (tid == 0) a.accepted[st] = acc;
+            }
         }
     }
     __syncthreads();                                   // LDS is reused by the caller's next chunk
@@ -6040,7 +6060,8 @@ int launch(fs_context* ctx, fs::Args a, int64_t rows, int64_t streams, hipStream
     int64_t items = 0, seg_grid = 0;
     rc = plan(ctx->cus, a, rows, items, seg_grid, 0, per_cu);
     if (rc != FS_OK) return rc;
-    rc = grow(ctx, (size_t)(items > 0 ? items : 1), (size_t)rows, (size_t)(streams > 0 ? streams : 1));
+    // verify: a 64-bit word per stream, then the 32-bit counters of streams longer than 32 rows
+    rc = grow(ctx, (size_t)(items > 0 ? items : 1), (size_t)rows, (size_t)(streams > 0 ? 3 * streams : 1));
     if (rc != FS_OK) return rc;
     if (capturing(st)) ctx->captured = true;
     a.cand = ctx->cand; a.meta = ctx->meta; a.rhist = ctx->rhist; a.rmass = ctx->rmass;
